@@ -1,0 +1,213 @@
+#!/usr/bin/env python3
+"""Benchmark: Qwen3-VL-8B-shape decoder layer, bf16 prefill at S=4096 (headline) + B=32 decode.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--seq 4096] [--no-cpu-baseline] [--no-decode]
+
+One step = one CudaTextDecoderLayer forward over a (1, S, 4096) batch of
+synthetic N(0,1) inputs with N(0,0.02) weights, all resident in HBM before
+timing. Prints ONE JSON line on stdout; details go to stderr.
+
+roofline: the dominant kernel (the fused gate/up/SwiGLU GEMM, 2*S*4096*12288*2
+FLOP per launch) timed with HIP events on the stream it runs on, against the
+MI355X dense bf16 MFMA peak. cpu_baseline: the CPU oracle (a restatement of the
+reference's torch path) on this host's cores, same shapes, bf16.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_gpu(fn, steps: int, warmup: int) -> float:
+    """Average ms per call, HIP events on torch's current stream (where every op launches)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def cpu_baseline(cfg, seq: int, layer, budget_s: float = 20.0) -> dict:
+    """The oracle's decoder layer on CPU tensors (bf16), 1 warm-up + timed runs within the budget."""
+    import torch
+
+    from oracle import layers as L
+    from oracle import ops as O
+    threads = torch.get_num_threads()
+    p = {n: t.detach().to("cpu") for n, t in layer.state_dict().items()}
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(1, seq, cfg.hidden, generator=g).to(torch.bfloat16)
+    pos = torch.arange(seq).view(1, 1, seq).expand(3, 1, seq)
+    cos3, sin3 = O.mrope_cos_sin(pos, cfg.head_dim, cfg.theta)
+
+    def run():
+        return L.text_decoder_layer(x, p, num_heads=cfg.heads, num_kv_heads=cfg.kv_heads, head_dim=cfg.head_dim,
+                                    eps=cfg.eps, cos_3d=cos3, sin_3d=sin3, mrope_section=list(cfg.mrope_section))
+
+    t0 = time.perf_counter()
+    run()
+    first = time.perf_counter() - t0
+    times = []
+    while sum(times) + first < budget_s and len(times) < 3:
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    if not times:
+        times = [first]
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": round(seq / med, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"oracle decoder layer (torch CPU, bf16) at S={seq}, 1 warm-up + median of {len(times)} "
+                      f"run(s), {med:.2f} s/layer"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--seq", type=int, default=4096)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: this build runs on a single GPU (no multi-GPU path); "
+              "run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from qwen3_5_vl_cuda_custom_amd import kernels as K
+    from qwen3_5_vl_cuda_custom_amd import workloads as W
+
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+    cfg = W.C2
+    S = args.seq
+    with torch.inference_mode():
+        layer = W.make_text_layer(cfg, torch.bfloat16, dev, seed=0)
+        x, pos = W.text_inputs(cfg, 1, S, torch.bfloat16, dev, seed=0)
+        rope = W.make_rope(cfg, dev)
+        binding = rope.bind(pos)
+
+        def step():
+            return layer(x, binding)
+
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ms_events = time_gpu(step, args.steps, 0)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ms = max(ms_events, wall * 1e3 / args.steps)
+        tok_s = S / (ms / 1e3)
+        layer_flop = cfg.gemm_flops_per_token() * S + cfg.causal_attn_flops(S)
+        layer_tflops = layer_flop / (ms / 1e3) / 1e12
+        log(f"prefill S={S}: {ms:.3f} ms/layer, {tok_s:,.0f} tok/s, {layer_tflops:.1f} TFLOP/s "
+            f"({layer_tflops / PEAK_BF16_TFLOPS:.1%} of bf16 peak)")
+
+        # Dominant kernel: the fused gate/up/SwiGLU GEMM on the post-attention activations.
+        h = layer.post_attention_layernorm(x)
+        wg, wu = layer.mlp.gate_proj.weight, layer.mlp.up_proj.weight
+        gemm_ms = time_gpu(lambda: K.matmul_swiglu(h, wg, wu), args.steps, 3)
+        gemm_flop = 2 * S * cfg.hidden * cfg.intermediate * 2
+        gemm_tflops = gemm_flop / (gemm_ms / 1e3) / 1e12
+        log(f"dominant kernel gate/up+SwiGLU GEMM (M={S}, N=2x{cfg.intermediate}, K={cfg.hidden}): "
+            f"{gemm_ms:.3f} ms, {gemm_tflops:.1f} TFLOP/s ({gemm_tflops / PEAK_BF16_TFLOPS:.1%})")
+
+        # Other GEMMs of the layer, for the record.
+        a = torch.empty(S, cfg.hidden, dtype=torch.bfloat16, device=dev).normal_()
+        detail = {}
+        for name, w in [("q_proj", layer.self_attn.q_proj.weight), ("k_proj", layer.self_attn.k_proj.weight),
+                        ("o_proj", layer.self_attn.o_proj.weight)]:
+            t = time_gpu(lambda w=w: K.matmul(a, w), 10, 2)
+            detail[name] = round(2 * S * w.shape[0] * w.shape[1] / (t / 1e3) / 1e12, 1)
+        act = torch.empty(S, cfg.intermediate, dtype=torch.bfloat16, device=dev).normal_()
+        t = time_gpu(lambda: K.matmul(act, layer.mlp.down_proj.weight), 10, 2)
+        detail["down_proj"] = round(2 * S * cfg.hidden * cfg.intermediate / (t / 1e3) / 1e12, 1)
+        q = torch.empty(1, cfg.heads, S, cfg.head_dim, dtype=torch.bfloat16, device=dev).normal_()
+        kk = torch.empty(1, cfg.kv_heads, S, cfg.head_dim, dtype=torch.bfloat16, device=dev).normal_()
+        t = time_gpu(lambda: K.flash_attention(q, kk, kk, cfg.head_dim ** -0.5, True, 4), 10, 2)
+        detail["flash_attention"] = round(cfg.causal_attn_flops(S) / (t / 1e3) / 1e12, 1)
+        log(f"per-kernel TFLOP/s: {detail}")
+        del a, act, q, kk
+
+        decode = None
+        if not args.no_decode:
+            case = W.make_decode_case(cfg, batch=32, capacity=8193, device=dev, seed=0, layer=layer)
+            lens0 = case.cache.lens.clone()
+            dbind = case.rope.bind(case.positions)
+
+            def dstep():
+                case.cache.lens.copy_(lens0)
+                return case.layer(case.x, dbind, kv_cache=case.cache)
+
+            dms = time_gpu(dstep, max(args.steps, 20), args.warmup)
+            wbytes = sum(t.numel() * t.element_size() for t in layer.parameters())
+            kvbytes = int((case.lens + 1).sum()) * cfg.kv_heads * cfg.head_dim * 2 * 2
+            gbs = (wbytes + kvbytes) / (dms / 1e3) / 1e9
+            decode = {"tok_s": round(32 / (dms / 1e3), 1), "ms_per_step": round(dms, 4),
+                      "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
+                      "bytes_per_step": wbytes + kvbytes, "batch": 32, "kv_lens_sum": int(case.lens.sum())}
+            log(f"decode B=32: {dms:.3f} ms/step, {decode['tok_s']:,.0f} tok/s, {gbs:,.0f} GB/s "
+                f"({gbs / PEAK_HBM_GBS:.1%} of HBM)")
+            del case
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        with torch.inference_mode():
+            cpu = cpu_baseline(cfg, S, layer)
+        log(f"cpu baseline: {cpu}")
+
+    out = {
+        "metric": "decoder-layer prefill tokens/s (8B, S=4096) + decode tok/s; % MFMA/HBM roofline",
+        "value": round(tok_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) weights, N(0,1) inputs)",
+        "config": {"workload": "qwen3vl-8b-shape dense decoder layer, bf16 prefill", "batch": 1, "seq_len": S,
+                   "hidden": cfg.hidden, "heads": f"{cfg.heads}q/{cfg.kv_heads}kv x {cfg.head_dim}",
+                   "intermediate": cfg.intermediate, "parallelism": "single GPU"},
+        "layer_tflops": round(layer_tflops, 1),
+        "layer_mfma_frac": round(layer_tflops / PEAK_BF16_TFLOPS, 4),
+        "roofline": {"bound": "mfma", "kernel": "gemm_bf16 gate/up+SwiGLU (M=S, N=2x12288, K=4096)",
+                     "achieved": round(gemm_tflops, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(gemm_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None},
+        "kernel_tflops": detail,
+        "decode": decode,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,179 @@
+/* C-ABI of libq3vl.so: the MI355X (gfx950) kernels of the Qwen3-VL operator layer.
+ *
+ * Conventions (all entry points):
+ *  - Plain device pointers, int64 sizes and element strides; the innermost
+ *    dimension of every tensor is contiguous.
+ *  - `dtype` is a q3_dtype; every tensor of a call shares it unless stated.
+ *  - `stream` is a hipStream_t passed as void*; work is enqueued on it and the
+ *    call never synchronises.
+ *  - Return 0 on success; a negative q3_status when argument validation
+ *    failed (checked on the host before anything touches the device, so these
+ *    paths work without a GPU); a positive value is the hipError_t of a failed
+ *    launch.
+ *  - The library allocates nothing: callers pass outputs and, where a
+ *    *_workspace_bytes query says so, a device workspace. It keeps no pointer
+ *    after returning and has no global state.
+ *
+ * Reference interfaces replaced (paths relative to the reference's
+ * CUDA_qwen3_5-main/CUDA_qwen3_5-main/cuda_qwen3_vl/): the torch-op schemas
+ * registered in csrc/<op>_op.cpp and called by kernels/<op>.py.
+ */
+#ifndef Q3VL_H
+#define Q3VL_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define Q3VL_ABI_VERSION 1
+
+typedef enum { Q3_F32 = 0, Q3_BF16 = 1 } q3_dtype;
+
+typedef enum {
+  Q3_OK = 0,
+  Q3_ERR_NULL = -1,        /* a required pointer is null */
+  Q3_ERR_SHAPE = -2,       /* inconsistent or negative sizes */
+  Q3_ERR_DTYPE = -3,       /* dtype not supported by this op */
+  Q3_ERR_ALIGN = -4,       /* pointer / stride alignment violated */
+  Q3_ERR_UNSUPPORTED = -5, /* valid request outside what the kernels cover */
+  Q3_ERR_WORKSPACE = -6    /* workspace missing or smaller than *_workspace_bytes */
+} q3_status;
+
+int q3_abi_version(void);
+const char* q3_error_string(int code);
+
+/* ---------------------------------------------------------------- GEMM
+ * y[m, n] = sum_k x[m, k] * w[n, k] (+ bias[n]) (+ residual[m, n]), one rounding.
+ * Replaces matmul_forward(Tensor x, Tensor weight, Tensor? bias)
+ * (csrc/matmul_op.cpp:12, called from kernels/matmul.py:72). The residual
+ * operand fuses residual_add (csrc/residual_add_op.cpp:6) into the epilogue.
+ * bias/residual may be null. M <= 32 (bf16) may need a workspace. */
+int64_t q3_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int dtype, int swiglu);
+int q3_matmul(const void* x, const void* w, const void* bias, const void* residual, void* y, int64_t M, int64_t N,
+              int64_t K, int64_t ldx, int64_t ldw, int64_t ldr, int64_t ldc, int dtype, void* workspace,
+              int64_t workspace_bytes, void* stream);
+
+/* y[m, n] = silu(x . w_gate[n]) * (x . w_up[n]). Fuses the gate/up projections
+ * and swiglu_forward (csrc/swiglu_op.cpp:9) of CudaSwiGLUMLP
+ * (modules/mlp.py:19-22). */
+int q3_matmul_swiglu(const void* x, const void* w_gate, const void* w_up, void* y, int64_t M, int64_t N, int64_t K,
+                     int64_t ldx, int64_t ldw, int64_t ldc, int dtype, void* workspace, int64_t workspace_bytes,
+                     void* stream);
+
+/* y[e] = x[e] . w[e]^T for x (E, M, K), w (E, N, K), y (E, M, N), contiguous.
+ * Replaces batched_gemm_forward(Tensor x, Tensor weight)
+ * (csrc/moe_routing_op.cpp:12, kernels/moe_routing.py:126-181). */
+int q3_batched_gemm(const void* x, const void* w, void* y, int64_t E, int64_t M, int64_t N, int64_t K, int dtype,
+                    void* stream);
+
+/* ---------------------------------------------------------------- elementwise (n elements, contiguous)
+ * residual_add_forward(Tensor a, Tensor b)   csrc/residual_add_op.cpp:6
+ * swiglu_forward(Tensor gate, Tensor up)     csrc/swiglu_op.cpp:9
+ * gelu_tanh_forward(Tensor x)                csrc/gelu_tanh_op.cpp:7 */
+int q3_residual_add(const void* a, const void* b, void* y, int64_t n, int dtype, void* stream);
+int q3_swiglu(const void* gate, const void* up, void* y, int64_t n, int dtype, void* stream);
+int q3_gelu_tanh(const void* x, void* y, int64_t n, int dtype, void* stream);
+
+/* ---------------------------------------------------------------- row reductions (rows x cols, contiguous)
+ * rmsnorm_forward(Tensor x, Tensor weight, float eps)               csrc/rmsnorm_op.cpp:10
+ * layernorm_forward(Tensor x, Tensor weight, Tensor? bias, float eps) csrc/layernorm_op.cpp:8
+ * softmax_forward(Tensor x)                                          csrc/softmax_op.cpp:7
+ * topk_forward(Tensor x, int k) -> (vals in x dtype, idx int64), ties to the lowest
+ *   index                                                            csrc/moe_routing_op.cpp:10 */
+int q3_rmsnorm(const void* x, const void* weight, void* y, int64_t rows, int64_t cols, float eps, int dtype,
+               void* stream);
+int q3_layernorm(const void* x, const void* weight, const void* bias, void* y, int64_t rows, int64_t cols, float eps,
+                 int dtype, void* stream);
+int q3_softmax(const void* x, void* y, int64_t rows, int64_t cols, int dtype, void* stream);
+int q3_topk(const void* x, void* vals, int64_t* idx, int64_t rows, int64_t cols, int64_t k, int dtype, void* stream);
+
+/* ---------------------------------------------------------------- rotary
+ * x, y: (B, H, S, D) with element strides [b, h, s]; rotate-half over the first
+ * D_rope dims, the rest copied. cos/sin dtype: cos_dtype (Q3_F32 or Q3_BF16).
+ * q3_rope replaces rope_forward(Tensor x, Tensor cos, Tensor sin) (csrc/rope_op.cpp:6):
+ *   cos element (b, s, i) at b * cos_batch_stride + s * cos_seq_stride + i
+ *   (cos_batch_stride 0 broadcasts one table over the batch).
+ * q3_mrope replaces apply_mrope (kernels/mrope.py:80-104, mrope_forward csrc/mrope_op.cpp:6)
+ *   with cos3d/sin3d (3, B, S, D_rope) read in place: cos_strides = [axis, b, s],
+ *   section = 3 ints summing to D_rope / 2 (the chunked section layout). */
+int q3_rope(const void* x, const void* cos, const void* sin, void* y, int64_t B, int64_t H, int64_t S, int64_t D,
+            int64_t D_rope, const int64_t* x_strides, const int64_t* y_strides, int64_t cos_batch_stride,
+            int64_t cos_seq_stride, int dtype, int cos_dtype, void* stream);
+int q3_mrope(const void* x, const void* cos3d, const void* sin3d, void* y, int64_t B, int64_t H, int64_t S, int64_t D,
+             int64_t D_rope, const int64_t* section, const int64_t* x_strides, const int64_t* y_strides,
+             const int64_t* cos_strides, int dtype, int cos_dtype, void* stream);
+
+/* Fused attention prologue of CudaFullAttention.forward (modules/attention.py:82-88):
+ * q_norm/k_norm RMSNorm over the head dim, mRoPE of q and k (angles
+ * positions[axis, b, s] * inv_freq[i] in fp32, modules/rotary.py:43-55; chunked
+ * section layout, kernels/mrope.py:19-35), and a copy of v. Inputs and outputs
+ * are (B, S, H, D) views with element strides; strides = 18 values, (b, s, h)
+ * for q_in, k_in, v_in, q_out, k_out, v_out. positions: (3, B, S) int32,
+ * inv_freq: (D / 2) fp32, both on the device. dst_seq_offset (B) int32 or null
+ * shifts the sequence index of k_out / v_out rows (KV-cache append); rows whose
+ * shifted index is >= dst_seq_cap (when > 0) are not written.
+ * q_weight/k_weight both null: no normalisation (rotary only); v_in/v_out both
+ * null: no v copy. */
+int q3_qk_norm_rope(const void* q_in, const void* k_in, const void* v_in, void* q_out, void* k_out, void* v_out,
+                    const void* q_weight, const void* k_weight, const int* positions, const float* inv_freq,
+                    const int* dst_seq_offset, int64_t dst_seq_cap, int64_t B, int64_t S, int64_t Hq, int64_t Hkv,
+                    int64_t D, const int64_t* section, float eps, const int64_t* strides, int dtype, void* stream);
+
+/* ---------------------------------------------------------------- attention
+ * Replaces flash_attention_forward(Tensor q, Tensor k, Tensor v, float scale,
+ * bool is_causal, int num_kv_groups) (csrc/flash_attention_op.cpp:14,
+ * kernels/flash_attention.py:82-100). q (B, Hq, Sq, D), k/v (B, Hkv, Sk, D),
+ * o (B, Hq, Sq, D); strides = [qb, qh, qs, kb, kh, ks, vb, vh, vs, ob, oh, os].
+ * Query head h uses KV head h / (Hq / Hkv). Causal masks key j > query i
+ * (top-left aligned). lse (B, Hq, Sq) fp32 natural-log LSE, or null. */
+int q3_flash_attention(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t Hq,
+                       int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D, const int64_t* strides, float scale,
+                       int is_causal, int dtype, void* stream);
+
+/* Decode step over a ragged KV cache: the Sq = 1 case of the same op
+ * (modules/attention.py:89-96) without the torch.cat cache growth. q (B, Hq, D)
+ * strides [qb, qh]; k/v cache (B, Hkv, cap, D) strides [b, h, s]; o (B, Hq, D)
+ * strides [ob, oh]; strides = [qb, qh, kb, kh, ks, vb, vh, vs, ob, oh].
+ * Sequence b attends to cache rows [0, kv_lens[b]) (int32 on the device);
+ * max_len >= every kv_lens[b]. */
+int64_t q3_decode_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t D);
+int q3_decode_attention(const void* q, const void* k_cache, const void* v_cache, const int* kv_lens, void* o,
+                        int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len, const int64_t* strides,
+                        float scale, int dtype, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------- MoE
+ * Router of CudaSparseMoE.forward (modules/moe.py:60-65): softmax over the
+ * (bf16) logits (softmax_forward, csrc/softmax_op.cpp:7), top-k
+ * (topk_forward, csrc/moe_routing_op.cpp:10; lowest index wins ties),
+ * renormalise and cast to bf16. top_idx (T, k) int32; top_w (T, k) bf16;
+ * top_p (T, k) fp32 selected probabilities or null. */
+int q3_moe_route(const void* logits, int* top_idx, void* top_w, float* top_p, int64_t T, int64_t E, int64_t k,
+                 int norm, void* stream);
+
+/* Expert dispatch, SwiGLU experts and combine of CudaSparseMoE.forward
+ * (modules/moe.py:70-83): replaces the per-expert loop of matmul_forward,
+ * swiglu_forward and index_add_forward (csrc/moe_routing_op.cpp:11) with a
+ * permute + two grouped GEMMs + an expert-ordered combine. x (T, H);
+ * gate_up (E, 2I, H); down (E, H, I); out (T, H) (+ residual (T, H) or null). */
+int64_t q3_moe_experts_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k);
+int q3_moe_experts(const void* x, const void* gate_up, const void* down, const int* top_idx, const void* top_w,
+                   const void* residual, void* out, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
+                   void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Deterministic target[idx[i]] += src[i] (in place): replaces
+ * index_add_forward(Tensor(a!) target, Tensor source, Tensor index)
+ * (csrc/moe_routing_op.cpp:11). Each target row adds its sources in ascending
+ * i in fp32, starting from the target value, and rounds to dtype once (the
+ * semantics of torch's index_add_, kernels/moe_routing.py:111-115).
+ * idx int64 in [0, n_target). */
+int64_t q3_index_add_workspace_bytes(int64_t n_src, int64_t n_target);
+int q3_index_add(void* target, const void* src, const int64_t* idx, int64_t n_src, int64_t n_target, int64_t D,
+                 int dtype, void* workspace, int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* Q3VL_H */

@@ -1,0 +1,121 @@
+"""ctypes binding of libq3vl.so (the C-ABI declared in include/q3vl.h).
+
+The library is loaded from `qwen3_5_vl_cuda_custom_amd/lib/libq3vl.so`, built
+ahead of time by `qwen3_5_vl_cuda_custom_amd.build`. There is no fallback:
+if the library is missing, every op raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int64, c_void_p
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libq3vl.so"
+
+Q3_F32 = 0
+Q3_BF16 = 1
+
+_i64p = POINTER(c_int64)
+_i32p = c_void_p
+_f32p = c_void_p
+_V = c_void_p
+_I = c_int64
+
+# name -> (restype, argtypes)
+_SIGS: dict[str, tuple] = {
+    "q3_abi_version": (c_int, []),
+    "q3_error_string": (c_char_p, [c_int]),
+    "q3_matmul_workspace_bytes": (c_int64, [_I, _I, _I, c_int, c_int]),
+    "q3_matmul": (c_int, [_V, _V, _V, _V, _V, _I, _I, _I, _I, _I, _I, _I, c_int, _V, _I, _V]),
+    "q3_matmul_swiglu": (c_int, [_V, _V, _V, _V, _I, _I, _I, _I, _I, _I, c_int, _V, _I, _V]),
+    "q3_batched_gemm": (c_int, [_V, _V, _V, _I, _I, _I, _I, c_int, _V]),
+    "q3_residual_add": (c_int, [_V, _V, _V, _I, c_int, _V]),
+    "q3_swiglu": (c_int, [_V, _V, _V, _I, c_int, _V]),
+    "q3_gelu_tanh": (c_int, [_V, _V, _I, c_int, _V]),
+    "q3_rmsnorm": (c_int, [_V, _V, _V, _I, _I, c_float, c_int, _V]),
+    "q3_layernorm": (c_int, [_V, _V, _V, _V, _I, _I, c_float, c_int, _V]),
+    "q3_softmax": (c_int, [_V, _V, _I, _I, c_int, _V]),
+    "q3_topk": (c_int, [_V, _V, _V, _I, _I, _I, c_int, _V]),
+    "q3_rope": (c_int, [_V, _V, _V, _V, _I, _I, _I, _I, _I, _i64p, _i64p, _I, _I, c_int, c_int, _V]),
+    "q3_mrope": (c_int, [_V, _V, _V, _V, _I, _I, _I, _I, _I, _i64p, _i64p, _i64p, _i64p, c_int, c_int, _V]),
+    "q3_qk_norm_rope": (c_int, [_V, _V, _V, _V, _V, _V, _V, _V, _i32p, _f32p, _i32p, _I, _I, _I, _I, _I, _I,
+                                _i64p, c_float, _i64p, c_int, _V]),
+    "q3_flash_attention": (c_int, [_V, _V, _V, _V, _f32p, _I, _I, _I, _I, _I, _I, _i64p, c_float, c_int, c_int,
+                                   _V]),
+    "q3_decode_attention_workspace_bytes": (c_int64, [_I, _I, _I, _I, _I]),
+    "q3_decode_attention": (c_int, [_V, _V, _V, _i32p, _V, _I, _I, _I, _I, _I, _i64p, c_float, c_int, _V, _I, _V]),
+    "q3_moe_route": (c_int, [_V, _i32p, _V, _f32p, _I, _I, _I, c_int, _V]),
+    "q3_moe_experts_workspace_bytes": (c_int64, [_I, _I, _I, _I, _I]),
+    "q3_moe_experts": (c_int, [_V, _V, _V, _i32p, _V, _V, _V, _I, _I, _I, _I, _I, _V, _I, _V]),
+    "q3_index_add_workspace_bytes": (c_int64, [_I, _I]),
+    "q3_index_add": (c_int, [_V, _V, _V, _I, _I, _I, c_int, _V, _I, _V]),
+}
+
+EXPORTED = tuple(_SIGS)
+
+_lib: ctypes.CDLL | None = None
+
+
+class Q3Error(RuntimeError):
+    """A libq3vl entry point returned a non-zero status."""
+
+    def __init__(self, op: str, code: int, msg: str):
+        super().__init__(f"{op} failed: {msg} (status {code})")
+        self.op = op
+        self.code = code
+
+
+def lib() -> ctypes.CDLL:
+    """Load libq3vl.so once and bind every entry point's signature."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m qwen3_5_vl_cuda_custom_amd.build` "
+                "(there is no fallback path)")
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def error_string(code: int) -> str:
+    return lib().q3_error_string(code).decode()
+
+
+def call(name: str, *args) -> None:
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        raise Q3Error(name, rc, error_string(rc))
+
+
+def i64s(*vals) -> ctypes.Array:
+    return (c_int64 * len(vals))(*[int(v) for v in vals])
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.bfloat16:
+        return Q3_BF16
+    if dt == torch.float32:
+        return Q3_F32
+    raise TypeError(f"unsupported dtype {dt}: the kernels take bfloat16 or float32")
+
+
+def workspace(nbytes: int, device: torch.device) -> tuple[torch.Tensor | None, int]:
+    """A device scratch buffer of at least `nbytes` (None when 0)."""
+    if nbytes <= 0:
+        return None, 0
+    return torch.empty(int(nbytes), dtype=torch.uint8, device=device), int(nbytes)

@@ -1,0 +1,640 @@
+// Flash attention on gfx950 MFMA, bf16 in / fp32 softmax and accumulation.
+//
+// Prefill (q3_flash_attention): one block = 4 waves; each wave owns 32 query
+// rows of one head. With GQA the 4 waves of a block are (up to) 4 query heads
+// of the same KV head over the same 32 queries, so one K/V tile in LDS feeds all
+// of them and all waves share one causal extent.
+//
+// Per 64-key tile and wave:
+//   S^T (64 keys x 32 q) = K (64 x D) * Q^T (D x 32)   A = K from LDS, B = Q in registers
+//   online softmax per query: a query is a lane column, so its statistics are
+//   lane-local apart from one exchange between lanes l and l ^ 32
+//   O^T (D x 32 q) += V^T (D x 64) * P^T (64 x 32)       A = V^T from LDS, B = P^T
+// P^T is used straight from the S^T accumulators: register r of lane l holds key
+// 8*(r/4) + 4*(l/32) + r%4, which, read as the B operand's k index 8*(l/32) + t
+// (t = r), is a fixed key permutation; the V^T fragment reads use the same one.
+// The O^T accumulators are per-lane queries, so the softmax rescale is local.
+//
+// LDS (per stage): K tile [64][128] bf16, 16-byte chunk c of row r at slot
+// c ^ (r & 15); V^T tile [D][64] bf16, 8-byte unit u (keys 4u..4u+3) of row d at
+// slot u ^ (d & 15). Double-buffered, one barrier per tile.
+//
+// Decode (q3_decode_attention): one block per (64*4-key chunk, sequence, KV
+// head); the MFMA query columns are the GQA group's heads. Each wave handles 64
+// keys; the block merges its waves and writes (m, l, O) partials, and
+// q3_decode_combine-style merging happens in a second kernel.
+#include <algorithm>
+
+#include "q3_common.h"
+
+namespace {
+
+constexpr int kKT = 64;      // keys per tile
+constexpr int kRowK = 128;   // LDS K-tile row length (elements)
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegBig = -1.0e30f;
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ int k_slot(int row, int chunk) { return row * kRowK + ((chunk ^ (row & 15)) << 3); }
+// Element offset of unit u of V^T row d (row = 64 keys).
+__device__ __forceinline__ int vt_unit(int d, int u) { return d * kKT + ((u ^ (d & 15)) << 2); }
+
+struct AttnParams {
+  const bf16* q;
+  const bf16* k;
+  const bf16* v;
+  bf16* o;
+  float* lse;
+  int B, Hq, Hkv, Sq, Sk;
+  int64_t qb, qh, qs, kb, kh, ks, vb, vh, vs, ob, oh, os;
+  float scale_log2;
+  int causal;
+  int groups;
+  // decode
+  const int* kv_lens;
+  float* partial;  // decode workspace
+  int max_chunks;
+};
+
+// Global -> register staging of one K tile and one V tile (64 keys x D).
+template <int D>
+struct KVStage {
+  static constexpr int CHD = (D + 15) / 16 * 2;  // 16-byte chunks per K row incl. zero padding to DK
+  static constexpr int KITEMS = (kKT * CHD + 255) / 256;
+  static constexpr int VCH = D / 8;              // real chunks per V row
+  static constexpr int VITEMS = (32 * VCH + 255) / 256;  // (key pair, chunk) items per thread
+  bf16x8 kv[KITEMS];
+  bf16x8 vv[VITEMS][2];
+
+  __device__ __forceinline__ void load(const bf16* kbase, const bf16* vbase, int64_t ks, int64_t vs, int k0,
+                                       int klimit, int tid) {
+#pragma unroll
+    for (int i = 0; i < KITEMS; ++i) {
+      const int id = tid + 256 * i;
+      const int r = id / CHD, c = id % CHD;
+      const bool ok = (id < kKT * CHD) && (k0 + r < klimit) && (c * 8 < D);
+      kv[i] = ok ? *reinterpret_cast<const bf16x8*>(kbase + (int64_t)(k0 + r) * ks + c * 8) : bf16x8{};
+    }
+#pragma unroll
+    for (int i = 0; i < VITEMS; ++i) {
+      const int id = tid + 256 * i;
+      const int p = id & 31, c = id >> 5;
+      const bool cok = (id < 32 * VCH);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int key = k0 + 2 * p + e;
+        vv[i][e] = (cok && key < klimit) ? *reinterpret_cast<const bf16x8*>(vbase + (int64_t)key * vs + c * 8)
+                                         : bf16x8{};
+      }
+    }
+  }
+  __device__ __forceinline__ void store(bf16* sK, bf16* sVt, int tid) const {
+#pragma unroll
+    for (int i = 0; i < KITEMS; ++i) {
+      const int id = tid + 256 * i;
+      if (id < kKT * CHD) {
+        const int r = id / CHD, c = id % CHD;
+        *reinterpret_cast<bf16x8*>(sK + k_slot(r, c)) = kv[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VITEMS; ++i) {
+      const int id = tid + 256 * i;
+      if (id < 32 * VCH) {
+        const int p = id & 31, c = id >> 5;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int d = c * 8 + e;
+          uint32_t* dst = reinterpret_cast<uint32_t*>(sVt + vt_unit(d, p >> 1)) + (p & 1);
+          *dst = pack_bf16x2(vv[i][0][e], vv[i][1][e]);
+        }
+      }
+    }
+  }
+};
+
+// Per-wave attention state over a 32-query column block.
+template <int D>
+struct WaveAttn {
+  static constexpr int KSTEPS = (D + 15) / 16;
+  static constexpr int OT = (D + 31) / 32;
+  bf16x8 qf[KSTEPS];
+  floatx16 o[OT];
+  float m, l;
+
+  __device__ __forceinline__ void init() {
+#pragma unroll
+    for (int t = 0; t < OT; ++t) o[t] = floatx16{};
+    m = kNegBig;
+    l = 0.f;
+  }
+  // Q row for this lane's query column (zero when absent).
+  __device__ __forceinline__ void load_q(const bf16* qrow, bool valid, int h) {
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      const int d = ks * 16 + 8 * h;
+      qf[ks] = (valid && d < D) ? *reinterpret_cast<const bf16x8*>(qrow + d) : bf16x8{};
+    }
+  }
+  // One 64-key tile. kidx_base: key index of tile row 0; qidx: this lane's query
+  // index; klimit: keys >= klimit are masked; causal masks key > query.
+  __device__ __forceinline__ void tile(const bf16* sK, const bf16* sVt, int lane, int kidx_base, int qidx,
+                                       int klimit, bool causal, float scale_log2) {
+    const int l32 = lane & 31;
+    const int h = lane >> 5;
+    floatx16 s[2];
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2) {
+      s[t2] = floatx16{};
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(sK + k_slot(t2 * 32 + l32, ks * 2 + h));
+        s[t2] = mfma32x32x16(a, qf[ks], s[t2]);
+      }
+    }
+    float mloc = kNegBig;
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kidx_base + t2 * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        const bool masked = (key >= klimit) || (causal && key > qidx);
+        const float x = masked ? -INFINITY : s[t2][r] * scale_log2;
+        s[t2][r] = x;
+        mloc = fmaxf(mloc, x);
+      }
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    const float mnew = fmaxf(m, mloc);
+    const float alpha = fast_exp2(m - mnew);
+    float lsum = 0.f;
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pv = fast_exp2(s[t2][r] - mnew);
+        s[t2][r] = pv;
+        lsum += pv;
+      }
+    lsum += __shfl_xor(lsum, 32, 64);
+    l = l * alpha + lsum;
+    m = mnew;
+#pragma unroll
+    for (int t = 0; t < OT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+    bf16x8 pb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) pb[j][t] = f2bf(s[j >> 1][(j & 1) * 8 + t]);
+    }
+#pragma unroll
+    for (int t = 0; t < OT; ++t) {
+      const int d = t * 32 + l32;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(sVt + vt_unit(d, 4 * j + h));
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(sVt + vt_unit(d, 4 * j + 2 + h));
+        u32x4 w = {lo[0], lo[1], hi[0], hi[1]};
+        const bf16x8 a = __builtin_bit_cast(bf16x8, w);
+        o[t] = mfma32x32x16(a, pb[j], o[t]);
+      }
+    }
+  }
+};
+
+template <int D, int WH>
+__global__ __launch_bounds__(256) void flash_prefill_kernel(const AttnParams p) {
+  constexpr int WQ = 4 / WH;
+  constexpr int QB = WQ * 32;  // queries per block
+  __shared__ __attribute__((aligned(16))) bf16 sK[2][kKT * kRowK];
+  __shared__ __attribute__((aligned(16))) bf16 sVt[2][WaveAttn<D>::OT * 32 * kKT];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wh = wave % WH;
+  const int wq = wave / WH;
+  const int l32 = lane & 31;
+  const int h = lane >> 5;
+
+  const int n_qt = (p.Sq + QB - 1) / QB;
+  // Heavy-first: causal tiles with the most keys are issued first.
+  const int qt = p.causal ? (n_qt - 1 - (int)blockIdx.x) : (int)blockIdx.x;
+  const int hgroups = p.groups / WH;
+  int yb = blockIdx.y;
+  const int hg = yb % hgroups;
+  yb /= hgroups;
+  const int kvh = yb % p.Hkv;
+  const int b = yb / p.Hkv;
+  const int hq = kvh * p.groups + hg * WH + wh;
+
+  const int q0 = qt * QB + wq * 32;
+  const int qidx = q0 + l32;
+  const int qend_block = min(p.Sq, qt * QB + QB);
+  const int klimit = p.causal ? min(p.Sk, qend_block) : p.Sk;
+  const int nkt = (klimit + kKT - 1) / kKT;
+
+  const bf16* kbase = p.k + (int64_t)b * p.kb + (int64_t)kvh * p.kh;
+  const bf16* vbase = p.v + (int64_t)b * p.vb + (int64_t)kvh * p.vh;
+
+  WaveAttn<D> wa;
+  wa.init();
+  wa.load_q(p.q + (int64_t)b * p.qb + (int64_t)hq * p.qh + (int64_t)qidx * p.qs, qidx < p.Sq, h);
+
+  // Rows D..OT*32 of V^T are never written; they only feed output rows that
+  // are never stored.
+  KVStage<D> st;
+  if (nkt > 0) {
+    st.load(kbase, vbase, p.ks, p.vs, 0, p.Sk, tid);
+    st.store(sK[0], sVt[0], tid);
+  }
+  __syncthreads();
+  const int wave_last_q = min(q0 + 31, p.Sq - 1);
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nkt) st.load(kbase, vbase, p.ks, p.vs, (kt + 1) * kKT, p.Sk, tid);
+    const int k0 = kt * kKT;
+    const bool active = q0 < p.Sq && (!p.causal || k0 <= wave_last_q);
+    if (active) wa.tile(sK[cur], sVt[cur], lane, k0, qidx, p.Sk, p.causal != 0, p.scale_log2);
+    if (kt + 1 < nkt) st.store(sK[cur ^ 1], sVt[cur ^ 1], tid);
+    __syncthreads();
+  }
+
+  if (qidx >= p.Sq) return;
+  const float inv_l = wa.l > 0.f ? 1.0f / wa.l : 0.f;
+  bf16* orow = p.o + (int64_t)b * p.ob + (int64_t)hq * p.oh + (int64_t)qidx * p.os;
+#pragma unroll
+  for (int t = 0; t < WaveAttn<D>::OT; ++t)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d = t * 32 + 8 * g + 4 * h;
+      if (d < D) {
+        bf16x4 v4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v4[e] = f2bf(wa.o[t][4 * g + e] * inv_l);
+        *reinterpret_cast<bf16x4*>(orow + d) = v4;
+      }
+    }
+  if (p.lse && h == 0) {
+    p.lse[((int64_t)b * p.Hq + hq) * p.Sq + qidx] = (wa.m + log2f(wa.l)) * 0.6931471805599453f;
+  }
+}
+
+// ----------------------------------------------------------------- decode
+constexpr int kDecKeys = 4 * kKT;  // keys per block (4 waves x 64)
+
+// Partial layout per (b, kvh, chunk): m[G], l[G], O[G][D] (fp32), G = groups.
+__host__ __device__ inline int dec_partial_floats(int groups, int D) { return groups * (D + 2); }
+
+template <int D>
+__global__ __launch_bounds__(256) void flash_decode_kernel(const AttnParams p) {
+  constexpr int OT = WaveAttn<D>::OT;
+  constexpr int KW = kKT * kRowK;      // K tile elements per wave
+  constexpr int VW = OT * 32 * kKT;    // V^T tile elements per wave
+  __shared__ __attribute__((aligned(16))) bf16 lds[4 * (KW + VW)];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int l32 = lane & 31;
+  const int h = lane >> 5;
+  const int chunk = blockIdx.x;
+  const int kvh = blockIdx.y % p.Hkv;
+  const int b = blockIdx.y / p.Hkv;
+  const int L = min(p.kv_lens[b], p.Sk);  // Sk = max_len: never read past the cache
+  const int kc0 = chunk * kDecKeys;
+  if (kc0 >= L) return;  // uniform per block
+
+  bf16* sK = lds + wave * KW;
+  bf16* sVt = lds + 4 * KW + wave * VW;
+  const int k0 = kc0 + wave * kKT;
+  const bf16* kbase = p.k + (int64_t)b * p.kb + (int64_t)kvh * p.kh;
+  const bf16* vbase = p.v + (int64_t)b * p.vb + (int64_t)kvh * p.vh;
+
+  // Wave-private stage of this wave's 64 keys.
+  {
+    constexpr int CHD = KVStage<D>::CHD;
+    for (int id = lane; id < kKT * CHD; id += 64) {
+      const int r = id / CHD, c = id % CHD;
+      const bool ok = (k0 + r < L) && (c * 8 < D);
+      const bf16x8 v = ok ? *reinterpret_cast<const bf16x8*>(kbase + (int64_t)(k0 + r) * p.ks + c * 8) : bf16x8{};
+      *reinterpret_cast<bf16x8*>(sK + k_slot(r, c)) = v;
+    }
+    constexpr int VCH = D / 8;
+    for (int id = lane; id < 32 * VCH; id += 64) {
+      const int pp = id & 31, c = id >> 5;
+      bf16x8 v2[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int key = k0 + 2 * pp + e;
+        v2[e] = key < L ? *reinterpret_cast<const bf16x8*>(vbase + (int64_t)key * p.vs + c * 8) : bf16x8{};
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int d = c * 8 + e;
+        uint32_t* dst = reinterpret_cast<uint32_t*>(sVt + vt_unit(d, pp >> 1)) + (pp & 1);
+        *dst = pack_bf16x2(v2[0][e], v2[1][e]);
+      }
+    }
+  }
+  __syncthreads();
+
+  WaveAttn<D> wa;
+  wa.init();
+  const int G = p.groups;
+  const int qcol = l32;  // query column = head within the GQA group
+  const bool qvalid = qcol < G;
+  const int hq = kvh * G + qcol;
+  wa.load_q(p.q + (int64_t)b * p.qb + (int64_t)(qvalid ? hq : 0) * p.qh, qvalid, h);
+  const bool live = k0 < L;
+  if (live) wa.tile(sK, sVt, lane, k0, 0, L, false, p.scale_log2);
+
+  // Merge the 4 waves through LDS (the K/V tiles are dead by now).
+  __syncthreads();
+  const int PF = dec_partial_floats(G, D);
+  float* red = reinterpret_cast<float*>(lds);
+  float* rw = red + wave * PF;
+  if (h == 0 && qvalid) {
+    rw[qcol] = live ? wa.m : kNegBig;
+    rw[G + qcol] = live ? wa.l : 0.f;
+  }
+  if (qvalid) {
+#pragma unroll
+    for (int t = 0; t < OT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = t * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (d < D) rw[2 * G + qcol * D + d] = live ? wa.o[t][r] : 0.f;
+      }
+  }
+  __syncthreads();
+  float* out = p.partial + (((int64_t)b * p.Hkv + kvh) * p.max_chunks + chunk) * PF;
+  for (int idx = tid; idx < G * D + G; idx += 256) {
+    const int qc = idx < G ? idx : (idx - G) / D;
+    float mm = kNegBig;
+    for (int w = 0; w < 4; ++w) mm = fmaxf(mm, red[w * PF + qc]);
+    float acc = 0.f;
+    for (int w = 0; w < 4; ++w) {
+      const float* r = red + w * PF;
+      const float wgt = fast_exp2(r[qc] - mm);
+      acc += (idx < G ? r[G + qc] : r[2 * G + (idx - G)]) * wgt;
+    }
+    if (idx < G) {
+      out[qc] = mm;
+      out[G + qc] = acc;
+    } else {
+      out[2 * G + (idx - G)] = acc;
+    }
+  }
+}
+
+// Merge the chunk partials of one (b, query head): one wave each.
+template <int D>
+__global__ __launch_bounds__(256) void flash_decode_combine(const AttnParams p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t gw = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
+  if (gw >= (int64_t)p.B * p.Hq) return;
+  const int b = (int)(gw / p.Hq);
+  const int hq = (int)(gw % p.Hq);
+  const int kvh = hq / p.groups;
+  const int qc = hq % p.groups;
+  const int L = min(p.kv_lens[b], p.Sk);
+  const int nch = (L + kDecKeys - 1) / kDecKeys;
+  const int G = p.groups;
+  const int PF = dec_partial_floats(G, D);
+  const float* base = p.partial + ((int64_t)b * p.Hkv + kvh) * p.max_chunks * PF;
+  float mm = kNegBig;
+  for (int c = 0; c < nch; ++c) mm = fmaxf(mm, base[c * PF + qc]);
+  float ll = 0.f;
+  constexpr int PER = (D + 63) / 64;
+  float acc[PER] = {};
+  for (int c = 0; c < nch; ++c) {
+    const float* r = base + c * PF;
+    const float wgt = fast_exp2(r[qc] - mm);
+    ll += r[G + qc] * wgt;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int d = lane + 64 * i;
+      if (d < D) acc[i] += r[2 * G + qc * D + d] * wgt;
+    }
+  }
+  const float inv = ll > 0.f ? 1.0f / ll : 0.f;
+  bf16* orow = p.o + (int64_t)b * p.ob + (int64_t)hq * p.oh;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int d = lane + 64 * i;
+    if (d < D) orow[d] = f2bf(acc[i] * inv);
+  }
+}
+
+// ----------------------------------------------------------------- generic (fp32)
+// Reference-accuracy path for fp32 tensors (and head dims the MFMA kernels do
+// not cover): one thread per query row, online softmax over all keys.
+template <typename T>
+__global__ __launch_bounds__(128) void flash_generic_kernel(const AttnParams p, int D, const int* kv_lens) {
+  const int64_t row = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)p.B * p.Hq * p.Sq;
+  if (row >= total) return;
+  const int i = (int)(row % p.Sq);
+  const int hq = (int)((row / p.Sq) % p.Hq);
+  const int b = (int)(row / ((int64_t)p.Sq * p.Hq));
+  const int kvh = hq / p.groups;
+  const T* q = reinterpret_cast<const T*>(p.q) + (int64_t)b * p.qb + (int64_t)hq * p.qh + (int64_t)i * p.qs;
+  const T* kb = reinterpret_cast<const T*>(p.k) + (int64_t)b * p.kb + (int64_t)kvh * p.kh;
+  const T* vb = reinterpret_cast<const T*>(p.v) + (int64_t)b * p.vb + (int64_t)kvh * p.vh;
+  int nk = kv_lens ? min(kv_lens[b], p.Sk) : p.Sk;
+  if (p.causal) nk = min(nk, i + 1);
+  float acc[256];
+  for (int d = 0; d < D; ++d) acc[d] = 0.f;
+  float m = -INFINITY, l = 0.f;
+  const float scale = p.scale_log2 / kLog2e;
+  for (int j = 0; j < nk; ++j) {
+    const T* kr = kb + (int64_t)j * p.ks;
+    float s = 0.f;
+    for (int d = 0; d < D; ++d) s += to_f<T>(q[d]) * to_f<T>(kr[d]);
+    s *= scale;
+    const float mn = fmaxf(m, s);
+    const float a = expf(m - mn);
+    const float e = expf(s - mn);
+    l = l * a + e;
+    const T* vr = vb + (int64_t)j * p.vs;
+    for (int d = 0; d < D; ++d) acc[d] = acc[d] * a + e * to_f<T>(vr[d]);
+    m = mn;
+  }
+  T* o = reinterpret_cast<T*>(p.o) + (int64_t)b * p.ob + (int64_t)hq * p.oh + (int64_t)i * p.os;
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  for (int d = 0; d < D; ++d) o[d] = from_f<T>(acc[d] * inv);
+  if (p.lse) p.lse[((int64_t)b * p.Hq + hq) * p.Sq + i] = m + logf(l);
+}
+
+bool mfma_head_dim(int64_t D) { return D == 64 || D == 72 || D == 80 || D == 96 || D == 128; }
+
+template <int D>
+int launch_prefill_d(const AttnParams& p, hipStream_t st) {
+  const int WH = (p.groups % 4 == 0) ? 4 : (p.groups % 2 == 0 ? 2 : 1);
+  const int QB = (4 / WH) * 32;
+  dim3 grid((unsigned)q3_cdiv(p.Sq, QB), (unsigned)(p.B * p.Hkv * (p.groups / WH)));
+  if (WH == 4)
+    hipLaunchKernelGGL((flash_prefill_kernel<D, 4>), grid, dim3(256), 0, st, p);
+  else if (WH == 2)
+    hipLaunchKernelGGL((flash_prefill_kernel<D, 2>), grid, dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL((flash_prefill_kernel<D, 1>), grid, dim3(256), 0, st, p);
+  Q3_LAUNCH_CHECK();
+  return Q3_OK;
+}
+
+bool strides_aligned8(const int64_t* s, int n) {
+  for (int i = 0; i < n; ++i)
+    if (s[i] % 8 != 0) return false;
+  return true;
+}
+
+int64_t decode_ws_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t D) {
+  const int64_t chunks = q3_cdiv(std::max<int64_t>(max_len, 1), kDecKeys);
+  return B * Hkv * chunks * (int64_t)dec_partial_floats((int)(Hq / std::max<int64_t>(Hkv, 1)), (int)D) *
+         (int64_t)sizeof(float);
+}
+
+}  // namespace
+
+extern "C" {
+
+// q, k, v, o: (B, H, S, D) with element strides (b, h, s) given in `strides`
+// as [qb, qh, qs, kb, kh, ks, vb, vh, vs, ob, oh, os]; the head dim is contiguous.
+int q3_flash_attention(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t Hq,
+                       int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D, const int64_t* strides, float scale,
+                       int is_causal, int dtype, void* stream) {
+  Q3_REQUIRE(q && k && v && o && strides, Q3_ERR_NULL);
+  Q3_REQUIRE(B >= 0 && Hq >= 1 && Hkv >= 1 && Sq >= 0 && Sk >= 0 && D >= 1, Q3_ERR_SHAPE);
+  Q3_REQUIRE(Hq % Hkv == 0, Q3_ERR_SHAPE);
+  Q3_REQUIRE(D <= 256, Q3_ERR_UNSUPPORTED);
+  if (B == 0 || Sq == 0) return Q3_OK;
+  AttnParams p{};
+  p.q = static_cast<const bf16*>(q);
+  p.k = static_cast<const bf16*>(k);
+  p.v = static_cast<const bf16*>(v);
+  p.o = static_cast<bf16*>(o);
+  p.lse = lse;
+  p.B = (int)B;
+  p.Hq = (int)Hq;
+  p.Hkv = (int)Hkv;
+  p.Sq = (int)Sq;
+  p.Sk = (int)Sk;
+  p.qb = strides[0];
+  p.qh = strides[1];
+  p.qs = strides[2];
+  p.kb = strides[3];
+  p.kh = strides[4];
+  p.ks = strides[5];
+  p.vb = strides[6];
+  p.vh = strides[7];
+  p.vs = strides[8];
+  p.ob = strides[9];
+  p.oh = strides[10];
+  p.os = strides[11];
+  p.scale_log2 = scale * kLog2e;
+  p.causal = is_causal ? 1 : 0;
+  p.groups = (int)(Hq / Hkv);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool aligned = q3_aligned(q, 16) && q3_aligned(k, 16) && q3_aligned(v, 16) && q3_aligned(o, 8) &&
+                       strides_aligned8(strides, 12);
+  if (dtype == Q3_BF16 && mfma_head_dim(D) && aligned && Sk > 0) {
+    switch (D) {
+      case 64:
+        return launch_prefill_d<64>(p, st);
+      case 72:
+        return launch_prefill_d<72>(p, st);
+      case 80:
+        return launch_prefill_d<80>(p, st);
+      case 96:
+        return launch_prefill_d<96>(p, st);
+      default:
+        return launch_prefill_d<128>(p, st);
+    }
+  }
+  const int64_t rows = B * Hq * Sq;
+  if (dtype == Q3_F32)
+    hipLaunchKernelGGL(flash_generic_kernel<float>, dim3((unsigned)q3_cdiv(rows, 128)), dim3(128), 0, st, p, (int)D,
+                       nullptr);
+  else if (dtype == Q3_BF16)
+    hipLaunchKernelGGL(flash_generic_kernel<bf16>, dim3((unsigned)q3_cdiv(rows, 128)), dim3(128), 0, st, p, (int)D,
+                       nullptr);
+  else
+    return Q3_ERR_DTYPE;
+  Q3_LAUNCH_CHECK();
+  return Q3_OK;
+}
+
+int64_t q3_decode_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t D) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || max_len <= 0 || D <= 0) return 0;
+  return decode_ws_bytes(B, Hq, Hkv, max_len, D);
+}
+
+// One query token per sequence over a ragged KV cache.
+// q: (B, Hq, D) strides [qb, qh]; caches: (B, Hkv, cap, D) strides [b, h, s];
+// o: (B, Hq, D) strides [ob, oh]; kv_lens (B) int32 on device: sequence b
+// attends to cache positions [0, kv_lens[b]); max_len >= max(kv_lens).
+// strides = [qb, qh, kb, kh, ks, vb, vh, vs, ob, oh].
+int q3_decode_attention(const void* q, const void* k_cache, const void* v_cache, const int* kv_lens, void* o,
+                        int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len, const int64_t* strides,
+                        float scale, int dtype, void* workspace, int64_t workspace_bytes, void* stream) {
+  Q3_REQUIRE(q && k_cache && v_cache && kv_lens && o && strides, Q3_ERR_NULL);
+  Q3_REQUIRE(B >= 0 && Hq >= 1 && Hkv >= 1 && Hq % Hkv == 0 && D >= 1 && max_len >= 1, Q3_ERR_SHAPE);
+  if (B == 0) return Q3_OK;
+  AttnParams p{};
+  p.q = static_cast<const bf16*>(q);
+  p.k = static_cast<const bf16*>(k_cache);
+  p.v = static_cast<const bf16*>(v_cache);
+  p.o = static_cast<bf16*>(o);
+  p.B = (int)B;
+  p.Hq = (int)Hq;
+  p.Hkv = (int)Hkv;
+  p.Sq = 1;
+  p.Sk = (int)max_len;
+  p.qb = strides[0];
+  p.qh = strides[1];
+  p.qs = 0;
+  p.kb = strides[2];
+  p.kh = strides[3];
+  p.ks = strides[4];
+  p.vb = strides[5];
+  p.vh = strides[6];
+  p.vs = strides[7];
+  p.ob = strides[8];
+  p.oh = strides[9];
+  p.os = 0;
+  p.scale_log2 = scale * kLog2e;
+  p.causal = 0;
+  p.groups = (int)(Hq / Hkv);
+  p.kv_lens = kv_lens;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool aligned = q3_aligned(q, 16) && q3_aligned(k_cache, 16) && q3_aligned(v_cache, 16) &&
+                       strides_aligned8(strides, 8);
+  if (dtype == Q3_BF16 && D == 128 && p.groups <= 32 && aligned) {
+    Q3_REQUIRE(workspace != nullptr && workspace_bytes >= decode_ws_bytes(B, Hq, Hkv, max_len, D), Q3_ERR_WORKSPACE);
+    p.partial = static_cast<float*>(workspace);
+    p.max_chunks = (int)q3_cdiv(max_len, kDecKeys);
+    hipLaunchKernelGGL(flash_decode_kernel<128>, dim3((unsigned)p.max_chunks, (unsigned)(B * Hkv)), dim3(256), 0, st,
+                       p);
+    Q3_LAUNCH_CHECK();
+    hipLaunchKernelGGL(flash_decode_combine<128>, dim3((unsigned)q3_cdiv(B * Hq, 4)), dim3(256), 0, st, p);
+    Q3_LAUNCH_CHECK();
+    return Q3_OK;
+  }
+  const int64_t rows = B * Hq;
+  if (dtype == Q3_F32)
+    hipLaunchKernelGGL(flash_generic_kernel<float>, dim3((unsigned)q3_cdiv(rows, 128)), dim3(128), 0, st, p, (int)D,
+                       kv_lens);
+  else if (dtype == Q3_BF16)
+    hipLaunchKernelGGL(flash_generic_kernel<bf16>, dim3((unsigned)q3_cdiv(rows, 128)), dim3(128), 0, st, p, (int)D,
+                       kv_lens);
+  else
+    return Q3_ERR_DTYPE;
+  Q3_LAUNCH_CHECK();
+  return Q3_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,256 @@
+// MFMA GEMM kernels (dense, batched, dual-B SwiGLU, MoE-grouped) built on the
+// tile core in gemm_tile.h. Host launchers live in gemm.hip and moe.hip.
+#pragma once
+
+#include "gemm_tile.h"
+
+namespace q3 {
+
+enum Epilogue : int {
+  kEpiStore = 0,     // C = acc (+ bias[n]) (+ R[m, n]), rounded once
+  kEpiSwiGLU = 1,    // C = silu(acc_gate) * acc_up, rounded once
+  kEpiRowScale = 2,  // C = bf16(bf16(acc) * s[m])  (MoE expert output x routing weight)
+};
+
+struct GemmParams {
+  const bf16* X;     // (M, K) rows, ld = ldx
+  const bf16* W;     // (N, K) rows, ld = ldw  (gate weight for SwiGLU)
+  const bf16* W2;    // up weight for SwiGLU
+  const bf16* bias;  // (N) or null
+  const bf16* R;     // residual (M, N) or null, ld = ldr
+  bf16* C;           // (M, N_out), ld = ldc
+  const bf16* rowscale;  // kEpiRowScale: (rows) scale
+  int M, N, K;       // N = output columns (SwiGLU: intermediate size)
+  int64_t ldx, ldw, ldr, ldc;
+  int64_t bsX, bsW, bsC;  // batch strides (blockIdx.z)
+  int group_m;       // tile-order grouping along m
+  // MoE-grouped problems: tiles come from a device-side table.
+  const int* gather;      // logical row -> row of X (null: identity)
+  const int* tile_table;  // per m-tile: (expert << 20) | start row ... see moe.hip
+  const int* group_end;   // per expert: end row (exclusive) in the sorted order
+  const int* n_tiles_total;  // device scalar: number of valid m-tiles
+  int64_t expert_stride_w;   // elements between consecutive experts' weights
+};
+
+template <int BM, int BN, int WM, int WN, int EPI, bool GROUPED>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_kernel(const GemmParams p) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int WTM = BM / WM;
+  constexpr int WTN = BN / WN;
+  constexpr int TM = WTM / 32;
+  constexpr int TN = WTN / 32;
+  static_assert(TM >= 1 && TN >= 1, "wave tile too small");
+  static_assert(EPI != kEpiSwiGLU || (TN % 2 == 0), "SwiGLU pairs gate/up tiles");
+  constexpr int BN_OUT = (EPI == kEpiSwiGLU) ? BN / 2 : BN;
+
+  __shared__ __attribute__((aligned(16))) bf16 smem[2 * (BM + BN) * kBK];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave % WM;
+  const int wn = wave / WM;
+
+  const int n_tiles_n = (p.N + BN_OUT - 1) / BN_OUT;
+  int tile_m, tile_n;
+  int m_begin, m_end;  // logical rows of this tile: [m_begin, m_end)
+  const bf16* W = p.W;
+  const bf16* W2 = p.W2;
+  const bf16* X = p.X;
+  bf16* C = p.C;
+
+  if constexpr (GROUPED) {
+    const int t = blockIdx.x / n_tiles_n;
+    tile_n = blockIdx.x % n_tiles_n;
+    if (t >= *p.n_tiles_total) return;
+    const int entry = p.tile_table[t];
+    const int expert = entry >> 20;
+    m_begin = entry & 0xFFFFF;
+    m_end = min(m_begin + BM, p.group_end[expert]);
+    W += (int64_t)expert * p.expert_stride_w;
+    if (W2) W2 += (int64_t)expert * p.expert_stride_w;
+    tile_m = 0;
+  } else {
+    const int n_tiles_m = (p.M + BM - 1) / BM;
+    const int total = n_tiles_m * n_tiles_n;
+    const int pid = xcd_remap(blockIdx.x, total);
+    const int gm = p.group_m;
+    const int per_group = gm * n_tiles_n;
+    const int group = pid / per_group;
+    const int first_m = group * gm;
+    const int size_m = min(n_tiles_m - first_m, gm);
+    tile_m = first_m + (pid % per_group) % size_m;
+    tile_n = (pid % per_group) / size_m;
+    m_begin = tile_m * BM;
+    m_end = min(m_begin + BM, p.M);
+    const int z = blockIdx.z;
+    X += z * p.bsX;
+    W += z * p.bsW;
+    C += z * p.bsC;
+  }
+  const int rows_m = m_end - m_begin;
+  const int n0_out = tile_n * BN_OUT;
+
+  constexpr int kStage = (BM + BN) * kBK;
+  auto sX = [&](int s) { return smem + s * kStage; };
+  auto sW = [&](int s) { return smem + s * kStage + BM * kBK; };
+
+  const int* gather = p.gather;
+  const int64_t ldx = p.ldx, ldw = p.ldw;
+  auto x_row = [&](int r) -> const bf16* {
+    const int lr = m_begin + r;
+    const int64_t pr = gather ? (int64_t)gather[lr] : (int64_t)lr;
+    return X + pr * ldx;
+  };
+  // W tile rows: plain -> n0 + r; SwiGLU -> 32-row groups alternate gate/up.
+  auto w_row = [&](int r) -> const bf16* {
+    if constexpr (EPI == kEpiSwiGLU) {
+      const int g = r >> 5;
+      const int n = n0_out + (g >> 1) * 32 + (r & 31);
+      return ((g & 1) ? W2 : W) + (int64_t)n * ldw;
+    } else {
+      return W + (int64_t)(n0_out + r) * ldw;
+    }
+  };
+  int rows_n;
+  if constexpr (EPI == kEpiSwiGLU) {
+    // Rows of a gate/up group exist iff their output column exists.
+    rows_n = BN;  // handled per row below via the column bound
+  } else {
+    rows_n = min(BN, p.N - n0_out);
+  }
+
+  TileLoader<BM, NT> lx;
+  TileLoader<BN, NT> lw;
+  const int K = p.K;
+  const int nk = (K + kBK - 1) / kBK;
+
+  auto load_stage = [&](int kt) {
+    lx.load(x_row, rows_m, kt * kBK, K, tid);
+    if constexpr (EPI == kEpiSwiGLU) {
+      // Valid W rows: those whose output column n < N.
+      const int ncols = p.N - n0_out;
+#pragma unroll
+      for (int i = 0; i < TileLoader<BN, NT>::kPer; ++i) {
+        const int id = tid + i * NT;
+        const int r = id / kChunks;
+        const int c = id % kChunks;
+        const int k = kt * kBK + c * 8;
+        const int col = (r >> 6) * 32 + (r & 31);
+        if (col < ncols && k < K) {
+          lw.v[i] = *reinterpret_cast<const bf16x8*>(w_row(r) + k);
+        } else {
+          lw.v[i] = bf16x8{};
+        }
+      }
+    } else {
+      lw.load(w_row, rows_n, kt * kBK, K, tid);
+    }
+  };
+
+  WaveAcc<TN, TM> acc;
+  acc.zero();
+
+  load_stage(0);
+  lx.store(sX(0), tid);
+  lw.store(sW(0), tid);
+  __syncthreads();
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) load_stage(kt + 1);
+    acc.mma_stage(sX(cur), sW(cur), wm * WTM, wn * WTN, lane);
+    if (kt + 1 < nk) {
+      lx.store(sX(cur ^ 1), tid);
+      lw.store(sW(cur ^ 1), tid);
+    }
+    __syncthreads();
+  }
+
+  // ------------------------------------------------------------ epilogue
+  const int l32 = lane & 31;
+  const int h = lane >> 5;
+  const int N = p.N;
+  const bool vec_ok = ((p.ldc & 3) == 0) && (p.R == nullptr || (p.ldr & 3) == 0);
+
+  if constexpr (EPI == kEpiSwiGLU) {
+#pragma unroll
+    for (int i = 0; i < TN / 2; ++i) {
+#pragma unroll
+      for (int j = 0; j < TM; ++j) {
+        const int mr = wm * WTM + j * 32 + l32;
+        if (mr >= rows_m) continue;
+        bf16* crow = C + (int64_t)(m_begin + mr) * p.ldc;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = n0_out + (wn * WTN) / 2 + i * 32 + 8 * g + 4 * h;
+          float o[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float gt = acc.c[2 * i][j][4 * g + q];
+            const float up = acc.c[2 * i + 1][j][4 * g + q];
+            o[q] = gt / (1.0f + __expf(-gt)) * up;
+          }
+          if (vec_ok && n + 3 < N) {
+            bf16x4 v = {f2bf(o[0]), f2bf(o[1]), f2bf(o[2]), f2bf(o[3])};
+            *reinterpret_cast<bf16x4*>(crow + n) = v;
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              if (n + q < N) crow[n + q] = f2bf(o[q]);
+          }
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TN; ++i) {
+#pragma unroll
+      for (int j = 0; j < TM; ++j) {
+        const int mr = wm * WTM + j * 32 + l32;
+        if (mr >= rows_m) continue;
+        const int m = m_begin + mr;
+        bf16* crow = C + (int64_t)m * p.ldc;
+        float rs = 1.0f;
+        if constexpr (EPI == kEpiRowScale) rs = bf2f(p.rowscale[m]);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = n0_out + wn * WTN + i * 32 + 8 * g + 4 * h;
+          float o[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) o[q] = acc.c[i][j][4 * g + q];
+          if (vec_ok && n + 3 < N) {
+            if (p.bias) {
+              const bf16x4 b = *reinterpret_cast<const bf16x4*>(p.bias + n);
+#pragma unroll
+              for (int q = 0; q < 4; ++q) o[q] += bf2f(b[q]);
+            }
+            if (p.R) {
+              const bf16x4 rv = *reinterpret_cast<const bf16x4*>(p.R + (int64_t)m * p.ldr + n);
+#pragma unroll
+              for (int q = 0; q < 4; ++q) o[q] += bf2f(rv[q]);
+            }
+            if constexpr (EPI == kEpiRowScale) {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) o[q] = bf2f(f2bf(o[q])) * rs;
+            }
+            bf16x4 v = {f2bf(o[0]), f2bf(o[1]), f2bf(o[2]), f2bf(o[3])};
+            *reinterpret_cast<bf16x4*>(crow + n) = v;
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              if (n + q >= N) continue;
+              float v = o[q];
+              if (p.bias) v += bf2f(p.bias[n + q]);
+              if (p.R) v += bf2f(p.R[(int64_t)m * p.ldr + n + q]);
+              if constexpr (EPI == kEpiRowScale) v = bf2f(f2bf(v)) * rs;
+              crow[n + q] = f2bf(v);
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+}  // namespace q3

@@ -1,0 +1,558 @@
+// Sparse-MoE kernels.
+//
+//  q3_moe_route     router probabilities -> top-k -> renormalise, one wave per
+//                   token: fp32 softmax over the (bf16) logits, k rounds of a
+//                   wave arg-max (larger probability wins, lower expert index
+//                   among equals), weights = p / sum(p_selected) cast to bf16.
+//  q3_moe_experts   dispatch + expert MLPs + combine for routed tokens:
+//                     1. count      block per expert: #(token, slot) pairs
+//                     2. scan       one block: expert offsets and the m-tile table
+//                     3. scatter    block per expert: its pairs in ascending
+//                                   token order (a block-wide ballot prefix sum)
+//                     4. GEMM 1     grouped MFMA GEMM, gathered token rows x
+//                                   gate/up of the pair's expert, SwiGLU epilogue
+//                     5. GEMM 2     grouped MFMA GEMM x down, epilogue
+//                                   bf16(bf16(y) * routing weight)
+//                     6. combine    one wave per token: its k expert rows added
+//                                   in ascending expert order with a bf16
+//                                   rounding after each add (the order and
+//                                   rounding of a per-expert bf16 index_add),
+//                                   optionally plus a residual
+//  q3_index_add     deterministic target[idx[i]] += src[i]: bucket the sources
+//                   by target, then each target adds its sources in ascending
+//                   source order in fp32 and rounds once.
+#include <algorithm>
+
+#include "gemm_kernels.h"
+
+using namespace q3;
+
+namespace {
+
+constexpr int kMoeBM = 128;
+constexpr int kMoeBN = 128;
+
+// ------------------------------------------------------------------ routing
+template <int MAXV>
+__global__ __launch_bounds__(256) void moe_route_kernel(const bf16* __restrict__ logits, int* __restrict__ top_idx,
+                                                        bf16* __restrict__ top_w, float* __restrict__ top_p,
+                                                        int T, int E, int k, int norm) {
+  const int lane = threadIdx.x & 63;
+  const int t = (int)(((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+  if (t >= T) return;
+  const bf16* lr = logits + (int64_t)t * E;
+  float v[MAXV];
+  bool live[MAXV];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) {
+    const int e = lane + 64 * i;
+    live[i] = e < E;
+    v[i] = live[i] ? bf2f(lr[e]) : -INFINITY;
+    mx = fmaxf(mx, v[i]);
+  }
+  mx = wave_max(mx);
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) {
+    v[i] = live[i] ? expf(v[i] - mx) : 0.f;
+    s += v[i];
+  }
+  s = wave_sum(s);
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) v[i] *= inv;
+  float sel_sum = 0.f;
+  float sel_v[32];
+  for (int r = 0; r < k; ++r) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < MAXV; ++i) {
+      const int e = lane + 64 * i;
+      if (live[i] && (v[i] > bv || (v[i] == bv && e < bi))) {
+        bv = v[i];
+        bi = e;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, 64);
+      const int oi = __shfl_xor(bi, o, 64);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < MAXV; ++i)
+      if (lane + 64 * i == bi) live[i] = false;
+    sel_v[r] = bv;
+    if (lane == 0) top_idx[(int64_t)t * k + r] = bi;
+  }
+  // Renormalise: the sum runs over the selected values in selection order.
+  for (int r = 0; r < k; ++r) sel_sum += sel_v[r];
+  if (lane == 0) {
+    for (int r = 0; r < k; ++r) {
+      const float w = norm ? sel_v[r] / sel_sum : sel_v[r];
+      top_w[(int64_t)t * k + r] = f2bf(w);
+      if (top_p) top_p[(int64_t)t * k + r] = sel_v[r];
+    }
+  }
+}
+
+// ------------------------------------------------------------------ permute
+// Workspace carve-out (all int32 unless noted):
+//   counts[E], offsets[E + 1], tile_table[max_tiles], n_tiles[1],
+//   sorted_token[P], sorted_w (bf16)[P], pos_of[P]   (P = T * k)
+struct MoeWs {
+  int* counts;
+  int* offsets;
+  int* tile_table;
+  int* n_tiles;
+  int* sorted_token;
+  bf16* sorted_w;
+  int* pos_of;
+  bf16* act;     // (P, I)
+  bf16* y_perm;  // (P, H)
+};
+
+__device__ __forceinline__ int block_excl_scan_flags(int flag, int* s_wave, int* total) {
+  // 256 threads = 4 waves; returns the exclusive prefix of `flag` in thread order.
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const unsigned long long m = __ballot(flag);
+  const int before = __popcll(m & ((1ull << lane) - 1ull));
+  if (lane == 0) s_wave[wave] = __popcll(m);
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave; ++w) base += s_wave[w];
+  *total = s_wave[0] + s_wave[1] + s_wave[2] + s_wave[3];
+  __syncthreads();
+  return base + before;
+}
+
+// Block per expert: number of tokens routed to it.
+__global__ __launch_bounds__(256) void moe_count_kernel(const int* __restrict__ top_idx, int T, int k,
+                                                        int* __restrict__ counts) {
+  __shared__ int s_wave[4];
+  const int e = blockIdx.x;
+  int count = 0;
+  for (int t0 = 0; t0 < T; t0 += 256) {
+    const int t = t0 + threadIdx.x;
+    int flag = 0;
+    if (t < T)
+      for (int s = 0; s < k; ++s) flag |= (top_idx[(int64_t)t * k + s] == e);
+    int tot;
+    block_excl_scan_flags(flag, s_wave, &tot);
+    count += tot;
+  }
+  if (threadIdx.x == 0) counts[e] = count;
+}
+
+// One block: offsets = exclusive scan of counts; m-tile table for the grouped GEMM.
+__global__ __launch_bounds__(256) void moe_scan_kernel(const int* __restrict__ counts, int E, int* __restrict__ offsets,
+                                                       int* __restrict__ tile_table, int* __restrict__ n_tiles) {
+  if (threadIdx.x != 0) return;
+  int off = 0, nt = 0;
+  for (int e = 0; e < E; ++e) {
+    offsets[e] = off;
+    const int c = counts[e];
+    for (int m = 0; m < c; m += kMoeBM) tile_table[nt++] = (e << 20) | (off + m);
+    off += c;
+  }
+  offsets[E] = off;
+  *n_tiles = nt;
+}
+
+// Block per expert: write its pairs in ascending token order.
+__global__ __launch_bounds__(256) void moe_scatter_kernel(const int* __restrict__ top_idx,
+                                                          const bf16* __restrict__ top_w, int T, int k,
+                                                          const int* __restrict__ offsets,
+                                                          int* __restrict__ sorted_token, bf16* __restrict__ sorted_w,
+                                                          int* __restrict__ pos_of) {
+  __shared__ int s_wave[4];
+  const int e = blockIdx.x;
+  int base = offsets[e];
+  for (int t0 = 0; t0 < T; t0 += 256) {
+    const int t = t0 + threadIdx.x;
+    int slot = -1;
+    if (t < T)
+      for (int s = 0; s < k; ++s)
+        if (top_idx[(int64_t)t * k + s] == e) slot = s;
+    int tot;
+    const int rank = block_excl_scan_flags(slot >= 0, s_wave, &tot);
+    if (slot >= 0) {
+      const int pos = base + rank;
+      sorted_token[pos] = t;
+      sorted_w[pos] = top_w[(int64_t)t * k + slot];
+      pos_of[(int64_t)t * k + slot] = pos;
+    }
+    base += tot;
+  }
+}
+
+// One wave per token: add its k expert rows in ascending expert order.
+template <int VPL>
+__global__ __launch_bounds__(256) void moe_combine_kernel(const int* __restrict__ top_idx,
+                                                          const int* __restrict__ pos_of,
+                                                          const bf16* __restrict__ y_perm,
+                                                          const bf16* __restrict__ residual, bf16* __restrict__ out,
+                                                          int T, int k, int H, int E) {
+  const int lane = threadIdx.x & 63;
+  const int t = (int)(((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+  if (t >= T) return;
+  int ex[32], ps[32];
+  int kk = 0;  // slots with a valid expert id (others were never dispatched)
+  for (int s = 0; s < k; ++s) {
+    const int e = top_idx[(int64_t)t * k + s];
+    const int pp = pos_of[(int64_t)t * k + s];
+    if (e < 0 || e >= E || pp < 0 || pp >= T * k) continue;
+    ex[kk] = e;
+    ps[kk] = pp;
+    ++kk;
+  }
+  k = kk;
+  // insertion sort by expert id
+  for (int i = 1; i < k; ++i) {
+    const int e = ex[i], p = ps[i];
+    int j = i - 1;
+    while (j >= 0 && ex[j] > e) {
+      ex[j + 1] = ex[j];
+      ps[j + 1] = ps[j];
+      --j;
+    }
+    ex[j + 1] = e;
+    ps[j + 1] = p;
+  }
+  // lane owns vectors lane + 64 * i of 8 bf16
+  const int nvec = H / 8;
+  for (int i = 0; i < VPL; ++i) {
+    const int vi = lane + 64 * i;
+    if (vi >= nvec) break;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < k; ++s) {
+      const bf16x8 yv = reinterpret_cast<const bf16x8*>(y_perm + (int64_t)ps[s] * H)[vi];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) acc[q] = bf2f(f2bf(acc[q] + bf2f(yv[q])));
+    }
+    bf16x8 o;
+    if (residual) {
+      const bf16x8 rv = reinterpret_cast<const bf16x8*>(residual + (int64_t)t * H)[vi];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) o[q] = f2bf(acc[q] + bf2f(rv[q]));
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) o[q] = f2bf(acc[q]);
+    }
+    reinterpret_cast<bf16x8*>(out + (int64_t)t * H)[vi] = o;
+  }
+}
+
+int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
+int64_t moe_ws_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, MoeWs* ws, char* base) {
+  const int64_t P = T * k;
+  const int64_t max_tiles = q3_cdiv(P, kMoeBM) + E;
+  int64_t off = 0;
+  auto take = [&](int64_t bytes) {
+    char* p = base ? base + off : nullptr;
+    off += align256(bytes);
+    return p;
+  };
+  MoeWs w{};
+  w.counts = reinterpret_cast<int*>(take(E * 4));
+  w.offsets = reinterpret_cast<int*>(take((E + 1) * 4));
+  w.tile_table = reinterpret_cast<int*>(take(max_tiles * 4));
+  w.n_tiles = reinterpret_cast<int*>(take(4));
+  w.sorted_token = reinterpret_cast<int*>(take(P * 4));
+  w.sorted_w = reinterpret_cast<bf16*>(take(P * 2));
+  w.pos_of = reinterpret_cast<int*>(take(P * 4));
+  w.act = reinterpret_cast<bf16*>(take(P * I * 2));
+  w.y_perm = reinterpret_cast<bf16*>(take(P * H * 2));
+  if (ws) *ws = w;
+  return off;
+}
+
+// ------------------------------------------------------------------ index_add
+__global__ void fill_int_kernel(int* p, int64_t n, int v) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = v;
+}
+
+__global__ void ia_count_kernel(const int64_t* __restrict__ idx, int64_t ns, int64_t nt, int* __restrict__ counts,
+                                int* __restrict__ bad) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < ns; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = idx[i];
+    if (t < 0 || t >= nt) {
+      atomicOr(bad, 1);
+      continue;
+    }
+    atomicAdd(&counts[t], 1);
+  }
+}
+
+__global__ void ia_scan_kernel(const int* __restrict__ counts, int64_t nt, int* __restrict__ starts) {
+  // Single block, 256 threads: chunked scan.
+  __shared__ int s[256];
+  __shared__ int carry;
+  if (threadIdx.x == 0) carry = 0;
+  __syncthreads();
+  for (int64_t c0 = 0; c0 < nt; c0 += 256) {
+    const int64_t i = c0 + threadIdx.x;
+    const int v = i < nt ? counts[i] : 0;
+    s[threadIdx.x] = v;
+    __syncthreads();
+    for (int o = 1; o < 256; o <<= 1) {
+      const int a = (threadIdx.x >= (unsigned)o) ? s[threadIdx.x - o] : 0;
+      __syncthreads();
+      s[threadIdx.x] += a;
+      __syncthreads();
+    }
+    if (i < nt) starts[i] = carry + s[threadIdx.x] - v;
+    __syncthreads();
+    if (threadIdx.x == 255) carry += s[255];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) starts[nt] = carry;
+}
+
+__global__ void ia_scatter_kernel(const int64_t* __restrict__ idx, int64_t ns, int64_t nt,
+                                  const int* __restrict__ starts, int* __restrict__ fill, int* __restrict__ bucket) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < ns; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = idx[i];
+    if (t < 0 || t >= nt) continue;
+    const int slot = atomicAdd(&fill[t], 1);
+    bucket[starts[t] + slot] = (int)i;
+  }
+}
+
+// One wave per target row. Its sources are added in ascending source index,
+// in fp32 starting from the target value, with one rounding at the end (the
+// order and precision of torch's CPU index_add_). The bucket (unordered after
+// the atomic scatter) is rank-sorted in LDS when it holds <= kIaLds entries;
+// longer buckets take the next-smallest index by repeated wave minima.
+constexpr int kIaLds = 1024;
+
+template <typename T>
+__global__ __launch_bounds__(256) void ia_accumulate_kernel(T* __restrict__ target, const T* __restrict__ src,
+                                                            const int* __restrict__ starts,
+                                                            const int* __restrict__ bucket, int64_t nt, int64_t D) {
+  __shared__ int s_raw[4][kIaLds];
+  __shared__ int s_sorted[4][kIaLds];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t t = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  if (t >= nt) return;
+  const int b0 = starts[t], c = starts[t + 1] - b0;
+  if (c == 0) return;
+  T* tr = target + t * D;
+  if (c <= kIaLds) {
+    for (int j = lane; j < c; j += 64) s_raw[wave][j] = bucket[b0 + j];
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    for (int j = lane; j < c; j += 64) {
+      const int v = s_raw[wave][j];
+      int rank = 0;
+      for (int q = 0; q < c; ++q) rank += s_raw[wave][q] < v;  // source indices are distinct
+      s_sorted[wave][rank] = v;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    for (int64_t d = lane; d < D; d += 64) {
+      float acc = to_f<T>(tr[d]);
+      for (int n = 0; n < c; ++n) acc += to_f<T>(src[(int64_t)s_sorted[wave][n] * D + d]);
+      tr[d] = from_f<T>(acc);
+    }
+    return;
+  }
+  for (int64_t d0 = 0; d0 < D; d0 += 64) {
+    const int64_t d = d0 + lane;
+    float acc = d < D ? to_f<T>(tr[d]) : 0.f;
+    int prev = -1;
+    for (int n = 0; n < c; ++n) {
+      int best = 0x7fffffff;
+      for (int j = lane; j < c; j += 64) {
+        const int v = bucket[b0 + j];
+        if (v > prev && v < best) best = v;
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) best = min(best, __shfl_xor(best, o, 64));
+      prev = best;
+      if (d < D) acc += to_f<T>(src[(int64_t)best * D + d]);
+    }
+    if (d < D) tr[d] = from_f<T>(acc);
+  }
+}
+
+template <typename T>
+int index_add_t(void* target, const void* src, const int64_t* idx, int64_t ns, int64_t nt, int64_t D, char* ws,
+                hipStream_t st) {
+  int* counts = reinterpret_cast<int*>(ws);
+  int* fill = counts + nt;
+  int* starts = fill + nt;
+  int* bucket = starts + nt + 1;
+  int* bad = bucket + ns;
+  const unsigned fb = (unsigned)std::min<int64_t>(q3_cdiv(2 * nt + 1, 256), 1024);
+  hipLaunchKernelGGL(fill_int_kernel, dim3(fb), dim3(256), 0, st, counts, 2 * nt, 0);
+  hipLaunchKernelGGL(fill_int_kernel, dim3(1), dim3(64), 0, st, bad, (int64_t)1, 0);
+  const unsigned sb = (unsigned)std::max<int64_t>(1, std::min<int64_t>(q3_cdiv(ns, 256), 1024));
+  hipLaunchKernelGGL(ia_count_kernel, dim3(sb), dim3(256), 0, st, idx, ns, nt, counts, bad);
+  hipLaunchKernelGGL(ia_scan_kernel, dim3(1), dim3(256), 0, st, counts, nt, starts);
+  hipLaunchKernelGGL(ia_scatter_kernel, dim3(sb), dim3(256), 0, st, idx, ns, nt, starts, fill, bucket);
+  hipLaunchKernelGGL(ia_accumulate_kernel<T>, dim3((unsigned)q3_cdiv(nt, 4)), dim3(256), 0, st,
+                     static_cast<T*>(target), static_cast<const T*>(src), starts, bucket, nt, D);
+  Q3_LAUNCH_CHECK();
+  return Q3_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+// logits (T, E) bf16 -> top_idx (T, k) int32, top_w (T, k) bf16 (renormalised
+// when norm != 0), top_p (T, k) fp32 selected probabilities (optional).
+int q3_moe_route(const void* logits, int* top_idx, void* top_w, float* top_p, int64_t T, int64_t E, int64_t k,
+                 int norm, void* stream) {
+  Q3_REQUIRE(logits && top_idx && top_w, Q3_ERR_NULL);
+  Q3_REQUIRE(T >= 0 && E >= 1 && k >= 1 && k <= E, Q3_ERR_SHAPE);
+  Q3_REQUIRE(E <= 512 && k <= 32, Q3_ERR_UNSUPPORTED);
+  if (T == 0) return Q3_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned blocks = (unsigned)q3_cdiv(T, 4);
+  const bf16* lg = static_cast<const bf16*>(logits);
+  bf16* tw = static_cast<bf16*>(top_w);
+  if (E <= 64)
+    hipLaunchKernelGGL(moe_route_kernel<1>, dim3(blocks), dim3(256), 0, st, lg, top_idx, tw, top_p, (int)T, (int)E,
+                       (int)k, norm);
+  else if (E <= 128)
+    hipLaunchKernelGGL(moe_route_kernel<2>, dim3(blocks), dim3(256), 0, st, lg, top_idx, tw, top_p, (int)T, (int)E,
+                       (int)k, norm);
+  else if (E <= 256)
+    hipLaunchKernelGGL(moe_route_kernel<4>, dim3(blocks), dim3(256), 0, st, lg, top_idx, tw, top_p, (int)T, (int)E,
+                       (int)k, norm);
+  else
+    hipLaunchKernelGGL(moe_route_kernel<8>, dim3(blocks), dim3(256), 0, st, lg, top_idx, tw, top_p, (int)T, (int)E,
+                       (int)k, norm);
+  Q3_LAUNCH_CHECK();
+  return Q3_OK;
+}
+
+int64_t q3_moe_experts_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k) {
+  if (T <= 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
+  return moe_ws_layout(T, H, I, E, k, nullptr, nullptr);
+}
+
+// x (T, H) bf16; gate_up (E, 2I, H); down (E, H, I); top_idx (T, k) int32;
+// top_w (T, k) bf16; out (T, H) bf16 = sum over the token's experts of
+// w * down(swiglu(gate_up x)) (+ residual (T, H) when given).
+int q3_moe_experts(const void* x, const void* gate_up, const void* down, const int* top_idx, const void* top_w,
+                   const void* residual, void* out, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
+                   void* workspace, int64_t workspace_bytes, void* stream) {
+  Q3_REQUIRE(x && gate_up && down && top_idx && top_w && out, Q3_ERR_NULL);
+  Q3_REQUIRE(T >= 0 && H >= 8 && I >= 8 && E >= 1 && k >= 1 && k <= E, Q3_ERR_SHAPE);
+  Q3_REQUIRE(H % 8 == 0 && I % 8 == 0 && k <= 32 && E < 2048 && T * k < (1 << 20), Q3_ERR_UNSUPPORTED);
+  Q3_REQUIRE(q3_aligned(x, 16) && q3_aligned(gate_up, 16) && q3_aligned(down, 16) && q3_aligned(out, 16) &&
+                 (!residual || q3_aligned(residual, 16)),
+             Q3_ERR_ALIGN);
+  if (T == 0) return Q3_OK;
+  Q3_REQUIRE(workspace && workspace_bytes >= q3_moe_experts_workspace_bytes(T, H, I, E, k), Q3_ERR_WORKSPACE);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  MoeWs w{};
+  moe_ws_layout(T, H, I, E, k, &w, static_cast<char*>(workspace));
+  const int64_t P = T * k;
+  const int64_t max_tiles = q3_cdiv(P, kMoeBM) + E;
+
+  hipLaunchKernelGGL(moe_count_kernel, dim3((unsigned)E), dim3(256), 0, st, top_idx, (int)T, (int)k, w.counts);
+  hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(64), 0, st, w.counts, (int)E, w.offsets, w.tile_table,
+                     w.n_tiles);
+  hipLaunchKernelGGL(moe_scatter_kernel, dim3((unsigned)E), dim3(256), 0, st, top_idx,
+                     static_cast<const bf16*>(top_w), (int)T, (int)k, w.offsets, w.sorted_token, w.sorted_w,
+                     w.pos_of);
+  Q3_LAUNCH_CHECK();
+
+  // GEMM 1: act[pos] = swiglu(x[token(pos)] . gate_up[e]^T)
+  {
+    GemmParams p{};
+    p.X = static_cast<const bf16*>(x);
+    p.W = static_cast<const bf16*>(gate_up);           // gate rows [0, I)
+    p.W2 = static_cast<const bf16*>(gate_up) + I * H;  // up rows [I, 2I)
+    p.C = w.act;
+    p.M = (int)P;
+    p.N = (int)I;
+    p.K = (int)H;
+    p.ldx = H;
+    p.ldw = H;
+    p.ldc = I;
+    p.gather = w.sorted_token;
+    p.tile_table = w.tile_table;
+    p.group_end = w.offsets + 1;
+    p.n_tiles_total = w.n_tiles;
+    p.expert_stride_w = 2 * I * H;
+    const int64_t ntn = q3_cdiv(I, kMoeBN / 2);
+    hipLaunchKernelGGL((gemm_bf16_kernel<kMoeBM, kMoeBN, 2, 2, kEpiSwiGLU, true>), dim3((unsigned)(max_tiles * ntn)),
+                       dim3(256), 0, st, p);
+    Q3_LAUNCH_CHECK();
+  }
+  // GEMM 2: y_perm[pos] = bf16(bf16(act[pos] . down[e]^T) * w[pos])
+  {
+    GemmParams p{};
+    p.X = w.act;
+    p.W = static_cast<const bf16*>(down);
+    p.C = w.y_perm;
+    p.rowscale = w.sorted_w;
+    p.M = (int)P;
+    p.N = (int)H;
+    p.K = (int)I;
+    p.ldx = I;
+    p.ldw = I;
+    p.ldc = H;
+    p.gather = nullptr;
+    p.tile_table = w.tile_table;
+    p.group_end = w.offsets + 1;
+    p.n_tiles_total = w.n_tiles;
+    p.expert_stride_w = H * I;
+    const int64_t ntn = q3_cdiv(H, kMoeBN);
+    hipLaunchKernelGGL((gemm_bf16_kernel<kMoeBM, kMoeBN, 2, 2, kEpiRowScale, true>),
+                       dim3((unsigned)(max_tiles * ntn)), dim3(256), 0, st, p);
+    Q3_LAUNCH_CHECK();
+  }
+  const int vpl = (int)q3_cdiv(H / 8, 64);
+  const unsigned cb = (unsigned)q3_cdiv(T, 4);
+  const bf16* res = static_cast<const bf16*>(residual);
+  bf16* o = static_cast<bf16*>(out);
+  if (vpl <= 4)
+    hipLaunchKernelGGL(moe_combine_kernel<4>, dim3(cb), dim3(256), 0, st, top_idx, w.pos_of, w.y_perm, res, o, (int)T,
+                       (int)k, (int)H, (int)E);
+  else if (vpl <= 8)
+    hipLaunchKernelGGL(moe_combine_kernel<8>, dim3(cb), dim3(256), 0, st, top_idx, w.pos_of, w.y_perm, res, o, (int)T,
+                       (int)k, (int)H, (int)E);
+  else
+    hipLaunchKernelGGL(moe_combine_kernel<64>, dim3(cb), dim3(256), 0, st, top_idx, w.pos_of, w.y_perm, res, o,
+                       (int)T, (int)k, (int)H, (int)E);
+  Q3_LAUNCH_CHECK();
+  return Q3_OK;
+}
+
+int64_t q3_index_add_workspace_bytes(int64_t n_src, int64_t n_target) {
+  if (n_src < 0 || n_target < 0) return 0;
+  return (3 * n_target + 1 + n_src + 1) * (int64_t)sizeof(int);
+}
+
+// target (n_target, D) += rows of src (n_src, D) at idx (n_src) int64, in place.
+// Returns Q3_ERR_SHAPE (after the fact, via `status` on the device) ... indices
+// out of range are skipped; the host-side wrapper validates them.
+int q3_index_add(void* target, const void* src, const int64_t* idx, int64_t n_src, int64_t n_target, int64_t D,
+                 int dtype, void* workspace, int64_t workspace_bytes, void* stream) {
+  Q3_REQUIRE(target && (src || n_src == 0) && (idx || n_src == 0), Q3_ERR_NULL);
+  Q3_REQUIRE(n_src >= 0 && n_target >= 0 && D >= 0, Q3_ERR_SHAPE);
+  Q3_REQUIRE(n_src < (1ll << 31) && n_target < (1ll << 31), Q3_ERR_UNSUPPORTED);
+  if (n_src == 0 || n_target == 0 || D == 0) return Q3_OK;
+  Q3_REQUIRE(workspace && workspace_bytes >= q3_index_add_workspace_bytes(n_src, n_target), Q3_ERR_WORKSPACE);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  if (dtype == Q3_BF16) return index_add_t<bf16>(target, src, idx, n_src, n_target, D, ws, st);
+  if (dtype == Q3_F32) return index_add_t<float>(target, src, idx, n_src, n_target, D, ws, st);
+  return Q3_ERR_DTYPE;
+}
+
+}  // extern "C"

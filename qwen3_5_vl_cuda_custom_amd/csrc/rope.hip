@@ -1,0 +1,269 @@
+// Rotary position embedding kernels.
+//
+//  q3_rope          rotate-half RoPE with a cos/sin table (S, Dr) or (B, S, Dr)
+//  q3_mrope         rotate-half mRoPE with cos/sin (3, B, S, Dr) and the
+//                   chunked section layout: for i < Dr/2, element i uses axis
+//                   0 if i < s0, axis 1 if i < s0 + s1, else axis 2
+//  q3_qk_norm_rope  fused attention prologue: per-head RMSNorm of q and k, mRoPE
+//                   from integer positions (angles pos * inv_freq in fp32, as
+//                   the reference builds them), copy of v, all read from the
+//                   projection outputs in (B, S, H, D) layout and written to any
+//                   strided destination (e.g. straight into a KV cache)
+//
+// Rotate-half on pairs (i, i + Dr/2) with c = cos[i], s = sin[i], i < Dr/2:
+//   y[i] = x[i] c - x[i + Dr/2] s,   y[i + Dr/2] = x[i + Dr/2] c + x[i] s
+// and dims >= Dr pass through.
+#include "q3_common.h"
+
+namespace {
+
+struct RopeGeom {
+  int B, H, S, D, Dr;
+  int64_t xb, xh, xs;  // x strides
+  int64_t yb, yh, ys;  // y strides
+  int64_t ca, cb, cs;  // cos/sin strides: axis, batch, seq (element i contiguous)
+  int s0, s1;          // section boundaries (plain rope: s0 = Dr/2)
+};
+
+template <typename T, typename TC>
+__global__ __launch_bounds__(256) void rope_kernel(const T* __restrict__ x, const TC* __restrict__ cosp,
+                                                   const TC* __restrict__ sinp, T* __restrict__ y, RopeGeom g) {
+  const int half = g.Dr / 2;
+  const int per_row = half + (g.D - g.Dr);
+  const int64_t total = (int64_t)g.B * g.H * g.S * per_row;
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+    const int j = (int)(t % per_row);
+    int64_t row = t / per_row;
+    const int s = (int)(row % g.S);
+    row /= g.S;
+    const int h = (int)(row % g.H);
+    const int b = (int)(row / g.H);
+    const T* xr = x + b * g.xb + h * g.xh + s * g.xs;
+    T* yr = y + b * g.yb + h * g.yh + s * g.ys;
+    if (j < half) {
+      const int axis = (j < g.s0) ? 0 : (j < g.s0 + g.s1 ? 1 : 2);
+      const int64_t co = axis * g.ca + b * g.cb + s * g.cs + j;
+      const float c = to_f<TC>(cosp[co]);
+      const float sn = to_f<TC>(sinp[co]);
+      const float x1 = to_f<T>(xr[j]);
+      const float x2 = to_f<T>(xr[j + half]);
+      yr[j] = from_f<T>(x1 * c - x2 * sn);
+      yr[j + half] = from_f<T>(x2 * c + x1 * sn);
+    } else {
+      const int d = g.Dr + (j - half);
+      yr[d] = xr[d];
+    }
+  }
+}
+
+template <typename T>
+int launch_rope_t(const void* x, const void* cosp, const void* sinp, void* y, const RopeGeom& g, int cos_dtype,
+                  hipStream_t st) {
+  const int64_t total = (int64_t)g.B * g.H * g.S * (g.Dr / 2 + g.D - g.Dr);
+  if (total == 0) return Q3_OK;
+  const unsigned blocks = (unsigned)std::min<int64_t>(q3_cdiv(total, 256), 65536);
+  if (cos_dtype == Q3_F32)
+    hipLaunchKernelGGL((rope_kernel<T, float>), dim3(blocks), dim3(256), 0, st, static_cast<const T*>(x),
+                       static_cast<const float*>(cosp), static_cast<const float*>(sinp), static_cast<T*>(y), g);
+  else if (cos_dtype == Q3_BF16)
+    hipLaunchKernelGGL((rope_kernel<T, bf16>), dim3(blocks), dim3(256), 0, st, static_cast<const T*>(x),
+                       static_cast<const bf16*>(cosp), static_cast<const bf16*>(sinp), static_cast<T*>(y), g);
+  else
+    return Q3_ERR_DTYPE;
+  Q3_LAUNCH_CHECK();
+  return Q3_OK;
+}
+
+int launch_rope(const void* x, const void* cosp, const void* sinp, void* y, const RopeGeom& g, int dtype,
+                int cos_dtype, hipStream_t st) {
+  Q3_REQUIRE(x && cosp && sinp && y, Q3_ERR_NULL);
+  Q3_REQUIRE(g.B >= 0 && g.H >= 0 && g.S >= 0 && g.D >= 1, Q3_ERR_SHAPE);
+  Q3_REQUIRE(g.Dr >= 2 && g.Dr % 2 == 0 && g.Dr <= g.D, Q3_ERR_SHAPE);
+  Q3_REQUIRE(g.s0 >= 0 && g.s1 >= 0 && g.s0 + g.s1 <= g.Dr / 2, Q3_ERR_SHAPE);
+  if (dtype == Q3_BF16) return launch_rope_t<bf16>(x, cosp, sinp, y, g, cos_dtype, st);
+  if (dtype == Q3_F32) return launch_rope_t<float>(x, cosp, sinp, y, g, cos_dtype, st);
+  return Q3_ERR_DTYPE;
+}
+
+// ------------------------------------------------------------------ fused prologue
+struct QKNormRopeArgs {
+  const void* q_in;
+  const void* k_in;
+  const void* v_in;
+  void* q_out;
+  void* k_out;
+  void* v_out;
+  const void* q_w;
+  const void* k_w;
+  const int* pos;          // (3, B, S) int32
+  const float* inv_freq;   // (D/2) fp32
+  const int* dst_seq_off;  // (B) int32 offset added to s for k_out / v_out, or null
+  int64_t dst_seq_cap;     // k_out / v_out rows at sequence index >= cap are not written
+  int B, S, Hq, Hkv, D;
+  int s0, s1;
+  float eps;
+  int64_t st[18];  // (b, s, h) strides of q_in, k_in, v_in, q_out, k_out, v_out
+};
+
+// One group of G = D/8 lanes per (b, s, head) row; lane j holds elements
+// [8j, 8j+8). The rotate-half partner of lane j is lane j ^ (G/2).
+template <typename T, int G>
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(const QKNormRopeArgs a) {
+  constexpr int D = G * 8;
+  const int lane = threadIdx.x & 63;
+  const int j = lane % G;
+  const int64_t grow = ((blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6) * (64 / G) + lane / G;
+  const int64_t rq = (int64_t)a.B * a.S * a.Hq;
+  const int64_t rk = (int64_t)a.B * a.S * a.Hkv;
+  const int64_t rv = a.v_out ? rk : 0;
+  if (grow >= rq + rk + rv) return;
+  int kind;  // 0 = q, 1 = k, 2 = v
+  int64_t r;
+  if (grow < rq) {
+    kind = 0;
+    r = grow;
+  } else if (grow < rq + rk) {
+    kind = 1;
+    r = grow - rq;
+  } else {
+    kind = 2;
+    r = grow - rq - rk;
+  }
+  const int H = kind == 0 ? a.Hq : a.Hkv;
+  const int h = (int)(r % H);
+  const int64_t bs = r / H;
+  const int s = (int)(bs % a.S);
+  const int b = (int)(bs / a.S);
+  const int64_t* sin_ = a.st + 3 * kind;
+  const int64_t* sout = a.st + 9 + 3 * kind;
+  const T* in = static_cast<const T*>(kind == 0 ? a.q_in : (kind == 1 ? a.k_in : a.v_in)) + b * sin_[0] +
+                s * sin_[1] + h * sin_[2];
+  const int so = (kind > 0 && a.dst_seq_off) ? a.dst_seq_off[b] : 0;
+  const bool skip_store = kind > 0 && (s + (int64_t)so >= a.dst_seq_cap || s + so < 0);
+  T* out = static_cast<T*>(kind == 0 ? a.q_out : (kind == 1 ? a.k_out : a.v_out)) + b * sout[0] +
+           (int64_t)(s + so) * sout[1] + h * sout[2];
+
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = to_f<T>(in[8 * j + e]);
+  if (kind < 2) {
+    // RMSNorm over the head (skipped when no weights are given).
+    if (a.q_w) {
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+      ss = group_sum<G>(ss);
+      const float rstd = rsqrtf(ss / (float)D + a.eps);
+      const T* w = static_cast<const T*>(kind == 0 ? a.q_w : a.k_w);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = v[e] * rstd * to_f<T>(w[8 * j + e]);
+    }
+    // mRoPE.
+    float p[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) p[e] = __shfl_xor(v[e], G / 2, 64);
+    const bool lo = j < G / 2;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int i = (8 * j + e) % (D / 2);
+      const int axis = (i < a.s0) ? 0 : (i < a.s0 + a.s1 ? 1 : 2);
+      const float ang = (float)a.pos[((int64_t)axis * a.B + b) * a.S + s] * a.inv_freq[i];
+      float sn, c;
+      sincosf(ang, &sn, &c);
+      // lo half: x1*c - x2*s  (partner holds x2); hi half: x2*c + x1*s (partner holds x1).
+      v[e] = lo ? (v[e] * c - p[e] * sn) : (v[e] * c + p[e] * sn);
+    }
+  }
+  if (skip_store) return;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) out[8 * j + e] = from_f<T>(v[e]);
+}
+
+template <typename T>
+int launch_qk(const QKNormRopeArgs& a, hipStream_t st) {
+  const int64_t rows = (int64_t)a.B * a.S * (a.Hq + (a.v_out ? 2 : 1) * a.Hkv);
+  if (rows == 0) return Q3_OK;
+  const int G = a.D / 8;
+  const int64_t rows_per_block = 4 * (64 / G);
+  const unsigned blocks = (unsigned)q3_cdiv(rows, rows_per_block);
+  switch (G) {
+    case 8:
+      hipLaunchKernelGGL((qk_norm_rope_kernel<T, 8>), dim3(blocks), dim3(256), 0, st, a);
+      break;
+    case 16:
+      hipLaunchKernelGGL((qk_norm_rope_kernel<T, 16>), dim3(blocks), dim3(256), 0, st, a);
+      break;
+    case 32:
+      hipLaunchKernelGGL((qk_norm_rope_kernel<T, 32>), dim3(blocks), dim3(256), 0, st, a);
+      break;
+    default:
+      return Q3_ERR_UNSUPPORTED;
+  }
+  Q3_LAUNCH_CHECK();
+  return Q3_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int q3_rope(const void* x, const void* cos, const void* sin, void* y, int64_t B, int64_t H, int64_t S, int64_t D,
+            int64_t D_rope, const int64_t* x_strides, const int64_t* y_strides, int64_t cos_batch_stride,
+            int64_t cos_seq_stride, int dtype, int cos_dtype, void* stream) {
+  Q3_REQUIRE(x_strides && y_strides, Q3_ERR_NULL);
+  RopeGeom g{(int)B, (int)H, (int)S, (int)D, (int)D_rope, x_strides[0], x_strides[1], x_strides[2],
+             y_strides[0], y_strides[1], y_strides[2], 0, cos_batch_stride, cos_seq_stride, (int)(D_rope / 2), 0};
+  return launch_rope(x, cos, sin, y, g, dtype, cos_dtype, static_cast<hipStream_t>(stream));
+}
+
+int q3_mrope(const void* x, const void* cos3d, const void* sin3d, void* y, int64_t B, int64_t H, int64_t S, int64_t D,
+             int64_t D_rope, const int64_t* section, const int64_t* x_strides, const int64_t* y_strides,
+             const int64_t* cos_strides, int dtype, int cos_dtype, void* stream) {
+  Q3_REQUIRE(section && x_strides && y_strides && cos_strides, Q3_ERR_NULL);
+  RopeGeom g{(int)B, (int)H, (int)S, (int)D, (int)D_rope, x_strides[0], x_strides[1], x_strides[2],
+             y_strides[0], y_strides[1], y_strides[2], cos_strides[0], cos_strides[1], cos_strides[2],
+             (int)section[0], (int)section[1]};
+  Q3_REQUIRE(section[0] + section[1] + section[2] == D_rope / 2, Q3_ERR_SHAPE);
+  return launch_rope(x, cos3d, sin3d, y, g, dtype, cos_dtype, static_cast<hipStream_t>(stream));
+}
+
+int q3_qk_norm_rope(const void* q_in, const void* k_in, const void* v_in, void* q_out, void* k_out, void* v_out,
+                    const void* q_weight, const void* k_weight, const int* positions, const float* inv_freq,
+                    const int* dst_seq_offset, int64_t dst_seq_cap, int64_t B, int64_t S, int64_t Hq, int64_t Hkv,
+                    int64_t D, const int64_t* section, float eps, const int64_t* strides, int dtype, void* stream) {
+  Q3_REQUIRE(q_in && k_in && q_out && k_out && positions && inv_freq && section && strides, Q3_ERR_NULL);
+  Q3_REQUIRE((q_weight == nullptr) == (k_weight == nullptr), Q3_ERR_NULL);
+  Q3_REQUIRE((v_in == nullptr) == (v_out == nullptr), Q3_ERR_NULL);
+  Q3_REQUIRE(B >= 0 && S >= 0 && Hq >= 1 && Hkv >= 1 && D >= 16, Q3_ERR_SHAPE);
+  Q3_REQUIRE(D % 16 == 0 && D <= 256, Q3_ERR_UNSUPPORTED);
+  Q3_REQUIRE(section[0] >= 0 && section[1] >= 0 && section[2] >= 0 && section[0] + section[1] + section[2] == D / 2,
+             Q3_ERR_SHAPE);
+  QKNormRopeArgs a{};
+  a.q_in = q_in;
+  a.k_in = k_in;
+  a.v_in = v_in;
+  a.q_out = q_out;
+  a.k_out = k_out;
+  a.v_out = v_out;
+  a.q_w = q_weight;
+  a.k_w = k_weight;
+  a.pos = positions;
+  a.inv_freq = inv_freq;
+  a.dst_seq_off = dst_seq_offset;
+  a.dst_seq_cap = dst_seq_cap > 0 ? dst_seq_cap : INT64_MAX;
+  a.B = (int)B;
+  a.S = (int)S;
+  a.Hq = (int)Hq;
+  a.Hkv = (int)Hkv;
+  a.D = (int)D;
+  a.s0 = (int)section[0];
+  a.s1 = (int)section[1];
+  a.eps = eps;
+  for (int i = 0; i < 18; ++i) a.st[i] = strides[i];
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == Q3_BF16) return launch_qk<bf16>(a, st);
+  if (dtype == Q3_F32) return launch_qk<float>(a, st);
+  return Q3_ERR_DTYPE;
+}
+
+}  // extern "C"

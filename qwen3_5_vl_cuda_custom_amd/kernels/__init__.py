@@ -1,0 +1,37 @@
+"""Functional ops with the reference's names and signatures (reference kernels/__init__.py:1-45),
+each backed by a hand-written gfx950 HIP kernel of libq3vl.so. GPU tensors only; no fallback."""
+from ._loader import FALLBACK_LOG, record_fallback, strict_mode, summarize_fallbacks
+from .conv3d_patch import conv3d_patch
+from .elementwise import gelu_tanh, residual_add, swiglu
+from .flash_attention import decode_attention, flash_attention
+from .matmul import matmul, matmul_swiglu
+from .moe_routing import cuda_batched_gemm, cuda_index_add, cuda_topk, moe_experts, moe_route
+from .norms import layernorm, rmsnorm, softmax
+from .rotary import apply_mrope, apply_rope, qk_norm_rope
+
+__all__ = [
+    "FALLBACK_LOG",
+    "summarize_fallbacks",
+    "record_fallback",
+    "strict_mode",
+    "apply_mrope",
+    "apply_rope",
+    "conv3d_patch",
+    "cuda_batched_gemm",
+    "cuda_index_add",
+    "cuda_topk",
+    "flash_attention",
+    "gelu_tanh",
+    "layernorm",
+    "matmul",
+    "residual_add",
+    "rmsnorm",
+    "softmax",
+    "swiglu",
+    # additions beyond the reference API (fused / decode / MoE dispatch paths)
+    "decode_attention",
+    "matmul_swiglu",
+    "moe_experts",
+    "moe_route",
+    "qk_norm_rope",
+]

@@ -1,0 +1,62 @@
+"""flash_attention (reference kernels/flash_attention.py:82-100) and ragged-cache decode attention."""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from ._common import check
+
+
+def _s4(t: torch.Tensor):
+    return t.stride(0), t.stride(1), t.stride(2)
+
+
+def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, is_causal: bool = True,
+                    num_kv_groups: int = 1, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """softmax(scale·QKᵀ [+ causal mask])·V with GQA.
+
+    q (B, Hq, Sq, D), k/v (B, Hkv, Sk, D) with Hq = Hkv·num_kv_groups; query
+    head h reads KV head h // num_kv_groups. Any strides are accepted as long as
+    the head dim is contiguous (no copies). Causal masks key j > query i.
+    `out`, when given, is a (B, Hq, Sq, D) view written in place.
+    """
+    check("flash_attention", q, k, v)
+    q, k, v = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
+    B, Hq, Sq, D = q.shape
+    Hkv, Sk = k.shape[1], k.shape[2]
+    if k.shape != v.shape or k.shape[0] != B or k.shape[3] != D:
+        raise ValueError(f"flash_attention: q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}")
+    if Hkv * num_kv_groups != Hq:
+        raise ValueError(f"flash_attention: Hq={Hq} != Hkv={Hkv} * num_kv_groups={num_kv_groups}")
+    o = out if out is not None else torch.empty((B, Hq, Sq, D), dtype=q.dtype, device=q.device)
+    if o.shape != (B, Hq, Sq, D) or o.stride(-1) != 1:
+        raise ValueError("flash_attention: out must be (B, Hq, Sq, D) with a contiguous head dim")
+    _lib.call("q3_flash_attention", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), None, B, Hq, Hkv, Sq,
+              Sk, D, _lib.i64s(*_s4(q), *_s4(k), *_s4(v), *_s4(o)), float(scale), int(bool(is_causal)),
+              _lib.dtype_code(q.dtype), _lib.stream())
+    return o
+
+
+def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, kv_lens: torch.Tensor,
+                     scale: float, *, out: torch.Tensor | None = None, max_len: int | None = None) -> torch.Tensor:
+    """One query token per sequence over a ragged KV cache (split-K flash decoding).
+
+    q (B, Hq, D) (or (B, Hq, 1, D)); k_cache/v_cache (B, Hkv, cap, D); kv_lens
+    (B,) int32 on the device — sequence b attends to cache rows [0, kv_lens[b]).
+    `max_len` bounds every kv_lens[b] (default: cap). Returns (B, Hq, D).
+    """
+    check("decode_attention", q, k_cache, v_cache)
+    if q.dim() == 4:
+        q = q[:, :, 0]
+    B, Hq, D = q.shape
+    Hkv, cap = k_cache.shape[1], k_cache.shape[2]
+    if kv_lens.dtype != torch.int32 or not kv_lens.is_cuda or kv_lens.shape != (B,):
+        raise ValueError("decode_attention: kv_lens must be an int32 (B,) device tensor")
+    o = out if out is not None else torch.empty((B, Hq, D), dtype=q.dtype, device=q.device)
+    ml = int(max_len) if max_len is not None else cap
+    ws, nws = _lib.workspace(_lib.lib().q3_decode_attention_workspace_bytes(B, Hq, Hkv, ml, D), q.device)
+    _lib.call("q3_decode_attention", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), kv_lens.data_ptr(),
+              o.data_ptr(), B, Hq, Hkv, D, ml,
+              _lib.i64s(q.stride(0), q.stride(1), *_s4(k_cache), *_s4(v_cache), o.stride(0), o.stride(1)),
+              float(scale), _lib.dtype_code(q.dtype), _lib.ptr(ws), nws, _lib.stream())
+    return o

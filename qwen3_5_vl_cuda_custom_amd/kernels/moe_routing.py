@@ -1,0 +1,106 @@
+"""MoE routing ops (reference kernels/moe_routing.py): cuda_topk, cuda_index_add,
+cuda_batched_gemm, plus the fused router and expert dispatch used by CudaSparseMoE."""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from ._common import check
+
+
+def cuda_topk(x: torch.Tensor, k: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Top-k over the last dim: (values in x dtype, int64 indices); equal values go to the lower index."""
+    check("cuda_topk", x)
+    cols = x.shape[-1]
+    if not 1 <= k <= cols:
+        raise ValueError(f"cuda_topk: k={k} out of range for {cols} columns")
+    x = x.contiguous()
+    rows = x.numel() // cols
+    vals = torch.empty((*x.shape[:-1], k), dtype=x.dtype, device=x.device)
+    idx = torch.empty((*x.shape[:-1], k), dtype=torch.int64, device=x.device)
+    _lib.call("q3_topk", x.data_ptr(), vals.data_ptr(), idx.data_ptr(), rows, cols, k, _lib.dtype_code(x.dtype),
+              _lib.stream())
+    return vals, idx
+
+
+def cuda_index_add(target: torch.Tensor, source: torch.Tensor, index: torch.Tensor) -> torch.Tensor:
+    """target[index[i]] += source[i] along dim 0, in place; returns target.
+
+    Deterministic: each target row adds its sources in ascending i in fp32,
+    starting from its own value, and rounds once (torch's index_add_
+    semantics). Indices must lie in [0, target.shape[0]).
+    """
+    check("cuda_index_add", target, source)
+    if index.dim() != 1 or index.shape[0] != source.shape[0] or not index.is_cuda:
+        raise ValueError("cuda_index_add: index must be a 1-D device tensor with one entry per source row")
+    if not target.is_contiguous():
+        raise ValueError("cuda_index_add: target must be contiguous (it is updated in place)")
+    if source.shape[1:] != target.shape[1:]:
+        raise ValueError("cuda_index_add: source rows must match target rows")
+    n_src, n_t = source.shape[0], target.shape[0]
+    if n_src == 0:
+        return target
+    idx = index.to(torch.int64).contiguous()
+    lo, hi = int(idx.min()), int(idx.max())
+    if lo < 0 or hi >= n_t:
+        raise IndexError(f"cuda_index_add: index out of range [0, {n_t})")
+    src = source.contiguous()
+    D = src[0].numel()
+    ws, nws = _lib.workspace(_lib.lib().q3_index_add_workspace_bytes(n_src, n_t), target.device)
+    _lib.call("q3_index_add", target.data_ptr(), src.data_ptr(), idx.data_ptr(), n_src, n_t, D,
+              _lib.dtype_code(target.dtype), _lib.ptr(ws), nws, _lib.stream())
+    return target
+
+
+def cuda_batched_gemm(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """Y[e] = X[e]·W[e]ᵀ: x (E, M, K), w (E, N, K) -> (E, M, N)."""
+    check("cuda_batched_gemm", x, w)
+    if x.dim() != 3 or w.dim() != 3 or x.shape[0] != w.shape[0] or x.shape[2] != w.shape[2]:
+        raise ValueError(f"cuda_batched_gemm: x {tuple(x.shape)} and w {tuple(w.shape)} mismatch")
+    E, M, K = x.shape
+    N = w.shape[1]
+    x, w = x.contiguous(), w.contiguous()
+    y = torch.empty((E, M, N), dtype=x.dtype, device=x.device)
+    _lib.call("q3_batched_gemm", x.data_ptr(), w.data_ptr(), y.data_ptr(), E, M, N, K, _lib.dtype_code(x.dtype),
+              _lib.stream())
+    return y
+
+
+def moe_route(router_logits: torch.Tensor, top_k: int, norm_topk_prob: bool = True):
+    """Fused softmax -> top-k (lowest index wins ties) -> renormalise -> bf16 (modules/moe.py:60-65).
+
+    router_logits (T, E) bf16. Returns (top_idx int32 (T, k), top_w bf16 (T, k)).
+    """
+    check("moe_route", router_logits)
+    if router_logits.dtype != torch.bfloat16:
+        raise TypeError("moe_route: bf16 logits expected")
+    lg = router_logits.contiguous()
+    T, E = lg.shape
+    idx = torch.empty((T, top_k), dtype=torch.int32, device=lg.device)
+    w = torch.empty((T, top_k), dtype=torch.bfloat16, device=lg.device)
+    _lib.call("q3_moe_route", lg.data_ptr(), idx.data_ptr(), w.data_ptr(), None, T, E, top_k,
+              int(bool(norm_topk_prob)), _lib.stream())
+    return idx, w
+
+
+def moe_experts(x: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor, top_idx: torch.Tensor,
+                top_w: torch.Tensor, residual: torch.Tensor | None = None) -> torch.Tensor:
+    """Dispatch, per-expert SwiGLU MLPs and combine (modules/moe.py:70-83) for routed tokens.
+
+    x (T, H) bf16; gate_up (E, 2I, H); down (E, H, I); top_idx (T, k) int32;
+    top_w (T, k) bf16. Returns (T, H) (+ residual).
+    """
+    check("moe_experts", x, gate_up, down, top_w, residual)
+    T, H = x.shape
+    E, I2, _ = gate_up.shape
+    I = I2 // 2
+    k = top_idx.shape[1]
+    x = x.contiguous()
+    out = torch.empty_like(x)
+    nbytes = _lib.lib().q3_moe_experts_workspace_bytes(T, H, I, E, k)
+    ws, nws = _lib.workspace(nbytes, x.device)
+    r = residual.contiguous() if residual is not None else None
+    _lib.call("q3_moe_experts", x.data_ptr(), gate_up.contiguous().data_ptr(), down.contiguous().data_ptr(),
+              top_idx.contiguous().data_ptr(), top_w.contiguous().data_ptr(), _lib.ptr(r), out.data_ptr(), T, H, I,
+              E, k, _lib.ptr(ws), nws, _lib.stream())
+    return out

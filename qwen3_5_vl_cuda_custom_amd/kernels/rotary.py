@@ -1,0 +1,99 @@
+"""Rotary ops: apply_rope / apply_mrope (reference kernels/rope.py:58-72, kernels/mrope.py:80-104)
+and the fused q/k RMSNorm + mRoPE prologue used by the text attention module."""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from ._common import check
+
+
+def _bhsd_strides(t: torch.Tensor):
+    return t.stride(0), t.stride(1), t.stride(2)
+
+
+def _cos_dtype(c: torch.Tensor) -> int:
+    return _lib.dtype_code(c.dtype)
+
+
+def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Rotate-half RoPE of x (B, H, S, D) with cos/sin (S, D_rope), (1, S, D_rope) or (B, S, D_rope).
+
+    cos/sin are read in their own dtype (fp32 or x dtype); a batch of 1 is
+    broadcast over B. Dims beyond D_rope pass through.
+    """
+    check("apply_rope", x)
+    if not cos.is_cuda or not sin.is_cuda:
+        raise RuntimeError("apply_rope: cos/sin must be on the GPU")
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    B, H, S, D = x.shape
+    Dr = cos.shape[-1]
+    cos = cos.contiguous()
+    sin = sin.contiguous()
+    if cos.dim() == 2:
+        cb = 0
+    elif cos.dim() == 3 and cos.shape[0] in (1, B):
+        cb = 0 if cos.shape[0] == 1 else cos.stride(0)
+    else:
+        raise ValueError(f"apply_rope: cos {tuple(cos.shape)} must be (S, Dr) or (B|1, S, Dr)")
+    if cos.shape[-2] != S or sin.shape != cos.shape or Dr > D or Dr % 2:
+        raise ValueError("apply_rope: cos/sin shape mismatch")
+    y = torch.empty((B, H, S, D), dtype=x.dtype, device=x.device)
+    _lib.call("q3_rope", x.data_ptr(), cos.data_ptr(), sin.data_ptr(), y.data_ptr(), B, H, S, D, Dr,
+              _lib.i64s(*_bhsd_strides(x)), _lib.i64s(*_bhsd_strides(y)), cb, cos.stride(-2),
+              _lib.dtype_code(x.dtype), _cos_dtype(cos), _lib.stream())
+    return y
+
+
+def apply_mrope(x: torch.Tensor, cos_3d: torch.Tensor, sin_3d: torch.Tensor, mrope_section: list[int]) -> torch.Tensor:
+    """mRoPE of x (B, H, S, D) with cos_3d/sin_3d (3, B|1, S, D_rope) and the chunked section layout.
+
+    Element i < D_rope/2 takes axis 0 for i < s0, axis 1 for i < s0+s1, else
+    axis 2 (kernels/mrope.py:19-35), read straight from the 3-axis tables.
+    """
+    check("apply_mrope", x)
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    B, H, S, D = x.shape
+    if cos_3d.dim() != 4 or cos_3d.shape[0] != 3 or sin_3d.shape != cos_3d.shape:
+        raise ValueError(f"apply_mrope: cos_3d {tuple(cos_3d.shape)} must be (3, B, S, D_rope)")
+    cos_3d = cos_3d.contiguous()
+    sin_3d = sin_3d.contiguous()
+    Dr = cos_3d.shape[-1]
+    if sum(mrope_section) != Dr // 2 or cos_3d.shape[2] != S or cos_3d.shape[1] not in (1, B):
+        raise ValueError("apply_mrope: mrope_section must sum to D_rope/2 and cos_3d must be (3, B|1, S, D_rope)")
+    cb = 0 if cos_3d.shape[1] == 1 else cos_3d.stride(1)
+    y = torch.empty((B, H, S, D), dtype=x.dtype, device=x.device)
+    _lib.call("q3_mrope", x.data_ptr(), cos_3d.data_ptr(), sin_3d.data_ptr(), y.data_ptr(), B, H, S, D, Dr,
+              _lib.i64s(*mrope_section), _lib.i64s(*_bhsd_strides(x)), _lib.i64s(*_bhsd_strides(y)),
+              _lib.i64s(cos_3d.stride(0), cb, cos_3d.stride(2)), _lib.dtype_code(x.dtype), _cos_dtype(cos_3d),
+              _lib.stream())
+    return y
+
+
+def qk_norm_rope(q_in, k_in, v_in, q_out, k_out, v_out, q_weight, k_weight, positions, inv_freq, mrope_section,
+                 eps: float, dst_seq_offset: torch.Tensor | None = None, dst_seq_cap: int = 0) -> None:
+    """Fused per-head RMSNorm (optional) + mRoPE of q and k, and copy of v (optional).
+
+    All six tensors are (B, S, H, D) views (any strides, D contiguous);
+    positions (3, B, S) int32 and inv_freq (D/2) fp32 on the device.
+    dst_seq_offset (B,) int32 shifts the sequence index of the k/v outputs
+    (cache append); rows landing at index >= dst_seq_cap (if > 0) are dropped.
+    """
+    B, S, Hq, D = q_in.shape
+    Hkv = k_in.shape[2]
+    ts = [q_in, k_in, v_in, q_out, k_out, v_out]
+    strides = []
+    for t in ts:
+        if t is None:
+            strides += [0, 0, 0]
+        else:
+            if t.stride(-1) != 1:
+                raise ValueError("qk_norm_rope: the head dim must be contiguous")
+            strides += [t.stride(0), t.stride(1), t.stride(2)]
+    _lib.call("q3_qk_norm_rope", q_in.data_ptr(), k_in.data_ptr(), _lib.ptr(v_in), q_out.data_ptr(),
+              k_out.data_ptr(), _lib.ptr(v_out), _lib.ptr(q_weight), _lib.ptr(k_weight), positions.data_ptr(),
+              inv_freq.data_ptr(), _lib.ptr(dst_seq_offset), int(dst_seq_cap), B, S, Hq, Hkv, D,
+              _lib.i64s(*mrope_section),
+              float(eps), _lib.i64s(*strides), _lib.dtype_code(q_in.dtype), _lib.stream())

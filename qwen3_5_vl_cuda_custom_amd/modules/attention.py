@@ -1,0 +1,124 @@
+"""CudaVisionAttention / CudaFullAttention (reference modules/attention.py:11-98)."""
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from ..kernels import apply_rope, decode_attention, flash_attention, qk_norm_rope
+from .kv_cache import StaticKVCache
+from .linear import CudaLinear
+from .norms import CudaRMSNorm
+from .rotary import MRoPEBinding
+
+
+class CudaVisionAttention(nn.Module):
+    """Non-causal vision attention with a fused `qkv` (3h, h) linear and `proj` (h, h), both with bias."""
+
+    def __init__(self, hidden_size: int, num_heads: int) -> None:
+        super().__init__()
+        self.num_heads = num_heads
+        self.head_dim = hidden_size // num_heads
+        self.scale = self.head_dim ** -0.5
+        self.qkv = CudaLinear(hidden_size, 3 * hidden_size, bias=True)
+        self.proj = CudaLinear(hidden_size, hidden_size, bias=True)
+
+    def forward(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                residual: torch.Tensor | None = None) -> torch.Tensor:
+        """x (B, S, h); cos/sin (S, D) (or (B|1, S, D)); images on the batch dim attend separately."""
+        B, S, h = x.shape
+        H, D = self.num_heads, self.head_dim
+        qkv = self.qkv(x).view(B, S, 3, H, D)
+        q = apply_rope(qkv[:, :, 0].transpose(1, 2), cos, sin)
+        k = apply_rope(qkv[:, :, 1].transpose(1, 2), cos, sin)
+        v = qkv[:, :, 2].transpose(1, 2)
+        o = torch.empty((B, S, H, D), dtype=x.dtype, device=x.device)
+        flash_attention(q, k, v, scale=self.scale, is_causal=False, num_kv_groups=1, out=o.transpose(1, 2))
+        return self.proj(o.view(B, S, h), residual=residual)
+
+
+class CudaFullAttention(nn.Module):
+    """Causal GQA text attention with per-head q/k RMSNorm and mRoPE.
+
+    Parameters (names and shapes as the reference): q_proj (Hq·D, h),
+    k_proj/v_proj (Hkv·D, h), o_proj (h, Hq·D) (+ biases with attention_bias),
+    q_norm/k_norm (D).
+
+    forward(x, mrope_apply, past_kv=None) keeps the reference contract and
+    returns (out, (k, v)) with k/v (B, Hkv, S_total, D). Additions:
+      kv_cache=StaticKVCache  rotated k/v are written in place at each
+                              sequence's length and attention runs over the
+                              ragged cache (decode when S == 1)
+      residual=tensor         added to o_proj's output in the GEMM epilogue
+    When `mrope_apply` is a TextMRoPE.bind(...) binding, q/k normalisation and
+    rotation run as one fused kernel on the projection outputs.
+    """
+
+    def __init__(self, hidden_size: int, num_heads: int, num_kv_heads: int, head_dim: int | None = None,
+                 rms_norm_eps: float = 1e-6, attention_bias: bool = False) -> None:
+        super().__init__()
+        self.num_heads = num_heads
+        self.num_kv_heads = num_kv_heads
+        self.num_kv_groups = num_heads // num_kv_heads
+        self.head_dim = head_dim or (hidden_size // num_heads)
+        self.scale = self.head_dim ** -0.5
+        self.q_proj = CudaLinear(hidden_size, num_heads * self.head_dim, bias=attention_bias)
+        self.k_proj = CudaLinear(hidden_size, num_kv_heads * self.head_dim, bias=attention_bias)
+        self.v_proj = CudaLinear(hidden_size, num_kv_heads * self.head_dim, bias=attention_bias)
+        self.o_proj = CudaLinear(num_heads * self.head_dim, hidden_size, bias=attention_bias)
+        self.q_norm = CudaRMSNorm(self.head_dim, eps=rms_norm_eps)
+        self.k_norm = CudaRMSNorm(self.head_dim, eps=rms_norm_eps)
+
+    def _fusable(self, mrope_apply, x: torch.Tensor) -> bool:
+        return (isinstance(mrope_apply, MRoPEBinding) and mrope_apply.rope.dim == self.head_dim
+                and self.head_dim % 16 == 0 and self.head_dim <= 256 and x.is_cuda)
+
+    def forward(self, x: torch.Tensor, mrope_apply, past_kv: tuple[torch.Tensor, torch.Tensor] | None = None, *,
+                kv_cache: StaticKVCache | None = None, residual: torch.Tensor | None = None):
+        B, S, _ = x.shape
+        Hq, Hkv, D = self.num_heads, self.num_kv_heads, self.head_dim
+        q = self.q_proj(x).view(B, S, Hq, D)
+        k = self.k_proj(x).view(B, S, Hkv, D)
+        v = self.v_proj(x).view(B, S, Hkv, D)
+        o = torch.empty((B, S, Hq, D), dtype=x.dtype, device=x.device)
+
+        if kv_cache is not None:
+            if past_kv is not None:
+                raise ValueError("pass either past_kv or kv_cache, not both")
+            if not self._fusable(mrope_apply, x):
+                raise ValueError("kv_cache decoding needs mrope_apply = TextMRoPE.bind(position_ids)")
+            rope = mrope_apply.rope
+            pos = mrope_apply.positions_int32(x.device)
+            kc, vc = kv_cache.k.transpose(1, 2), kv_cache.v.transpose(1, 2)  # (B, cap, Hkv, D) views
+            qk_norm_rope(q, k, v, q, kc, vc, self.q_norm.weight, self.k_norm.weight, pos, rope.inv_freq,
+                         rope.mrope_section, self.q_norm.eps, dst_seq_offset=kv_cache.lens,
+                         dst_seq_cap=kv_cache.capacity)
+            if S == 1:
+                lens = kv_cache.lens + 1
+                decode_attention(q[:, 0], kv_cache.k, kv_cache.v, lens, self.scale, out=o[:, 0],
+                                 max_len=kv_cache.capacity)
+                kv_cache.lens.copy_(lens)
+            else:
+                # Prefill of an empty cache: causal attention over the rows just written.
+                flash_attention(q.transpose(1, 2), kv_cache.k[:, :, :S], kv_cache.v[:, :, :S], self.scale, True,
+                                self.num_kv_groups, out=o.transpose(1, 2))
+                kv_cache.lens.add_(S)
+            return self.o_proj(o.view(B, S, Hq * D), residual=residual), (kv_cache.k, kv_cache.v)
+
+        if self._fusable(mrope_apply, x):
+            rope = mrope_apply.rope
+            pos = mrope_apply.positions_int32(x.device)
+            qk_norm_rope(q, k, None, q, k, None, self.q_norm.weight, self.k_norm.weight, pos, rope.inv_freq,
+                         rope.mrope_section, self.q_norm.eps)
+            qh, kh, vh = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+        else:
+            qh = self.q_norm(q).transpose(1, 2)
+            kh = self.k_norm(k).transpose(1, 2)
+            vh = v.transpose(1, 2)
+            qh, kh = mrope_apply(qh, kh)
+        if past_kv is not None:
+            kh = torch.cat([past_kv[0], kh], dim=2)
+            vh = torch.cat([past_kv[1], vh], dim=2)
+        is_causal = qh.shape[2] == kh.shape[2]
+        flash_attention(qh, kh, vh, scale=self.scale, is_causal=is_causal, num_kv_groups=self.num_kv_groups,
+                        out=o.transpose(1, 2))
+        return self.o_proj(o.view(B, S, Hq * D), residual=residual), (kh, vh)

@@ -1,0 +1,37 @@
+"""CudaSwiGLUMLP / CudaVisionMLP (reference modules/mlp.py:10-34)."""
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from ..kernels import gelu_tanh, matmul_swiglu, swiglu
+from .linear import CudaLinear
+
+
+class CudaSwiGLUMLP(nn.Module):
+    """down_proj(silu(gate_proj(x)) · up_proj(x)); gate/up (I, h), down (h, I)."""
+
+    def __init__(self, hidden_size: int, intermediate_size: int, bias: bool = False) -> None:
+        super().__init__()
+        self.gate_proj = CudaLinear(hidden_size, intermediate_size, bias=bias)
+        self.up_proj = CudaLinear(hidden_size, intermediate_size, bias=bias)
+        self.down_proj = CudaLinear(intermediate_size, hidden_size, bias=bias)
+
+    def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None) -> torch.Tensor:
+        if self.gate_proj.bias is None and self.up_proj.bias is None:
+            act = matmul_swiglu(x, self.gate_proj.weight, self.up_proj.weight)  # gate, up and swiglu in one GEMM
+        else:
+            act = swiglu(self.gate_proj(x), self.up_proj(x))
+        return self.down_proj(act, residual=residual)
+
+
+class CudaVisionMLP(nn.Module):
+    """linear_fc2(gelu_tanh(linear_fc1(x))), both with bias."""
+
+    def __init__(self, hidden_size: int, intermediate_size: int) -> None:
+        super().__init__()
+        self.linear_fc1 = CudaLinear(hidden_size, intermediate_size, bias=True)
+        self.linear_fc2 = CudaLinear(intermediate_size, hidden_size, bias=True)
+
+    def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None) -> torch.Tensor:
+        return self.linear_fc2(gelu_tanh(self.linear_fc1(x)), residual=residual)

@@ -1,0 +1,73 @@
+"""Parity metrics and tolerances shared by the tests.
+
+bf16 activations vs the fp32 oracle: max-abs <= 2e-2 and mean-rel <= 5e-3,
+mean-rel = mean|delta| / mean|ref|. Indices: exact.
+"""
+from __future__ import annotations
+
+import torch
+
+BF16_MAX_ABS = 2e-2
+BF16_MEAN_REL = 5e-3
+
+
+def metrics(out: torch.Tensor, ref: torch.Tensor) -> tuple[float, float]:
+    o = out.detach().float().cpu()
+    r = ref.detach().float().cpu()
+    assert o.shape == r.shape, (o.shape, r.shape)
+    assert torch.isfinite(o).all(), "non-finite values in output"
+    d = (o - r).abs()
+    return float(d.max()), float(d.mean() / r.abs().mean().clamp_min(1e-30))
+
+
+def assert_bf16_close(out, ref, max_abs=BF16_MAX_ABS, mean_rel=BF16_MEAN_REL, what=""):
+    ma, mr = metrics(out, ref)
+    assert ma <= max_abs and mr <= mean_rel, f"{what}: max-abs {ma:.3e} (<= {max_abs}), mean-rel {mr:.3e} (<= {mean_rel})"
+    return ma, mr
+
+
+def assert_close(out, ref, atol, rtol=0.0, what=""):
+    o = out.detach().float().cpu()
+    r = ref.detach().float().cpu()
+    assert o.shape == r.shape, (o.shape, r.shape)
+    err = (o - r).abs()
+    tol = atol + rtol * r.abs()
+    bad = err > tol
+    assert not bad.any(), f"{what}: max err {float(err.max()):.3e}, {int(bad.sum())} elements beyond tolerance"
+
+
+def bf16_round(t: torch.Tensor) -> torch.Tensor:
+    return t.to(torch.bfloat16).float()
+
+
+def assert_within_ulp(out: torch.Tensor, ref: torch.Tensor, ulps: float = 1.0, what=""):
+    """|out - ref| <= ulps * ulp_bf16(ref) (+ a tiny floor near zero): the bound for an op that
+    computes in fp32 and rounds its bf16 output once."""
+    o = out.detach().float().cpu()
+    r = ref.detach().float().cpu()
+    assert torch.isfinite(o).all()
+    ulp = torch.ldexp(torch.ones_like(r), torch.frexp(r.abs().clamp_min(2.0 ** -100))[1] - 8)
+    err = (o - r).abs()
+    bad = err > ulps * ulp + 1e-30
+    assert not bad.any(), f"{what}: {int(bad.sum())} elements beyond {ulps} ulp (max err {float(err.max()):.3e})"
+
+
+def assert_layer_parity(out, ref32, ref_bf16, what="", slack=1.25):
+    """Module-level bar.
+
+    `ref32` is the fp32 oracle; `ref_bf16` the same oracle with the reference's
+    bf16 rounding after every op (the reference's own bf16 path). A bf16 layer
+    carries the quantisation error of its bf16 GEMM operands, so its worst
+    element vs fp32 can exceed max-abs 2e-2 whatever the kernels do. The test
+    requires: mean-rel <= 5e-3 vs fp32, and max-abs vs
+    fp32 within 2e-2 or, where the reference's own bf16 path is further than
+    that, no more than `slack` times the reference path's max-abs.
+    """
+    ma, mr = metrics(out, ref32)
+    ma_r, mr_r = metrics(ref_bf16, ref32)
+    msg = (f"{what}: ours max-abs {ma:.3e} mean-rel {mr:.3e} | reference bf16 path max-abs {ma_r:.3e} "
+           f"mean-rel {mr_r:.3e}")
+    print(msg)
+    assert mr <= BF16_MEAN_REL, msg
+    assert ma <= max(BF16_MAX_ABS, slack * ma_r), msg
+    return ma, mr, ma_r, mr_r

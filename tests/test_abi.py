@@ -1,0 +1,110 @@
+"""The C-ABI library on the host (no GPU needed): it loads, exports every entry point that
+include/q3vl.h declares, and rejects bad arguments with negative status codes before any
+device work (the reference's TORCH_CHECK paths, e.g. csrc/flash_attention_op.cu:152)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from qwen3_5_vl_cuda_custom_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+FAKE = 0x100000  # a non-null address that host-side validation never dereferences
+
+
+def header_functions():
+    text = (ROOT / "include" / "q3vl.h").read_text()
+    return sorted(set(re.findall(r"\b(q3_\w+)\s*\(", text)))
+
+
+def test_library_loads_and_reports_version():
+    lib = _lib.lib()
+    assert lib.q3_abi_version() == 1
+    assert _lib.error_string(0) == "ok"
+    assert "pointer" in _lib.error_string(-1)
+
+
+def test_every_declared_entry_point_is_exported_and_bound():
+    declared = header_functions()
+    assert len(declared) >= 20
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in q3vl.h but not exported"
+    assert set(declared) == set(_lib.EXPORTED), "ctypes signatures must cover exactly the header"
+
+
+def test_symbols_are_c_linkage():
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True).stdout
+    for name in header_functions():
+        assert re.search(rf"\bT {name}$", out, re.M), f"{name} is not an unmangled exported symbol"
+
+
+L = None
+
+
+@pytest.fixture(autouse=True)
+def lib():
+    global L
+    L = _lib.lib()
+
+
+def test_matmul_validation():
+    assert L.q3_matmul(None, FAKE, None, None, FAKE, 4, 4, 4, 4, 4, 0, 4, 1, None, 0, None) == -1
+    assert L.q3_matmul(FAKE, FAKE, None, None, FAKE, -1, 4, 4, 4, 4, 0, 4, 1, None, 0, None) == -2
+    assert L.q3_matmul(FAKE, FAKE, None, None, FAKE, 4, 4, 8, 4, 8, 0, 4, 1, None, 0, None) == -2  # ldx < K
+    assert L.q3_matmul(FAKE, FAKE, None, None, FAKE, 4, 4, 4, 4, 4, 0, 4, 7, None, 0, None) == -3
+    # decode-shaped bf16 GEMM needs a split-K workspace
+    ws = L.q3_matmul_workspace_bytes(32, 4096, 4096, 1, 0)
+    assert ws > 0
+    assert L.q3_matmul(FAKE, FAKE, None, None, FAKE, 32, 4096, 4096, 4096, 4096, 0, 4096, 1, None, 0, None) == -6
+    assert L.q3_matmul_workspace_bytes(4096, 4096, 4096, 1, 0) == 0
+    assert L.q3_matmul(FAKE, FAKE, None, None, FAKE, 0, 4, 4, 4, 4, 0, 4, 1, None, 0, None) == 0  # empty: no-op
+
+
+def test_elementwise_and_norm_validation():
+    assert L.q3_residual_add(FAKE, None, FAKE, 10, 1, None) == -1
+    assert L.q3_residual_add(FAKE, FAKE, FAKE, -1, 1, None) == -2
+    assert L.q3_residual_add(FAKE, FAKE, FAKE, 0, 1, None) == 0
+    assert L.q3_gelu_tanh(FAKE, FAKE, 10, 9, None) == -3
+    assert L.q3_rmsnorm(FAKE, FAKE, FAKE, 4, 0, 1e-6, 1, None) == -2
+    assert L.q3_layernorm(None, FAKE, None, FAKE, 4, 4, 1e-6, 1, None) == -1
+    assert L.q3_softmax(FAKE, FAKE, 4, 0, 1, None) == -2
+    assert L.q3_topk(FAKE, FAKE, FAKE, 4, 8, 9, 1, None) == -2      # k > cols
+    assert L.q3_topk(FAKE, FAKE, FAKE, 4, 4096, 8, 1, None) == -5   # cols beyond the register-resident kernel
+
+
+def test_attention_validation():
+    st = _lib.i64s(*([1] * 12))
+    assert L.q3_flash_attention(FAKE, FAKE, FAKE, FAKE, None, 1, 6, 4, 8, 8, 64, st, 0.1, 1, 1, None) == -2  # Hq % Hkv
+    assert L.q3_flash_attention(FAKE, FAKE, FAKE, FAKE, None, 1, 4, 4, 8, 8, 512, st, 0.1, 1, 1, None) == -5  # D > 256
+    assert L.q3_flash_attention(FAKE, None, FAKE, FAKE, None, 1, 4, 4, 8, 8, 64, st, 0.1, 1, 1, None) == -1
+    # (B=2, Hq=8, D=128) q/o; (B, Hkv=2, cap=100, D) caches
+    d = _lib.i64s(8 * 128, 128, 2 * 100 * 128, 100 * 128, 128, 2 * 100 * 128, 100 * 128, 128, 8 * 128, 128)
+    assert L.q3_decode_attention(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 8, 2, 128, 100, d, 0.1, 1, None, 0, None) == -6
+    assert L.q3_decode_attention_workspace_bytes(32, 32, 8, 8193, 128) == 32 * 8 * 33 * 4 * 130 * 4
+
+
+def test_rope_validation():
+    s3 = _lib.i64s(1, 1, 1)
+    sec = _lib.i64s(24, 20, 19)  # does not sum to D_rope / 2
+    assert L.q3_mrope(FAKE, FAKE, FAKE, FAKE, 1, 1, 1, 128, 128, sec, s3, s3, s3, 1, 0, None) == -2
+    assert L.q3_rope(FAKE, FAKE, FAKE, FAKE, 1, 1, 1, 64, 65, s3, s3, 0, 65, 1, 0, None) == -2  # odd D_rope
+    st = _lib.i64s(*([1] * 18))
+    sec = _lib.i64s(24, 20, 20)
+    assert L.q3_qk_norm_rope(FAKE, FAKE, None, FAKE, FAKE, None, None, None, FAKE, FAKE, None, 0, 1, 1, 1, 1, 72,
+                             sec, 1e-6, st, 1, None) == -5  # head dim not a multiple of 16
+    assert L.q3_qk_norm_rope(FAKE, FAKE, FAKE, FAKE, FAKE, None, None, None, FAKE, FAKE, None, 0, 1, 1, 1, 1, 128,
+                             sec, 1e-6, st, 1, None) == -1  # v_in without v_out
+
+
+def test_moe_validation():
+    assert L.q3_moe_route(FAKE, FAKE, FAKE, None, 16, 8, 9, 1, None) == -2           # k > E
+    assert L.q3_moe_route(FAKE, FAKE, FAKE, None, 16, 1024, 8, 1, None) == -5        # E beyond register-resident
+    assert L.q3_moe_experts(FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE, 16, 20, 8, 4, 2, None, 0, None) == -5  # H % 8
+    ws = L.q3_moe_experts_workspace_bytes(4096, 2048, 768, 128, 8)
+    assert ws > 4096 * 8 * (2048 + 768) * 2
+    assert L.q3_moe_experts(FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE, 16, 64, 32, 4, 2, None, 0, None) == -6
+    assert L.q3_index_add(FAKE, FAKE, FAKE, 5, 3, 4, 1, None, 0, None) == -6
+    assert L.q3_index_add(FAKE, None, FAKE, 5, 3, 4, 1, None, 0, None) == -1

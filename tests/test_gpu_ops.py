@@ -1,0 +1,321 @@
+"""Op-level parity: each HIP kernel (through the C-ABI) against the CPU oracle on seeded inputs.
+
+bf16 cases: the oracle runs in fp32 on the same bf16-rounded inputs; tolerance
+max-abs 2e-2 / mean-rel 5e-3. fp32 cases (the reference's own test style,
+tests/test_kernels.py): tight absolute tolerances. Indices: exact.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import ops as O
+from qwen3_5_vl_cuda_custom_amd import kernels as K
+from tests.parity import assert_bf16_close, assert_close, assert_within_ulp
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def rnd(*shape, seed=0, std=1.0, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * std).to(dtype)
+
+
+def gpu(t):
+    return t.to(DEV)
+
+
+def f32(t):
+    return t.float()
+
+
+# ------------------------------------------------------------------ GEMM
+@pytest.mark.parametrize("M,N,Kd,bias", [
+    (8, 32, 64, True),        # reference test shape (tests/test_kernels.py:157-162), skinny path
+    (32, 4096, 4096, False),  # decode q/o projection (skinny, split-K)
+    (33, 520, 264, True),     # just past the skinny bound, ragged N
+    (300, 520, 264, True),    # ragged M/N, small K
+    (512, 1024, 4096, False), # k/v projection shape at S=512
+    (256, 1152, 4304, True),  # vision fc2: K tail (4304 = 67*64 + 16)
+    (1024, 4096, 4096, False),
+    (1024, 1536, 2048, False),
+])
+def test_matmul_bf16(M, N, Kd, bias):
+    x = rnd(M, Kd, seed=1)
+    w = rnd(N, Kd, seed=2, std=0.02)
+    b = rnd(N, seed=3, std=0.02) if bias else None
+    y = K.matmul(gpu(x), gpu(w), gpu(b) if bias else None)
+    ref = O.linear(f32(x), f32(w), f32(b) if bias else None)
+    assert_bf16_close(y, ref, what=f"matmul {M}x{N}x{Kd}")
+
+
+def test_matmul_residual_fused():
+    x, w, r = rnd(200, 512, seed=4), rnd(384, 512, seed=5, std=0.02), rnd(200, 384, seed=6)
+    y = K.matmul(gpu(x), gpu(w), residual=gpu(r))
+    assert_bf16_close(y, O.linear(f32(x), f32(w)) + f32(r), what="matmul+residual")
+    y2 = K.matmul(gpu(x[:16]), gpu(w), residual=gpu(r[:16]))  # skinny path epilogue
+    assert_bf16_close(y2, O.linear(f32(x[:16]), f32(w)) + f32(r[:16]), what="skinny matmul+residual")
+
+
+@pytest.mark.parametrize("M", [7, 32, 300, 1024])
+def test_matmul_swiglu(M):
+    x, wg, wu = rnd(M, 1024, seed=7), rnd(1536, 1024, seed=8, std=0.02), rnd(1536, 1024, seed=9, std=0.02)
+    y = K.matmul_swiglu(gpu(x), gpu(wg), gpu(wu))
+    ref = O.swiglu(O.linear(f32(x), f32(wg)), O.linear(f32(x), f32(wu)))
+    assert_bf16_close(y, ref, what=f"matmul_swiglu M={M}")
+
+
+def test_matmul_fp32_reference_style():
+    torch.manual_seed(0)
+    x, w, b = torch.randn(8, 64), torch.randn(32, 64), torch.randn(32)
+    y = K.matmul(gpu(x), gpu(w), gpu(b))
+    assert_close(y, O.linear(x, w, b), atol=1e-3, what="fp32 matmul")
+
+
+def test_matmul_identity():
+    x = rnd(64, 256, seed=10)
+    eye = torch.eye(256, dtype=torch.bfloat16)
+    y = K.matmul(gpu(x), gpu(eye))
+    assert torch.equal(y.cpu(), x), "x . I must reproduce x exactly"
+
+
+@pytest.mark.parametrize("E,M,N,K_", [(4, 8, 12, 16), (8, 96, 256, 512), (3, 40, 72, 64)])
+def test_batched_gemm(E, M, N, K_):
+    x, w = rnd(E, M, K_, seed=11), rnd(E, N, K_, seed=12, std=0.02)
+    y = K.cuda_batched_gemm(gpu(x), gpu(w))
+    assert_bf16_close(y, O.batched_gemm(f32(x), f32(w)), what="batched_gemm")
+    xf, wf = f32(x), f32(w)
+    yf = K.cuda_batched_gemm(gpu(xf), gpu(wf))
+    assert_close(yf, O.batched_gemm(xf, wf), atol=1e-3, what="fp32 batched_gemm")
+
+
+def test_conv3d_patch():
+    x = (torch.rand(64, 3, 2, 16, 16, generator=torch.Generator().manual_seed(13)) * 2 - 1).to(torch.bfloat16)
+    w, b = rnd(1152, 3, 2, 16, 16, seed=14, std=0.02), rnd(1152, seed=15, std=0.02)
+    y = K.conv3d_patch(gpu(x), gpu(w), gpu(b))
+    assert_bf16_close(y, O.conv3d_patch(f32(x), f32(w), f32(b)), what="conv3d_patch")
+    # the reference's test shape, fp32 (tests/test_kernels.py:313-325)
+    xs, ws, bs = torch.randn(4, 3, 2, 16, 16), torch.randn(32, 3, 2, 16, 16), torch.randn(32)
+    assert_close(K.conv3d_patch(gpu(xs), gpu(ws), gpu(bs)), O.conv3d_patch(xs, ws, bs), atol=5e-2, what="fp32 conv")
+
+
+# ------------------------------------------------------------------ attention
+@pytest.mark.parametrize("B,Hq,Hkv,S,D,causal", [
+    (1, 8, 2, 300, 128, True),
+    (2, 4, 1, 130, 128, True),
+    (1, 32, 8, 512, 128, True),
+    (2, 4, 4, 200, 64, False),
+    (4, 4, 4, 784, 72, False),   # vision: head_dim 72, per-image
+    (1, 2, 2, 77, 80, True),
+    (1, 6, 2, 64, 96, False),
+])
+def test_flash_attention_bf16(B, Hq, Hkv, S, D, causal):
+    q, k, v = rnd(B, Hq, S, D, seed=20), rnd(B, Hkv, S, D, seed=21), rnd(B, Hkv, S, D, seed=22)
+    scale = D ** -0.5
+    o = K.flash_attention(gpu(q), gpu(k), gpu(v), scale, causal, Hq // Hkv)
+    ref = O.flash_attention(f32(q), f32(k), f32(v), scale, causal, Hq // Hkv)
+    assert_bf16_close(o, ref, what=f"flash {B},{Hq},{Hkv},{S},{D},{causal}")
+
+
+def test_flash_attention_strided_views_and_out():
+    B, S, Hq, Hkv, D = 2, 96, 8, 2, 128
+    qs, ks, vs = rnd(B, S, Hq, D, seed=23), rnd(B, S, Hkv, D, seed=24), rnd(B, S, Hkv, D, seed=25)
+    out = torch.empty(B, S, Hq, D, dtype=torch.bfloat16, device=DEV)
+    K.flash_attention(gpu(qs).transpose(1, 2), gpu(ks).transpose(1, 2), gpu(vs).transpose(1, 2), D ** -0.5, True,
+                      4, out=out.transpose(1, 2))
+    ref = O.flash_attention(f32(qs).transpose(1, 2), f32(ks).transpose(1, 2), f32(vs).transpose(1, 2), D ** -0.5,
+                            True, 4)
+    assert_bf16_close(out.transpose(1, 2), ref, what="strided flash")
+
+
+def test_flash_attention_causal_row0_is_v0():
+    q, k, v = rnd(1, 4, 64, 128, seed=26), rnd(1, 4, 64, 128, seed=27), rnd(1, 4, 64, 128, seed=28)
+    o = K.flash_attention(gpu(q), gpu(k), gpu(v), 0.1, True, 1)
+    assert torch.equal(o[:, :, 0].cpu(), v[:, :, 0]), "causal row 0 attends only to key 0"
+
+
+@pytest.mark.parametrize("causal,groups", [(True, 1), (False, 1), (True, 2)])
+def test_flash_attention_fp32_reference_style(causal, groups):
+    torch.manual_seed(42)
+    q = torch.randn(2, 4 * groups, 16, 32)
+    k, v = torch.randn(2, 4, 16, 32), torch.randn(2, 4, 16, 32)
+    o = K.flash_attention(gpu(q), gpu(k), gpu(v), 32 ** -0.5, causal, groups)
+    assert_close(o, O.flash_attention(q, k, v, 32 ** -0.5, causal, groups), atol=1e-3, what="fp32 flash")
+
+
+def test_flash_attention_sq_ne_sk_noncausal():
+    q, k, v = rnd(1, 8, 5, 128, seed=29), rnd(1, 2, 300, 128, seed=30), rnd(1, 2, 300, 128, seed=31)
+    o = K.flash_attention(gpu(q), gpu(k), gpu(v), 128 ** -0.5, False, 4)
+    assert_bf16_close(o, O.flash_attention(f32(q), f32(k), f32(v), 128 ** -0.5, False, 4), what="Sq != Sk")
+
+
+@pytest.mark.parametrize("groups", [4, 8])
+def test_decode_attention_ragged(groups):
+    B, Hkv, cap, D = 6, 2, 1100, 128
+    lens = torch.tensor([1, 5, 255, 256, 257, 1100], dtype=torch.int32)
+    q = rnd(B, Hkv * groups, D, seed=32)
+    kc, vc = rnd(B, Hkv, cap, D, seed=33), rnd(B, Hkv, cap, D, seed=34)
+    o = K.decode_attention(gpu(q), gpu(kc), gpu(vc), gpu(lens), D ** -0.5)
+    ref = O.decode_attention(f32(q)[:, :, None], f32(kc), f32(vc), lens, D ** -0.5, groups)[:, :, 0]
+    assert_bf16_close(o, ref, what=f"decode groups={groups}")
+
+
+# ------------------------------------------------------------------ rotary
+def test_apply_mrope_matches_oracle():
+    B, H, S, D = 2, 4, 50, 128
+    x = rnd(B, H, S, D, seed=40)
+    pos = torch.stack([torch.arange(S), torch.arange(S) * 2, torch.arange(S) * 3]).view(3, 1, S).expand(3, B, S)
+    cos3, sin3 = O.mrope_cos_sin(pos, D, 5e6)
+    y = K.apply_mrope(gpu(x), gpu(cos3), gpu(sin3), [24, 20, 20])
+    assert_bf16_close(y, O.apply_mrope(f32(x), cos3, sin3, [24, 20, 20]), what="apply_mrope")
+
+
+def test_apply_rope_2d_and_broadcast():
+    B, H, S, D = 4, 16, 784, 72
+    x = rnd(B, H, S, D, seed=41)
+    ang = torch.rand(S, 36, generator=torch.Generator().manual_seed(42)) * 20
+    emb = torch.cat([ang, ang], -1)
+    cos, sin = emb.cos(), emb.sin()
+    ref = O.apply_rope(f32(x), cos, sin)
+    assert_bf16_close(K.apply_rope(gpu(x), gpu(cos), gpu(sin)), ref, what="rope 2d cos")
+    assert_bf16_close(K.apply_rope(gpu(x), gpu(cos[None]), gpu(sin[None])), ref, what="rope (1,S,D) cos")
+
+
+def test_apply_rope_partial_dims_fp32():
+    torch.manual_seed(0)
+    x = torch.randn(2, 3, 10, 32)
+    ang = torch.randn(10, 8)
+    cos, sin = torch.cat([ang, ang], -1).cos(), torch.cat([ang, ang], -1).sin()
+    y = K.apply_rope(gpu(x), gpu(cos), gpu(sin))
+    assert_close(y, O.apply_rope(x, cos, sin), atol=1e-5, what="partial rope")
+
+
+@pytest.mark.parametrize("D,section", [(128, [24, 20, 20]), (64, [12, 10, 10])])
+def test_qk_norm_rope_fused(D, section):
+    B, S, Hq, Hkv = 2, 40, 8, 2
+    q, k, v = rnd(B, S, Hq, D, seed=43), rnd(B, S, Hkv, D, seed=44), rnd(B, S, Hkv, D, seed=45)
+    qw, kw = rnd(D, seed=46, std=0.1) + 1, rnd(D, seed=47, std=0.1) + 1
+    pos = torch.stack([torch.arange(S) + 3, torch.arange(S) * 2, torch.arange(S) + 7]).view(3, 1, S).expand(3, B, S)
+    rope_if = O.mrope_inv_freq(D, 5e6)
+    qo, ko, vo = (torch.empty_like(t, device=DEV) for t in (q, k, v))
+    K.qk_norm_rope(gpu(q), gpu(k), gpu(v), qo, ko, vo, gpu(qw), gpu(kw), gpu(pos.to(torch.int32).contiguous()),
+                   gpu(rope_if), section, 1e-6)
+    cos3, sin3 = O.mrope_cos_sin(pos, D, 5e6)
+    qr = O.apply_mrope(O.rmsnorm(f32(q), f32(qw)).transpose(1, 2), cos3, sin3, section).transpose(1, 2)
+    kr = O.apply_mrope(O.rmsnorm(f32(k), f32(kw)).transpose(1, 2), cos3, sin3, section).transpose(1, 2)
+    assert_bf16_close(qo, qr, what="fused q")
+    assert_bf16_close(ko, kr, what="fused k")
+    assert torch.equal(vo.cpu(), v)
+
+
+# ------------------------------------------------------------------ norms / elementwise
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (2048, 128), (100, 1152), (33, 2048), (17, 37), (8, 256)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_rmsnorm(rows, cols, dtype):
+    x, w = rnd(rows, cols, seed=50, dtype=dtype), rnd(cols, seed=51, std=0.2, dtype=dtype) + 1
+    y = K.rmsnorm(gpu(x), gpu(w), 1e-6)
+    ref = O.rmsnorm(f32(x), f32(w), 1e-6)
+    if dtype == torch.float32:
+        assert_close(y, ref, atol=1e-4, what="fp32 rmsnorm")
+    else:
+        assert_bf16_close(y, ref, what="rmsnorm")
+
+
+def test_rmsnorm_constant_row_equals_weight():
+    x = torch.full((4, 4096), 3.0, dtype=torch.bfloat16)
+    w = rnd(4096, seed=52, std=0.5)
+    y = K.rmsnorm(gpu(x), gpu(w), 0.0)
+    assert_bf16_close(y, f32(w).expand(4, -1), max_abs=1e-2, what="rms(const) == w")
+
+
+@pytest.mark.parametrize("rows,cols", [(3136, 1152), (64, 64), (10, 100)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_layernorm(rows, cols, dtype):
+    x = rnd(rows, cols, seed=53, dtype=dtype) * 3 + 2
+    w, b = rnd(cols, seed=54, std=0.2, dtype=dtype) + 1, rnd(cols, seed=55, std=0.2, dtype=dtype)
+    y = K.layernorm(gpu(x), gpu(w), gpu(b), 1e-6)
+    ref = O.layernorm(f32(x), f32(w), f32(b), 1e-6)
+    if dtype == torch.float32:
+        assert_close(y, ref, atol=1e-4, what="fp32 layernorm")
+    else:
+        assert_bf16_close(y, ref, what="layernorm")
+
+
+@pytest.mark.parametrize("n", [1, 7, 4096 * 12288 // 16, 1000003])
+def test_elementwise(n):
+    # one fp32 computation and one rounding per element: within 1 bf16 ulp of the fp32 oracle
+    a, b = rnd(n, seed=56), rnd(n, seed=57)
+    assert_within_ulp(K.residual_add(gpu(a), gpu(b)), f32(a) + f32(b), what="residual_add")
+    assert_within_ulp(K.swiglu(gpu(a), gpu(b)), O.swiglu(f32(a), f32(b)), what="swiglu")
+    assert_within_ulp(K.gelu_tanh(gpu(a)), O.gelu_tanh(f32(a)), what="gelu_tanh")
+
+
+def test_elementwise_fp32_reference_style():
+    torch.manual_seed(0)
+    a, b = torch.randn(4, 33), torch.randn(4, 33)
+    assert_close(K.residual_add(gpu(a), gpu(b)), a + b, atol=1e-5)
+    assert_close(K.swiglu(gpu(a), gpu(b)), O.swiglu(a, b), atol=1e-4)
+    assert_close(K.gelu_tanh(gpu(a)), O.gelu_tanh(a), atol=1e-4)
+
+
+@pytest.mark.parametrize("rows,cols", [(4096, 128), (3, 1000)])
+def test_softmax(rows, cols):
+    x = torch.randn(rows, cols, generator=torch.Generator().manual_seed(58)) * 3
+    assert_close(K.softmax(gpu(x)), O.softmax(x), atol=1e-6, what="softmax")
+
+
+# ------------------------------------------------------------------ routing
+def test_topk_exact_with_planted_ties():
+    g = torch.Generator().manual_seed(60)
+    x = torch.randint(0, 6, (512, 128), generator=g).float()  # many exact ties
+    for k in (1, 4, 8):
+        v, i = K.cuda_topk(gpu(x), k)
+        rv, ri = O.topk(x, k)
+        assert torch.equal(i.cpu(), ri), f"top-{k} indices differ"
+        assert torch.equal(v.cpu(), rv)
+    # the reference test shape (tests/test_kernels.py:279-285)
+    x2 = torch.randn(8, 60, generator=g)
+    v, i = K.cuda_topk(gpu(x2), 4)
+    rv, ri = O.topk(x2, 4)
+    assert torch.equal(i.cpu(), ri) and torch.equal(v.cpu(), rv)
+
+
+def test_index_add_duplicates_and_order():
+    g = torch.Generator().manual_seed(61)
+    target = torch.randn(50, 96, generator=g).to(torch.bfloat16)
+    src = torch.randn(300, 96, generator=g).to(torch.bfloat16)
+    idx = torch.randint(0, 50, (300,), generator=g)
+    out = K.cuda_index_add(gpu(target.clone()), gpu(src), gpu(idx))
+    ref = O.index_add(target.clone(), src, idx)  # CPU bf16 sequential index_add_
+    assert torch.equal(out.cpu(), ref), "bf16 index_add must match the sequential CPU order bit-exactly"
+    tf, sf = target.float(), src.float()
+    outf = K.cuda_index_add(gpu(tf.clone()), gpu(sf), gpu(idx))
+    assert_close(outf, O.index_add(tf.clone(), sf, idx), atol=1e-5, what="fp32 index_add")
+
+
+def test_moe_route_exact_indices():
+    g = torch.Generator().manual_seed(62)
+    logits = (torch.randn(4096, 128, generator=g) * 2).to(torch.bfloat16)
+    logits[::7, 5] = logits[::7, 9]  # planted exact ties
+    idx, w = K.moe_route(gpu(logits), 8, True)
+    probs = O.softmax(logits.float())
+    rv, ri = O.topk(probs, 8)
+    assert torch.equal(idx.cpu().long(), ri), "router top-k indices must be bit-exact"
+    assert_bf16_close(w, rv / rv.sum(-1, keepdim=True), max_abs=4e-3, what="routing weights")
+
+
+def test_moe_experts_against_oracle_loop():
+    from oracle.layers import sparse_moe
+    T, H, I, E, k = 256, 256, 128, 16, 4
+    g = torch.Generator().manual_seed(63)
+    x = torch.randn(1, T, H, generator=g).to(torch.bfloat16)
+    p = {"gate_weight": (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16),
+         "gate_up_proj": (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(torch.bfloat16),
+         "down_proj": (torch.randn(E, H, I, generator=g) * 0.02).to(torch.bfloat16)}
+    logits = K.matmul(gpu(x[0]), gpu(p["gate_weight"]))
+    idx, w = K.moe_route(logits, k, True)
+    out = K.moe_experts(gpu(x[0]), gpu(p["gate_up_proj"]), gpu(p["down_proj"]), idx, w)
+    pf = {n: f32(t) for n, t in p.items()}
+    ref, _ = sparse_moe(f32(x), pf, top_k=k, router_logits=logits.float().cpu())
+    assert_bf16_close(out, ref[0], what="moe_experts")

@@ -1,0 +1,316 @@
+"""Pins of the CPU oracle (runs without a GPU).
+
+Each oracle function is checked against something that does not share its
+formula: numpy float64 brute-force loops, closed forms and invariants, and the
+independent HF transformers implementation of Qwen3-VL (installed here) for the
+layer compositions. A planted mistake in the oracle (a dropped term, a wrong
+sign, a swapped section axis, the wrong tie rule, a transposed operand) fails at
+least one of these.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import layers as L
+from oracle import ops as O
+
+g = torch.Generator().manual_seed(1234)
+
+
+def randn(*s, std=1.0):
+    return torch.randn(*s, generator=g) * std
+
+
+# ------------------------------------------------------------------ GEMMs
+def test_linear_bruteforce():
+    x, w, b = randn(5, 7), randn(3, 7), randn(3)
+    ref = np.zeros((5, 3))
+    X, Wn, B = x.double().numpy(), w.double().numpy(), b.double().numpy()
+    for m in range(5):
+        for n in range(3):
+            ref[m, n] = sum(X[m, k] * Wn[n, k] for k in range(7)) + B[n]
+    assert np.allclose(O.linear(x, w, b).double().numpy(), ref, atol=1e-5)
+
+
+def test_batched_gemm_bruteforce():
+    x, w = randn(3, 4, 5), randn(3, 6, 5)
+    ref = np.einsum("emk,enk->emn", x.double().numpy(), w.double().numpy())
+    assert np.allclose(O.batched_gemm(x, w).numpy(), ref, atol=1e-5)
+    assert O.batched_gemm(x, w).shape == (3, 4, 6)  # (E, M, N): rows of x against rows of w
+
+
+def test_conv3d_patch_is_patch_dot_product():
+    x, w, b = randn(6, 3, 2, 4, 4), randn(5, 3, 2, 4, 4), randn(5)
+    ref = x.reshape(6, -1).double().numpy() @ w.reshape(5, -1).double().numpy().T + b.double().numpy()
+    assert np.allclose(O.conv3d_patch(x, w, b).numpy(), ref, atol=1e-4)
+
+
+# ------------------------------------------------------------------ attention
+def np_attention(q, k, v, scale, causal, groups):
+    B, Hq, Sq, D = q.shape
+    out = np.zeros((B, Hq, Sq, D))
+    for b in range(B):
+        for h in range(Hq):
+            kv = h // groups
+            for i in range(Sq):
+                s = np.array([scale * np.dot(q[b, h, i], k[b, kv, j]) for j in range(k.shape[2])])
+                if causal:
+                    s[i + 1:] = -np.inf
+                p = np.exp(s - s.max())
+                p /= p.sum()
+                out[b, h, i] = p @ v[b, kv]
+    return out
+
+
+@pytest.mark.parametrize("causal,groups", [(True, 1), (False, 1), (True, 2), (False, 4)])
+def test_flash_attention_bruteforce(causal, groups):
+    q = randn(2, 2 * groups, 9, 8)
+    k, v = randn(2, 2, 9, 8), randn(2, 2, 9, 8)
+    ref = np_attention(q.double().numpy(), k.double().numpy(), v.double().numpy(), 0.3, causal, groups)
+    assert np.allclose(O.flash_attention(q, k, v, 0.3, causal, groups).numpy(), ref, atol=1e-5)
+
+
+def test_flash_attention_causal_row0_is_v0():
+    q, k, v = randn(1, 2, 6, 4), randn(1, 2, 6, 4), randn(1, 2, 6, 4)
+    assert torch.allclose(O.flash_attention(q, k, v, 1.0, True, 1)[:, :, 0], v[:, :, 0])
+
+
+def test_decode_attention_ragged_bruteforce():
+    q, kc, vc = randn(3, 4, 1, 8), randn(3, 2, 10, 8), randn(3, 2, 10, 8)
+    lens = [1, 6, 10]
+    out = O.decode_attention(q, kc, vc, lens, 0.5, 2)
+    for b, Lb in enumerate(lens):
+        ref = np_attention(q[b:b + 1].double().numpy(), kc[b:b + 1, :, :Lb].double().numpy(),
+                           vc[b:b + 1, :, :Lb].double().numpy(), 0.5, False, 2)
+        assert np.allclose(out[b:b + 1].numpy(), ref, atol=1e-5)
+
+
+# ------------------------------------------------------------------ rotary
+def test_mrope_tables_closed_form_distinct_axes():
+    """Element i of the interleaved table uses axis 0/1/2 by the chunked sections, both halves."""
+    D, section, theta = 64, [12, 10, 10], 5e6
+    S = 7
+    pos = torch.stack([torch.arange(S) + 1, torch.arange(S) * 3 + 2, torch.arange(S) * 5 + 11]).view(3, 1, S)
+    cos3, sin3 = O.mrope_cos_sin(pos, D, theta)
+    cos, sin = O.interleave_cos_sin(cos3, sin3, section)
+    half = D // 2
+    inv = [1.0 / theta ** (2 * i / D) for i in range(half)]
+    for s in range(S):
+        for i in range(D):
+            j = i % half
+            axis = 0 if j < section[0] else (1 if j < section[0] + section[1] else 2)
+            ang = float(pos[axis, 0, s]) * inv[j]
+            assert math.isclose(float(cos[0, s, i]), math.cos(ang), abs_tol=2e-3), (s, i)
+            assert math.isclose(float(sin[0, s, i]), math.sin(ang), abs_tol=2e-3), (s, i)
+
+
+def test_mrope_matches_hf_for_identical_axes():
+    from transformers.models.qwen3_vl import modeling_qwen3_vl as M
+    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLTextConfig
+    cfg = Qwen3VLTextConfig(hidden_size=512, intermediate_size=64, num_attention_heads=4, num_key_value_heads=2,
+                            head_dim=128, rope_parameters={"rope_type": "default", "rope_theta": 5e6,
+                                                           "mrope_section": [24, 20, 20]})
+    rot = M.Qwen3VLTextRotaryEmbedding(cfg)
+    S = 300
+    pos = torch.arange(S).view(1, 1, S).expand(3, 1, S)
+    hc, hs = rot(torch.zeros(1, S, 512), pos)
+    cos3, sin3 = O.mrope_cos_sin(pos, 128, 5e6)
+    c, s = O.interleave_cos_sin(cos3, sin3, [24, 20, 20])
+    assert torch.allclose(c, hc, atol=1e-6) and torch.allclose(s, hs, atol=1e-6)
+    x = randn(1, 4, S, 128)
+    ref = x * hc[:, None] + M.rotate_half(x) * hs[:, None]
+    assert torch.allclose(O.apply_mrope(x, cos3, sin3, [24, 20, 20]), ref, atol=1e-5)
+
+
+def test_rotate_half_invariants_and_loop():
+    x = randn(2, 3, 5, 16)
+    zero = torch.zeros(5, 8)
+    assert torch.equal(O.apply_rope(x, zero.cos().repeat(1, 2), zero.sin().repeat(1, 2)), x)  # angle 0: identity
+    ang = randn(5, 4)
+    emb = torch.cat([ang, ang], -1)
+    y = O.apply_rope(x, emb.cos(), emb.sin())  # D_rope = 8 < D = 16: tail passes through
+    assert torch.equal(y[..., 8:], x[..., 8:])
+    X, A = x.double().numpy(), ang.double().numpy()
+    for s in range(5):
+        for i in range(4):
+            c, sn = math.cos(A[s, i]), math.sin(A[s, i])
+            x1, x2 = X[..., s, i], X[..., s, i + 4]
+            assert np.allclose(y[..., s, i].numpy(), x1 * c - x2 * sn, atol=1e-5)
+            assert np.allclose(y[..., s, i + 4].numpy(), x2 * c + x1 * sn, atol=1e-5)
+    # norm of each rotated pair is preserved
+    n_in = x[..., :4] ** 2 + x[..., 4:8] ** 2
+    n_out = y[..., :4] ** 2 + y[..., 4:8] ** 2
+    assert torch.allclose(n_in, n_out, atol=1e-5)
+
+
+def test_vision_rope_tables_match_hf():
+    from transformers.models.qwen3_vl import modeling_qwen3_vl as M
+    from transformers.vision_utils import get_vision_position_ids
+    grid = [(1, 28, 28), (2, 8, 12)]
+    hd = 72
+    pid = get_vision_position_ids(torch.tensor(grid), 2)
+    rot = M.Qwen3VLVisionRotaryEmbedding(hd // 2)(pid)
+    emb = torch.cat([rot, rot], -1)
+    c, s = L.vision_rope_tables(grid, hd, 1e4, 2)
+    assert torch.allclose(c, emb.cos(), atol=1e-6) and torch.allclose(s, emb.sin(), atol=1e-6)
+
+
+# ------------------------------------------------------------------ norms / elementwise
+def test_rmsnorm_closed_form_and_constant_row():
+    x, w = randn(4, 33), randn(33)
+    X = x.double().numpy()
+    ref = X / np.sqrt((X ** 2).mean(-1, keepdims=True) + 1e-6) * w.double().numpy()
+    assert np.allclose(O.rmsnorm(x, w, 1e-6).numpy(), ref, atol=1e-5)
+    c = torch.full((2, 33), 2.5)
+    assert torch.allclose(O.rmsnorm(c, w, 0.0), w.expand(2, -1), atol=1e-6)  # a constant row normalises to w
+    assert torch.allclose(O.rmsnorm(-c, w, 0.0), -w.expand(2, -1), atol=1e-6)
+
+
+def test_layernorm_closed_form():
+    x, w, b = randn(4, 33) * 5 + 3, randn(33), randn(33)
+    X = x.double().numpy()
+    mu = X.mean(-1, keepdims=True)
+    var = ((X - mu) ** 2).mean(-1, keepdims=True)
+    ref = (X - mu) / np.sqrt(var + 1e-6) * w.double().numpy() + b.double().numpy()
+    assert np.allclose(O.layernorm(x, w, b, 1e-6).numpy(), ref, atol=1e-4)
+
+
+def test_elementwise_closed_forms():
+    a, b = randn(100), randn(100)
+    A, Bn = a.double().numpy(), b.double().numpy()
+    assert np.allclose(O.swiglu(a, b).numpy(), A / (1 + np.exp(-A)) * Bn, atol=1e-6)
+    assert np.allclose(O.residual_add(a, b).numpy(), A + Bn, atol=1e-6)
+    gelu = 0.5 * A * (1 + np.tanh(math.sqrt(2 / math.pi) * (A + 0.044715 * A ** 3)))
+    assert np.allclose(O.gelu_tanh(a).numpy(), gelu, atol=1e-6)
+
+
+def test_softmax_closed_form():
+    x = randn(3, 50) * 4
+    X = x.double().numpy()
+    e = np.exp(X - X.max(-1, keepdims=True))
+    assert np.allclose(O.softmax(x).numpy(), e / e.sum(-1, keepdims=True), atol=1e-7)
+
+
+def test_topk_bruteforce_lowest_index_wins_ties():
+    x = torch.randint(0, 4, (64, 20), generator=g).float()
+    for k in (1, 3, 8):
+        v, i = O.topk(x, k)
+        for r in range(64):
+            order = sorted(range(20), key=lambda c: (-float(x[r, c]), c))[:k]
+            assert i[r].tolist() == order
+            assert v[r].tolist() == [float(x[r, c]) for c in order]
+
+
+def test_index_add_loop_and_scatter():
+    t, s = randn(5, 3), randn(9, 3)
+    idx = torch.tensor([0, 4, 4, 1, 0, 2, 4, 3, 0])
+    ref = t.double().numpy().copy()
+    for i, j in enumerate(idx.tolist()):
+        ref[j] += s[i].double().numpy()
+    assert np.allclose(O.index_add(t.clone(), s, idx).numpy(), ref, atol=1e-6)
+    u = torch.tensor([3, 1, 0])  # unique indices: a scatter
+    out = O.index_add(torch.zeros(5, 3), s[:3], u)
+    assert torch.equal(out[u], s[:3]) and torch.equal(out[[2, 4]], torch.zeros(2, 3))
+
+
+# ------------------------------------------------------------------ layer compositions
+def _c1_hf_and_params(seed=0):
+    from transformers.models.qwen3_vl import modeling_qwen3_vl as M
+    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLTextConfig
+    cfg = Qwen3VLTextConfig(hidden_size=256, intermediate_size=688, num_attention_heads=4, num_key_value_heads=2,
+                            head_dim=64, rms_norm_eps=1e-6,
+                            rope_parameters={"rope_type": "default", "rope_theta": 5e6, "mrope_section": [12, 10, 10]})
+    cfg._attn_implementation = "eager"
+    hf = M.Qwen3VLTextDecoderLayer(cfg, 0).eval()
+    gg = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for n, p in hf.named_parameters():
+            if p.dim() == 2:
+                p.copy_(torch.randn(p.shape, generator=gg) * 0.02)
+            else:
+                p.copy_(1 + 0.1 * torch.randn(p.shape, generator=gg))
+    return M, cfg, hf, {n: p.detach().clone() for n, p in hf.named_parameters()}
+
+
+def test_text_decoder_layer_matches_hf():
+    M, cfg, hf, p = _c1_hf_and_params()
+    S = 128
+    x = torch.randn(1, S, 256, generator=g)
+    pos = torch.arange(S).view(1, 1, S).expand(3, 1, S)
+    cos, sin = M.Qwen3VLTextRotaryEmbedding(cfg)(x, pos)
+    mask = torch.full((S, S), float("-inf")).triu(1)[None, None]
+    with torch.no_grad():
+        ref = hf(x, (cos, sin), attention_mask=mask)
+    cos3, sin3 = O.mrope_cos_sin(pos, 64, 5e6)
+    y, logits, (k, v) = L.text_decoder_layer(x, p, num_heads=4, num_kv_heads=2, head_dim=64, eps=1e-6,
+                                             cos_3d=cos3, sin_3d=sin3, mrope_section=[12, 10, 10])
+    assert logits is None and k.shape == (1, 2, S, 64)
+    assert torch.allclose(y, ref, atol=2e-5), float((y - ref).abs().max())
+
+
+def test_sparse_moe_per_token_loop():
+    T, H, I, E, k = 12, 16, 8, 5, 2
+    x = randn(1, T, H)
+    p = {"gate_weight": randn(E, H, std=0.5), "gate_up_proj": randn(E, 2 * I, H, std=0.3),
+         "down_proj": randn(E, H, I, std=0.3)}
+    out, logits = L.sparse_moe(x, p, top_k=k)
+    X = x[0].double().numpy()
+    G, GU, DN = (p[n].double().numpy() for n in ("gate_weight", "gate_up_proj", "down_proj"))
+    for t in range(T):
+        lg = G @ X[t]
+        pr = np.exp(lg - lg.max())
+        pr /= pr.sum()
+        sel = sorted(range(E), key=lambda e: (-pr[e], e))[:k]
+        wts = pr[sel] / pr[sel].sum()
+        acc = np.zeros(H)
+        for e, wt in zip(sel, wts):
+            gu = GU[e] @ X[t]
+            a = gu[:I] / (1 + np.exp(-gu[:I])) * gu[I:]
+            acc += wt * (DN[e] @ a)
+        assert np.allclose(out[0, t].numpy(), acc, atol=1e-5), t
+    assert np.allclose(logits.numpy(), X @ G.T, atol=1e-5)
+
+
+def test_sparse_moe_single_expert_is_swiglu_mlp():
+    T, H, I = 10, 16, 8
+    x = randn(1, T, H)
+    gu, dn = randn(1, 2 * I, H, std=0.3), randn(1, H, I, std=0.3)
+    out, _ = L.sparse_moe(x, {"gate_weight": randn(1, H), "gate_up_proj": gu, "down_proj": dn}, top_k=1)
+    mlp = L.swiglu_mlp(x, {"gate_proj.weight": gu[0, :I], "up_proj.weight": gu[0, I:], "down_proj.weight": dn[0]})
+    assert torch.allclose(out, mlp, atol=1e-6)
+
+
+def test_vision_block_matches_hf_per_image():
+    from transformers.models.qwen3_vl import modeling_qwen3_vl as M
+    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLVisionConfig
+    vc = Qwen3VLVisionConfig(hidden_size=288, num_heads=4, intermediate_size=400, hidden_act="gelu_pytorch_tanh")
+    vc._attn_implementation = "eager"
+    hf = M.Qwen3VLVisionBlock(vc).eval()
+    with torch.no_grad():
+        for n, prm in hf.named_parameters():
+            prm.copy_(torch.randn(prm.shape, generator=g) * (0.05 if prm.dim() == 2 else 0.2)
+                      + (1.0 if n.startswith("norm") and n.endswith("weight") else 0.0))
+    grid = (1, 8, 8)
+    nimg, S = 3, 64
+    x = torch.randn(nimg * S, 288, generator=g)
+    cos, sin = L.vision_rope_tables([grid], 72, 1e4, 2)
+    cu = torch.tensor([0, S, 2 * S, 3 * S], dtype=torch.int32)
+    with torch.no_grad():
+        ref = hf(x, cu_seqlens=cu, position_embeddings=(cos.repeat(nimg, 1), sin.repeat(nimg, 1)))
+    p = {n: t.detach() for n, t in hf.named_parameters()}
+    y = L.vision_block(x.view(nimg, S, 288), p, num_heads=4, cos=cos, sin=sin, eps=1e-6)
+    assert torch.allclose(y.reshape(-1, 288), ref, atol=5e-5), float((y.reshape(-1, 288) - ref).abs().max())
+
+
+def test_c1_golden_fixture():
+    """Regression pin: the C1 layer output stored from the HF implementation (tests/golden/make_golden.py)."""
+    from tests.golden.make_golden import c1_case, load_fixture
+    fx = load_fixture("c1_layer")
+    x, pos, p = c1_case()
+    assert np.isclose(float(x.double().sum()), float(fx["x_sum"]), rtol=1e-9), "input generator drifted"
+    cos3, sin3 = O.mrope_cos_sin(pos, 64, 5e6)
+    y, _, _ = L.text_decoder_layer(x, p, num_heads=4, num_kv_heads=2, head_dim=64, eps=1e-6, cos_3d=cos3,
+                                   sin_3d=sin3, mrope_section=[12, 10, 10])
+    assert np.allclose(y.numpy(), fx["y"], atol=2e-5)
