@@ -21,6 +21,7 @@ struct GemmParams {
   bf16* C;           // (M, N_out), ld = ldc
   const bf16* rowscale;  // kEpiRowScale: (rows) scale
   int M, N, K;       // N = output columns (SwiGLU: intermediate size)
+  int M_src;         // rows of X addressable through `gather` (grouped problems)
   int64_t ldx, ldw, ldr, ldc;
   int64_t bsX, bsW, bsC;  // batch strides (blockIdx.z)
   int group_m;       // tile-order grouping along m
@@ -47,7 +48,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_kernel(const GemmParams
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int wm = wave % WM;
   const int wn = wave / WM;
 
@@ -92,80 +93,110 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_kernel(const GemmParams
   const int n0_out = tile_n * BN_OUT;
 
   constexpr int kStage = (BM + BN) * kBK;
-  auto sX = [&](int s) { return smem + s * kStage; };
-  auto sW = [&](int s) { return smem + s * kStage + BM * kBK; };
+  // Register staging: thread t owns 16-byte chunks t + i*NT of the X tile
+  // (PX of them) and of the W tile (PW).
+  constexpr int PX = BM * kChunks / NT;
+  constexpr int PW = BN * kChunks / NT;
+  static_assert(BM * kChunks % NT == 0 && BN * kChunks % NT == 0, "tile not divisible by threads");
 
-  const int* gather = p.gather;
-  const int64_t ldx = p.ldx, ldw = p.ldw;
-  auto x_row = [&](int r) -> const bf16* {
-    const int lr = m_begin + r;
-    const int64_t pr = gather ? (int64_t)gather[lr] : (int64_t)lr;
-    return X + pr * ldx;
-  };
-  // W tile rows: plain -> n0 + r; SwiGLU -> 32-row groups alternate gate/up.
-  auto w_row = [&](int r) -> const bf16* {
-    if constexpr (EPI == kEpiSwiGLU) {
-      const int g = r >> 5;
-      const int n = n0_out + (g >> 1) * 32 + (r & 31);
-      return ((g & 1) ? W2 : W) + (int64_t)n * ldw;
-    } else {
-      return W + (int64_t)(n0_out + r) * ldw;
-    }
-  };
-  int rows_n;
-  if constexpr (EPI == kEpiSwiGLU) {
-    // Rows of a gate/up group exist iff their output column exists.
-    rows_n = BN;  // handled per row below via the column bound
-  } else {
-    rows_n = min(BN, p.N - n0_out);
-  }
-
-  TileLoader<BM, NT> lx;
-  TileLoader<BN, NT> lw;
   const int K = p.K;
   const int nk = (K + kBK - 1) / kBK;
+  const int64_t ldx = p.ldx, ldw = p.ldw;
 
-  auto load_stage = [&](int kt) {
-    lx.load(x_row, rows_m, kt * kBK, K, tid);
-    if constexpr (EPI == kEpiSwiGLU) {
-      // Valid W rows: those whose output column n < N.
-      const int ncols = p.N - n0_out;
+  // Per chunk: byte offset of its global row (kOOB: no such row) and its K chunk.
+  uint32_t xoff[PX], woff[PW];
 #pragma unroll
-      for (int i = 0; i < TileLoader<BN, NT>::kPer; ++i) {
-        const int id = tid + i * NT;
-        const int r = id / kChunks;
-        const int c = id % kChunks;
-        const int k = kt * kBK + c * 8;
-        const int col = (r >> 6) * 32 + (r & 31);
-        if (col < ncols && k < K) {
-          lw.v[i] = *reinterpret_cast<const bf16x8*>(w_row(r) + k);
-        } else {
-          lw.v[i] = bf16x8{};
-        }
-      }
+  for (int i = 0; i < PX; ++i) {
+    const int r = (tid + i * NT) / kChunks;
+    if (r < rows_m) {
+      const int lr = m_begin + r;
+      const int64_t pr = p.gather ? (int64_t)p.gather[lr] : (int64_t)lr;
+      xoff[i] = (uint32_t)(pr * ldx * 2);
     } else {
-      lw.load(w_row, rows_n, kt * kBK, K, tid);
+      xoff[i] = kOOB;
     }
+  }
+#pragma unroll
+  for (int i = 0; i < PW; ++i) {
+    const int r = (tid + i * NT) / kChunks;
+    int n;
+    if constexpr (EPI == kEpiSwiGLU) {
+      n = n0_out + (r >> 6) * 32 + (r & 31);  // 32-row groups alternate gate / up
+    } else {
+      n = n0_out + r;
+    }
+    woff[i] = n < p.N ? (uint32_t)((int64_t)n * ldw * 2) : kOOB;
+  }
+  const __amdgpu_buffer_rsrc_t rx =
+      make_rsrc(X, p.gather ? (int64_t)p.M_src * ldx * 2 : (int64_t)(m_begin + rows_m) * ldx * 2);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(W, (int64_t)p.N * ldw * 2);
+  const __amdgpu_buffer_rsrc_t rw2 = make_rsrc(EPI == kEpiSwiGLU ? W2 : W, (int64_t)p.N * ldw * 2);
+
+  struct Stage {
+    bf16x8 x[PX], w[PW];
+  };
+  // Loads of K-stage kt (zeros past the end: offsets resolve out of range).
+  auto load = [&](Stage& st, int kt) {
+    const int k0 = kt * kBK;
+#pragma unroll
+    for (int i = 0; i < PX; ++i) {
+      const int k = k0 + ((tid + i * NT) % kChunks) * 8;
+      st.x[i] = buffer_load16(rx, (k < K && xoff[i] != kOOB) ? xoff[i] + (uint32_t)k * 2u : kOOB);
+    }
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+      const int id = tid + i * NT;
+      const int k = k0 + (id % kChunks) * 8;
+      const uint32_t off = (k < K && woff[i] != kOOB) ? woff[i] + (uint32_t)k * 2u : kOOB;
+      if constexpr (EPI == kEpiSwiGLU) {
+        st.w[i] = buffer_load16((((id / kChunks) >> 5) & 1) ? rw2 : rw, off);
+      } else {
+        st.w[i] = buffer_load16(rw, off);
+      }
+    }
+  };
+  auto store = [&](const Stage& st, int slot) {
+    bf16* sx = smem + slot * kStage;
+    bf16* sw = sx + BM * kBK;
+#pragma unroll
+    for (int i = 0; i < PX; ++i) {
+      const int id = tid + i * NT;
+      *reinterpret_cast<bf16x8*>(sx + swz(id / kChunks, id % kChunks)) = st.x[i];
+    }
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+      const int id = tid + i * NT;
+      *reinterpret_cast<bf16x8*>(sw + swz(id / kChunks, id % kChunks)) = st.w[i];
+    }
+  };
+  auto compute = [&](auto& acc, int slot) {
+    const bf16* sx = smem + slot * kStage;
+    acc.mma_stage(sx, sx + BM * kBK, wm * WTM, wn * WTN, lane);
   };
 
   WaveAcc<TN, TM> acc;
   acc.zero();
 
-  load_stage(0);
-  lx.store(sX(0), tid);
-  lw.store(sW(0), tid);
+  // Two register stages in flight (prefetch distance 2): the loads of stage
+  // kt+2 are issued before the MFMAs of stage kt, and stage kt+1 (issued one
+  // phase earlier) is written to LDS after them.
+  Stage sa, sb;
+  load(sa, 0);
+  load(sb, 1);
+  store(sa, 0);
   __syncthreads();
-
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) load_stage(kt + 1);
-    acc.mma_stage(sX(cur), sW(cur), wm * WTM, wn * WTN, lane);
-    if (kt + 1 < nk) {
-      lx.store(sX(cur ^ 1), tid);
-      lw.store(sW(cur ^ 1), tid);
-    }
+  int kt = 0;
+  for (; kt + 1 < nk; kt += 2) {  // slot 0 holds stage kt, sb stage kt+1 (in flight)
+    load(sa, kt + 2);
+    compute(acc, 0);
+    store(sb, 1);
+    __syncthreads();
+    load(sb, kt + 3);
+    compute(acc, 1);
+    store(sa, 0);
     __syncthreads();
   }
+  if (kt < nk) compute(acc, 0);  // odd number of stages: the last one is in slot 0
 
   // ------------------------------------------------------------ epilogue
   const int l32 = lane & 31;

@@ -484,6 +484,7 @@ int q3_moe_experts(const void* x, const void* gate_up, const void* down, const i
     p.ldw = H;
     p.ldc = I;
     p.gather = w.sorted_token;
+    p.M_src = (int)T;
     p.tile_table = w.tile_table;
     p.group_end = w.offsets + 1;
     p.n_tiles_total = w.n_tiles;
