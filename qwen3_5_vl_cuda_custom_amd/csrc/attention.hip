@@ -15,16 +15,13 @@
 // (t = r), is a fixed key permutation; the V^T fragment reads use the same one.
 // The O^T accumulators are per-lane queries, so the softmax rescale is local.
 //
-// LDS (per stage): K tile [64][128] bf16, 16-byte chunk c of row r at slot
-// c ^ (r & 15); V^T tile [D][64] bf16, 8-byte unit u (keys 4u..4u+3) of row d at
-// slot u ^ (d & 15). Double-buffered, one barrier per tile.
-//
 // Decode (q3_decode_attention): one block per (64*4-key chunk, sequence, KV
 // head); the MFMA query columns are the GQA group's heads. Each wave handles 64
-// keys; the block merges its waves and writes (m, l, O) partials, and
-// q3_decode_combine-style merging happens in a second kernel.
+// keys; the block merges its waves and writes (m, l, O) partials, which a
+// second kernel combines per query head.
 #include <algorithm>
 
+#include "gemm_tile.h"
 #include "q3_common.h"
 
 namespace {
@@ -55,63 +52,6 @@ struct AttnParams {
   const int* kv_lens;
   float* partial;  // decode workspace
   int max_chunks;
-};
-
-// Global -> register staging of one K tile and one V tile (64 keys x D).
-template <int D>
-struct KVStage {
-  static constexpr int CHD = (D + 15) / 16 * 2;  // 16-byte chunks per K row incl. zero padding to DK
-  static constexpr int KITEMS = (kKT * CHD + 255) / 256;
-  static constexpr int VCH = D / 8;              // real chunks per V row
-  static constexpr int VITEMS = (32 * VCH + 255) / 256;  // (key pair, chunk) items per thread
-  bf16x8 kv[KITEMS];
-  bf16x8 vv[VITEMS][2];
-
-  __device__ __forceinline__ void load(const bf16* kbase, const bf16* vbase, int64_t ks, int64_t vs, int k0,
-                                       int klimit, int tid) {
-#pragma unroll
-    for (int i = 0; i < KITEMS; ++i) {
-      const int id = tid + 256 * i;
-      const int r = id / CHD, c = id % CHD;
-      const bool ok = (id < kKT * CHD) && (k0 + r < klimit) && (c * 8 < D);
-      kv[i] = ok ? *reinterpret_cast<const bf16x8*>(kbase + (int64_t)(k0 + r) * ks + c * 8) : bf16x8{};
-    }
-#pragma unroll
-    for (int i = 0; i < VITEMS; ++i) {
-      const int id = tid + 256 * i;
-      const int p = id & 31, c = id >> 5;
-      const bool cok = (id < 32 * VCH);
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int key = k0 + 2 * p + e;
-        vv[i][e] = (cok && key < klimit) ? *reinterpret_cast<const bf16x8*>(vbase + (int64_t)key * vs + c * 8)
-                                         : bf16x8{};
-      }
-    }
-  }
-  __device__ __forceinline__ void store(bf16* sK, bf16* sVt, int tid) const {
-#pragma unroll
-    for (int i = 0; i < KITEMS; ++i) {
-      const int id = tid + 256 * i;
-      if (id < kKT * CHD) {
-        const int r = id / CHD, c = id % CHD;
-        *reinterpret_cast<bf16x8*>(sK + k_slot(r, c)) = kv[i];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < VITEMS; ++i) {
-      const int id = tid + 256 * i;
-      if (id < 32 * VCH) {
-        const int p = id & 31, c = id >> 5;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int d = c * 8 + e;
-          uint32_t* dst = reinterpret_cast<uint32_t*>(sVt + vt_unit(d, p >> 1)) + (p & 1);
-          *dst = pack_bf16x2(vv[i][0][e], vv[i][1][e]);
-        }
-      }
-    }
-  }
 };
 
 // Per-wave attention state over a 32-query column block.
@@ -204,26 +144,61 @@ struct WaveAttn {
   }
 };
 
+// ----------------------------------------------------------------- prefill
+// Prefill kernel, sized for two blocks (8 waves) per CU:
+//  * K tiles go global -> LDS with buffer_load ... lds (no staging
+//    registers); rows are 128 elements (256 B) apart whatever D is, and row
+//    r's 16-byte chunk c sits at slot c ^ (r & 15). Chunks at or past D load
+//    as zeros (out-of-range buffer offsets), which pads D to the MFMA K step.
+//  * V tiles are staged through registers and written transposed: V^T row d
+//    holds the tile's 64 keys as 8 chunks of 16 bytes, chunk 2j + h holding
+//    the 4-key units 4j + h and 4j + 2 + h (the two units one lane feeds to a
+//    PV MFMA), at slot chunk ^ ((d >> 1) & 7). One ds_read_b128 per fragment,
+//    conflict-free for 16 consecutive rows.
+//  * The running max is raised only when a tile's max exceeds it by more than
+//    kRescale (log2 units), so the O rescale almost never runs; P stays below
+//    2^kRescale and O / l is unchanged.
+//  * The row max is exchanged between the two lane halves that share a query
+//    with v_permlane32_swap; the row sums stay per half until the end.
+namespace fwd {
+constexpr float kRescale = 8.0f;
+
+__device__ __forceinline__ int k_off(int r, int c) { return r * kRowK + ((c ^ (r & 15)) << 3); }
+__device__ __forceinline__ int vt_off(int d, int chunk) { return d * kKT + ((chunk ^ ((d >> 1) & 7)) << 3); }
+
+__device__ __forceinline__ float half_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+}  // namespace fwd
+
 template <int D, int WH>
-__global__ __launch_bounds__(256) void flash_prefill_kernel(const AttnParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_fwd_kernel(
+    const AttnParams p) {
+  using namespace fwd;
+  static_assert(D % 8 == 0 && D <= kRowK, "head_dim");
+  constexpr int KSTEPS = (D + 15) / 16;  // MFMA K steps over the (zero-padded) head dim
+  constexpr int OT = (D + 31) / 32;      // 32-row output tiles of O^T
+  constexpr int VCH = D / 8;             // 16-byte chunks per V row
   constexpr int WQ = 4 / WH;
-  constexpr int QB = WQ * 32;  // queries per block
-  __shared__ __attribute__((aligned(16))) bf16 sK[2][kKT * kRowK];
-  __shared__ __attribute__((aligned(16))) bf16 sVt[2][WaveAttn<D>::OT * 32 * kKT];
+  constexpr int QB = WQ * 32;
+  __shared__ __attribute__((aligned(1024))) bf16 sK[2][kKT * kRowK];
+  __shared__ __attribute__((aligned(1024))) bf16 sV[2][OT * 32 * kKT];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wh = wave % WH;
   const int wq = wave / WH;
   const int l32 = lane & 31;
   const int h = lane >> 5;
 
+  // Blocks are dispatched x-fastest: heads vary fastest and query tiles go
+  // heaviest-first (causal) in the slow dimension.
   const int n_qt = (p.Sq + QB - 1) / QB;
-  // Heavy-first: causal tiles with the most keys are issued first.
-  const int qt = p.causal ? (n_qt - 1 - (int)blockIdx.x) : (int)blockIdx.x;
+  const int qt = p.causal ? (n_qt - 1 - (int)blockIdx.y) : (int)blockIdx.y;
   const int hgroups = p.groups / WH;
-  int yb = blockIdx.y;
+  int yb = blockIdx.x;
   const int hg = yb % hgroups;
   yb /= hgroups;
   const int kvh = yb % p.Hkv;
@@ -238,47 +213,157 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const AttnParams p) 
 
   const bf16* kbase = p.k + (int64_t)b * p.kb + (int64_t)kvh * p.kh;
   const bf16* vbase = p.v + (int64_t)b * p.vb + (int64_t)kvh * p.vh;
+  const int ks2 = (int)p.ks * 2;  // host guarantees Sk * ks * 2 < 2^31
+  const __amdgpu_buffer_rsrc_t krs = q3::make_rsrc(kbase, (int64_t)(p.Sk - 1) * ks2 + D * 2);
+  (void)VCH;
 
-  WaveAttn<D> wa;
-  wa.init();
-  wa.load_q(p.q + (int64_t)b * p.qb + (int64_t)hq * p.qh + (int64_t)qidx * p.qs, qidx < p.Sq, h);
-
-  // Rows D..OT*32 of V^T are never written; they only feed output rows that
-  // are never stored.
-  KVStage<D> st;
-  if (nkt > 0) {
-    st.load(kbase, vbase, p.ks, p.vs, 0, p.Sk, tid);
-    st.store(sK[0], sVt[0], tid);
+  // Q fragments (B operand): lane supplies Q[qidx][16 ks + 8 h .. +7].
+  bf16x8 qf[KSTEPS];
+  {
+    const bf16* qrow = p.q + (int64_t)b * p.qb + (int64_t)hq * p.qh + (int64_t)qidx * p.qs;
+    const bool ok = qidx < p.Sq;
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks)
+      qf[ks] = (ok && ks * 16 + 8 * h < D) ? *reinterpret_cast<const bf16x8*>(qrow + ks * 16 + 8 * h) : bf16x8{};
   }
+  floatx16 o[OT];
+#pragma unroll
+  for (int t = 0; t < OT; ++t) o[t] = floatx16{};
+  float m = -INFINITY, lpart = 0.f;
+
+  // K: this wave's 16 rows of the tile, 4 rows per DMA instruction.
+  auto issue_k = [&](int kt, int stage) {
+    const uint32_t lds0 = q3::lds_addr(&sK[stage][0]) + wave * (16 * kRowK * 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 16 * wave + 4 * i + (lane >> 4);
+      const int c = (lane & 15) ^ (r & 15);
+      const uint32_t off = c * 8 < D ? (uint32_t)((kt * kKT + r) * ks2 + c * 16) : q3::kOOB;
+      q3::dma16(krs, off, lds0 + i * 1024);
+    }
+  };
+  // V: thread = (d chunk cd = tid & 15, key quad u = tid >> 4).
+  const int vcd = tid & 15, vu = tid >> 4;
+  const bool vlive = vcd < VCH;
+  bf16x8 vreg[4];
+  auto load_v = [&](int kt) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int key = kt * kKT + 4 * vu + kk;
+      vreg[kk] = (vlive && key < p.Sk) ? *reinterpret_cast<const bf16x8*>(vbase + (int64_t)key * p.vs + vcd * 8)
+                                       : bf16x8{};
+    }
+  };
+  // Rows D .. 32*OT of V^T are never written; they only feed O^T rows that
+  // are never stored.
+  auto store_v = [&](int stage) {
+    if (!vlive) return;
+    bf16* dst = sV[stage];
+    const int chunk = 2 * (vu >> 2) + (vu & 1);
+    const int half = (vu >> 1) & 1;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int d = vcd * 8 + e;
+      u32x2 w = {pack_bf16x2(vreg[0][e], vreg[1][e]), pack_bf16x2(vreg[2][e], vreg[3][e])};
+      *reinterpret_cast<u32x2*>(dst + vt_off(d, chunk) + 4 * half) = w;
+    }
+  };
+
+  if (nkt > 0) {
+    issue_k(0, 0);
+    load_v(0);
+    store_v(0);
+  }
+  q3::vm_wait<0>();
   __syncthreads();
+
   const int wave_last_q = min(q0 + 31, p.Sq - 1);
+  const float c = p.scale_log2;
   for (int kt = 0; kt < nkt; ++kt) {
     const int cur = kt & 1;
-    if (kt + 1 < nkt) st.load(kbase, vbase, p.ks, p.vs, (kt + 1) * kKT, p.Sk, tid);
+    const bool more = kt + 1 < nkt;
+    if (more) {
+      issue_k(kt + 1, cur ^ 1);
+      load_v(kt + 1);
+    }
     const int k0 = kt * kKT;
-    const bool active = q0 < p.Sq && (!p.causal || k0 <= wave_last_q);
-    if (active) wa.tile(sK[cur], sVt[cur], lane, k0, qidx, p.Sk, p.causal != 0, p.scale_log2);
-    if (kt + 1 < nkt) st.store(sK[cur ^ 1], sVt[cur ^ 1], tid);
+    if (q0 < p.Sq && (!p.causal || k0 <= wave_last_q)) {
+      const bf16* sKc = sK[cur];
+      const bf16* sVc = sV[cur];
+      floatx16 s0 = floatx16{}, s1 = floatx16{};
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) {
+        const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(sKc + k_off(l32, 2 * ks + h));
+        const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(sKc + k_off(32 + l32, 2 * ks + h));
+        s0 = mfma32x32x16(a0, qf[ks], s0);
+        s1 = mfma32x32x16(a1, qf[ks], s1);
+      }
+      // Wave-uniform: does any key of this tile need masking for this wave?
+      const bool need_mask = (p.causal && k0 + kKT - 1 > q0) || (k0 + kKT > p.Sk);
+      if (need_mask) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (key >= p.Sk || (p.causal && key > qidx)) s0[r] = -INFINITY;
+          if (key + 32 >= p.Sk || (p.causal && key + 32 > qidx)) s1[r] = -INFINITY;
+        }
+      }
+      float mloc = fmaxf(s0[0], s1[0]);
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, fmaxf(s0[r], s1[r]));
+      mloc = half_max(mloc) * c;
+      const bool raise = mloc > m + kRescale;
+      if (__builtin_amdgcn_ballot_w64(raise) != 0) {
+        const float mnew = raise ? mloc : m;
+        const float alpha = fast_exp2(m - mnew);
+        lpart *= alpha;
+#pragma unroll
+        for (int t = 0; t < OT; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+        m = mnew;
+      }
+      const float nm = (m == -INFINITY) ? 0.f : -m;
+      bf16x8 pb[4];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p0 = fast_exp2(fmaf(s0[r], c, nm));
+        const float p1 = fast_exp2(fmaf(s1[r], c, nm));
+        lpart += p0 + p1;
+        pb[r >> 3][r & 7] = f2bf(p0);
+        pb[2 + (r >> 3)][r & 7] = f2bf(p1);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int t = 0; t < OT; ++t) {
+          const bf16x8 a = *reinterpret_cast<const bf16x8*>(sVc + vt_off(t * 32 + l32, 2 * j + h));
+          o[t] = mfma32x32x16(a, pb[j], o[t]);
+        }
+    }
+    if (more) store_v(cur ^ 1);
+    q3::vm_wait<0>();
     __syncthreads();
   }
 
   if (qidx >= p.Sq) return;
-  const float inv_l = wa.l > 0.f ? 1.0f / wa.l : 0.f;
+  const float l = lpart + __shfl_xor(lpart, 32, 64);
+  const float inv_l = l > 0.f ? 1.0f / l : 0.f;
   bf16* orow = p.o + (int64_t)b * p.ob + (int64_t)hq * p.oh + (int64_t)qidx * p.os;
 #pragma unroll
-  for (int t = 0; t < WaveAttn<D>::OT; ++t)
+  for (int t = 0; t < OT; ++t)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int d = t * 32 + 8 * g + 4 * h;
       if (d < D) {
         bf16x4 v4;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v4[e] = f2bf(wa.o[t][4 * g + e] * inv_l);
+        for (int e = 0; e < 4; ++e) v4[e] = f2bf(o[t][4 * g + e] * inv_l);
         *reinterpret_cast<bf16x4*>(orow + d) = v4;
       }
     }
   if (p.lse && h == 0) {
-    p.lse[((int64_t)b * p.Hq + hq) * p.Sq + qidx] = (wa.m + log2f(wa.l)) * 0.6931471805599453f;
+    p.lse[((int64_t)b * p.Hq + hq) * p.Sq + qidx] = (m + log2f(l)) * 0.6931471805599453f;
   }
 }
 
@@ -315,7 +400,7 @@ __global__ __launch_bounds__(256) void flash_decode_kernel(const AttnParams p) {
 
   // Wave-private stage of this wave's 64 keys.
   {
-    constexpr int CHD = KVStage<D>::CHD;
+    constexpr int CHD = (D + 15) / 16 * 2;  // 16-byte chunks per K row incl. zero padding
     for (int id = lane; id < kKT * CHD; id += 64) {
       const int r = id / CHD, c = id % CHD;
       const bool ok = (k0 + r < L) && (c * 8 < D);
@@ -472,19 +557,21 @@ __global__ __launch_bounds__(128) void flash_generic_kernel(const AttnParams p, 
 bool mfma_head_dim(int64_t D) { return D == 64 || D == 72 || D == 80 || D == 96 || D == 128; }
 
 template <int D>
-int launch_prefill_d(const AttnParams& p, hipStream_t st) {
+int launch_fwd(const AttnParams& p, hipStream_t st) {
   const int WH = (p.groups % 4 == 0) ? 4 : (p.groups % 2 == 0 ? 2 : 1);
-  const int QB = (4 / WH) * 32;
-  dim3 grid((unsigned)q3_cdiv(p.Sq, QB), (unsigned)(p.B * p.Hkv * (p.groups / WH)));
+  const int QB = 32 * (4 / WH);
+  Q3_REQUIRE(q3_cdiv(p.Sq, QB) <= 65535, Q3_ERR_UNSUPPORTED);
+  dim3 grid((unsigned)(p.B * p.Hkv * (p.groups / WH)), (unsigned)q3_cdiv(p.Sq, QB));
   if (WH == 4)
-    hipLaunchKernelGGL((flash_prefill_kernel<D, 4>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((flash_fwd_kernel<D, 4>), grid, dim3(256), 0, st, p);
   else if (WH == 2)
-    hipLaunchKernelGGL((flash_prefill_kernel<D, 2>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((flash_fwd_kernel<D, 2>), grid, dim3(256), 0, st, p);
   else
-    hipLaunchKernelGGL((flash_prefill_kernel<D, 1>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((flash_fwd_kernel<D, 1>), grid, dim3(256), 0, st, p);
   Q3_LAUNCH_CHECK();
   return Q3_OK;
 }
+
 
 bool strides_aligned8(const int64_t* s, int n) {
   for (int i = 0; i < n; ++i)
@@ -541,18 +628,19 @@ int q3_flash_attention(const void* q, const void* k, const void* v, void* o, flo
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool aligned = q3_aligned(q, 16) && q3_aligned(k, 16) && q3_aligned(v, 16) && q3_aligned(o, 8) &&
                        strides_aligned8(strides, 12);
-  if (dtype == Q3_BF16 && mfma_head_dim(D) && aligned && Sk > 0) {
+  // The MFMA path addresses K with 32-bit buffer offsets.
+  if (dtype == Q3_BF16 && mfma_head_dim(D) && aligned && Sk > 0 && (Sk + 1) * strides[5] * 2 < 0x7fffffffLL) {
     switch (D) {
       case 64:
-        return launch_prefill_d<64>(p, st);
+        return launch_fwd<64>(p, st);
       case 72:
-        return launch_prefill_d<72>(p, st);
+        return launch_fwd<72>(p, st);
       case 80:
-        return launch_prefill_d<80>(p, st);
+        return launch_fwd<80>(p, st);
       case 96:
-        return launch_prefill_d<96>(p, st);
+        return launch_fwd<96>(p, st);
       default:
-        return launch_prefill_d<128>(p, st);
+        return launch_fwd<128>(p, st);
     }
   }
   const int64_t rows = B * Hq * Sq;

@@ -105,6 +105,8 @@ def test_conv3d_patch():
     (1, 8, 2, 300, 128, True),
     (2, 4, 1, 130, 128, True),
     (1, 32, 8, 512, 128, True),
+    (1, 4, 4, 200, 128, False),  # one head per KV head: 4 query tiles per block
+    (1, 4, 2, 100, 128, True),   # groups 2
     (2, 4, 4, 200, 64, False),
     (4, 4, 4, 784, 72, False),   # vision: head_dim 72, per-image
     (1, 2, 2, 77, 80, True),
@@ -127,6 +129,21 @@ def test_flash_attention_strided_views_and_out():
     ref = O.flash_attention(f32(qs).transpose(1, 2), f32(ks).transpose(1, 2), f32(vs).transpose(1, 2), D ** -0.5,
                             True, 4)
     assert_bf16_close(out.transpose(1, 2), ref, what="strided flash")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_flash_attention_sharp_scores(causal):
+    """Large logits (scale 1 at D=128): the running max keeps rising over key tiles."""
+    B, Hq, Hkv, S, D = 1, 8, 2, 640, 128
+    q, k, v = rnd(B, Hq, S, D, seed=32), rnd(B, Hkv, S, D, seed=33), rnd(B, Hkv, S, D, seed=34)
+    # keys whose norm grows with the index make later tiles dominate
+    k = (k.float() * torch.linspace(0.2, 1.5, S).view(1, 1, S, 1)).to(torch.bfloat16)
+    # a sharp softmax returns nearly single rows of v: keep |v| < 2 so one bf16
+    # output rounding stays well inside the tolerance
+    v = (v.float() * 0.5).to(torch.bfloat16)
+    o = K.flash_attention(gpu(q), gpu(k), gpu(v), 1.0, causal, Hq // Hkv)
+    ref = O.flash_attention(f32(q), f32(k), f32(v), 1.0, causal, Hq // Hkv)
+    assert_bf16_close(o, ref, what=f"sharp flash causal={causal}")
 
 
 def test_flash_attention_causal_row0_is_v0():
