@@ -33,10 +33,6 @@ constexpr float kNegBig = -1.0e30f;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-__device__ __forceinline__ int k_slot(int row, int chunk) { return row * kRowK + ((chunk ^ (row & 15)) << 3); }
-// Element offset of unit u of V^T row d (row = 64 keys).
-__device__ __forceinline__ int vt_unit(int d, int u) { return d * kKT + ((u ^ (d & 15)) << 2); }
-
 struct AttnParams {
   const bf16* q;
   const bf16* k;
@@ -52,96 +48,6 @@ struct AttnParams {
   const int* kv_lens;
   float* partial;  // decode workspace
   int max_chunks;
-};
-
-// Per-wave attention state over a 32-query column block.
-template <int D>
-struct WaveAttn {
-  static constexpr int KSTEPS = (D + 15) / 16;
-  static constexpr int OT = (D + 31) / 32;
-  bf16x8 qf[KSTEPS];
-  floatx16 o[OT];
-  float m, l;
-
-  __device__ __forceinline__ void init() {
-#pragma unroll
-    for (int t = 0; t < OT; ++t) o[t] = floatx16{};
-    m = kNegBig;
-    l = 0.f;
-  }
-  // Q row for this lane's query column (zero when absent).
-  __device__ __forceinline__ void load_q(const bf16* qrow, bool valid, int h) {
-#pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) {
-      const int d = ks * 16 + 8 * h;
-      qf[ks] = (valid && d < D) ? *reinterpret_cast<const bf16x8*>(qrow + d) : bf16x8{};
-    }
-  }
-  // One 64-key tile. kidx_base: key index of tile row 0; qidx: this lane's query
-  // index; klimit: keys >= klimit are masked; causal masks key > query.
-  __device__ __forceinline__ void tile(const bf16* sK, const bf16* sVt, int lane, int kidx_base, int qidx,
-                                       int klimit, bool causal, float scale_log2) {
-    const int l32 = lane & 31;
-    const int h = lane >> 5;
-    floatx16 s[2];
-#pragma unroll
-    for (int t2 = 0; t2 < 2; ++t2) {
-      s[t2] = floatx16{};
-#pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(sK + k_slot(t2 * 32 + l32, ks * 2 + h));
-        s[t2] = mfma32x32x16(a, qf[ks], s[t2]);
-      }
-    }
-    float mloc = kNegBig;
-#pragma unroll
-    for (int t2 = 0; t2 < 2; ++t2)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kidx_base + t2 * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        const bool masked = (key >= klimit) || (causal && key > qidx);
-        const float x = masked ? -INFINITY : s[t2][r] * scale_log2;
-        s[t2][r] = x;
-        mloc = fmaxf(mloc, x);
-      }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-    const float mnew = fmaxf(m, mloc);
-    const float alpha = fast_exp2(m - mnew);
-    float lsum = 0.f;
-#pragma unroll
-    for (int t2 = 0; t2 < 2; ++t2)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float pv = fast_exp2(s[t2][r] - mnew);
-        s[t2][r] = pv;
-        lsum += pv;
-      }
-    lsum += __shfl_xor(lsum, 32, 64);
-    l = l * alpha + lsum;
-    m = mnew;
-#pragma unroll
-    for (int t = 0; t < OT; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
-    bf16x8 pb[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-      for (int t = 0; t < 8; ++t) pb[j][t] = f2bf(s[j >> 1][(j & 1) * 8 + t]);
-    }
-#pragma unroll
-    for (int t = 0; t < OT; ++t) {
-      const int d = t * 32 + l32;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(sVt + vt_unit(d, 4 * j + h));
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(sVt + vt_unit(d, 4 * j + 2 + h));
-        u32x4 w = {lo[0], lo[1], hi[0], hi[1]};
-        const bf16x8 a = __builtin_bit_cast(bf16x8, w);
-        o[t] = mfma32x32x16(a, pb[j], o[t]);
-      }
-    }
-  }
 };
 
 // ----------------------------------------------------------------- prefill
@@ -368,82 +274,147 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 }
 
 // ----------------------------------------------------------------- decode
-constexpr int kDecKeys = 4 * kKT;  // keys per block (4 waves x 64)
+// One block = WPB waves over a chunk of WPB * 64 keys of one (sequence, KV
+// head); each wave owns one 64-key tile in wave-private LDS, filled by
+// direct-to-LDS loads (all 32 KB of K and V in flight at once, no staging
+// registers). The MFMA query columns are the GQA group's heads (G <= 32).
+//   K tile: 64 rows x 128, chunk c of row r at slot c ^ (r & 15) (as prefill).
+//   V tile: 64 rows x 128 in natural layout, chunk c of row r at slot
+//   c ^ ((r & 3) << 2). The PV A operand (V^T fragments) is read with
+//   ds_read_b64_tr_b16, which transposes within 16-lane groups: lane i of a
+//   group receives element i%4 of the 8-byte piece each lane 4r + i/4
+//   addressed, for r = 0..3. With lane 4r + q addressing V[key_r][d0 + 4q],
+//   lane i gets V[key_0..3][d0 + i]: four keys of its head-dim row.
+// The block merges its waves and writes one (m, l, O) partial per chunk; a
+// second kernel combines the chunks of each query head.
+constexpr int kDecWaves = 2;
+constexpr int kDecKeys = kDecWaves * kKT;  // keys per block
 
 // Partial layout per (b, kvh, chunk): m[G], l[G], O[G][D] (fp32), G = groups.
 __host__ __device__ inline int dec_partial_floats(int groups, int D) { return groups * (D + 2); }
 
-template <int D>
-__global__ __launch_bounds__(256) void flash_decode_kernel(const AttnParams p) {
-  constexpr int OT = WaveAttn<D>::OT;
-  constexpr int KW = kKT * kRowK;      // K tile elements per wave
-  constexpr int VW = OT * 32 * kKT;    // V^T tile elements per wave
-  __shared__ __attribute__((aligned(16))) bf16 lds[4 * (KW + VW)];
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef short short8v __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ short4v lds_read_tr16(const bf16* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (short4v __attribute__((address_space(3)))*)(reinterpret_cast<uintptr_t>(p)));
+}
+
+__device__ __forceinline__ int dec_v_off(int r, int c) { return r * kRowK + ((c ^ ((r & 3) << 2)) << 3); }
+
+template <int WPB>
+__global__ __launch_bounds__(64 * WPB) void flash_decode_kernel(const AttnParams p) {
+  constexpr int D = 128;
+  constexpr int KSTEPS = D / 16;
+  constexpr int OT = D / 32;
+  constexpr int TILE = kKT * kRowK;  // elements per K or V tile
+  __shared__ __attribute__((aligned(1024))) bf16 lds[WPB * 2 * TILE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31;
   const int h = lane >> 5;
   const int chunk = blockIdx.x;
   const int kvh = blockIdx.y % p.Hkv;
   const int b = blockIdx.y / p.Hkv;
   const int L = min(p.kv_lens[b], p.Sk);  // Sk = max_len: never read past the cache
-  const int kc0 = chunk * kDecKeys;
+  const int kc0 = chunk * (WPB * kKT);
   if (kc0 >= L) return;  // uniform per block
 
-  bf16* sK = lds + wave * KW;
-  bf16* sVt = lds + 4 * KW + wave * VW;
+  bf16* sK = lds + wave * 2 * TILE;
+  bf16* sV = sK + TILE;
   const int k0 = kc0 + wave * kKT;
+  const bool live = k0 < L;
   const bf16* kbase = p.k + (int64_t)b * p.kb + (int64_t)kvh * p.kh;
   const bf16* vbase = p.v + (int64_t)b * p.vb + (int64_t)kvh * p.vh;
-
-  // Wave-private stage of this wave's 64 keys.
-  {
-    constexpr int CHD = (D + 15) / 16 * 2;  // 16-byte chunks per K row incl. zero padding
-    for (int id = lane; id < kKT * CHD; id += 64) {
-      const int r = id / CHD, c = id % CHD;
-      const bool ok = (k0 + r < L) && (c * 8 < D);
-      const bf16x8 v = ok ? *reinterpret_cast<const bf16x8*>(kbase + (int64_t)(k0 + r) * p.ks + c * 8) : bf16x8{};
-      *reinterpret_cast<bf16x8*>(sK + k_slot(r, c)) = v;
+  if (live) {
+    const int ks2 = (int)p.ks * 2, vs2 = (int)p.vs * 2;  // host guarantees max_len * stride * 2 < 2^31
+    const __amdgpu_buffer_rsrc_t krs = q3::make_rsrc(kbase, (int64_t)(L - 1) * ks2 + D * 2);
+    const __amdgpu_buffer_rsrc_t vrs = q3::make_rsrc(vbase, (int64_t)(L - 1) * vs2 + D * 2);
+    const uint32_t lk = q3::lds_addr(sK), lv = q3::lds_addr(sV);
+    const int slot = lane & 15;
+#pragma unroll
+    for (int i = 0; i < kKT / 4; ++i) {
+      const int r = 4 * i + (lane >> 4);
+      const int kc = slot ^ (r & 15);
+      const int vc = slot ^ ((r & 3) << 2);
+      q3::dma16(krs, (uint32_t)((k0 + r) * ks2 + kc * 16), lk + i * 1024);
+      q3::dma16(vrs, (uint32_t)((k0 + r) * vs2 + vc * 16), lv + i * 1024);
     }
-    constexpr int VCH = D / 8;
-    for (int id = lane; id < 32 * VCH; id += 64) {
-      const int pp = id & 31, c = id >> 5;
-      bf16x8 v2[2];
+  }
+  const int G = p.groups;
+  const bool qvalid = l32 < G;
+  bf16x8 qf[KSTEPS];
+  {
+    const bf16* qrow = p.q + (int64_t)b * p.qb + (int64_t)(kvh * G + (qvalid ? l32 : 0)) * p.qh;
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int key = k0 + 2 * pp + e;
-        v2[e] = key < L ? *reinterpret_cast<const bf16x8*>(vbase + (int64_t)key * p.vs + c * 8) : bf16x8{};
+    for (int ks = 0; ks < KSTEPS; ++ks)
+      qf[ks] = qvalid ? *reinterpret_cast<const bf16x8*>(qrow + ks * 16 + 8 * h) : bf16x8{};
+  }
+  floatx16 o[OT];
+#pragma unroll
+  for (int t = 0; t < OT; ++t) o[t] = floatx16{};
+  float m = kNegBig, lsum = 0.f;
+  q3::vm_wait<0>();  // this wave's tiles have landed in its own LDS
+  if (live) {
+    floatx16 s0 = floatx16{}, s1 = floatx16{};
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(sK + fwd::k_off(l32, 2 * ks + h));
+      const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(sK + fwd::k_off(32 + l32, 2 * ks + h));
+      s0 = mfma32x32x16(a0, qf[ks], s0);
+      s1 = mfma32x32x16(a1, qf[ks], s1);
+    }
+    if (k0 + kKT > L) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = k0 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (key >= L) s0[r] = -INFINITY;
+        if (key + 32 >= L) s1[r] = -INFINITY;
       }
+    }
+    const float c = p.scale_log2;
+    float mloc = fmaxf(s0[0], s1[0]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int d = c * 8 + e;
-        uint32_t* dst = reinterpret_cast<uint32_t*>(sVt + vt_unit(d, pp >> 1)) + (pp & 1);
-        *dst = pack_bf16x2(v2[0][e], v2[1][e]);
+    for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, fmaxf(s0[r], s1[r]));
+    m = fwd::half_max(mloc) * c;  // finite: key k0 < L is live
+    bf16x8 pb[4];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p0 = fast_exp2(fmaf(s0[r], c, -m));
+      const float p1 = fast_exp2(fmaf(s1[r], c, -m));
+      lsum += p0 + p1;
+      pb[r >> 3][r & 7] = f2bf(p0);
+      pb[2 + (r >> 3)][r & 7] = f2bf(p1);
+    }
+    lsum += __shfl_xor(lsum, 32, 64);
+    // V^T fragments by transposed reads: lane (g16, r, q) addresses
+    // V[16 j + 4 h + r (+8)][32 t + 16 g16 + 4 q].
+    const int g16 = (lane >> 4) & 1, rr = (lane & 15) >> 2, qq = lane & 3;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int key = 16 * j + 4 * h + rr;
+#pragma unroll
+      for (int t = 0; t < OT; ++t) {
+        const int d = 32 * t + 16 * g16 + 4 * qq;
+        const short4v lo = lds_read_tr16(sV + dec_v_off(key, d >> 3) + (d & 7));
+        const short4v hi = lds_read_tr16(sV + dec_v_off(key + 8, d >> 3) + (d & 7));
+        const short8v a8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        o[t] = mfma32x32x16(__builtin_bit_cast(bf16x8, a8), pb[j], o[t]);
       }
     }
   }
-  __syncthreads();
 
-  WaveAttn<D> wa;
-  wa.init();
-  const int G = p.groups;
-  const int qcol = l32;  // query column = head within the GQA group
-  const bool qvalid = qcol < G;
-  const int hq = kvh * G + qcol;
-  wa.load_q(p.q + (int64_t)b * p.qb + (int64_t)(qvalid ? hq : 0) * p.qh, qvalid, h);
-  const bool live = k0 < L;
-  if (live) wa.tile(sK, sVt, lane, k0, 0, L, false, p.scale_log2);
-
-  // Merge the 4 waves through LDS (the K/V tiles are dead by now).
+  // Merge the block's waves through LDS (the tiles are dead by now).
   __syncthreads();
   const int PF = dec_partial_floats(G, D);
   float* red = reinterpret_cast<float*>(lds);
   float* rw = red + wave * PF;
   if (h == 0 && qvalid) {
-    rw[qcol] = live ? wa.m : kNegBig;
-    rw[G + qcol] = live ? wa.l : 0.f;
+    rw[l32] = live ? m : kNegBig;
+    rw[G + l32] = live ? lsum : 0.f;
   }
   if (qvalid) {
 #pragma unroll
@@ -451,17 +422,19 @@ __global__ __launch_bounds__(256) void flash_decode_kernel(const AttnParams p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int d = t * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        if (d < D) rw[2 * G + qcol * D + d] = live ? wa.o[t][r] : 0.f;
+        rw[2 * G + l32 * D + d] = live ? o[t][r] : 0.f;
       }
   }
   __syncthreads();
   float* out = p.partial + (((int64_t)b * p.Hkv + kvh) * p.max_chunks + chunk) * PF;
-  for (int idx = tid; idx < G * D + G; idx += 256) {
+  for (int idx = tid; idx < G * D + G; idx += 64 * WPB) {
     const int qc = idx < G ? idx : (idx - G) / D;
     float mm = kNegBig;
-    for (int w = 0; w < 4; ++w) mm = fmaxf(mm, red[w * PF + qc]);
+#pragma unroll
+    for (int w = 0; w < WPB; ++w) mm = fmaxf(mm, red[w * PF + qc]);
     float acc = 0.f;
-    for (int w = 0; w < 4; ++w) {
+#pragma unroll
+    for (int w = 0; w < WPB; ++w) {
       const float* r = red + w * PF;
       const float wgt = fast_exp2(r[qc] - mm);
       acc += (idx < G ? r[G + qc] : r[2 * G + (idx - G)]) * wgt;
@@ -475,7 +448,9 @@ __global__ __launch_bounds__(256) void flash_decode_kernel(const AttnParams p) {
   }
 }
 
-// Merge the chunk partials of one (b, query head): one wave each.
+// Wave per (sequence, query head): merges the chunk partials. Lanes first
+// reduce the chunk maxima and weights in parallel, then each lane owns D/64
+// output elements and walks the chunks.
 template <int D>
 __global__ __launch_bounds__(256) void flash_decode_combine(const AttnParams p) {
   const int lane = threadIdx.x & 63;
@@ -491,32 +466,37 @@ __global__ __launch_bounds__(256) void flash_decode_combine(const AttnParams p) 
   const int PF = dec_partial_floats(G, D);
   const float* base = p.partial + ((int64_t)b * p.Hkv + kvh) * p.max_chunks * PF;
   float mm = kNegBig;
-  for (int c = 0; c < nch; ++c) mm = fmaxf(mm, base[c * PF + qc]);
+  for (int c = lane; c < nch; c += 64) mm = fmaxf(mm, base[c * PF + qc]);
+  mm = wave_max(mm);
   float ll = 0.f;
+  for (int c = lane; c < nch; c += 64) ll += base[c * PF + G + qc] * fast_exp2(base[c * PF + qc] - mm);
+  ll = wave_sum(ll);
   constexpr int PER = (D + 63) / 64;
   float acc[PER] = {};
-  for (int c = 0; c < nch; ++c) {
-    const float* r = base + c * PF;
-    const float wgt = fast_exp2(r[qc] - mm);
-    ll += r[G + qc] * wgt;
+  for (int c0 = 0; c0 < nch; c0 += 64) {
+    const int cl = c0 + lane;
+    const float wl = cl < nch ? fast_exp2(base[cl * PF + qc] - mm) : 0.f;
+    const int n = min(64, nch - c0);
+#pragma unroll 4
+    for (int i = 0; i < n; ++i) {
+      const float wgt = __shfl(wl, i, 64);
+      const float* r = base + (c0 + i) * PF + 2 * G + qc * D;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int d = lane + 64 * i;
-      if (d < D) acc[i] += r[2 * G + qc * D + d] * wgt;
+      for (int e = 0; e < PER; ++e) {
+        const int d = lane + 64 * e;
+        if (d < D) acc[e] += r[d] * wgt;
+      }
     }
   }
   const float inv = ll > 0.f ? 1.0f / ll : 0.f;
   bf16* orow = p.o + (int64_t)b * p.ob + (int64_t)hq * p.oh;
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int d = lane + 64 * i;
-    if (d < D) orow[d] = f2bf(acc[i] * inv);
+  for (int e = 0; e < PER; ++e) {
+    const int d = lane + 64 * e;
+    if (d < D) orow[d] = f2bf(acc[e] * inv);
   }
 }
 
-// ----------------------------------------------------------------- generic (fp32)
-// Reference-accuracy path for fp32 tensors (and head dims the MFMA kernels do
-// not cover): one thread per query row, online softmax over all keys.
 template <typename T>
 __global__ __launch_bounds__(128) void flash_generic_kernel(const AttnParams p, int D, const int* kv_lens) {
   const int64_t row = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
@@ -701,12 +681,14 @@ int q3_decode_attention(const void* q, const void* k_cache, const void* v_cache,
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool aligned = q3_aligned(q, 16) && q3_aligned(k_cache, 16) && q3_aligned(v_cache, 16) &&
                        strides_aligned8(strides, 8);
-  if (dtype == Q3_BF16 && D == 128 && p.groups <= 32 && aligned) {
+  // The MFMA path addresses the cache with 32-bit buffer offsets.
+  if (dtype == Q3_BF16 && D == 128 && p.groups <= 32 && aligned && (max_len + 1) * strides[4] * 2 < 0x7fffffffLL &&
+      (max_len + 1) * strides[7] * 2 < 0x7fffffffLL) {
     Q3_REQUIRE(workspace != nullptr && workspace_bytes >= decode_ws_bytes(B, Hq, Hkv, max_len, D), Q3_ERR_WORKSPACE);
     p.partial = static_cast<float*>(workspace);
     p.max_chunks = (int)q3_cdiv(max_len, kDecKeys);
-    hipLaunchKernelGGL(flash_decode_kernel<128>, dim3((unsigned)p.max_chunks, (unsigned)(B * Hkv)), dim3(256), 0, st,
-                       p);
+    hipLaunchKernelGGL(flash_decode_kernel<kDecWaves>, dim3((unsigned)p.max_chunks, (unsigned)(B * Hkv)),
+                       dim3(64 * kDecWaves), 0, st, p);
     Q3_LAUNCH_CHECK();
     hipLaunchKernelGGL(flash_decode_combine<128>, dim3((unsigned)q3_cdiv(B * Hq, 4)), dim3(256), 0, st, p);
     Q3_LAUNCH_CHECK();
