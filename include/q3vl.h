@@ -55,6 +55,18 @@ int q3_matmul(const void* x, const void* w, const void* bias, const void* residu
               int64_t K, int64_t ldx, int64_t ldw, int64_t ldr, int64_t ldc, int dtype, void* workspace,
               int64_t workspace_bytes, void* stream);
 
+/* Several weight matrices over the same input in one launch: y[:, c_i + j] =
+ * x . w[i][j] (+ bias[i][j]) with c_i = n[0] + ... + n[i-1], 1 <= nseg <= 4,
+ * every w[i] (n[i], K) with row stride ldw. Replaces the three
+ * matmul_forward calls of CudaFullAttention's q/k/v projections
+ * (modules/attention.py:82-84, csrc/matmul_op.cpp:12) with one GEMM over the
+ * stacked weights, without copying them. bias may be null, or hold null
+ * entries. Workspace: q3_matmul_segments_workspace_bytes. */
+int64_t q3_matmul_segments_workspace_bytes(int64_t M, const int64_t* n, int64_t nseg, int64_t K, int dtype);
+int q3_matmul_segments(const void* x, const void* const* w, const void* const* bias, const int64_t* n, int64_t nseg,
+                       void* y, int64_t M, int64_t K, int64_t ldx, int64_t ldw, int64_t ldc, int dtype,
+                       void* workspace, int64_t workspace_bytes, void* stream);
+
 /* y[m, n] = silu(x . w_gate[n]) * (x . w_up[n]). Fuses the gate/up projections
  * and swiglu_forward (csrc/swiglu_op.cpp:9) of CudaSwiGLUMLP
  * (modules/mlp.py:19-22). */

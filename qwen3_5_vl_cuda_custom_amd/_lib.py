@@ -30,6 +30,8 @@ _SIGS: dict[str, tuple] = {
     "q3_matmul_workspace_bytes": (c_int64, [_I, _I, _I, c_int, c_int]),
     "q3_matmul": (c_int, [_V, _V, _V, _V, _V, _I, _I, _I, _I, _I, _I, _I, c_int, _V, _I, _V]),
     "q3_matmul_swiglu": (c_int, [_V, _V, _V, _V, _I, _I, _I, _I, _I, _I, c_int, _V, _I, _V]),
+    "q3_matmul_segments_workspace_bytes": (c_int64, [_I, _i64p, _I, _I, c_int]),
+    "q3_matmul_segments": (c_int, [_V, _V, _V, _i64p, _I, _V, _I, _I, _I, _I, _I, c_int, _V, _I, _V]),
     "q3_batched_gemm": (c_int, [_V, _V, _V, _I, _I, _I, _I, c_int, _V]),
     "q3_residual_add": (c_int, [_V, _V, _V, _I, c_int, _V]),
     "q3_swiglu": (c_int, [_V, _V, _V, _I, c_int, _V]),
@@ -96,6 +98,11 @@ def call(name: str, *args) -> None:
 
 def i64s(*vals) -> ctypes.Array:
     return (c_int64 * len(vals))(*[int(v) for v in vals])
+
+
+def ptrs(*ts) -> ctypes.Array:
+    """A C array of device pointers (NULL for None)."""
+    return (c_void_p * len(ts))(*[None if t is None else t.data_ptr() for t in ts])
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

@@ -448,52 +448,60 @@ __global__ __launch_bounds__(64 * WPB) void flash_decode_kernel(const AttnParams
   }
 }
 
-// Wave per (sequence, query head): merges the chunk partials. Lanes first
-// reduce the chunk maxima and weights in parallel, then each lane owns D/64
-// output elements and walks the chunks.
+// Block per (sequence, KV head): merges the chunk partials of the G query
+// heads of the group. The chunk maxima and weights go through LDS (one pass
+// over m and l), then each thread owns output elements (head, d) and sums
+// the chunks' O rows, 8 chunks' loads in flight at a time.
+constexpr int kCombineMaxChunks = 256;  // LDS budget for the per-chunk weights
 template <int D>
 __global__ __launch_bounds__(256) void flash_decode_combine(const AttnParams p) {
-  const int lane = threadIdx.x & 63;
-  const int64_t gw = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
-  if (gw >= (int64_t)p.B * p.Hq) return;
-  const int b = (int)(gw / p.Hq);
-  const int hq = (int)(gw % p.Hq);
-  const int kvh = hq / p.groups;
-  const int qc = hq % p.groups;
+  __shared__ float s_w[kCombineMaxChunks * 4];
+  __shared__ float s_inv[32];
+  const int tid = threadIdx.x;
+  const int kvh = blockIdx.x % p.Hkv;
+  const int b = blockIdx.x / p.Hkv;
   const int L = min(p.kv_lens[b], p.Sk);
   const int nch = (L + kDecKeys - 1) / kDecKeys;
   const int G = p.groups;
   const int PF = dec_partial_floats(G, D);
   const float* base = p.partial + ((int64_t)b * p.Hkv + kvh) * p.max_chunks * PF;
-  float mm = kNegBig;
-  for (int c = lane; c < nch; c += 64) mm = fmaxf(mm, base[c * PF + qc]);
-  mm = wave_max(mm);
-  float ll = 0.f;
-  for (int c = lane; c < nch; c += 64) ll += base[c * PF + G + qc] * fast_exp2(base[c * PF + qc] - mm);
-  ll = wave_sum(ll);
-  constexpr int PER = (D + 63) / 64;
-  float acc[PER] = {};
-  for (int c0 = 0; c0 < nch; c0 += 64) {
-    const int cl = c0 + lane;
-    const float wl = cl < nch ? fast_exp2(base[cl * PF + qc] - mm) : 0.f;
-    const int n = min(64, nch - c0);
-#pragma unroll 4
-    for (int i = 0; i < n; ++i) {
-      const float wgt = __shfl(wl, i, 64);
-      const float* r = base + (c0 + i) * PF + 2 * G + qc * D;
-#pragma unroll
-      for (int e = 0; e < PER; ++e) {
-        const int d = lane + 64 * e;
-        if (d < D) acc[e] += r[d] * wgt;
+  // Heads are handled GH at a time so that the weights of all chunks fit in LDS.
+  const int GH = max(1, min(G, kCombineMaxChunks * 4 / max(nch, 1)));
+  for (int g0 = 0; g0 < G; g0 += GH) {
+    const int gn = min(GH, G - g0);
+    // Per head: max over chunks, then weights w_c = 2^(m_c - max) and 1 / sum(l_c w_c).
+    // One wave per head (4 waves per pass).
+    for (int gg = tid >> 6; gg < gn; gg += 4) {
+      const int lane = tid & 63, qc = g0 + gg;
+      float mm = kNegBig;
+      for (int c = lane; c < nch; c += 64) mm = fmaxf(mm, base[(int64_t)c * PF + qc]);
+      mm = wave_max(mm);
+      float ll = 0.f;
+      for (int c = lane; c < nch; c += 64) {
+        const float w = fast_exp2(base[(int64_t)c * PF + qc] - mm);
+        s_w[gg * nch + c] = w;
+        ll += base[(int64_t)c * PF + G + qc] * w;
       }
+      ll = wave_sum(ll);
+      if (lane == 0) s_inv[gg] = ll > 0.f ? 1.0f / ll : 0.f;
     }
-  }
-  const float inv = ll > 0.f ? 1.0f / ll : 0.f;
-  bf16* orow = p.o + (int64_t)b * p.ob + (int64_t)hq * p.oh;
+    __syncthreads();
+    for (int e = tid; e < gn * D; e += 256) {
+      const int gg = e / D, d = e % D, qc = g0 + gg;
+      const float* src = base + 2 * G + qc * D + d;
+      float acc = 0.f;
+      int c = 0;
+      for (; c + 8 <= nch; c += 8) {
+        float v[8];
 #pragma unroll
-  for (int e = 0; e < PER; ++e) {
-    const int d = lane + 64 * e;
-    if (d < D) orow[d] = f2bf(acc[e] * inv);
+        for (int i = 0; i < 8; ++i) v[i] = src[(int64_t)(c + i) * PF];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc += v[i] * s_w[gg * nch + c + i];
+      }
+      for (; c < nch; ++c) acc += src[(int64_t)c * PF] * s_w[gg * nch + c];
+      p.o[(int64_t)b * p.ob + (int64_t)(kvh * G + qc) * p.oh + d] = f2bf(acc * s_inv[gg]);
+    }
+    __syncthreads();
   }
 }
 
@@ -690,7 +698,7 @@ int q3_decode_attention(const void* q, const void* k_cache, const void* v_cache,
     hipLaunchKernelGGL(flash_decode_kernel<kDecWaves>, dim3((unsigned)p.max_chunks, (unsigned)(B * Hkv)),
                        dim3(64 * kDecWaves), 0, st, p);
     Q3_LAUNCH_CHECK();
-    hipLaunchKernelGGL(flash_decode_combine<128>, dim3((unsigned)q3_cdiv(B * Hq, 4)), dim3(256), 0, st, p);
+    hipLaunchKernelGGL(flash_decode_combine<128>, dim3((unsigned)(B * Hkv)), dim3(256), 0, st, p);
     Q3_LAUNCH_CHECK();
     return Q3_OK;
   }

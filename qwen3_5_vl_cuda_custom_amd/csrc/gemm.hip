@@ -21,6 +21,7 @@ using namespace q3;
 namespace {
 
 constexpr int kSkinnyWaves = 4;
+constexpr int kSkinnyUnroll = 2;  // k steps per wave iteration (loads in flight)
 
 struct SkinnyParams {
   const bf16* X;    // (M <= 32, K)
@@ -34,17 +35,26 @@ struct SkinnyParams {
   int64_t ldx, ldw, ldr, ldc;
   int ksplit;
   int k_per_split;  // multiple of 64*kSkinnyWaves except possibly the last
+  WeightSegments seg;  // stacked weights (plain store only); starts are multiples of 32
 };
 
+// Bias of output column n, re-based like the weights of its segment.
+__device__ __forceinline__ const bf16* skinny_bias(const SkinnyParams& p, int n) {
+  if (p.seg.n <= 1) return p.bias;
+  const int s = segment_of(p.seg, n);
+  return p.seg.b[s] ? p.seg.b[s] - p.seg.start[s] : nullptr;
+}
+
 template <bool SWIGLU>
-__device__ __forceinline__ void skinny_epilogue(const SkinnyParams& p, int m, int n, float g, float u) {
+__device__ __forceinline__ void skinny_epilogue(const SkinnyParams& p, const bf16* bias, int m, int n, float g,
+                                                float u) {
   if (m >= p.M || n >= p.N) return;
   float v;
   if constexpr (SWIGLU) {
     v = g / (1.0f + __expf(-g)) * u;
   } else {
     v = g;
-    if (p.bias) v += bf2f(p.bias[n]);
+    if (bias) v += bf2f(bias[n]);
     if (p.R) v += bf2f(p.R[(int64_t)m * p.ldr + n]);
   }
   p.C[(int64_t)m * p.ldc + n] = f2bf(v);
@@ -66,10 +76,20 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Sk
   const int kb = split * p.k_per_split;
   const int ke = min(p.K, kb + p.k_per_split);
 
+  // Stacked weights: re-base W so that column n addresses row n of its segment.
+  const bf16* Wp = p.W;
+  int n_base = 0, n_lim = p.N;
+  if (!SWIGLU && p.seg.n > 1) {
+    const int s = segment_of(p.seg, n0);
+    n_base = p.seg.start[s];
+    n_lim = s + 1 < p.seg.n ? p.seg.start[s + 1] : p.N;
+    Wp = p.seg.w[s] - (int64_t)n_base * p.ldw;
+  }
+  const bf16* bias = skinny_bias(p, n0);
   const int n = n0 + l32;
-  const bool nvalid = n < p.N;
+  const bool nvalid = n < n_lim;
   const bool mvalid = l32 < p.M;
-  const bf16* wrow = p.W + (int64_t)(nvalid ? n : 0) * p.ldw;
+  const bf16* wrow = Wp + (int64_t)(nvalid ? n : n_base) * p.ldw;
   const bf16* wrow2 = SWIGLU ? p.W2 + (int64_t)(nvalid ? n : 0) * p.ldw : nullptr;
   const bf16* xrow = p.X + (int64_t)(mvalid ? l32 : 0) * p.ldx;
 
@@ -77,23 +97,30 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Sk
 #pragma unroll
   for (int a = 0; a < NACC; ++a) acc[a] = floatx16{};
 
-  // Wave w handles steps w, w + 4, w + 8, ... of 64 elements in [kb, ke).
-  for (int k = kb + wave * 64; k < ke; k += 64 * kSkinnyWaves) {
-    const int kk = k + 32 * h;
-    bf16x8 wa[4], wb[4], xb[4];
+  // Wave w handles steps w, w + 4, w + 8, ... of 64 elements in [kb, ke),
+  // kSkinnyUnroll steps per iteration with all their loads issued up front.
+  constexpr int U = kSkinnyUnroll;
+  for (int k = kb + wave * 64; k < ke; k += 64 * kSkinnyWaves * U) {
+    bf16x8 wa[U][4], wb[U][4], xb[U][4];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int kv = kk + 8 * v;
-      const bool kin = kv < ke;
-      wa[v] = (nvalid && kin) ? *reinterpret_cast<const bf16x8*>(wrow + kv) : bf16x8{};
-      if constexpr (SWIGLU) wb[v] = (nvalid && kin) ? *reinterpret_cast<const bf16x8*>(wrow2 + kv) : bf16x8{};
-      xb[v] = (mvalid && kin) ? *reinterpret_cast<const bf16x8*>(xrow + kv) : bf16x8{};
+    for (int u = 0; u < U; ++u) {
+      const int kk = k + u * 64 * kSkinnyWaves + 32 * h;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int kv = kk + 8 * v;
+        const bool kin = kv < ke;
+        wa[u][v] = (nvalid && kin) ? *reinterpret_cast<const bf16x8*>(wrow + kv) : bf16x8{};
+        if constexpr (SWIGLU) wb[u][v] = (nvalid && kin) ? *reinterpret_cast<const bf16x8*>(wrow2 + kv) : bf16x8{};
+        xb[u][v] = (mvalid && kin) ? *reinterpret_cast<const bf16x8*>(xrow + kv) : bf16x8{};
+      }
     }
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      acc[0] = mfma32x32x16(wa[v], xb[v], acc[0]);
-      if constexpr (SWIGLU) acc[1] = mfma32x32x16(wb[v], xb[v], acc[1]);
-    }
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        acc[0] = mfma32x32x16(wa[u][v], xb[u][v], acc[0]);
+        if constexpr (SWIGLU) acc[1] = mfma32x32x16(wb[u][v], xb[u][v], acc[1]);
+      }
   }
 
   // Cross-wave reduction through LDS. Register r of lane l holds output
@@ -121,7 +148,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Sk
       for (int w = 0; w < kSkinnyWaves; ++w) s[a] += red[w][a][nn * 33 + m];
     }
     if (p.ksplit == 1) {
-      skinny_epilogue<SWIGLU>(p, m, n0 + nn, s[0], NACC > 1 ? s[NACC - 1] : 0.f);
+      skinny_epilogue<SWIGLU>(p, bias, m, n0 + nn, s[0], NACC > 1 ? s[NACC - 1] : 0.f);
     } else {
       const int ncols = p.N * NACC;
       float* dst = p.partial + ((int64_t)split * 32 + m) * ncols;
@@ -145,7 +172,7 @@ __global__ void gemm_skinny_finalize(const SkinnyParams p) {
       s[0] += src[n];
       if (SWIGLU) s[1] += src[p.N + n];
     }
-    skinny_epilogue<SWIGLU>(p, m, n, s[0], s[1]);
+    skinny_epilogue<SWIGLU>(p, skinny_bias(p, n), m, n, s[0], s[1]);
   }
 }
 
@@ -350,9 +377,95 @@ int matmul_impl(const void* x, const void* w, const void* w2, const void* bias, 
   return swiglu ? launch_tiled<kEpiSwiGLU>(p, batch, st) : launch_tiled<kEpiStore>(p, batch, st);
 }
 
+int segments_impl(const void* x, const void* const* w, const void* const* bias, const int64_t* n, int64_t nseg,
+                  void* y, int64_t M, int64_t K, int64_t ldx, int64_t ldw, int64_t ldc, int dtype, void* ws,
+                  int64_t ws_bytes, hipStream_t st) {
+  Q3_REQUIRE(x && w && n && y, Q3_ERR_NULL);
+  Q3_REQUIRE(nseg >= 1 && nseg <= 4, Q3_ERR_SHAPE);
+  int64_t N = 0;
+  bool tiled_ok = true, skinny_ok = true;
+  for (int64_t i = 0; i < nseg; ++i) {
+    Q3_REQUIRE(w[i], Q3_ERR_NULL);
+    Q3_REQUIRE(n[i] >= 0, Q3_ERR_SHAPE);
+    tiled_ok = tiled_ok && (N % 256 == 0) && bf16_rows_ok(w[i], ldw, K);
+    skinny_ok = skinny_ok && (N % 32 == 0) && bf16_rows_ok(w[i], ldw, K);
+    N += n[i];
+  }
+  Q3_REQUIRE(M >= 0 && K >= 0 && N < (1ll << 31) && ldx >= K && ldw >= K && ldc >= N, Q3_ERR_SHAPE);
+  Q3_REQUIRE(dtype == Q3_F32 || dtype == Q3_BF16, Q3_ERR_DTYPE);
+  if (M == 0 || N == 0) return Q3_OK;
+  const bool one = dtype == Q3_BF16 && K > 0 && bf16_rows_ok(x, ldx, K) && (M <= 32 ? skinny_ok : tiled_ok);
+  if (!one || nseg == 1) {
+    // One launch per segment, into its column slice of y.
+    const size_t esz = dtype == Q3_BF16 ? 2 : 4;
+    int64_t col = 0;
+    for (int64_t i = 0; i < nseg; ++i) {
+      const int rc = matmul_impl(x, w[i], nullptr, bias ? bias[i] : nullptr, nullptr,
+                                 static_cast<char*>(y) + col * esz, M, n[i], K, 1, ldx, ldw, 0, ldc, 0, 0, 0, dtype,
+                                 false, ws, ws_bytes, st);
+      if (rc != Q3_OK) return rc;
+      col += n[i];
+    }
+    return Q3_OK;
+  }
+  WeightSegments seg{};
+  seg.n = (int)nseg;
+  int64_t col = 0;
+  for (int64_t i = 0; i < nseg; ++i) {
+    seg.start[i] = (int)col;
+    seg.w[i] = static_cast<const bf16*>(w[i]);
+    seg.b[i] = bias ? static_cast<const bf16*>(bias[i]) : nullptr;
+    col += n[i];
+  }
+  if (M <= 32) {
+    SkinnyParams sp{};
+    sp.X = static_cast<const bf16*>(x);
+    sp.W = seg.w[0];
+    sp.C = static_cast<bf16*>(y);
+    sp.M = (int)M;
+    sp.N = (int)N;
+    sp.K = (int)K;
+    sp.ldx = ldx;
+    sp.ldw = ldw;
+    sp.ldc = ldc;
+    sp.seg = seg;
+    return launch_skinny<false>(sp, ws, ws_bytes, st);
+  }
+  GemmParams p{};
+  p.X = static_cast<const bf16*>(x);
+  p.W = seg.w[0];
+  p.C = static_cast<bf16*>(y);
+  p.M = (int)M;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.ldx = ldx;
+  p.ldw = ldw;
+  p.ldc = ldc;
+  p.seg = seg;
+  return launch_tiled<kEpiStore>(p, 1, st);
+}
+
 }  // namespace
 
 extern "C" {
+
+int64_t q3_matmul_segments_workspace_bytes(int64_t M, const int64_t* n, int64_t nseg, int64_t K, int dtype) {
+  if (!n || nseg < 1 || nseg > 4 || dtype != Q3_BF16 || M > 32 || M <= 0 || K <= 0) return 0;
+  int64_t N = 0, need = 0;
+  for (int64_t i = 0; i < nseg; ++i) {
+    if (n[i] <= 0) continue;
+    N += n[i];
+    need = std::max(need, skinny_workspace_bytes(n[i], K, false));
+  }
+  return N > 0 ? std::max(need, skinny_workspace_bytes(N, K, false)) : 0;
+}
+
+int q3_matmul_segments(const void* x, const void* const* w, const void* const* bias, const int64_t* n, int64_t nseg,
+                       void* y, int64_t M, int64_t K, int64_t ldx, int64_t ldw, int64_t ldc, int dtype,
+                       void* workspace, int64_t workspace_bytes, void* stream) {
+  return segments_impl(x, w, bias, n, nseg, y, M, K, ldx, ldw, ldc, dtype, workspace, workspace_bytes,
+                       static_cast<hipStream_t>(stream));
+}
 
 int64_t q3_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int dtype, int swiglu) {
   if (dtype != Q3_BF16 || M > 32 || M <= 0 || N <= 0 || K <= 0) return 0;

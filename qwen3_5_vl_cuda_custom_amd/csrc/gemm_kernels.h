@@ -12,6 +12,33 @@ enum Epilogue : int {
   kEpiRowScale = 2,  // C = bf16(bf16(acc) * s[m])  (MoE expert output x routing weight)
 };
 
+// Up to 4 weight matrices stacked along N and computed in one launch (the
+// q/k/v projections of one input): segment i covers output columns
+// [start[i], start[i+1]) (the last one up to N), rows of w[i], bias b[i] (or
+// null). n <= 1: the plain W / bias of the params.
+struct WeightSegments {
+  int n;
+  int start[4];
+  const bf16* w[4];
+  const bf16* b[4];
+};
+
+template <typename T>
+__device__ __forceinline__ const T* uniform_ptr(const T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<const T*>(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ int segment_of(const WeightSegments& s, int col) {
+  int i = 0;
+#pragma unroll
+  for (int j = 1; j < 4; ++j)
+    if (j < s.n && col >= s.start[j]) i = j;
+  return i;
+}
+
 struct GemmParams {
   const bf16* X;     // (M, K) rows, ld = ldx
   const bf16* W;     // (N, K) rows, ld = ldw  (gate weight for SwiGLU)
@@ -31,6 +58,7 @@ struct GemmParams {
   const int* group_end;   // per expert: end row (exclusive) in the sorted order
   const int* n_tiles_total;  // device scalar: number of valid m-tiles
   int64_t expert_stride_w;   // elements between consecutive experts' weights
+  WeightSegments seg;        // dense (non-grouped, batch 1) store epilogue only
 };
 
 template <int BM, int BN, int WM, int WN, int EPI, bool GROUPED>
@@ -91,6 +119,26 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_kernel(const GemmParams
   }
   const int rows_m = m_end - m_begin;
   const int n0_out = tile_n * BN_OUT;
+  // Stacked weights: a tile never straddles segments (the host checks that
+  // every segment start is a multiple of BN). W and bias are re-based so that
+  // output column n still addresses row n.
+  int n_lim = p.N;
+  const bf16* bias = p.bias;
+  if constexpr (!GROUPED && EPI == kEpiStore) {
+    if (p.seg.n > 1) {
+      // Constant-index selects keep the segment's pointers in scalar registers
+      // (a dynamic index into the by-value params would go through memory and
+      // make the buffer resource per-lane).
+      const int s = __builtin_amdgcn_readfirstlane(segment_of(p.seg, n0_out));
+      const bf16* sw = s == 0 ? p.seg.w[0] : s == 1 ? p.seg.w[1] : s == 2 ? p.seg.w[2] : p.seg.w[3];
+      const bf16* sb = s == 0 ? p.seg.b[0] : s == 1 ? p.seg.b[1] : s == 2 ? p.seg.b[2] : p.seg.b[3];
+      const int st0 = s == 0 ? p.seg.start[0] : s == 1 ? p.seg.start[1] : s == 2 ? p.seg.start[2] : p.seg.start[3];
+      const int nxt = s == 0 ? p.seg.start[1] : s == 1 ? p.seg.start[2] : p.seg.start[3];
+      W = uniform_ptr(sw - (int64_t)st0 * p.ldw);
+      bias = sb ? uniform_ptr(sb - st0) : nullptr;
+      n_lim = s + 1 < p.seg.n ? nxt : p.N;
+    }
+  }
 
   constexpr int kStage = (BM + BN) * kBK;
   // Register staging: thread t owns 16-byte chunks t + i*NT of the X tile
@@ -125,11 +173,11 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_kernel(const GemmParams
     } else {
       n = n0_out + r;
     }
-    woff[i] = n < p.N ? (uint32_t)((int64_t)n * ldw * 2) : kOOB;
+    woff[i] = n < n_lim ? (uint32_t)((int64_t)n * ldw * 2) : kOOB;
   }
   const __amdgpu_buffer_rsrc_t rx =
       make_rsrc(X, p.gather ? (int64_t)p.M_src * ldx * 2 : (int64_t)(m_begin + rows_m) * ldx * 2);
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(W, (int64_t)p.N * ldw * 2);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(W, (int64_t)n_lim * ldw * 2);
   const __amdgpu_buffer_rsrc_t rw2 = make_rsrc(EPI == kEpiSwiGLU ? W2 : W, (int64_t)p.N * ldw * 2);
 
   struct Stage {
@@ -149,7 +197,11 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_kernel(const GemmParams
       const int k = k0 + (id % kChunks) * 8;
       const uint32_t off = (k < K && woff[i] != kOOB) ? woff[i] + (uint32_t)k * 2u : kOOB;
       if constexpr (EPI == kEpiSwiGLU) {
-        st.w[i] = buffer_load16((((id / kChunks) >> 5) & 1) ? rw2 : rw, off);
+        // The 64 chunks of a wave lie in 16 consecutive rows, all of one
+        // 32-row gate or up group: the choice is wave-uniform, so the buffer
+        // resource stays scalar (no per-lane selection loop).
+        const bool up = (((wave * 64 + i * NT) / kChunks) >> 5) & 1;
+        st.w[i] = buffer_load16(up ? rw2 : rw, off);
       } else {
         st.w[i] = buffer_load16(rw, off);
       }
@@ -251,8 +303,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_kernel(const GemmParams
 #pragma unroll
           for (int q = 0; q < 4; ++q) o[q] = acc.c[i][j][4 * g + q];
           if (vec_ok && n + 3 < N) {
-            if (p.bias) {
-              const bf16x4 b = *reinterpret_cast<const bf16x4*>(p.bias + n);
+            if (bias) {
+              const bf16x4 b = *reinterpret_cast<const bf16x4*>(bias + n);
 #pragma unroll
               for (int q = 0; q < 4; ++q) o[q] += bf2f(b[q]);
             }
@@ -272,7 +324,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_kernel(const GemmParams
             for (int q = 0; q < 4; ++q) {
               if (n + q >= N) continue;
               float v = o[q];
-              if (p.bias) v += bf2f(p.bias[n + q]);
+              if (bias) v += bf2f(bias[n + q]);
               if (p.R) v += bf2f(p.R[(int64_t)m * p.ldr + n + q]);
               if constexpr (EPI == kEpiRowScale) v = bf2f(f2bf(v)) * rs;
               crow[n + q] = f2bf(v);

@@ -63,3 +63,40 @@ def matmul_swiglu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor) -> 
     _lib.call("q3_matmul_swiglu", x2.data_ptr(), wg.data_ptr(), wu.data_ptr(), y.data_ptr(), M, N, K,
               x2.stride(0), wg.stride(0), N, dt, _lib.ptr(ws), nws, _lib.stream())
     return y
+
+
+def matmul_segments(x: torch.Tensor, weights, biases=None, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Y = X·[W_0; W_1; ...]ᵀ (+ [b_0; b_1; ...]) over up to 4 weights in one GEMM.
+
+    The weights are not concatenated: the kernel picks each output tile's
+    weight matrix (q/k/v projections of modules/attention.py:82-84 in one
+    launch). Returns (..., ΣN_i); the segment outputs are its column slices.
+    """
+    weights = list(weights)
+    biases = list(biases) if biases is not None else [None] * len(weights)
+    if not 1 <= len(weights) <= 4 or len(biases) != len(weights):
+        raise ValueError("matmul_segments: 1 to 4 weights, one bias (or None) each")
+    check("matmul_segments", x, *weights, *biases)
+    K = x.shape[-1]
+    ws_ = [w if w.stride(-1) == 1 and w.stride(0) == K else w.contiguous() for w in weights]
+    for w, b in zip(ws_, biases):
+        if w.dim() != 2 or w.shape[1] != K:
+            raise ValueError(f"matmul_segments: weight {tuple(w.shape)} does not match x (..., {K})")
+        if b is not None and b.shape != (w.shape[0],):
+            raise ValueError(f"matmul_segments: bias {tuple(b.shape)} != ({w.shape[0]},)")
+    bs = [b.contiguous() if b is not None else None for b in biases]
+    ns = [w.shape[0] for w in ws_]
+    N = sum(ns)
+    x2 = x.reshape(-1, K)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    M = x2.shape[0]
+    y = out if out is not None else torch.empty((*x.shape[:-1], N), dtype=x.dtype, device=x.device)
+    y2 = y.view(-1, N)
+    dt = _lib.dtype_code(x.dtype)
+    n_arr = _lib.i64s(*ns)
+    ws, nws = _lib.workspace(_lib.lib().q3_matmul_segments_workspace_bytes(M, n_arr, len(ns), K, dt), x.device)
+    _lib.call("q3_matmul_segments", x2.data_ptr(), _lib.ptrs(*ws_),
+              _lib.ptrs(*bs) if any(b is not None for b in bs) else None, n_arr, len(ns), y2.data_ptr(), M, K,
+              x2.stride(0), K, y2.stride(0), dt, _lib.ptr(ws), nws, _lib.stream())
+    return y

@@ -1,6 +1,7 @@
 """nn.Module drop-ins with the reference's class names, parameter names and shapes
 (reference modules/__init__.py:1-28), running on libq3vl.so kernels."""
 from .attention import CudaFullAttention, CudaVisionAttention
+from .graph import StepGraph
 from .kv_cache import StaticKVCache
 from .linear import CudaLinear
 from .mlp import CudaSwiGLUMLP, CudaVisionMLP
@@ -27,4 +28,5 @@ __all__ = [
     "CudaVisionBlock",
     "CudaVisionPatchEmbed",
     "StaticKVCache",
+    "StepGraph",
 ]

@@ -4,7 +4,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from ..kernels import apply_rope, decode_attention, flash_attention, qk_norm_rope
+from ..kernels import apply_rope, decode_attention, flash_attention, matmul_segments, qk_norm_rope
 from .kv_cache import StaticKVCache
 from .linear import CudaLinear
 from .norms import CudaRMSNorm
@@ -76,9 +76,13 @@ class CudaFullAttention(nn.Module):
                 kv_cache: StaticKVCache | None = None, residual: torch.Tensor | None = None):
         B, S, _ = x.shape
         Hq, Hkv, D = self.num_heads, self.num_kv_heads, self.head_dim
-        q = self.q_proj(x).view(B, S, Hq, D)
-        k = self.k_proj(x).view(B, S, Hkv, D)
-        v = self.v_proj(x).view(B, S, Hkv, D)
+        # q/k/v projections in one GEMM over the three weights (no concatenated
+        # copy); q, k, v are column views of its output.
+        qkv = matmul_segments(x, (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight),
+                              (self.q_proj.bias, self.k_proj.bias, self.v_proj.bias))
+        q = qkv[..., :Hq * D].view(B, S, Hq, D)
+        k = qkv[..., Hq * D:(Hq + Hkv) * D].view(B, S, Hkv, D)
+        v = qkv[..., (Hq + Hkv) * D:].view(B, S, Hkv, D)
         o = torch.empty((B, S, Hq, D), dtype=x.dtype, device=x.device)
 
         if kv_cache is not None:

@@ -1,0 +1,44 @@
+"""HIP-graph capture of a stream-ordered step (one decode token through the layers).
+
+The reference runs its per-token decode step eagerly from Python
+(models/dense.py:123-162): every op is a separate host launch, so at batch 32
+the step is bound by launch overhead rather than by HBM. Every kernel of this
+package is stream-ordered, allocation-free inside the C-ABI and free of host
+synchronisation on the decode path, so a whole step can be captured once and
+replayed as one graph launch.
+
+Rules for a captured step:
+  * inputs are static device tensors, updated in place between replays
+    (token hidden states, int32 positions for `MRoPEBinding`, KV-cache lengths);
+  * the step's outputs are the same tensors on every replay (`StepGraph.out`);
+  * workspaces the wrappers allocate during capture live in the graph's pool
+    for as long as the `StepGraph` does.
+"""
+from __future__ import annotations
+
+from typing import Any, Callable
+
+import torch
+
+
+class StepGraph:
+    """Capture `fn()` (after `warmup` eager runs on a side stream) and replay it."""
+
+    def __init__(self, fn: Callable[[], Any], warmup: int = 2) -> None:
+        if not torch.cuda.is_available():
+            raise RuntimeError("StepGraph needs a GPU")
+        self.fn = fn
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                fn()
+        torch.cuda.current_stream().wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.out = fn()
+
+    def replay(self) -> Any:
+        """Launch the captured step on the current stream; returns the static outputs."""
+        self.graph.replay()
+        return self.out

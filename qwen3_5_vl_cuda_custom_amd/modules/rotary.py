@@ -42,6 +42,9 @@ class MRoPEBinding:
         self._pos32: torch.Tensor | None = None
 
     def positions_int32(self, device: torch.device) -> torch.Tensor:
+        """(3, B, S) int32 positions on `device`. An int32 contiguous device tensor
+        passed at construction is used as is, so in-place updates of it reach
+        the kernels (a captured decode step reads its positions from there)."""
         if self._pos32 is None or self._pos32.device != device:
             self._pos32 = self.position_ids.to(device=device, dtype=torch.int32).contiguous()
         return self._pos32

@@ -63,6 +63,24 @@ def test_matmul_validation():
     assert L.q3_matmul(FAKE, FAKE, None, None, FAKE, 0, 4, 4, 4, 4, 0, 4, 1, None, 0, None) == 0  # empty: no-op
 
 
+def test_matmul_segments_validation():
+    import ctypes
+    ns = _lib.i64s(4096, 1024, 1024)
+    ws3 = (ctypes.c_void_p * 3)(FAKE, FAKE, FAKE)
+    assert L.q3_matmul_segments(FAKE, ws3, None, ns, 0, FAKE, 8, 4096, 4096, 4096, 6144, 1, None, 0, None) == -2
+    assert L.q3_matmul_segments(FAKE, ws3, None, ns, 5, FAKE, 8, 4096, 4096, 4096, 6144, 1, None, 0, None) == -2
+    assert L.q3_matmul_segments(FAKE, None, None, ns, 3, FAKE, 8, 4096, 4096, 4096, 6144, 1, None, 0, None) == -1
+    holes = (ctypes.c_void_p * 3)(FAKE, None, FAKE)
+    assert L.q3_matmul_segments(FAKE, holes, None, ns, 3, FAKE, 8, 4096, 4096, 4096, 6144, 1, None, 0, None) == -1
+    assert L.q3_matmul_segments(FAKE, ws3, None, ns, 3, FAKE, 8, 4096, 4096, 4096, 6000, 1, None, 0, None) == -2
+    assert L.q3_matmul_segments(FAKE, ws3, None, ns, 3, FAKE, 8, 4096, 4096, 4096, 6144, 7, None, 0, None) == -3
+    need = L.q3_matmul_segments_workspace_bytes(8, ns, 3, 4096, 1)
+    assert need > 0
+    assert L.q3_matmul_segments(FAKE, ws3, None, ns, 3, FAKE, 8, 4096, 4096, 4096, 6144, 1, None, 0, None) == -6
+    assert L.q3_matmul_segments_workspace_bytes(4096, ns, 3, 4096, 1) == 0
+    assert L.q3_matmul_segments(FAKE, ws3, None, ns, 3, FAKE, 0, 4096, 4096, 4096, 6144, 1, None, 0, None) == 0
+
+
 def test_elementwise_and_norm_validation():
     assert L.q3_residual_add(FAKE, None, FAKE, 10, 1, None) == -1
     assert L.q3_residual_add(FAKE, FAKE, FAKE, -1, 1, None) == -2
@@ -83,7 +101,8 @@ def test_attention_validation():
     # (B=2, Hq=8, D=128) q/o; (B, Hkv=2, cap=100, D) caches
     d = _lib.i64s(8 * 128, 128, 2 * 100 * 128, 100 * 128, 128, 2 * 100 * 128, 100 * 128, 128, 8 * 128, 128)
     assert L.q3_decode_attention(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 8, 2, 128, 100, d, 0.1, 1, None, 0, None) == -6
-    assert L.q3_decode_attention_workspace_bytes(32, 32, 8, 8193, 128) == 32 * 8 * 33 * 4 * 130 * 4
+    # one (m, l, O) record per (sequence, KV head, 128-key chunk) for the 4 heads of the group
+    assert L.q3_decode_attention_workspace_bytes(32, 32, 8, 8193, 128) == 32 * 8 * 65 * 4 * 130 * 4
 
 
 def test_rope_validation():

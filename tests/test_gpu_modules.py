@@ -103,6 +103,58 @@ def test_c3_decode_layer_against_per_sequence_oracle():
     assert_layer_parity(torch.cat(outs), torch.cat(refs), torch.cat(emus), what="C3 decode B=32")
 
 
+def test_decode_step_graph_replays_match_eager():
+    """Three decode tokens through a captured layer step equal three eager steps, bit for bit."""
+    from qwen3_5_vl_cuda_custom_amd.modules import StepGraph
+    cfg = W.TextLayerConfig(hidden=1024, heads=8, kv_heads=2, head_dim=128, intermediate=2816)
+    B, cap, steps = 4, 300, 3
+    layer = W.make_text_layer(cfg, torch.bfloat16, DEV, seed=3)
+    rope = W.make_rope(cfg, DEV)
+    g = torch.Generator(device=DEV).manual_seed(4)
+    xs = [torch.randn(B, 1, cfg.hidden, generator=g, device=DEV).to(torch.bfloat16) for _ in range(steps)]
+    lens0 = torch.tensor([5, 17, 64, 200], dtype=torch.int32)
+
+    def fresh_cache():
+        c = W.StaticKVCache(B, cfg.kv_heads, cap, cfg.head_dim, dtype=torch.bfloat16, device=DEV, lens=lens0)
+        gg = torch.Generator(device=DEV).manual_seed(5)
+        c.k.normal_(generator=gg)
+        c.v.normal_(generator=gg)
+        return c
+
+    # eager reference
+    cache = fresh_cache()
+    eager = []
+    for t in range(steps):
+        pos = (lens0 + t).to(DEV).view(1, B, 1).expand(3, B, 1).to(torch.int32).contiguous()
+        y, _, _ = layer(xs[t], rope.bind(pos), kv_cache=cache)
+        eager.append(y.clone())
+    k_ref, v_ref = cache.k.clone(), cache.v.clone()
+
+    # captured step: static x / positions, the cache lengths advance inside the graph
+    cache = fresh_cache()
+    x_in = torch.empty_like(xs[0])
+    pos32 = torch.empty(3, B, 1, dtype=torch.int32, device=DEV)
+    binding = rope.bind(pos32)
+    lens_saved = cache.lens.clone()
+    x_in.copy_(xs[0])
+    pos32.copy_(lens0.to(DEV).view(1, B, 1).expand(3, B, 1))
+    graph = StepGraph(lambda: layer(x_in, binding, kv_cache=cache)[0], warmup=1)
+    # warm-up and capture advanced the lengths and wrote rows: start over
+    cache.lens.copy_(lens_saved)
+    junk = torch.randn(1 << 20, device=DEV)
+    for t in range(steps):
+        x_in.copy_(xs[t])
+        pos32.copy_((lens0 + t).to(DEV).view(1, B, 1).expand(3, B, 1))
+        out = graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager[t]), f"replay {t} differs from the eager step"
+        float(junk.sum())  # eager work between replays
+    assert torch.equal(cache.lens.cpu(), lens0 + steps)
+    for b in range(B):
+        n = int(lens0[b]) + steps
+        assert torch.equal(cache.k[b, :, :n], k_ref[b, :, :n]) and torch.equal(cache.v[b, :, :n], v_ref[b, :, :n])
+
+
 def test_c4_moe_layer_reduced_tokens():
     cfg = W.C4
     layer = W.make_text_layer(cfg, torch.bfloat16, DEV, seed=0)

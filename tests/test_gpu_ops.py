@@ -66,6 +66,30 @@ def test_matmul_swiglu(M):
     assert_bf16_close(y, ref, what=f"matmul_swiglu M={M}")
 
 
+@pytest.mark.parametrize("M,ns,bias", [
+    (600, (1024, 256, 256), False),   # tiled, one launch (starts are multiples of 256)
+    (600, (512, 256, 256), True),     # tiled with per-segment bias
+    (300, (200, 72, 72), True),       # unaligned starts: one launch per segment
+    (32, (1024, 256, 256), False),    # skinny, one launch
+    (5, (96, 32, 32), True),          # skinny with bias
+    (9, (100, 20), False),            # skinny, unaligned: per segment
+])
+def test_matmul_segments(M, ns, bias):
+    Kd = 512
+    x = rnd(M, Kd, seed=40)
+    ws = [rnd(n, Kd, seed=41 + i, std=0.02) for i, n in enumerate(ns)]
+    bs = [rnd(n, seed=50 + i, std=0.02) if bias and i != 1 else None for i, n in enumerate(ns)]
+    y = K.matmul_segments(gpu(x), [gpu(w) for w in ws], [gpu(b) if b is not None else None for b in bs])
+    ref = torch.cat([O.linear(f32(x), f32(w), f32(b) if b is not None else None) for w, b in zip(ws, bs)], dim=-1)
+    assert_bf16_close(y, ref, what=f"matmul_segments M={M} {ns}")
+    # each column slice equals the single-weight GEMM bit for bit (same kernel math)
+    col = 0
+    for w, b in zip(ws, bs):
+        single = K.matmul(gpu(x), gpu(w), gpu(b) if b is not None else None)
+        assert torch.equal(y[:, col:col + w.shape[0]].cpu(), single.cpu()), f"segment at column {col}"
+        col += w.shape[0]
+
+
 def test_matmul_fp32_reference_style():
     torch.manual_seed(0)
     x, w, b = torch.randn(8, 64), torch.randn(32, 64), torch.randn(32)
