@@ -31,6 +31,11 @@ __device__ __forceinline__ const T* uniform_ptr(const T* p) {
   return reinterpret_cast<const T*>(((uint64_t)hi << 32) | lo);
 }
 
+template <typename T>
+__device__ __forceinline__ T pick4(int s, T a, T b, T c, T d) {
+  return s == 0 ? a : s == 1 ? b : s == 2 ? c : d;
+}
+
 __device__ __forceinline__ int segment_of(const WeightSegments& s, int col) {
   int i = 0;
 #pragma unroll
@@ -61,25 +66,21 @@ struct GemmParams {
   WeightSegments seg;        // dense (non-grouped, batch 1) store epilogue only
 };
 
-template <int BM, int BN, int WM, int WN, int EPI, bool GROUPED>
-__global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_kernel(const GemmParams p) {
-  constexpr int NT = WM * WN * 64;
-  constexpr int WTM = BM / WM;
-  constexpr int WTN = BN / WN;
-  constexpr int TM = WTM / 32;
-  constexpr int TN = WTN / 32;
-  static_assert(TM >= 1 && TN >= 1, "wave tile too small");
-  static_assert(EPI != kEpiSwiGLU || (TN % 2 == 0), "SwiGLU pairs gate/up tiles");
-  constexpr int BN_OUT = (EPI == kEpiSwiGLU) ? BN / 2 : BN;
+// Where a block's tile sits: logical rows [m_begin, m_begin + rows_m), output
+// columns from n0_out, and the (possibly re-based) operand pointers.
+struct TileCtx {
+  int m_begin, rows_m, n0_out, n_lim;
+  const bf16* X;
+  const bf16* W;
+  const bf16* W2;
+  const bf16* bias;
+  bf16* C;
+};
 
-  __shared__ __attribute__((aligned(16))) bf16 smem[2 * (BM + BN) * kBK];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
-  const int wm = wave % WM;
-  const int wn = wave / WM;
-
+// Returns false when the block has no tile (grouped problems past the last
+// valid m-tile).
+template <int BM, int BN_OUT, int EPI, bool GROUPED>
+__device__ __forceinline__ bool tile_ctx(const GemmParams& p, TileCtx& t) {
   const int n_tiles_n = (p.N + BN_OUT - 1) / BN_OUT;
   int tile_m, tile_n;
   int m_begin, m_end;  // logical rows of this tile: [m_begin, m_end)
@@ -89,10 +90,10 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_kernel(const GemmParams
   bf16* C = p.C;
 
   if constexpr (GROUPED) {
-    const int t = blockIdx.x / n_tiles_n;
+    const int tt = blockIdx.x / n_tiles_n;
     tile_n = blockIdx.x % n_tiles_n;
-    if (t >= *p.n_tiles_total) return;
-    const int entry = p.tile_table[t];
+    if (tt >= *p.n_tiles_total) return false;
+    const int entry = p.tile_table[tt];
     const int expert = entry >> 20;
     m_begin = entry & 0xFFFFF;
     m_end = min(m_begin + BM, p.group_end[expert]);
@@ -129,16 +130,179 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_kernel(const GemmParams
       // Constant-index selects keep the segment's pointers in scalar registers
       // (a dynamic index into the by-value params would go through memory and
       // make the buffer resource per-lane).
+      // Each field passes through readfirstlane before the select, so the
+      // selects cannot be folded back into one dynamically indexed load.
       const int s = __builtin_amdgcn_readfirstlane(segment_of(p.seg, n0_out));
-      const bf16* sw = s == 0 ? p.seg.w[0] : s == 1 ? p.seg.w[1] : s == 2 ? p.seg.w[2] : p.seg.w[3];
-      const bf16* sb = s == 0 ? p.seg.b[0] : s == 1 ? p.seg.b[1] : s == 2 ? p.seg.b[2] : p.seg.b[3];
-      const int st0 = s == 0 ? p.seg.start[0] : s == 1 ? p.seg.start[1] : s == 2 ? p.seg.start[2] : p.seg.start[3];
-      const int nxt = s == 0 ? p.seg.start[1] : s == 1 ? p.seg.start[2] : p.seg.start[3];
+      const bf16* sw = pick4(s, uniform_ptr(p.seg.w[0]), uniform_ptr(p.seg.w[1]), uniform_ptr(p.seg.w[2]),
+                             uniform_ptr(p.seg.w[3]));
+      const bf16* sb = pick4(s, uniform_ptr(p.seg.b[0]), uniform_ptr(p.seg.b[1]), uniform_ptr(p.seg.b[2]),
+                             uniform_ptr(p.seg.b[3]));
+      const int st0 = pick4(s, __builtin_amdgcn_readfirstlane(p.seg.start[0]),
+                            __builtin_amdgcn_readfirstlane(p.seg.start[1]),
+                            __builtin_amdgcn_readfirstlane(p.seg.start[2]),
+                            __builtin_amdgcn_readfirstlane(p.seg.start[3]));
+      const int nxt = pick4(s, __builtin_amdgcn_readfirstlane(p.seg.start[1]),
+                            __builtin_amdgcn_readfirstlane(p.seg.start[2]),
+                            __builtin_amdgcn_readfirstlane(p.seg.start[3]), p.N);
       W = uniform_ptr(sw - (int64_t)st0 * p.ldw);
       bias = sb ? uniform_ptr(sb - st0) : nullptr;
       n_lim = s + 1 < p.seg.n ? nxt : p.N;
     }
   }
+
+  // Everything here is block-uniform; integer division may still have left it
+  // in vector registers. Pin it to scalars so buffer resources stay scalar.
+  t.m_begin = __builtin_amdgcn_readfirstlane(m_begin);
+  t.rows_m = __builtin_amdgcn_readfirstlane(rows_m);
+  t.n0_out = __builtin_amdgcn_readfirstlane(n0_out);
+  t.n_lim = __builtin_amdgcn_readfirstlane(n_lim);
+  t.X = uniform_ptr(X);
+  t.W = uniform_ptr(W);
+  t.W2 = W2 ? uniform_ptr(W2) : nullptr;
+  t.bias = bias ? uniform_ptr(bias) : nullptr;
+  t.C = const_cast<bf16*>(uniform_ptr(C));
+  return true;
+}
+
+// Epilogue of one wave's (TN x TM) 32x32 accumulator tiles at wave offset
+// (wm * WTM, wn * WTN) of the block tile.
+template <int WTM, int WTN, int TN, int TM, int EPI>
+__device__ __forceinline__ void store_tile(const GemmParams& p, const TileCtx& t, const floatx16 (&c)[TN][TM],
+                                           int wm, int wn, int lane) {
+  const int m_begin = t.m_begin, rows_m = t.rows_m, n0_out = t.n0_out;
+  const bf16* bias = t.bias;
+  bf16* C = t.C;
+  const int l32 = lane & 31;
+  const int h = lane >> 5;
+  const int N = p.N;
+  const bool vec_ok = ((p.ldc & 3) == 0) && (p.R == nullptr || (p.ldr & 3) == 0);
+
+  if constexpr (EPI == kEpiSwiGLU) {
+#pragma unroll
+    for (int i = 0; i < TN / 2; ++i) {
+#pragma unroll
+      for (int j = 0; j < TM; ++j) {
+        const int mr = wm * WTM + j * 32 + l32;
+        if (mr >= rows_m) continue;
+        bf16* crow = C + (int64_t)(m_begin + mr) * p.ldc;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = n0_out + (wn * WTN) / 2 + i * 32 + 8 * g + 4 * h;
+          float o[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float gt = c[2 * i][j][4 * g + q];
+            const float up = c[2 * i + 1][j][4 * g + q];
+            o[q] = gt / (1.0f + __expf(-gt)) * up;
+          }
+          if (vec_ok && n + 3 < N) {
+            bf16x4 v = {f2bf(o[0]), f2bf(o[1]), f2bf(o[2]), f2bf(o[3])};
+            *reinterpret_cast<bf16x4*>(crow + n) = v;
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              if (n + q < N) crow[n + q] = f2bf(o[q]);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // one accumulator tile live at a time
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TN; ++i) {
+#pragma unroll
+      for (int j = 0; j < TM; ++j) {
+        const int mr = wm * WTM + j * 32 + l32;
+        if (mr >= rows_m) continue;
+        const int m = m_begin + mr;
+        bf16* crow = C + (int64_t)m * p.ldc;
+        float rs = 1.0f;
+        if constexpr (EPI == kEpiRowScale) rs = bf2f(p.rowscale[m]);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = n0_out + wn * WTN + i * 32 + 8 * g + 4 * h;
+          float o[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) o[q] = c[i][j][4 * g + q];
+          if (vec_ok && n + 3 < N) {
+            if (bias) {
+              const bf16x4 b = *reinterpret_cast<const bf16x4*>(bias + n);
+#pragma unroll
+              for (int q = 0; q < 4; ++q) o[q] += bf2f(b[q]);
+            }
+            if (p.R) {
+              const bf16x4 rv = *reinterpret_cast<const bf16x4*>(p.R + (int64_t)m * p.ldr + n);
+#pragma unroll
+              for (int q = 0; q < 4; ++q) o[q] += bf2f(rv[q]);
+            }
+            if constexpr (EPI == kEpiRowScale) {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) o[q] = bf2f(f2bf(o[q])) * rs;
+            }
+            bf16x4 v = {f2bf(o[0]), f2bf(o[1]), f2bf(o[2]), f2bf(o[3])};
+            *reinterpret_cast<bf16x4*>(crow + n) = v;
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              if (n + q >= N) continue;
+              float v = o[q];
+              if (bias) v += bf2f(bias[n + q]);
+              if (p.R) v += bf2f(p.R[(int64_t)m * p.ldr + n + q]);
+              if constexpr (EPI == kEpiRowScale) v = bf2f(f2bf(v)) * rs;
+              crow[n + q] = f2bf(v);
+            }
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // one accumulator tile live at a time
+      }
+    }
+  }
+}
+
+// Instruction order for one phase of the register-staged loop (one stage of
+// MFMAs, the next stage's global loads and the previous stage's LDS stores):
+// all fragment reads first, then the global loads and LDS stores spread
+// between MFMAs, so neither the memory pipes nor the MFMA pipe idle.
+template <int BK, int TN, int TM, int NV>
+__device__ __forceinline__ void sched_phase() {
+  constexpr int NR = (BK / 16) * (TN + TM), NM = (BK / 16) * TN * TM;
+  static_assert(NM >= 2 * NV, "not enough MFMAs to interleave the memory operations");
+  __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);  // DS reads
+#pragma unroll
+  for (int r = 0; r < NV; ++r) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, NM - 2 * NV, 0);
+}
+
+template <int BM, int BN, int WM, int WN, int EPI, bool GROUPED>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_kernel(const GemmParams p) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int WTM = BM / WM;
+  constexpr int WTN = BN / WN;
+  constexpr int TM = WTM / 32;
+  constexpr int TN = WTN / 32;
+  static_assert(TM >= 1 && TN >= 1, "wave tile too small");
+  static_assert(EPI != kEpiSwiGLU || (TN % 2 == 0), "SwiGLU pairs gate/up tiles");
+  constexpr int BN_OUT = (EPI == kEpiSwiGLU) ? BN / 2 : BN;
+
+  __shared__ __attribute__((aligned(16))) bf16 smem[2 * (BM + BN) * kBK];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int wm = wave % WM;
+  const int wn = wave / WM;
+
+  TileCtx tc;
+  if (!tile_ctx<BM, BN_OUT, EPI, GROUPED>(p, tc)) return;
+  const int m_begin = tc.m_begin, rows_m = tc.rows_m, n0_out = tc.n0_out, n_lim = tc.n_lim;
+  const bf16* X = tc.X;
+  const bf16* W = tc.W;
+  const bf16* W2 = tc.W2;
 
   constexpr int kStage = (BM + BN) * kBK;
   // Register staging: thread t owns 16-byte chunks t + i*NT of the X tile
@@ -242,98 +406,17 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_kernel(const GemmParams
     load(sa, kt + 2);
     compute(acc, 0);
     store(sb, 1);
+    sched_phase<kBK, TN, TM, PX + PW>();
     __syncthreads();
     load(sb, kt + 3);
     compute(acc, 1);
     store(sa, 0);
+    sched_phase<kBK, TN, TM, PX + PW>();
     __syncthreads();
   }
   if (kt < nk) compute(acc, 0);  // odd number of stages: the last one is in slot 0
 
-  // ------------------------------------------------------------ epilogue
-  const int l32 = lane & 31;
-  const int h = lane >> 5;
-  const int N = p.N;
-  const bool vec_ok = ((p.ldc & 3) == 0) && (p.R == nullptr || (p.ldr & 3) == 0);
-
-  if constexpr (EPI == kEpiSwiGLU) {
-#pragma unroll
-    for (int i = 0; i < TN / 2; ++i) {
-#pragma unroll
-      for (int j = 0; j < TM; ++j) {
-        const int mr = wm * WTM + j * 32 + l32;
-        if (mr >= rows_m) continue;
-        bf16* crow = C + (int64_t)(m_begin + mr) * p.ldc;
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int n = n0_out + (wn * WTN) / 2 + i * 32 + 8 * g + 4 * h;
-          float o[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float gt = acc.c[2 * i][j][4 * g + q];
-            const float up = acc.c[2 * i + 1][j][4 * g + q];
-            o[q] = gt / (1.0f + __expf(-gt)) * up;
-          }
-          if (vec_ok && n + 3 < N) {
-            bf16x4 v = {f2bf(o[0]), f2bf(o[1]), f2bf(o[2]), f2bf(o[3])};
-            *reinterpret_cast<bf16x4*>(crow + n) = v;
-          } else {
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-              if (n + q < N) crow[n + q] = f2bf(o[q]);
-          }
-        }
-      }
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < TN; ++i) {
-#pragma unroll
-      for (int j = 0; j < TM; ++j) {
-        const int mr = wm * WTM + j * 32 + l32;
-        if (mr >= rows_m) continue;
-        const int m = m_begin + mr;
-        bf16* crow = C + (int64_t)m * p.ldc;
-        float rs = 1.0f;
-        if constexpr (EPI == kEpiRowScale) rs = bf2f(p.rowscale[m]);
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int n = n0_out + wn * WTN + i * 32 + 8 * g + 4 * h;
-          float o[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) o[q] = acc.c[i][j][4 * g + q];
-          if (vec_ok && n + 3 < N) {
-            if (bias) {
-              const bf16x4 b = *reinterpret_cast<const bf16x4*>(bias + n);
-#pragma unroll
-              for (int q = 0; q < 4; ++q) o[q] += bf2f(b[q]);
-            }
-            if (p.R) {
-              const bf16x4 rv = *reinterpret_cast<const bf16x4*>(p.R + (int64_t)m * p.ldr + n);
-#pragma unroll
-              for (int q = 0; q < 4; ++q) o[q] += bf2f(rv[q]);
-            }
-            if constexpr (EPI == kEpiRowScale) {
-#pragma unroll
-              for (int q = 0; q < 4; ++q) o[q] = bf2f(f2bf(o[q])) * rs;
-            }
-            bf16x4 v = {f2bf(o[0]), f2bf(o[1]), f2bf(o[2]), f2bf(o[3])};
-            *reinterpret_cast<bf16x4*>(crow + n) = v;
-          } else {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              if (n + q >= N) continue;
-              float v = o[q];
-              if (bias) v += bf2f(bias[n + q]);
-              if (p.R) v += bf2f(p.R[(int64_t)m * p.ldr + n + q]);
-              if constexpr (EPI == kEpiRowScale) v = bf2f(f2bf(v)) * rs;
-              crow[n + q] = f2bf(v);
-            }
-          }
-        }
-      }
-    }
-  }
+  store_tile<WTM, WTN, TN, TM, EPI>(p, tc, acc.c, wm, wn, lane);
 }
 
 }  // namespace q3

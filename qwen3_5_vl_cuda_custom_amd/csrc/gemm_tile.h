@@ -71,24 +71,29 @@ struct WaveAcc {
 #pragma unroll
       for (int j = 0; j < TM; ++j) c[i][j] = floatx16{};
   }
-  // One BK stage: sX holds the block's X tile, sW the W tile.
+  // One BK stage: sX holds the block's X tile, sW the W tile. All fragment
+  // reads of the stage are issued before its MFMAs, so the LDS latency of the
+  // second K step hides behind the first step's MFMAs.
   __device__ __forceinline__ void mma_stage(const bf16* sX, const bf16* sW, int wrow_m, int wrow_n, int lane) {
+    constexpr int KS = kBK / 16;
     const int l32 = lane & 31;
     const int h = lane >> 5;
+    bf16x8 a[KS][TN], b[KS][TM];
 #pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      bf16x8 a[TN], b[TM];
+    for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
       for (int i = 0; i < TN; ++i)
-        a[i] = *reinterpret_cast<const bf16x8*>(sW + swz(wrow_n + i * 32 + l32, ks * 2 + h));
+        a[ks][i] = *reinterpret_cast<const bf16x8*>(sW + swz(wrow_n + i * 32 + l32, ks * 2 + h));
 #pragma unroll
       for (int j = 0; j < TM; ++j)
-        b[j] = *reinterpret_cast<const bf16x8*>(sX + swz(wrow_m + j * 32 + l32, ks * 2 + h));
+        b[ks][j] = *reinterpret_cast<const bf16x8*>(sX + swz(wrow_m + j * 32 + l32, ks * 2 + h));
+    }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
       for (int i = 0; i < TN; ++i)
 #pragma unroll
-        for (int j = 0; j < TM; ++j) c[i][j] = mfma32x32x16(a[i], b[j], c[i][j]);
-    }
+        for (int j = 0; j < TM; ++j) c[i][j] = mfma32x32x16(a[ks][i], b[ks][j], c[i][j]);
   }
 };
 

@@ -40,6 +40,8 @@ def f32(t):
     (256, 1152, 4304, True),  # vision fc2: K tail (4304 = 67*64 + 16)
     (1024, 4096, 4096, False),
     (1024, 1536, 2048, False),
+    (4096, 4096, 512, True),     # >= 256 tiles of 256x256: the direct-to-LDS kernel
+    (4000, 4200, 520, True),     # same kernel with ragged M, N and a K tail
 ])
 def test_matmul_bf16(M, N, Kd, bias):
     x = rnd(M, Kd, seed=1)
@@ -54,11 +56,16 @@ def test_matmul_residual_fused():
     x, w, r = rnd(200, 512, seed=4), rnd(384, 512, seed=5, std=0.02), rnd(200, 384, seed=6)
     y = K.matmul(gpu(x), gpu(w), residual=gpu(r))
     assert_bf16_close(y, O.linear(f32(x), f32(w)) + f32(r), what="matmul+residual")
+    # large: residual and bias enter the direct-to-LDS kernel's accumulators
+    xl, wl, rl, bl = rnd(4096, 320, seed=60), rnd(4100, 320, seed=61, std=0.02), rnd(4096, 4100, seed=62), \
+        rnd(4100, seed=63, std=0.02)
+    yl = K.matmul(gpu(xl), gpu(wl), gpu(bl), residual=gpu(rl))
+    assert_bf16_close(yl, O.linear(f32(xl), f32(wl), f32(bl)) + f32(rl), what="large matmul+bias+residual")
     y2 = K.matmul(gpu(x[:16]), gpu(w), residual=gpu(r[:16]))  # skinny path epilogue
     assert_bf16_close(y2, O.linear(f32(x[:16]), f32(w)) + f32(r[:16]), what="skinny matmul+residual")
 
 
-@pytest.mark.parametrize("M", [7, 32, 300, 1024])
+@pytest.mark.parametrize("M", [7, 32, 300, 1024, 8192])
 def test_matmul_swiglu(M):
     x, wg, wu = rnd(M, 1024, seed=7), rnd(1536, 1024, seed=8, std=0.02), rnd(1536, 1024, seed=9, std=0.02)
     y = K.matmul_swiglu(gpu(x), gpu(wg), gpu(wu))
