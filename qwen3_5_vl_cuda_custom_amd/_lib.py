@@ -126,3 +126,28 @@ def workspace(nbytes: int, device: torch.device) -> tuple[torch.Tensor | None, i
     if nbytes <= 0:
         return None, 0
     return torch.empty(int(nbytes), dtype=torch.uint8, device=device), int(nbytes)
+
+
+# Per-device GEMM workspaces (M <= 32 path). They start zero-filled: their
+# first 16 KiB are tile counters that every call leaves at zero again. A larger
+# request allocates a new buffer; the old ones are kept, because captured HIP
+# graphs may still point at them. Calls on different streams that run at the
+# same time must not share one: these are for the stream-ordered decode step.
+_gemm_ws: dict[tuple[str, int | None], list[torch.Tensor]] = {}
+
+
+def gemm_workspace(nbytes: int, device: torch.device) -> tuple[torch.Tensor | None, int]:
+    """The zero-initialised, persistent workspace of the GEMM entry points."""
+    if nbytes <= 0:
+        return None, 0
+    dev = torch.device(device)
+    key = (dev.type, dev.index if dev.index is not None else torch.cuda.current_device())
+    bufs = _gemm_ws.setdefault(key, [])
+    if not bufs or bufs[-1].numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("gemm_workspace: first use of this GEMM size inside HIP-graph capture; run the "
+                               "step once eagerly before capturing it (StepGraph does)")
+        size = max(int(nbytes), 2 * bufs[-1].numel() if bufs else 0, 16 << 20)
+        bufs.append(torch.zeros(size, dtype=torch.uint8, device=dev))
+    buf = bufs[-1]
+    return buf, buf.numel()

@@ -33,6 +33,14 @@ HIPFLAGS = [
 ]
 
 
+# Per-source extra flags. gemv.hip: thread 0's tile-counter increments must not
+# be rewritten into wave-combined atomics, whose result the compiler then waits
+# for at once (that wait would drain the kernel's in-flight DMA ring).
+EXTRA_FLAGS = {
+    "gemv.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
+}
+
+
 def _hipcc() -> str:
     p = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(p).exists():
@@ -41,7 +49,7 @@ def _hipcc() -> str:
 
 
 def _compile(src: Path, obj: Path, verbose: bool) -> None:
-    cmd = [_hipcc(), *HIPFLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [_hipcc(), *HIPFLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -15,10 +15,9 @@
 // (t = r), is a fixed key permutation; the V^T fragment reads use the same one.
 // The O^T accumulators are per-lane queries, so the softmax rescale is local.
 //
-// Decode (q3_decode_attention): one block per (64*4-key chunk, sequence, KV
-// head); the MFMA query columns are the GQA group's heads. Each wave handles 64
-// keys; the block merges its waves and writes (m, l, O) partials, which a
-// second kernel combines per query head.
+// Decode (q3_decode_attention): stream-K over 32-key units of all (sequence,
+// KV head) pairs, one wave-private DMA ring per wave; the MFMA query columns
+// are the GQA group's heads (see the decode section below).
 #include <algorithm>
 
 #include "gemm_tile.h"
@@ -47,7 +46,6 @@ struct AttnParams {
   // decode
   const int* kv_lens;
   float* partial;  // decode workspace
-  int max_chunks;
 };
 
 // ----------------------------------------------------------------- prefill
@@ -274,23 +272,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 }
 
 // ----------------------------------------------------------------- decode
-// One block = WPB waves over a chunk of WPB * 64 keys of one (sequence, KV
-// head); each wave owns one 64-key tile in wave-private LDS, filled by
-// direct-to-LDS loads (all 32 KB of K and V in flight at once, no staging
-// registers). The MFMA query columns are the GQA group's heads (G <= 32).
-//   K tile: 64 rows x 128, chunk c of row r at slot c ^ (r & 15) (as prefill).
-//   V tile: 64 rows x 128 in natural layout, chunk c of row r at slot
-//   c ^ ((r & 3) << 2). The PV A operand (V^T fragments) is read with
-//   ds_read_b64_tr_b16, which transposes within 16-lane groups: lane i of a
-//   group receives element i%4 of the 8-byte piece each lane 4r + i/4
-//   addressed, for r = 0..3. With lane 4r + q addressing V[key_r][d0 + 4q],
-//   lane i gets V[key_0..3][d0 + i]: four keys of its head-dim row.
-// The block merges its waves and writes one (m, l, O) partial per chunk; a
-// second kernel combines the chunks of each query head.
-constexpr int kDecWaves = 2;
-constexpr int kDecKeys = kDecWaves * kKT;  // keys per block
+// One query token per (sequence, query head) over a ragged cache, split so
+// that every wave streams the same number of K/V bytes whatever the lengths:
+//
+//  * Work units are 32-key tiles of a (sequence b, KV head) pair, listed
+//    pair-major (pair p = b * Hkv + kvh has n_b = ceil(L_b / 32) units). The
+//    grid has one block of kDecBlockWaves waves per CU; of its
+//    W = min(U, kDecWavesTotal) first waves, wave w takes units
+//    [w * U / W, (w + 1) * U / W) of the U in all (at least one each).
+//  * Each wave owns a ring of kDecSlots LDS slots. A unit's slot holds its K
+//    tile, its V tile and the group's query rows, all filled by direct-to-LDS
+//    loads (buffer_load ... lds), issued kDecSlots - 1 units ahead, so the
+//    wave's stream never stops between units or pairs.
+//      K tile: 32 rows x 128, chunk c of row r at slot c ^ (r & 15).
+//      V tile: 32 rows x 128, chunk c of row r at slot c ^ ((r & 3) << 2).
+//    The PV A operand (V^T fragments) is read with ds_read_b64_tr_b16, which
+//    transposes within 16-lane groups: lane i of a group receives element
+//    i % 4 of the 8-byte piece that lane 4r + i / 4 addressed, r = 0..3. With
+//    lane 4r + q addressing V[key_r][d0 + 4q], lane i gets V[key_0..3][d0 + i].
+//  * MFMA query columns are the G heads of the group: S^T = K Q^T, online
+//    softmax per column (exp2 on log2e-scaled scores, max raised only when a
+//    tile exceeds it by kRescale), O^T += V^T P^T with P^T straight from the
+//    S^T accumulators.
+//  * A pair finished inside one wave is normalised and stored at once; a pair
+//    split between waves leaves one (m, l, O) record per wave in the
+//    workspace (record w + p, unique and increasing in (w, p)), merged by
+//    flash_decode_combine.
+constexpr int kDecUnit = 32;                                   // keys per unit
+constexpr int kDecBlockWaves = 2;                              // waves per block (one block per CU)
+constexpr int kDecBlocks = 256;
+constexpr int kDecWavesTotal = kDecBlocks * kDecBlockWaves;
+constexpr int kDecMaxBatch = 1024;                             // sequences the fast path takes
+constexpr int kDecTile = kDecUnit * kRowK;                     // elements of a K or V tile
 
-// Partial layout per (b, kvh, chunk): m[G], l[G], O[G][D] (fp32), G = groups.
+// Partial layout per record: m[G], l[G], O[G][D] (fp32), G = groups.
 __host__ __device__ inline int dec_partial_floats(int groups, int D) { return groups * (D + 2); }
 
 typedef short short4v __attribute__((ext_vector_type(4)));
@@ -303,98 +318,259 @@ __device__ __forceinline__ short4v lds_read_tr16(const bf16* p) {
 
 __device__ __forceinline__ int dec_v_off(int r, int c) { return r * kRowK + ((c ^ ((r & 3) << 2)) << 3); }
 
-template <int WPB>
-__global__ __launch_bounds__(64 * WPB) void flash_decode_kernel(const AttnParams p) {
+// Waves that get work: min(U, kDecWavesTotal), so every one of them has at
+// least one unit; wave w takes units [w * U / nw, (w + 1) * U / nw).
+__device__ __forceinline__ int dec_active_waves(int64_t U) { return (int)min<int64_t>(U, kDecWavesTotal); }
+// Active wave whose unit range contains unit u.
+__device__ __forceinline__ int dec_wave_of(int64_t u, int64_t U) {
+  return (int)(((u + 1) * dec_active_waves(U) - 1) / U);
+}
+
+// Exclusive prefix over sequences of their unit counts, into s_pre[0..B]
+// (and the clamped lengths into s_len). Block-wide; ends with a barrier.
+__device__ void dec_prefix(const AttnParams& p, int* s_pre, int* s_len) {
+  const int B = p.B, tid = threadIdx.x, nt = blockDim.x;
+  const int per = (B + nt - 1) / nt;
+  int local = 0;
+  for (int i = 0; i < per; ++i) {
+    const int b = tid * per + i;
+    if (b < B) {
+      const int L = min(max(p.kv_lens[b], 0), p.Sk);
+      s_len[b] = L;
+      local += (L + kDecUnit - 1) / kDecUnit;
+    }
+  }
+  // exclusive scan of `local` over the block: wave scan, then wave totals
+  __shared__ int s_wsum[16];
+  const int lane = tid & 63, wv = tid >> 6;
+  int incl = local;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int v = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += v;
+  }
+  if (lane == 63) s_wsum[wv] = incl;
+  __syncthreads();
+  int base = 0;
+  for (int j = 0; j < wv; ++j) base += s_wsum[j];
+  int run = base + incl - local;
+  for (int i = 0; i < per; ++i) {
+    const int b = tid * per + i;
+    if (b < B) {
+      s_pre[b] = run;
+      run += (s_len[b] + kDecUnit - 1) / kDecUnit;
+    }
+  }
+  if (tid == nt - 1) s_pre[B] = run;
+  __syncthreads();
+}
+
+// Position of a unit: sequence, KV head, tile, units of the sequence.
+struct DecCursor {
+  int b, kvh, tile, nb;
+};
+
+template <int QI, int NSLOT>
+__global__ __launch_bounds__(64 * kDecBlockWaves) void flash_decode_kernel(const AttnParams p) {
   constexpr int D = 128;
   constexpr int KSTEPS = D / 16;
   constexpr int OT = D / 32;
-  constexpr int TILE = kKT * kRowK;  // elements per K or V tile
-  __shared__ __attribute__((aligned(1024))) bf16 lds[WPB * 2 * TILE];
+  constexpr int SLOT = 2 * kDecTile + QI * 4 * kRowK;  // elements per ring slot: K, V, 4 QI query rows
+  constexpr int PER_UNIT = 2 * (kDecUnit / 4) + QI;     // DMA instructions per unit
+  __shared__ int s_pre[kDecMaxBatch + 1];
+  __shared__ int s_len[kDecMaxBatch];
+  __shared__ __attribute__((aligned(1024))) bf16 ring[kDecBlockWaves * NSLOT * SLOT];
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
+  dec_prefix(p, s_pre, s_len);  // block-wide, before the waves part ways
+
+  const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int l32 = lane & 31;
-  const int h = lane >> 5;
-  const int chunk = blockIdx.x;
-  const int kvh = blockIdx.y % p.Hkv;
-  const int b = blockIdx.y / p.Hkv;
-  const int L = min(p.kv_lens[b], p.Sk);  // Sk = max_len: never read past the cache
-  const int kc0 = chunk * (WPB * kKT);
-  if (kc0 >= L) return;  // uniform per block
+  const int l32 = lane & 31, h = lane >> 5;
+  const int B = p.B, Hkv = p.Hkv, G = p.groups;
+  const int64_t U = (int64_t)Hkv * s_pre[B];
+  const int w = blockIdx.x * kDecBlockWaves + wave;
+  const int nw = dec_active_waves(U);
+  if (w >= nw) return;
+  const int64_t u0 = (int64_t)w * U / nw, u1 = (int64_t)(w + 1) * U / nw;
 
-  bf16* sK = lds + wave * 2 * TILE;
-  bf16* sV = sK + TILE;
-  const int k0 = kc0 + wave * kKT;
-  const bool live = k0 < L;
-  const bf16* kbase = p.k + (int64_t)b * p.kb + (int64_t)kvh * p.kh;
-  const bf16* vbase = p.v + (int64_t)b * p.vb + (int64_t)kvh * p.vh;
-  if (live) {
-    const int ks2 = (int)p.ks * 2, vs2 = (int)p.vs * 2;  // host guarantees max_len * stride * 2 < 2^31
+  auto locate = [&](int64_t u) {
+    int lo = 0, hi = B - 1;  // largest b with Hkv * s_pre[b] <= u
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if ((int64_t)Hkv * s_pre[mid] <= u) lo = mid;
+      else hi = mid - 1;
+    }
+    DecCursor c;
+    c.b = lo;
+    c.nb = s_pre[lo + 1] - s_pre[lo];
+    const int r = (int)(u - (int64_t)Hkv * s_pre[lo]);
+    c.kvh = r / c.nb;
+    c.tile = r - c.kvh * c.nb;
+    return c;
+  };
+  auto advance = [&](DecCursor& c) {
+    if (++c.tile < c.nb) return;
+    c.tile = 0;
+    if (++c.kvh < Hkv) return;
+    c.kvh = 0;
+    do {
+      ++c.b;
+    } while (c.b < B && s_pre[c.b + 1] == s_pre[c.b]);
+    c.nb = c.b < B ? s_pre[c.b + 1] - s_pre[c.b] : 0;
+  };
+
+  bf16* myring = ring + wave * NSLOT * SLOT;
+  const uint32_t lring = q3::lds_addr(myring);
+  const int ks2 = (int)p.ks * 2, vs2 = (int)p.vs * 2;  // host guarantees Sk * stride * 2 < 2^31
+
+  // DMA of one unit into ring slot `slot` (zeros when `live` is false).
+  auto issue = [&](const DecCursor& c, bool live, bool need_q, int slot) {
+    const int L = live ? s_len[c.b] : 1;
+    const bf16* kbase = p.k + (int64_t)c.b * p.kb + (int64_t)c.kvh * p.kh;
+    const bf16* vbase = p.v + (int64_t)c.b * p.vb + (int64_t)c.kvh * p.vh;
+    const bf16* qbase = p.q + (int64_t)c.b * p.qb + (int64_t)c.kvh * G * p.qh;
     const __amdgpu_buffer_rsrc_t krs = q3::make_rsrc(kbase, (int64_t)(L - 1) * ks2 + D * 2);
     const __amdgpu_buffer_rsrc_t vrs = q3::make_rsrc(vbase, (int64_t)(L - 1) * vs2 + D * 2);
-    const uint32_t lk = q3::lds_addr(sK), lv = q3::lds_addr(sV);
-    const int slot = lane & 15;
+    const __amdgpu_buffer_rsrc_t qrs = q3::make_rsrc(qbase, (int64_t)(G - 1) * p.qh * 2 + D * 2);
+    const uint32_t lk = lring + (uint32_t)(slot * SLOT * 2);
+    const uint32_t lv = lk + kDecTile * 2, lq = lv + kDecTile * 2;
+    const int k0 = c.tile * kDecUnit;
+    const int cs = lane & 15;
 #pragma unroll
-    for (int i = 0; i < kKT / 4; ++i) {
+    for (int i = 0; i < kDecUnit / 4; ++i) {
       const int r = 4 * i + (lane >> 4);
-      const int kc = slot ^ (r & 15);
-      const int vc = slot ^ ((r & 3) << 2);
-      q3::dma16(krs, (uint32_t)((k0 + r) * ks2 + kc * 16), lk + i * 1024);
-      q3::dma16(vrs, (uint32_t)((k0 + r) * vs2 + vc * 16), lv + i * 1024);
+      const uint32_t ko = live ? (uint32_t)((k0 + r) * ks2 + ((cs ^ (r & 15)) << 4)) : q3::kOOB;
+      const uint32_t vo = live ? (uint32_t)((k0 + r) * vs2 + ((cs ^ ((r & 3) << 2)) << 4)) : q3::kOOB;
+      q3::dma16(krs, ko, lk + i * 1024);
+      q3::dma16(vrs, vo, lv + i * 1024);
     }
-  }
-  const int G = p.groups;
+#pragma unroll
+    for (int i = 0; i < QI; ++i) {
+      const int j = 4 * i + (lane >> 4);  // query head of the group
+      const uint32_t qo = (live && need_q && j < G) ? (uint32_t)(j * (int)p.qh * 2 + cs * 16) : q3::kOOB;
+      q3::dma16(qrs, qo, lq + i * 1024);
+    }
+  };
+
+  const float c2 = p.scale_log2;
   const bool qvalid = l32 < G;
   bf16x8 qf[KSTEPS];
-  {
-    const bf16* qrow = p.q + (int64_t)b * p.qb + (int64_t)(kvh * G + (qvalid ? l32 : 0)) * p.qh;
-#pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks)
-      qf[ks] = qvalid ? *reinterpret_cast<const bf16x8*>(qrow + ks * 16 + 8 * h) : bf16x8{};
-  }
   floatx16 o[OT];
+  float m = -INFINITY, lsum = 0.f;
+  auto reset = [&]() {
 #pragma unroll
-  for (int t = 0; t < OT; ++t) o[t] = floatx16{};
-  float m = kNegBig, lsum = 0.f;
-  q3::vm_wait<0>();  // this wave's tiles have landed in its own LDS
-  if (live) {
-    floatx16 s0 = floatx16{}, s1 = floatx16{};
+    for (int t = 0; t < OT; ++t) o[t] = floatx16{};
+    m = -INFINITY;
+    lsum = 0.f;
+  };
+  reset();
+
+  // Stores the finished (or this wave's part of the) pair of cursor c.
+  auto flush = [&](const DecCursor& c, int64_t pair_u0) {
+    const int pair = c.b * Hkv + c.kvh;
+    const int64_t pair_u1 = pair_u0 + c.nb;
+    const float l = lsum + __shfl_xor(lsum, 32, 64);
+    const bool whole = pair_u0 >= u0 && pair_u1 <= u1;
+    if (whole) {
+      if (!qvalid) return;
+      const float inv = l > 0.f ? 1.0f / l : 0.f;
+      bf16* orow = p.o + (int64_t)c.b * p.ob + (int64_t)(c.kvh * G + l32) * p.oh;
+#pragma unroll
+      for (int t = 0; t < OT; ++t)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d = 32 * t + 8 * g + 4 * h;
+          bf16x4 v4;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v4[e] = f2bf(o[t][4 * g + e] * inv);
+          *reinterpret_cast<bf16x4*>(orow + d) = v4;
+        }
+    } else {
+      const int PF = dec_partial_floats(G, D);
+      float* rec = p.partial + (int64_t)(w + pair) * PF;
+      if (!qvalid) return;
+      if (h == 0) {
+        rec[l32] = m;
+        rec[G + l32] = l;
+      }
+#pragma unroll
+      for (int t = 0; t < OT; ++t)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d = 32 * t + 8 * g + 4 * h;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) rec[2 * G + l32 * D + d + e] = o[t][4 * g + e];
+        }
+    }
+  };
+
+  DecCursor cc = locate(u0);  // compute cursor
+  DecCursor ic = cc;          // issue cursor, NSLOT - 1 units ahead
+  int64_t pair_u0 = u0 - cc.tile;  // first unit of the current pair
+#pragma unroll
+  for (int s = 0; s < NSLOT - 1; ++s) {
+    const int64_t u = u0 + s;
+    issue(ic, u < u1, ic.tile == 0 || u == u0, s);
+    if (u < u1) advance(ic);
+  }
+
+  for (int64_t u = u0; u < u1; ++u) {
+    const int slot = (int)((u - u0) % NSLOT);
+    {
+      const int64_t un = u + NSLOT - 1;
+      issue(ic, un < u1, ic.tile == 0, (int)((un - u0) % NSLOT));
+      if (un < u1) advance(ic);
+    }
+    q3::vm_wait<(NSLOT - 1) * PER_UNIT>();  // unit u's K, V (and Q) are in LDS
+
+    const bf16* sK = myring + slot * SLOT;
+    const bf16* sV = sK + kDecTile;
+    const bf16* sQ = sV + kDecTile;
+    if (cc.tile == 0 || u == u0) {
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks)
+        qf[ks] = qvalid ? *reinterpret_cast<const bf16x8*>(sQ + l32 * kRowK + ks * 16 + 8 * h) : bf16x8{};
+    }
+    floatx16 s = floatx16{};
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
-      const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(sK + fwd::k_off(l32, 2 * ks + h));
-      const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(sK + fwd::k_off(32 + l32, 2 * ks + h));
-      s0 = mfma32x32x16(a0, qf[ks], s0);
-      s1 = mfma32x32x16(a1, qf[ks], s1);
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(sK + fwd::k_off(l32, 2 * ks + h));
+      s = mfma32x32x16(a, qf[ks], s);
     }
-    if (k0 + kKT > L) {
+    const int L = s_len[cc.b];
+    const int k0 = cc.tile * kDecUnit;
+    if (k0 + kDecUnit > L) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = k0 + 8 * (r >> 2) + 4 * h + (r & 3);
-        if (key >= L) s0[r] = -INFINITY;
-        if (key + 32 >= L) s1[r] = -INFINITY;
-      }
+      for (int r = 0; r < 16; ++r)
+        if (k0 + 8 * (r >> 2) + 4 * h + (r & 3) >= L) s[r] = -INFINITY;
     }
-    const float c = p.scale_log2;
-    float mloc = fmaxf(s0[0], s1[0]);
+    float mloc = s[0];
 #pragma unroll
-    for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, fmaxf(s0[r], s1[r]));
-    m = fwd::half_max(mloc) * c;  // finite: key k0 < L is live
-    bf16x8 pb[4];
+    for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, s[r]);
+    mloc = fwd::half_max(mloc) * c2;  // finite: key k0 < L is live
+    const bool raise = mloc > m + fwd::kRescale;
+    if (__builtin_amdgcn_ballot_w64(raise) != 0) {
+      const float mnew = raise ? mloc : m;
+      const float alpha = fast_exp2(m - mnew);
+      lsum *= alpha;
+#pragma unroll
+      for (int t = 0; t < OT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+      m = mnew;
+    }
+    bf16x8 pb[2];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float p0 = fast_exp2(fmaf(s0[r], c, -m));
-      const float p1 = fast_exp2(fmaf(s1[r], c, -m));
-      lsum += p0 + p1;
-      pb[r >> 3][r & 7] = f2bf(p0);
-      pb[2 + (r >> 3)][r & 7] = f2bf(p1);
+      const float pr = fast_exp2(fmaf(s[r], c2, -m));
+      lsum += pr;
+      pb[r >> 3][r & 7] = f2bf(pr);
     }
-    lsum += __shfl_xor(lsum, 32, 64);
-    // V^T fragments by transposed reads: lane (g16, r, q) addresses
-    // V[16 j + 4 h + r (+8)][32 t + 16 g16 + 4 q].
+    // V^T fragments by transposed reads: lane (g16, rr, qq) addresses
+    // V[16 j + 4 h + rr (+ 8)][32 t + 16 g16 + 4 qq].
     const int g16 = (lane >> 4) & 1, rr = (lane & 15) >> 2, qq = lane & 3;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 2; ++j) {
       const int key = 16 * j + 4 * h + rr;
 #pragma unroll
       for (int t = 0; t < OT; ++t) {
@@ -405,103 +581,51 @@ __global__ __launch_bounds__(64 * WPB) void flash_decode_kernel(const AttnParams
         o[t] = mfma32x32x16(__builtin_bit_cast(bf16x8, a8), pb[j], o[t]);
       }
     }
-  }
 
-  // Merge the block's waves through LDS (the tiles are dead by now).
-  __syncthreads();
-  const int PF = dec_partial_floats(G, D);
-  float* red = reinterpret_cast<float*>(lds);
-  float* rw = red + wave * PF;
-  if (h == 0 && qvalid) {
-    rw[l32] = live ? m : kNegBig;
-    rw[G + l32] = live ? lsum : 0.f;
-  }
-  if (qvalid) {
-#pragma unroll
-    for (int t = 0; t < OT; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int d = t * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        rw[2 * G + l32 * D + d] = live ? o[t][r] : 0.f;
-      }
-  }
-  __syncthreads();
-  float* out = p.partial + (((int64_t)b * p.Hkv + kvh) * p.max_chunks + chunk) * PF;
-  for (int idx = tid; idx < G * D + G; idx += 64 * WPB) {
-    const int qc = idx < G ? idx : (idx - G) / D;
-    float mm = kNegBig;
-#pragma unroll
-    for (int w = 0; w < WPB; ++w) mm = fmaxf(mm, red[w * PF + qc]);
-    float acc = 0.f;
-#pragma unroll
-    for (int w = 0; w < WPB; ++w) {
-      const float* r = red + w * PF;
-      const float wgt = fast_exp2(r[qc] - mm);
-      acc += (idx < G ? r[G + qc] : r[2 * G + (idx - G)]) * wgt;
+    const bool pair_end = cc.tile == cc.nb - 1;
+    if (pair_end || u == u1 - 1) {
+      flush(cc, pair_u0);
+      reset();
     }
-    if (idx < G) {
-      out[qc] = mm;
-      out[G + qc] = acc;
-    } else {
-      out[2 * G + (idx - G)] = acc;
-    }
+    if (pair_end) pair_u0 += cc.nb;
+    advance(cc);
   }
+  q3::vm_wait<0>();  // no DMA may still target this block's LDS when the wave retires
 }
 
-// Block per (sequence, KV head): merges the chunk partials of the G query
-// heads of the group. The chunk maxima and weights go through LDS (one pass
-// over m and l), then each thread owns output elements (head, d) and sums
-// the chunks' O rows, 8 chunks' loads in flight at a time.
-constexpr int kCombineMaxChunks = 256;  // LDS budget for the per-chunk weights
+// Merges the per-wave records of the pairs split between waves: one block
+// per pair, one thread per (head, d) output.
 template <int D>
 __global__ __launch_bounds__(256) void flash_decode_combine(const AttnParams p) {
-  __shared__ float s_w[kCombineMaxChunks * 4];
-  __shared__ float s_inv[32];
-  const int tid = threadIdx.x;
-  const int kvh = blockIdx.x % p.Hkv;
-  const int b = blockIdx.x / p.Hkv;
-  const int L = min(p.kv_lens[b], p.Sk);
-  const int nch = (L + kDecKeys - 1) / kDecKeys;
-  const int G = p.groups;
+  __shared__ int s_pre[kDecMaxBatch + 1];
+  __shared__ int s_len[kDecMaxBatch];
+  dec_prefix(p, s_pre, s_len);
+  const int pair = blockIdx.x;
+  const int Hkv = p.Hkv, G = p.groups;
+  const int b = pair / Hkv, kvh = pair % Hkv;
+  const int nb = s_pre[b + 1] - s_pre[b];
+  bf16* obase = p.o + (int64_t)b * p.ob + (int64_t)kvh * G * p.oh;
+  if (nb == 0) {  // empty sequence: zeros
+    for (int e = threadIdx.x; e < G * D; e += blockDim.x) obase[(int64_t)(e / D) * p.oh + e % D] = f2bf(0.f);
+    return;
+  }
+  const int64_t U = (int64_t)Hkv * s_pre[p.B];
+  const int64_t pu0 = (int64_t)Hkv * s_pre[b] + (int64_t)kvh * nb;
+  const int wf = dec_wave_of(pu0, U), wl = dec_wave_of(pu0 + nb - 1, U);
+  if (wf == wl) return;  // finished by its wave
   const int PF = dec_partial_floats(G, D);
-  const float* base = p.partial + ((int64_t)b * p.Hkv + kvh) * p.max_chunks * PF;
-  // Heads are handled GH at a time so that the weights of all chunks fit in LDS.
-  const int GH = max(1, min(G, kCombineMaxChunks * 4 / max(nch, 1)));
-  for (int g0 = 0; g0 < G; g0 += GH) {
-    const int gn = min(GH, G - g0);
-    // Per head: max over chunks, then weights w_c = 2^(m_c - max) and 1 / sum(l_c w_c).
-    // One wave per head (4 waves per pass).
-    for (int gg = tid >> 6; gg < gn; gg += 4) {
-      const int lane = tid & 63, qc = g0 + gg;
-      float mm = kNegBig;
-      for (int c = lane; c < nch; c += 64) mm = fmaxf(mm, base[(int64_t)c * PF + qc]);
-      mm = wave_max(mm);
-      float ll = 0.f;
-      for (int c = lane; c < nch; c += 64) {
-        const float w = fast_exp2(base[(int64_t)c * PF + qc] - mm);
-        s_w[gg * nch + c] = w;
-        ll += base[(int64_t)c * PF + G + qc] * w;
-      }
-      ll = wave_sum(ll);
-      if (lane == 0) s_inv[gg] = ll > 0.f ? 1.0f / ll : 0.f;
+  for (int e = threadIdx.x; e < G * D; e += blockDim.x) {
+    const int qc = e / D, d = e % D;
+    float mm = -INFINITY;
+    for (int w = wf; w <= wl; ++w) mm = fmaxf(mm, p.partial[(int64_t)(w + pair) * PF + qc]);
+    float l = 0.f, acc = 0.f;
+    for (int w = wf; w <= wl; ++w) {
+      const float* rec = p.partial + (int64_t)(w + pair) * PF;
+      const float wt = fast_exp2(rec[qc] - mm);
+      l += rec[G + qc] * wt;
+      acc += rec[2 * G + qc * D + d] * wt;
     }
-    __syncthreads();
-    for (int e = tid; e < gn * D; e += 256) {
-      const int gg = e / D, d = e % D, qc = g0 + gg;
-      const float* src = base + 2 * G + qc * D + d;
-      float acc = 0.f;
-      int c = 0;
-      for (; c + 8 <= nch; c += 8) {
-        float v[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = src[(int64_t)(c + i) * PF];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc += v[i] * s_w[gg * nch + c + i];
-      }
-      for (; c < nch; ++c) acc += src[(int64_t)c * PF] * s_w[gg * nch + c];
-      p.o[(int64_t)b * p.ob + (int64_t)(kvh * G + qc) * p.oh + d] = f2bf(acc * s_inv[gg]);
-    }
-    __syncthreads();
+    obase[(int64_t)qc * p.oh + d] = f2bf(l > 0.f ? acc / l : 0.f);
   }
 }
 
@@ -568,8 +692,9 @@ bool strides_aligned8(const int64_t* s, int n) {
 }
 
 int64_t decode_ws_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t D) {
-  const int64_t chunks = q3_cdiv(std::max<int64_t>(max_len, 1), kDecKeys);
-  return B * Hkv * chunks * (int64_t)dec_partial_floats((int)(Hq / std::max<int64_t>(Hkv, 1)), (int)D) *
+  (void)max_len;
+  // one record per (wave, pair) piece: at most one per pair plus one per wave boundary
+  return (kDecWavesTotal + B * Hkv) * (int64_t)dec_partial_floats((int)(Hq / std::max<int64_t>(Hkv, 1)), (int)D) *
          (int64_t)sizeof(float);
 }
 
@@ -690,13 +815,17 @@ int q3_decode_attention(const void* q, const void* k_cache, const void* v_cache,
   const bool aligned = q3_aligned(q, 16) && q3_aligned(k_cache, 16) && q3_aligned(v_cache, 16) &&
                        strides_aligned8(strides, 8);
   // The MFMA path addresses the cache with 32-bit buffer offsets.
-  if (dtype == Q3_BF16 && D == 128 && p.groups <= 32 && aligned && (max_len + 1) * strides[4] * 2 < 0x7fffffffLL &&
-      (max_len + 1) * strides[7] * 2 < 0x7fffffffLL) {
+  if (dtype == Q3_BF16 && D == 128 && p.groups <= 32 && B <= kDecMaxBatch && aligned &&
+      (max_len + 1) * strides[4] * 2 < 0x7fffffffLL && (max_len + 1) * strides[7] * 2 < 0x7fffffffLL) {
     Q3_REQUIRE(workspace != nullptr && workspace_bytes >= decode_ws_bytes(B, Hq, Hkv, max_len, D), Q3_ERR_WORKSPACE);
     p.partial = static_cast<float*>(workspace);
-    p.max_chunks = (int)q3_cdiv(max_len, kDecKeys);
-    hipLaunchKernelGGL(flash_decode_kernel<kDecWaves>, dim3((unsigned)p.max_chunks, (unsigned)(B * Hkv)),
-                       dim3(64 * kDecWaves), 0, st, p);
+    const dim3 grid(kDecBlocks), block(64 * kDecBlockWaves);
+    if (p.groups <= 4)
+      hipLaunchKernelGGL((flash_decode_kernel<1, 4>), grid, block, 0, st, p);
+    else if (p.groups <= 8)
+      hipLaunchKernelGGL((flash_decode_kernel<2, 4>), grid, block, 0, st, p);
+    else
+      hipLaunchKernelGGL((flash_decode_kernel<8, 3>), grid, block, 0, st, p);
     Q3_LAUNCH_CHECK();
     hipLaunchKernelGGL(flash_decode_combine<128>, dim3((unsigned)(B * Hkv)), dim3(256), 0, st, p);
     Q3_LAUNCH_CHECK();

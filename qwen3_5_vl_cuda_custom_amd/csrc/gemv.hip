@@ -1,0 +1,458 @@
+// Weight-streaming GEMV for decode-shaped GEMMs (M <= 32 activation rows):
+//
+//   C[m, n] = sum_k X[m, k] * W[n, k] (+ bias[n]) (+ R[m, n])      plain
+//   C[m, n] = silu(X . Wg[n]) * (X . Wu[n])                        SwiGLU
+//
+// At M <= 32 the GEMM moves N*K*2 bytes of weights for 2*M*N*K FLOP, so it is
+// bound by HBM and the kernel is built to keep the weight stream at full rate:
+//
+//  * Work units are (tile, k-stage) pairs: a tile is 128 weight rows (plain:
+//    128 output columns; SwiGLU: 32-row gate / up groups alternating, 64
+//    output columns), a stage is 64 k (128 bytes of every row). One block
+//    runs per CU and takes an equal contiguous range of the tile-major unit
+//    order (stream-K), so every CU streams the same number of bytes whatever
+//    N and K are.
+//  * A stage (128 weight rows + the 32 X rows) goes global -> LDS with
+//    buffer_load ... lds; a 4-stage ring keeps three stages in flight while
+//    the MFMAs (v_mfma_f32_32x32x16_bf16, W rows as A, X rows as B) consume
+//    the fourth. One DMA instruction fills 8 rows x 128 bytes; the lane that
+//    lands at slot s of row r fetches chunk s ^ swz(r), so fragment reads are
+//    bank-conflict free.
+//  * A tile that lies inside one block's range is finished in that block. A
+//    tile split between blocks is summed by the block that contributes its
+//    last piece: each block writes its fp32 piece with device-coherent stores,
+//    and bumps the tile's counter only once its own pipeline waits have shown
+//    those stores complete (vmcnt retires in order, so the wait for a later
+//    stage's DMA covers them); the counter's return values are read after the
+//    loop, and the block that completes a count sums the pieces in piece
+//    order (deterministic) and resets the counter to zero.
+#include "gemv.h"
+
+namespace q3 {
+namespace {
+
+constexpr int kGvBK = 64;                     // k per stage
+constexpr int kGvBN = 128;                    // weight rows per tile
+constexpr int kGvRows = kGvBN + 32;           // rows per stage: W tile + X
+constexpr int kGvStage = kGvRows * kGvBK;     // elements per stage
+constexpr int kGvPerWave = kGvRows / 8 / 4;   // DMA instructions per wave per stage
+constexpr int kGvStages = 4;                  // LDS ring depth
+constexpr int kGvGrid = 256;                  // one block per CU (MI355X)
+constexpr int kGvPiece = 32 * kGvBN;          // floats per partial piece: [m 32][tile row 128]
+// The workspace starts with a counter region of fixed size, so calls of any
+// shape that share a workspace never write partials over another shape's
+// counters.
+constexpr int kGvMaxTiles = 4096;
+constexpr int64_t kGvCounterBytes = kGvMaxTiles * 4;
+
+struct GemvParams {
+  GemvArgs a;
+  int* counters;
+  float* partial;
+  int n_tiles, k_stages, total, grid, max_pieces;
+  int vec4, vec8;  // C (and R) rows allow 8-byte / 16-byte vector access
+};
+
+__device__ __forceinline__ int gv_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+// Block whose unit range [b*total/G, (b+1)*total/G) contains unit u.
+__host__ __device__ inline int gv_block_of(int64_t u, int G, int64_t total) {
+  return (int)(((u + 1) * G - 1) / total);
+}
+
+// Wave-uniform weight source of the plain tile starting at output column col.
+struct SegPick {
+  const bf16* w;
+  const bf16* b;
+  int start, end;
+};
+__device__ __forceinline__ SegPick seg_pick(const WeightSegments& sg, int N, int col) {
+  const int s = __builtin_amdgcn_readfirstlane(segment_of(sg, col));
+  SegPick r;
+  r.w = pick4(s, uniform_ptr(sg.w[0]), uniform_ptr(sg.w[1]), uniform_ptr(sg.w[2]), uniform_ptr(sg.w[3]));
+  r.b = pick4(s, uniform_ptr(sg.b[0]), uniform_ptr(sg.b[1]), uniform_ptr(sg.b[2]), uniform_ptr(sg.b[3]));
+  r.start = pick4(s, __builtin_amdgcn_readfirstlane(sg.start[0]), __builtin_amdgcn_readfirstlane(sg.start[1]),
+                  __builtin_amdgcn_readfirstlane(sg.start[2]), __builtin_amdgcn_readfirstlane(sg.start[3]));
+  const int nxt = pick4(s, __builtin_amdgcn_readfirstlane(sg.start[1]), __builtin_amdgcn_readfirstlane(sg.start[2]),
+                        __builtin_amdgcn_readfirstlane(sg.start[3]), N);
+  r.end = s + 1 < sg.n ? nxt : N;
+  return r;
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + __expf(-g)) * u; }
+
+template <bool SWIGLU>
+__global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
+  constexpr int NST = kGvStages;
+  __shared__ __attribute__((aligned(1024))) bf16 ring[NST * kGvStage];
+  __shared__ float xbuf[2][32 * 33];  // SwiGLU: up accumulators handed to the gate waves
+  __shared__ int s_last[2];
+
+  const GemvArgs& a = p.a;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, h = lane >> 5;
+  const int G = p.grid, b = blockIdx.x;
+  const int64_t total = p.total;
+  const int u0 = (int)((int64_t)b * total / G), u1 = (int)((int64_t)(b + 1) * total / G);
+  const int KS = p.k_stages, K = a.K, N = a.N, M = a.M;
+
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.X, (int64_t)M * a.ldx * 2);
+  const __amdgpu_buffer_rsrc_t rg = make_rsrc(a.seg.w[0], (int64_t)N * a.ldw * 2);           // SwiGLU gate
+  const __amdgpu_buffer_rsrc_t ru = make_rsrc(SWIGLU ? a.W2 : a.seg.w[0], (int64_t)N * a.ldw * 2);  // SwiGLU up
+  const uint32_t lbase = lds_addr(ring);
+
+  // DMA of unit u's stage into ring slot u % NST (zeros past the range).
+  auto issue = [&](int u) {
+    const bool live = u < u1;
+    const int t = u / KS;
+    const int k0 = (u - t * KS) * kGvBK;
+    const uint32_t sbase = lbase + (uint32_t)((u % NST) * kGvStage * 2);
+    __amdgpu_buffer_rsrc_t rw = rg;
+    int rowbase = 0, lim = 0;
+    if constexpr (!SWIGLU) {
+      const SegPick sp = seg_pick(a.seg, N, t * kGvBN);
+      rw = make_rsrc(sp.w, (int64_t)(sp.end - sp.start) * a.ldw * 2);
+      rowbase = t * kGvBN - sp.start;
+      lim = sp.end - t * kGvBN;
+    }
+#pragma unroll
+    for (int i = 0; i < kGvPerWave; ++i) {
+      const int j = wave + 4 * i;  // stage rows 8j .. 8j+7
+      const int r = 8 * j + (lane >> 3);
+      const int k = k0 + 8 * ((lane & 7) ^ gv_swz(r));
+      const uint32_t dst = sbase + (uint32_t)(j * 1024);
+      if (i < 4) {  // weight rows
+        if constexpr (SWIGLU) {
+          const int grp = j >> 2;
+          const int n = t * 64 + (grp >> 1) * 32 + (r & 31);
+          const uint32_t off = (live && n < N && k < K) ? (uint32_t)(((int64_t)n * a.ldw + k) * 2) : kOOB;
+          dma16((grp & 1) ? ru : rg, off, dst);
+        } else {
+          const uint32_t off = (live && r < lim && k < K) ? (uint32_t)(((int64_t)(rowbase + r) * a.ldw + k) * 2) : kOOB;
+          dma16(rw, off, dst);
+        }
+      } else {  // X rows
+        const int m = r - kGvBN;
+        const uint32_t off = (live && m < M && k < K) ? (uint32_t)(((int64_t)m * a.ldx + k) * 2) : kOOB;
+        dma16(rx, off, dst);
+      }
+    }
+  };
+
+  // Epilogue of a tile finished inside this block.
+  auto store_whole = [&](int t, const floatx16& acc) {
+    if constexpr (SWIGLU) {
+      if (wave & 1) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xbuf[wave >> 1][(8 * (r >> 2) + 4 * h + (r & 3)) * 33 + l32] = acc[r];
+      }
+      __syncthreads();
+      if (!(wave & 1) && l32 < M) {
+        bf16* crow = a.C + (int64_t)l32 * a.ldc;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int nn = 8 * g + 4 * h;
+          const int n = t * 64 + (wave >> 1) * 32 + nn;
+          float o[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = silu_mul(acc[4 * g + e], xbuf[wave >> 1][(nn + e) * 33 + l32]);
+          if (p.vec4 && n + 3 < N) {
+            *reinterpret_cast<bf16x4*>(crow + n) = bf16x4{f2bf(o[0]), f2bf(o[1]), f2bf(o[2]), f2bf(o[3])};
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (n + e < N) crow[n + e] = f2bf(o[e]);
+          }
+        }
+      }
+      __syncthreads();
+    } else {
+      if (l32 >= M) return;
+      const SegPick sp = seg_pick(a.seg, N, t * kGvBN);
+      const bf16* bias = sp.b ? sp.b - sp.start : nullptr;
+      bf16* crow = a.C + (int64_t)l32 * a.ldc;
+      const bf16* rrow = a.R ? a.R + (int64_t)l32 * a.ldr : nullptr;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = t * kGvBN + 32 * wave + 8 * g + 4 * h;
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = acc[4 * g + e];
+        if (p.vec4 && n + 3 < N) {
+          if (bias) {
+            const bf16x4 bv = *reinterpret_cast<const bf16x4*>(bias + n);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] += bf2f(bv[e]);
+          }
+          if (rrow) {
+            const bf16x4 rv = *reinterpret_cast<const bf16x4*>(rrow + n);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] += bf2f(rv[e]);
+          }
+          *reinterpret_cast<bf16x4*>(crow + n) = bf16x4{f2bf(o[0]), f2bf(o[1]), f2bf(o[2]), f2bf(o[3])};
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (n + e >= N) continue;
+            float v = o[e];
+            if (bias) v += bf2f(bias[n + e]);
+            if (rrow) v += bf2f(rrow[n + e]);
+            crow[n + e] = f2bf(v);
+          }
+        }
+      }
+    }
+  };
+
+  // Sum of a split tile's pieces (in piece order) and its epilogue.
+  auto reduce_tile = [&](int t, int npieces) {
+    const __amdgpu_buffer_rsrc_t rp =
+        make_rsrc(p.partial + (int64_t)t * p.max_pieces * kGvPiece, (int64_t)p.max_pieces * kGvPiece * 4);
+    const int m = tid >> 3;
+    if constexpr (SWIGLU) {
+      const int cc0 = (tid & 7) * 8;
+      const int nng = (cc0 >> 5) * 64 + (cc0 & 31);
+      floatx4 g0 = {}, g1 = {}, v0 = {}, v1 = {};
+      for (int pc = 0; pc < npieces; ++pc) {
+        const uint32_t o = (uint32_t)((pc * kGvPiece + m * kGvBN + nng) * 4);
+        g0 += __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o, 0, 16));
+        g1 += __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o + 16, 0, 16));
+        v0 += __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o + 128, 0, 16));
+        v1 += __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o + 144, 0, 16));
+      }
+      if (m >= M) return;
+      const int n0 = t * 64 + cc0;
+      float f[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        f[e] = silu_mul(g0[e], v0[e]);
+        f[4 + e] = silu_mul(g1[e], v1[e]);
+      }
+      bf16* crow = a.C + (int64_t)m * a.ldc;
+      if (p.vec8 && n0 + 7 < N) {
+        *reinterpret_cast<bf16x8*>(crow + n0) = pack8(f);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (n0 + e < N) crow[n0 + e] = f2bf(f[e]);
+      }
+    } else {
+      const int nn0 = (tid & 7) * 16;
+      floatx4 s[4] = {};
+      for (int pc = 0; pc < npieces; ++pc) {
+        const uint32_t o = (uint32_t)((pc * kGvPiece + m * kGvBN + nn0) * 4);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          s[q] += __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o + 16 * q, 0, 16));
+      }
+      if (m >= M) return;
+      const int n0 = t * kGvBN + nn0;
+      const SegPick sp = seg_pick(a.seg, N, t * kGvBN);
+      const bf16* bias = sp.b ? sp.b - sp.start : nullptr;
+      float f[16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) f[4 * q + e] = s[q][e];
+      bf16* crow = a.C + (int64_t)m * a.ldc;
+      const bf16* rrow = a.R ? a.R + (int64_t)m * a.ldr : nullptr;
+      if (p.vec8 && n0 + 15 < N) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          if (bias) {
+            const bf16x8 bv = *reinterpret_cast<const bf16x8*>(bias + n0 + 8 * hh);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[8 * hh + e] += bf2f(bv[e]);
+          }
+          if (rrow) {
+            const bf16x8 rv = *reinterpret_cast<const bf16x8*>(rrow + n0 + 8 * hh);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[8 * hh + e] += bf2f(rv[e]);
+          }
+          *reinterpret_cast<bf16x8*>(crow + n0 + 8 * hh) = pack8(f + 8 * hh);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          if (n0 + e >= N) continue;
+          float v = f[e];
+          if (bias) v += bf2f(bias[n0 + e]);
+          if (rrow) v += bf2f(rrow[n0 + e]);
+          crow[n0 + e] = f2bf(v);
+        }
+      }
+    }
+  };
+
+  // Split tiles this block contributes to (at most its first and its last).
+  int np_ = 0, ninc = 0;
+  int pt0 = 0, pt1 = 0, pn0 = 0, pn1 = 0, pu0 = 0;
+  int old0 = 0, old1 = 0;  // counter values returned to thread 0
+  auto bump = [&](int idx) {
+    if (tid == 0) {
+      const int v = __hip_atomic_fetch_add(&p.counters[idx == 0 ? pt0 : pt1], 1, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+      if (idx == 0) old0 = v;
+      else old1 = v;
+    }
+  };
+
+  floatx16 acc = floatx16{};
+#pragma unroll
+  for (int s = 0; s < NST - 1; ++s) issue(u0 + s);
+
+  for (int u = u0; u < u1; ++u) {
+    vm_wait<(NST - 2) * kGvPerWave>();  // this wave's DMAs of stage u have landed
+    __syncthreads();                     // ... and every wave's; slot (u - 1) % NST is free
+    // The piece stored at iteration pu0 preceded the DMAs issued from
+    // iteration pu0 + 1 on, so the wait above has retired it once u >= pu0 + NST.
+    if (ninc == 0 && np_ > 0 && u >= pu0 + NST) {
+      bump(0);
+      ninc = 1;
+    }
+    issue(u + NST - 1);
+    const bf16* st = ring + (u % NST) * kGvStage;
+    const int ra = 32 * wave + l32, rb = kGvBN + l32;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = 2 * q + h;
+      const bf16x8 fa = *reinterpret_cast<const bf16x8*>(st + ra * kGvBK + ((c ^ gv_swz(ra)) << 3));
+      const bf16x8 fb = *reinterpret_cast<const bf16x8*>(st + rb * kGvBK + ((c ^ gv_swz(rb)) << 3));
+      acc = mfma32x32x16(fa, fb, acc);
+    }
+    const int t = u / KS;
+    if (u - t * KS == KS - 1 || u == u1 - 1) {
+      if (t * KS >= u0 && t * KS + KS <= u1) {
+        store_whole(t, acc);
+      } else {
+        const int fb = gv_block_of((int64_t)t * KS, G, total);
+        const int lb = gv_block_of((int64_t)t * KS + KS - 1, G, total);
+        const int piece = b - fb;
+        const __amdgpu_buffer_rsrc_t rp =
+            make_rsrc(p.partial + (int64_t)t * p.max_pieces * kGvPiece, (int64_t)p.max_pieces * kGvPiece * 4);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int nn = 32 * wave + 8 * g + 4 * h;
+          const floatx4 v = {acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]};
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rp,
+                                                 (uint32_t)((piece * kGvPiece + l32 * kGvBN + nn) * 4), 0, 16);
+        }
+        if (np_ == 0) {
+          pt0 = t;
+          pn0 = lb - fb + 1;
+          pu0 = u;
+        } else {
+          pt1 = t;
+          pn1 = lb - fb + 1;
+        }
+        ++np_;
+      }
+      acc = floatx16{};
+    }
+  }
+
+  vm_wait<0>();  // every piece store of this wave has completed
+  __syncthreads();
+  if (ninc == 0 && np_ > 0) bump(0);
+  if (np_ > 1) bump(1);
+  if (tid == 0) {
+    vm_wait<0>();
+    s_last[0] = np_ > 0 && old0 == pn0 - 1;
+    s_last[1] = np_ > 1 && old1 == pn1 - 1;
+  }
+  __syncthreads();
+  if (s_last[0]) {
+    reduce_tile(pt0, pn0);
+    if (tid == 0) __hip_atomic_store(&p.counters[pt0], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (s_last[1]) {
+    reduce_tile(pt1, pn1);
+    if (tid == 0) __hip_atomic_store(&p.counters[pt1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+struct GemvPlan {
+  int n_tiles, k_stages, total, grid, max_pieces;
+  int64_t counter_bytes, bytes;
+};
+
+GemvPlan gemv_plan(int64_t N, int64_t K, bool swiglu) {
+  GemvPlan pl{};
+  pl.n_tiles = (int)q3_cdiv(N, swiglu ? 64 : kGvBN);
+  pl.k_stages = (int)q3_cdiv(K, kGvBK);
+  const int64_t total = (int64_t)pl.n_tiles * pl.k_stages;
+  pl.total = (int)total;
+  pl.grid = (int)std::min<int64_t>(kGvGrid, total);
+  int mp = 0;
+  for (int t = 0; t < pl.n_tiles; ++t) {
+    const int fb = gv_block_of((int64_t)t * pl.k_stages, pl.grid, total);
+    const int lb = gv_block_of((int64_t)t * pl.k_stages + pl.k_stages - 1, pl.grid, total);
+    if (lb > fb) mp = std::max(mp, lb - fb + 1);
+  }
+  pl.max_pieces = mp;
+  pl.counter_bytes = kGvCounterBytes;
+  pl.bytes = pl.counter_bytes + (int64_t)pl.n_tiles * mp * kGvPiece * 4;
+  return pl;
+}
+
+}  // namespace
+
+bool gemv_eligible(const GemvArgs& a) {
+  if (a.M < 1 || a.M > kGemvMaxRows || a.N < 1 || a.K < 8 || (a.K % 8) != 0) return false;
+  if (q3_cdiv(a.N, a.W2 ? 64 : kGvBN) > kGvMaxTiles) return false;
+  if (a.seg.n < 1 || a.seg.n > 4) return false;
+  if (!q3_aligned(a.X, 16) || (a.ldx % 8) != 0 || (a.ldw % 8) != 0) return false;
+  if ((int64_t)a.M * a.ldx * 2 >= 0x7fffffffLL) return false;
+  const bool swiglu = a.W2 != nullptr;
+  if (swiglu) {
+    if (a.seg.n != 1 || !q3_aligned(a.W2, 16)) return false;
+    if (!q3_aligned(a.seg.w[0], 16) || (int64_t)a.N * a.ldw * 2 >= 0x7fffffffLL) return false;
+    return true;
+  }
+  for (int i = 0; i < a.seg.n; ++i) {
+    const int64_t end = i + 1 < a.seg.n ? a.seg.start[i + 1] : a.N;
+    if (!a.seg.w[i] || !q3_aligned(a.seg.w[i], 16) || (a.seg.start[i] % kGvBN) != 0) return false;
+    if ((end - a.seg.start[i]) * a.ldw * 2 >= 0x7fffffffLL) return false;
+  }
+  return true;
+}
+
+int64_t gemv_workspace_bytes(int64_t N, int64_t K, bool swiglu) {
+  if (N <= 0 || K <= 0) return 0;
+  return gemv_plan(N, K, swiglu).bytes;
+}
+
+int gemv_launch(const GemvArgs& a, void* ws, int64_t ws_bytes, hipStream_t st) {
+  const bool swiglu = a.W2 != nullptr;
+  const GemvPlan pl = gemv_plan(a.N, a.K, swiglu);
+  Q3_REQUIRE(ws != nullptr && ws_bytes >= pl.bytes, Q3_ERR_WORKSPACE);
+  Q3_REQUIRE(q3_aligned(ws, 256), Q3_ERR_ALIGN);
+  GemvParams p{};
+  p.a = a;
+  p.counters = static_cast<int*>(ws);
+  p.partial = reinterpret_cast<float*>(static_cast<char*>(ws) + pl.counter_bytes);
+  p.n_tiles = pl.n_tiles;
+  p.k_stages = pl.k_stages;
+  p.total = pl.total;
+  p.grid = pl.grid;
+  p.max_pieces = pl.max_pieces;
+  const bool r_ok4 = a.R == nullptr || (q3_aligned(a.R, 8) && a.ldr % 4 == 0);
+  const bool r_ok8 = a.R == nullptr || (q3_aligned(a.R, 16) && a.ldr % 8 == 0);
+  bool b_ok4 = true, b_ok8 = true;
+  for (int i = 0; i < a.seg.n; ++i) {
+    if (!a.seg.b[i]) continue;
+    b_ok4 = b_ok4 && q3_aligned(a.seg.b[i], 8);
+    b_ok8 = b_ok8 && q3_aligned(a.seg.b[i], 16);
+  }
+  p.vec4 = q3_aligned(a.C, 8) && a.ldc % 4 == 0 && r_ok4 && b_ok4;
+  p.vec8 = q3_aligned(a.C, 16) && a.ldc % 8 == 0 && r_ok8 && b_ok8;
+  if (swiglu)
+    hipLaunchKernelGGL(gemv_kernel<true>, dim3(pl.grid), dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL(gemv_kernel<false>, dim3(pl.grid), dim3(256), 0, st, p);
+  Q3_LAUNCH_CHECK();
+  return Q3_OK;
+}
+
+}  // namespace q3

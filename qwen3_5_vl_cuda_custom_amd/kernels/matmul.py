@@ -38,7 +38,7 @@ def matmul(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
             r2 = r2.contiguous()
     b = bias.contiguous() if bias is not None else None
     dt = _lib.dtype_code(x.dtype)
-    ws, nws = _lib.workspace(_lib.lib().q3_matmul_workspace_bytes(M, N, K, dt, 0), x.device)
+    ws, nws = _lib.gemm_workspace(_lib.lib().q3_matmul_workspace_bytes(M, N, K, dt, 0), x.device)
     _lib.call("q3_matmul", x2.data_ptr(), w.data_ptr(), _lib.ptr(b), _lib.ptr(r2), y2.data_ptr(), M, N, K,
               x2.stride(0), w.stride(0), r2.stride(0) if r2 is not None else 0, y2.stride(0), dt,
               _lib.ptr(ws), nws, _lib.stream())
@@ -59,7 +59,7 @@ def matmul_swiglu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor) -> 
     M = x2.shape[0]
     y = torch.empty((*x.shape[:-1], N), dtype=x.dtype, device=x.device)
     dt = _lib.dtype_code(x.dtype)
-    ws, nws = _lib.workspace(_lib.lib().q3_matmul_workspace_bytes(M, N, K, dt, 1), x.device)
+    ws, nws = _lib.gemm_workspace(_lib.lib().q3_matmul_workspace_bytes(M, N, K, dt, 1), x.device)
     _lib.call("q3_matmul_swiglu", x2.data_ptr(), wg.data_ptr(), wu.data_ptr(), y.data_ptr(), M, N, K,
               x2.stride(0), wg.stride(0), N, dt, _lib.ptr(ws), nws, _lib.stream())
     return y
@@ -95,7 +95,7 @@ def matmul_segments(x: torch.Tensor, weights, biases=None, *, out: torch.Tensor 
     y2 = y.view(-1, N)
     dt = _lib.dtype_code(x.dtype)
     n_arr = _lib.i64s(*ns)
-    ws, nws = _lib.workspace(_lib.lib().q3_matmul_segments_workspace_bytes(M, n_arr, len(ns), K, dt), x.device)
+    ws, nws = _lib.gemm_workspace(_lib.lib().q3_matmul_segments_workspace_bytes(M, n_arr, len(ns), K, dt), x.device)
     _lib.call("q3_matmul_segments", x2.data_ptr(), _lib.ptrs(*ws_),
               _lib.ptrs(*bs) if any(b is not None for b in bs) else None, n_arr, len(ns), y2.data_ptr(), M, K,
               x2.stride(0), K, y2.stride(0), dt, _lib.ptr(ws), nws, _lib.stream())

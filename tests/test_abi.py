@@ -101,8 +101,9 @@ def test_attention_validation():
     # (B=2, Hq=8, D=128) q/o; (B, Hkv=2, cap=100, D) caches
     d = _lib.i64s(8 * 128, 128, 2 * 100 * 128, 100 * 128, 128, 2 * 100 * 128, 100 * 128, 128, 8 * 128, 128)
     assert L.q3_decode_attention(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 8, 2, 128, 100, d, 0.1, 1, None, 0, None) == -6
-    # one (m, l, O) record per (sequence, KV head, 128-key chunk) for the 4 heads of the group
-    assert L.q3_decode_attention_workspace_bytes(32, 32, 8, 8193, 128) == 32 * 8 * 65 * 4 * 130 * 4
+    # one (m, l, O) record of the group's 4 heads per piece of a (sequence, KV head) pair: at most one
+    # per pair plus one per boundary between the 512 waves of the grid
+    assert L.q3_decode_attention_workspace_bytes(32, 32, 8, 8193, 128) == (512 + 32 * 8) * 4 * 130 * 4
 
 
 def test_rope_validation():

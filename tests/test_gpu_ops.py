@@ -198,15 +198,35 @@ def test_flash_attention_sq_ne_sk_noncausal():
     assert_bf16_close(o, O.flash_attention(f32(q), f32(k), f32(v), 128 ** -0.5, False, 4), what="Sq != Sk")
 
 
-@pytest.mark.parametrize("groups", [4, 8])
+@pytest.mark.parametrize("groups", [1, 3, 4, 8, 16])
 def test_decode_attention_ragged(groups):
-    B, Hkv, cap, D = 6, 2, 1100, 128
-    lens = torch.tensor([1, 5, 255, 256, 257, 1100], dtype=torch.int32)
+    B, Hkv, cap, D = 7, 2, 1100, 128
+    lens = torch.tensor([1, 5, 0, 255, 256, 257, 1100], dtype=torch.int32)
     q = rnd(B, Hkv * groups, D, seed=32)
     kc, vc = rnd(B, Hkv, cap, D, seed=33), rnd(B, Hkv, cap, D, seed=34)
     o = K.decode_attention(gpu(q), gpu(kc), gpu(vc), gpu(lens), D ** -0.5)
     ref = O.decode_attention(f32(q)[:, :, None], f32(kc), f32(vc), lens, D ** -0.5, groups)[:, :, 0]
     assert_bf16_close(o, ref, what=f"decode groups={groups}")
+
+
+def test_decode_attention_c3_lengths():
+    # the C3 decode shape: 32 sequences x 8 KV heads, lengths U[1024, 8192] (a work split where
+    # pairs straddle waves), plus a second call with most sequences short (pairs inside one wave)
+    B, Hkv, G, D, cap = 32, 8, 4, 128, 8193
+    g = torch.Generator().manual_seed(0)
+    gd = torch.Generator(device="cuda").manual_seed(0)
+    kd = torch.randn(B, Hkv, cap, D, generator=gd, device="cuda").to(torch.bfloat16)
+    vd = torch.randn(B, Hkv, cap, D, generator=gd, device="cuda").to(torch.bfloat16)
+    q = torch.randn(B, Hkv * G, D, generator=g).to(torch.bfloat16)
+    qd = gpu(q)
+    for lens in (torch.randint(1024, 8193, (B,), generator=g, dtype=torch.int32),
+                 torch.randint(1, 40, (B,), generator=g, dtype=torch.int32)):
+        o = K.decode_attention(qd, kd, vd, gpu(lens), D ** -0.5).float().cpu()
+        for b in (0, 7, 31):  # per-sequence fp32 reference on a sample of sequences
+            L = int(lens[b])
+            kb, vb = kd[b:b + 1, :, :L].float().cpu(), vd[b:b + 1, :, :L].float().cpu()
+            ref = O.flash_attention(q[b:b + 1, :, None].float(), kb, vb, D ** -0.5, False, G)[0, :, 0]
+            assert_bf16_close(o[b], ref, what=f"C3 decode b={b} L={L}")
 
 
 # ------------------------------------------------------------------ rotary
