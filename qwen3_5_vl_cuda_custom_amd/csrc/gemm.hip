@@ -3,7 +3,7 @@
 //   Y[m, n] = sum_k X[m, k] * W[n, k] (+ bias[n]) (+ R[m, n])   (nn.Linear layout)
 //
 // Three device paths, chosen on the host from the shape:
-//  * tiled   : bf16, M > 32     -> 32x32x16 MFMA, LDS double-buffered tiles
+//  * tiled   : bf16, M > 32     -> 32x32x16 MFMA over a ring of direct-to-LDS tiles
 //  * gemv    : bf16, M <= 32    -> weight-streaming stream-K kernel (gemv.hip)
 //  * generic : fp32, or bf16 whose rows are not 16-byte aligned -> SIMT fp32
 #include "gemm_kernels.h"
@@ -95,23 +95,38 @@ int launch_generic(const void* x, const void* w, const void* w2, const void* bia
 // =====================================================================
 // Tiled MFMA path.
 // =====================================================================
-template <int BM, int BN, int WM, int WN, int EPI>
+template <int BM, int BN, int WM, int WN, int EPI, int NST, int BKT>
 int launch_tiled_cfg(GemmParams p, int64_t batch, hipStream_t st) {
   constexpr int BN_OUT = (EPI == kEpiSwiGLU) ? BN / 2 : BN;
   const int64_t tiles = q3_cdiv(p.M, BM) * q3_cdiv(p.N, BN_OUT);
   p.group_m = 8;
-  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, EPI, false>), dim3((unsigned)tiles, 1, (unsigned)batch),
-                     dim3(WM * WN * 64), 0, st, p);
+  hipLaunchKernelGGL((gemm_bf16_dma_kernel<BM, BN, WM, WN, EPI, false, NST, BKT>),
+                     dim3((unsigned)tiles, 1, (unsigned)batch), dim3(WM * WN * 64), 0, st, p);
   Q3_LAUNCH_CHECK();
   return Q3_OK;
 }
 
+// Tile configuration by estimated time: full waves of blocks over 256 CUs,
+// times the block's work over its relative MFMA efficiency (measured on
+// MI355X): 256x256 (8 waves; 1 block per CU) 1.0, 256x192 (8 waves, 64-wide
+// K stages; plain epilogue only) 0.95, 128x128 (4 waves; 2 blocks per CU) 0.75.
 template <int EPI>
 int launch_tiled(GemmParams p, int64_t batch, hipStream_t st) {
-  // Big tiles when they still give at least one full wave of 256 CUs.
-  const int64_t big = q3_cdiv(p.M, 256) * q3_cdiv(p.N, EPI == kEpiSwiGLU ? 128 : 256) * batch;
-  if (big >= 256) return launch_tiled_cfg<256, 256, 2, 4, EPI>(p, batch, st);
-  return launch_tiled_cfg<128, 128, 2, 2, EPI>(p, batch, st);
+  constexpr int kCUs = 256;
+  auto waves = [](int64_t tiles, int64_t slots) { return (double)q3_cdiv(tiles, slots); };
+  const int bo = EPI == kEpiSwiGLU ? 128 : 256;
+  const double cost_a = waves(q3_cdiv(p.M, 256) * q3_cdiv(p.N, bo) * batch, kCUs) * 256.0 * 256.0;
+  const double cost_c =
+      waves(q3_cdiv(p.M, 128) * q3_cdiv(p.N, bo / 2) * batch, 2 * kCUs) * 2.0 * 128.0 * 128.0 / 0.75;
+  if constexpr (EPI == kEpiSwiGLU) {
+    if (cost_c < cost_a) return launch_tiled_cfg<128, 128, 2, 2, EPI, 4, 32>(p, batch, st);
+    return launch_tiled_cfg<256, 256, 2, 4, EPI, 2, 64>(p, batch, st);
+  } else {
+    const double cost_b = waves(q3_cdiv(p.M, 256) * q3_cdiv(p.N, 192) * batch, kCUs) * 256.0 * 192.0 / 0.95;
+    if (cost_c < cost_a && cost_c < cost_b) return launch_tiled_cfg<128, 128, 2, 2, EPI, 4, 32>(p, batch, st);
+    if (cost_b < cost_a) return launch_tiled_cfg<256, 192, 4, 2, EPI, 2, 64>(p, batch, st);
+    return launch_tiled_cfg<256, 256, 2, 4, EPI, 4, 32>(p, batch, st);
+  }
 }
 
 bool bf16_rows_ok(const void* base, int64_t ld, int64_t K) {
@@ -186,7 +201,9 @@ int segments_impl(const void* x, const void* const* w, const void* const* bias, 
   for (int64_t i = 0; i < nseg; ++i) {
     Q3_REQUIRE(w[i], Q3_ERR_NULL);
     Q3_REQUIRE(n[i] >= 0, Q3_ERR_SHAPE);
-    tiled_ok = tiled_ok && (N % 256 == 0) && bf16_rows_ok(w[i], ldw, K);
+    // Each DMA instruction of the tiled kernels loads 16 (or 8) weight rows
+    // of one segment.
+    tiled_ok = tiled_ok && (N % 16 == 0) && bf16_rows_ok(w[i], ldw, K);
     N += n[i];
   }
   Q3_REQUIRE(M >= 0 && K >= 0 && N < (1ll << 31) && ldx >= K && ldw >= K && ldc >= N, Q3_ERR_SHAPE);
@@ -309,7 +326,7 @@ int q3_batched_gemm(const void* x, const void* w, void* y, int64_t E, int64_t M,
     p.bsX = M * K;
     p.bsW = N * K;
     p.bsC = M * N;
-    return launch_tiled_cfg<128, 128, 2, 2, kEpiStore>(p, E, static_cast<hipStream_t>(stream));
+    return launch_tiled_cfg<128, 128, 2, 2, kEpiStore, 4, 32>(p, E, static_cast<hipStream_t>(stream));
   }
   return matmul_impl(x, w, nullptr, nullptr, nullptr, y, M, N, K, E, K, K, 0, N, M * K, N * K, M * N, dtype, false,
                      nullptr, 0, static_cast<hipStream_t>(stream));

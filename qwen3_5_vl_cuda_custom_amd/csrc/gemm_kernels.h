@@ -120,35 +120,10 @@ __device__ __forceinline__ bool tile_ctx(const GemmParams& p, TileCtx& t) {
   }
   const int rows_m = m_end - m_begin;
   const int n0_out = tile_n * BN_OUT;
-  // Stacked weights: a tile never straddles segments (the host checks that
-  // every segment start is a multiple of BN). W and bias are re-based so that
-  // output column n still addresses row n.
+  // Stacked weights (p.seg.n > 1): W and bias stay those of the params; the
+  // kernel picks each loaded row's and each stored column's segment.
   int n_lim = p.N;
   const bf16* bias = p.bias;
-  if constexpr (!GROUPED && EPI == kEpiStore) {
-    if (p.seg.n > 1) {
-      // Constant-index selects keep the segment's pointers in scalar registers
-      // (a dynamic index into the by-value params would go through memory and
-      // make the buffer resource per-lane).
-      // Each field passes through readfirstlane before the select, so the
-      // selects cannot be folded back into one dynamically indexed load.
-      const int s = __builtin_amdgcn_readfirstlane(segment_of(p.seg, n0_out));
-      const bf16* sw = pick4(s, uniform_ptr(p.seg.w[0]), uniform_ptr(p.seg.w[1]), uniform_ptr(p.seg.w[2]),
-                             uniform_ptr(p.seg.w[3]));
-      const bf16* sb = pick4(s, uniform_ptr(p.seg.b[0]), uniform_ptr(p.seg.b[1]), uniform_ptr(p.seg.b[2]),
-                             uniform_ptr(p.seg.b[3]));
-      const int st0 = pick4(s, __builtin_amdgcn_readfirstlane(p.seg.start[0]),
-                            __builtin_amdgcn_readfirstlane(p.seg.start[1]),
-                            __builtin_amdgcn_readfirstlane(p.seg.start[2]),
-                            __builtin_amdgcn_readfirstlane(p.seg.start[3]));
-      const int nxt = pick4(s, __builtin_amdgcn_readfirstlane(p.seg.start[1]),
-                            __builtin_amdgcn_readfirstlane(p.seg.start[2]),
-                            __builtin_amdgcn_readfirstlane(p.seg.start[3]), p.N);
-      W = uniform_ptr(sw - (int64_t)st0 * p.ldw);
-      bias = sb ? uniform_ptr(sb - st0) : nullptr;
-      n_lim = s + 1 < p.seg.n ? nxt : p.N;
-    }
-  }
 
   // Everything here is block-uniform; integer division may still have left it
   // in vector registers. Pin it to scalars so buffer resources stay scalar.
@@ -162,6 +137,17 @@ __device__ __forceinline__ bool tile_ctx(const GemmParams& p, TileCtx& t) {
   t.bias = bias ? uniform_ptr(bias) : nullptr;
   t.C = const_cast<bf16*>(uniform_ptr(C));
   return true;
+}
+
+// Bias of the stacked-weight segment holding output column n (wave-uniform),
+// re-based so that it is indexed by the column (null when the segment has no
+// bias). Constant-index selects pinned to scalars: a dynamic index into the
+// by-value params would move them to memory.
+__device__ __forceinline__ const bf16* seg_bias(const WeightSegments& sg, int n) {
+  const int s = __builtin_amdgcn_readfirstlane(segment_of(sg, n));
+  const bf16* b = uniform_ptr(pick4(s, sg.b[0], sg.b[1], sg.b[2], sg.b[3]));
+  const int st = __builtin_amdgcn_readfirstlane(pick4(s, sg.start[0], sg.start[1], sg.start[2], sg.start[3]));
+  return b ? b - st : nullptr;
 }
 
 // Epilogue of one wave's (TN x TM) 32x32 accumulator tiles at wave offset
@@ -224,6 +210,10 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, const TileCtx& t
           float o[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) o[q] = c[i][j][4 * g + q];
+          if constexpr (EPI == kEpiStore) {
+            // segment starts are multiples of 16: both lane halves' columns share a segment
+            if (p.seg.n > 1) bias = seg_bias(p.seg, n - 4 * h);
+          }
           if (vec_ok && n + 3 < N) {
             if (bias) {
               const bf16x4 b = *reinterpret_cast<const bf16x4*>(bias + n);
@@ -259,67 +249,74 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, const TileCtx& t
   }
 }
 
-// Instruction order for one phase of the register-staged loop (one stage of
-// MFMAs, the next stage's global loads and the previous stage's LDS stores):
-// all fragment reads first, then the global loads and LDS stores spread
-// between MFMAs, so neither the memory pipes nor the MFMA pipe idle.
-template <int BK, int TN, int TM, int NV>
-__device__ __forceinline__ void sched_phase() {
-  constexpr int NR = (BK / 16) * (TN + TM), NM = (BK / 16) * TN * TM;
-  static_assert(NM >= 2 * NV, "not enough MFMAs to interleave the memory operations");
-  __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);  // DS reads
-#pragma unroll
-  for (int r = 0; r < NV; ++r) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
-  }
-  __builtin_amdgcn_sched_group_barrier(0x008, NM - 2 * NV, 0);
+// Swizzle of a BKT-element LDS row (BKT / 8 chunks of 16 bytes): chunk c of
+// row r sits at slot c ^ dma_swz<BKT>(r). For 32 or 16 consecutive rows read
+// one chunk each (a fragment read), the slots land on distinct 16-byte
+// positions of every 128-byte (8 rows) and 256-byte (16 rows) window, so
+// ds_read_b128 is conflict-free.
+template <int BKT>
+__device__ __forceinline__ int dma_swz(int r) {
+  if constexpr (BKT == 32) return ((r >> 1) & 3) ^ ((r >> 3) & 1);
+  else return (r & 7) ^ ((r >> 3) & 1);
 }
 
-template <int BM, int BN, int WM, int WN, int EPI, bool GROUPED>
-__global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_kernel(const GemmParams p) {
-  constexpr int NT = WM * WN * 64;
+// The tile GEMM with direct-to-LDS operand loads: stage kt's X and W tiles
+// (BKT-wide in K) go global -> LDS by buffer_load ... lds into a ring of NST
+// slots, issued NST - 1 stages ahead, so neither staging registers nor LDS
+// store instructions sit in the loop. One DMA instruction fills 64 / (BKT / 8)
+// rows; the lane that lands at slot s of row r fetches chunk s ^ dma_swz(r)
+// (an involution), which keeps fragment reads conflict-free.
+//
+// The loop is software-pipelined over 16-wide K steps: the fragments of step
+// q + 1 are read while the MFMAs of step q run, and each stage's barrier sits
+// before its last step's MFMAs (which overlap the first reads of the next
+// stage), so no wave starts a stage waiting on LDS.
+template <int BM, int BN, int WM, int WN, int EPI, bool GROUPED, int NST, int BKT>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmParams p) {
+  constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM;
   constexpr int WTN = BN / WN;
   constexpr int TM = WTM / 32;
   constexpr int TN = WTN / 32;
   static_assert(TM >= 1 && TN >= 1, "wave tile too small");
   static_assert(EPI != kEpiSwiGLU || (TN % 2 == 0), "SwiGLU pairs gate/up tiles");
+  static_assert(BKT == 32 || BKT == 64, "stage width");
   constexpr int BN_OUT = (EPI == kEpiSwiGLU) ? BN / 2 : BN;
+  constexpr int CH = BKT / 8;              // 16-byte chunks per LDS row
+  constexpr int KS = BKT / 16;             // MFMA K steps per stage
+  constexpr int kStage = (BM + BN) * BKT;  // elements per ring slot
+  constexpr int RPI = 64 / CH;             // rows per DMA instruction
+  constexpr int DX = BM / RPI, DW = BN / RPI;
+  static_assert((DX + DW) % NW == 0 && DX % NW == 0, "DMA instructions must split evenly over the waves");
+  constexpr int PX = DX / NW, PW = DW / NW;  // per wave and stage
+  static_assert(TN * TM >= TN + TM, "the interleave needs more MFMAs than fragment reads");
 
-  __shared__ __attribute__((aligned(16))) bf16 smem[2 * (BM + BN) * kBK];
+  __shared__ __attribute__((aligned(1024))) bf16 smem[NST * kStage];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave % WM;
   const int wn = wave / WM;
 
   TileCtx tc;
   if (!tile_ctx<BM, BN_OUT, EPI, GROUPED>(p, tc)) return;
   const int m_begin = tc.m_begin, rows_m = tc.rows_m, n0_out = tc.n0_out, n_lim = tc.n_lim;
-  const bf16* X = tc.X;
-  const bf16* W = tc.W;
-  const bf16* W2 = tc.W2;
-
-  constexpr int kStage = (BM + BN) * kBK;
-  // Register staging: thread t owns 16-byte chunks t + i*NT of the X tile
-  // (PX of them) and of the W tile (PW).
-  constexpr int PX = BM * kChunks / NT;
-  constexpr int PW = BN * kChunks / NT;
-  static_assert(BM * kChunks % NT == 0 && BN * kChunks % NT == 0, "tile not divisible by threads");
-
   const int K = p.K;
-  const int nk = (K + kBK - 1) / kBK;
+  const int nk = (K + BKT - 1) / BKT;
   const int64_t ldx = p.ldx, ldw = p.ldw;
 
-  // Per chunk: byte offset of its global row (kOOB: no such row) and its K chunk.
+  // Lane geometry of instruction i of this wave: tile row, and the global
+  // chunk that lands in the lane's LDS slot.
+  const int lrow = lane / CH, lslot = lane % CH;
   uint32_t xoff[PX], woff[PW];
+  int xc[PX], wc[PW];
+  const bf16* wsrc[PW];  // weight matrix of each W instruction (its rows share one segment) ...
+  int wrows[PW];         // ... and its rows
 #pragma unroll
   for (int i = 0; i < PX; ++i) {
-    const int r = (tid + i * NT) / kChunks;
+    const int r = (wave + NW * i) * RPI + lrow;
+    xc[i] = lslot ^ dma_swz<BKT>(r);
     if (r < rows_m) {
       const int lr = m_begin + r;
       const int64_t pr = p.gather ? (int64_t)p.gather[lr] : (int64_t)lr;
@@ -330,91 +327,117 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_kernel(const GemmParams
   }
 #pragma unroll
   for (int i = 0; i < PW; ++i) {
-    const int r = (tid + i * NT) / kChunks;
-    int n;
+    const int r = (wave + NW * i) * RPI + lrow;
+    wc[i] = lslot ^ dma_swz<BKT>(r);
+    int n, rbase = 0, rlim;  // global row n; rows of the source matrix: [rbase, rbase + rlim)
+    const bf16* wb;
     if constexpr (EPI == kEpiSwiGLU) {
       n = n0_out + (r >> 6) * 32 + (r & 31);  // 32-row groups alternate gate / up
+      const bool up = (((wave + NW * i) * RPI) >> 5) & 1;  // the instruction's rows share one group
+      wb = up ? tc.W2 : tc.W;
+      rlim = p.N;
     } else {
       n = n0_out + r;
-    }
-    woff[i] = n < n_lim ? (uint32_t)((int64_t)n * ldw * 2) : kOOB;
-  }
-  const __amdgpu_buffer_rsrc_t rx =
-      make_rsrc(X, p.gather ? (int64_t)p.M_src * ldx * 2 : (int64_t)(m_begin + rows_m) * ldx * 2);
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(W, (int64_t)n_lim * ldw * 2);
-  const __amdgpu_buffer_rsrc_t rw2 = make_rsrc(EPI == kEpiSwiGLU ? W2 : W, (int64_t)p.N * ldw * 2);
-
-  struct Stage {
-    bf16x8 x[PX], w[PW];
-  };
-  // Loads of K-stage kt (zeros past the end: offsets resolve out of range).
-  auto load = [&](Stage& st, int kt) {
-    const int k0 = kt * kBK;
-#pragma unroll
-    for (int i = 0; i < PX; ++i) {
-      const int k = k0 + ((tid + i * NT) % kChunks) * 8;
-      st.x[i] = buffer_load16(rx, (k < K && xoff[i] != kOOB) ? xoff[i] + (uint32_t)k * 2u : kOOB);
-    }
-#pragma unroll
-    for (int i = 0; i < PW; ++i) {
-      const int id = tid + i * NT;
-      const int k = k0 + (id % kChunks) * 8;
-      const uint32_t off = (k < K && woff[i] != kOOB) ? woff[i] + (uint32_t)k * 2u : kOOB;
-      if constexpr (EPI == kEpiSwiGLU) {
-        // The 64 chunks of a wave lie in 16 consecutive rows, all of one
-        // 32-row gate or up group: the choice is wave-uniform, so the buffer
-        // resource stays scalar (no per-lane selection loop).
-        const bool up = (((wave * 64 + i * NT) / kChunks) >> 5) & 1;
-        st.w[i] = buffer_load16(up ? rw2 : rw, off);
-      } else {
-        st.w[i] = buffer_load16(rw, off);
+      wb = tc.W;
+      rlim = n_lim;
+      if (!GROUPED && p.seg.n > 1) {
+        const int n_first = n0_out + (wave + NW * i) * RPI;  // host: segment starts are multiples of RPI
+        const int sgi = __builtin_amdgcn_readfirstlane(segment_of(p.seg, n_first));
+        wb = pick4(sgi, p.seg.w[0], p.seg.w[1], p.seg.w[2], p.seg.w[3]);
+        rbase = pick4(sgi, p.seg.start[0], p.seg.start[1], p.seg.start[2], p.seg.start[3]);
+        const int end = sgi + 1 < p.seg.n ? pick4(sgi, p.seg.start[1], p.seg.start[2], p.seg.start[3], p.N) : p.N;
+        rlim = end - rbase;
       }
     }
-  };
-  auto store = [&](const Stage& st, int slot) {
-    bf16* sx = smem + slot * kStage;
-    bf16* sw = sx + BM * kBK;
+    // Selects can leave uniform values in vector registers: pin them to scalars
+    // so that the buffer resource is scalar.
+    wb = uniform_ptr(wb);
+    rbase = __builtin_amdgcn_readfirstlane(rbase);
+    rlim = __builtin_amdgcn_readfirstlane(rlim);
+    wsrc[i] = wb;
+    wrows[i] = rlim;
+    woff[i] = (n - rbase < rlim) ? (uint32_t)((int64_t)(n - rbase) * ldw * 2) : kOOB;
+  }
+  const __amdgpu_buffer_rsrc_t rx =
+      make_rsrc(tc.X, p.gather ? (int64_t)p.M_src * ldx * 2 : (int64_t)(m_begin + rows_m) * ldx * 2);
+  const uint32_t lbase = lds_addr(smem);
+
+  auto issue = [&](int kt) {
+    const int k0 = kt * BKT;
+    const uint32_t sb = lbase + (uint32_t)((kt % NST) * kStage * 2);
 #pragma unroll
     for (int i = 0; i < PX; ++i) {
-      const int id = tid + i * NT;
-      *reinterpret_cast<bf16x8*>(sx + swz(id / kChunks, id % kChunks)) = st.x[i];
+      const int k = k0 + xc[i] * 8;
+      const uint32_t off = (k < K && xoff[i] != kOOB) ? xoff[i] + (uint32_t)k * 2u : kOOB;
+      dma16(rx, off, sb + (uint32_t)((wave + NW * i) * 1024));
     }
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
-      const int id = tid + i * NT;
-      *reinterpret_cast<bf16x8*>(sw + swz(id / kChunks, id % kChunks)) = st.w[i];
+      const int j = wave + NW * i;
+      const int k = k0 + wc[i] * 8;
+      const uint32_t off = (k < K && woff[i] != kOOB) ? woff[i] + (uint32_t)k * 2u : kOOB;
+      dma16(make_rsrc(wsrc[i], (int64_t)wrows[i] * ldw * 2), off, sb + (uint32_t)(BM * BKT * 2 + j * 1024));
     }
-  };
-  auto compute = [&](auto& acc, int slot) {
-    const bf16* sx = smem + slot * kStage;
-    acc.mma_stage(sx, sx + BM * kBK, wm * WTM, wn * WTN, lane);
   };
 
   WaveAcc<TN, TM> acc;
   acc.zero();
+  const int l32 = lane & 31, h = lane >> 5;
+  const int rn = wn * WTN, rm = wm * WTM;
+  bf16x8 fa[2][TN], fb[2][TM];
+  auto read = [&](int buf, int kt, int ks) {
+    const bf16* sx = smem + (kt % NST) * kStage;
+    const bf16* sw = sx + BM * BKT;
+    const int c = ks * 2 + h;
+#pragma unroll
+    for (int i = 0; i < TN; ++i) {
+      const int r = rn + i * 32 + l32;
+      fa[buf][i] = *reinterpret_cast<const bf16x8*>(sw + r * BKT + ((c ^ dma_swz<BKT>(r)) << 3));
+    }
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+      const int r = rm + j * 32 + l32;
+      fb[buf][j] = *reinterpret_cast<const bf16x8*>(sx + r * BKT + ((c ^ dma_swz<BKT>(r)) << 3));
+    }
+  };
+  auto mma = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+      for (int j = 0; j < TM; ++j) acc.c[i][j] = mfma32x32x16(fa[buf][i], fb[buf][j], acc.c[i][j]);
+  };
+  auto interleave = [&]() {
+    constexpr int NR = TN + TM, NM = TN * TM;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, NM - NR, 0);
+  };
 
-  // Two register stages in flight (prefetch distance 2): the loads of stage
-  // kt+2 are issued before the MFMAs of stage kt, and stage kt+1 (issued one
-  // phase earlier) is written to LDS after them.
-  Stage sa, sb;
-  load(sa, 0);
-  load(sb, 1);
-  store(sa, 0);
+#pragma unroll
+  for (int s = 0; s < NST - 1; ++s) issue(s);
+  vm_wait<(NST - 2) * (PX + PW)>();
   __syncthreads();
-  int kt = 0;
-  for (; kt + 1 < nk; kt += 2) {  // slot 0 holds stage kt, sb stage kt+1 (in flight)
-    load(sa, kt + 2);
-    compute(acc, 0);
-    store(sb, 1);
-    sched_phase<kBK, TN, TM, PX + PW>();
-    __syncthreads();
-    load(sb, kt + 3);
-    compute(acc, 1);
-    store(sa, 0);
-    sched_phase<kBK, TN, TM, PX + PW>();
-    __syncthreads();
+  issue(NST - 1);
+  read(0, 0, 0);
+  for (int kt = 0; kt < nk; ++kt) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + 1 < KS) {
+        read((ks + 1) & 1, kt, ks + 1);
+      } else {
+        vm_wait<(NST - 2) * (PX + PW)>();  // this wave's part of stage kt + 1 has landed
+        __syncthreads();                    // every wave's; nobody reads stage kt any more
+        issue(kt + NST);                    // into stage kt's slot (zeros past the end of K)
+        read((ks + 1) & 1, kt + 1, 0);
+      }
+      mma(ks & 1);
+      interleave();
+    }
   }
-  if (kt < nk) compute(acc, 0);  // odd number of stages: the last one is in slot 0
+  vm_wait<0>();  // the trailing zero-fill DMAs must land before the block's LDS is reused
 
   store_tile<WTM, WTN, TN, TM, EPI>(p, tc, acc.c, wm, wn, lane);
 }

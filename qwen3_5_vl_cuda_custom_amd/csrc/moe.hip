@@ -490,7 +490,7 @@ int q3_moe_experts(const void* x, const void* gate_up, const void* down, const i
     p.n_tiles_total = w.n_tiles;
     p.expert_stride_w = 2 * I * H;
     const int64_t ntn = q3_cdiv(I, kMoeBN / 2);
-    hipLaunchKernelGGL((gemm_bf16_kernel<kMoeBM, kMoeBN, 2, 2, kEpiSwiGLU, true>), dim3((unsigned)(max_tiles * ntn)),
+    hipLaunchKernelGGL((gemm_bf16_dma_kernel<kMoeBM, kMoeBN, 2, 2, kEpiSwiGLU, true, kStages, kBK>), dim3((unsigned)(max_tiles * ntn)),
                        dim3(256), 0, st, p);
     Q3_LAUNCH_CHECK();
   }
@@ -513,7 +513,7 @@ int q3_moe_experts(const void* x, const void* gate_up, const void* down, const i
     p.n_tiles_total = w.n_tiles;
     p.expert_stride_w = H * I;
     const int64_t ntn = q3_cdiv(H, kMoeBN);
-    hipLaunchKernelGGL((gemm_bf16_kernel<kMoeBM, kMoeBN, 2, 2, kEpiRowScale, true>),
+    hipLaunchKernelGGL((gemm_bf16_dma_kernel<kMoeBM, kMoeBN, 2, 2, kEpiRowScale, true, kStages, kBK>),
                        dim3((unsigned)(max_tiles * ntn)), dim3(256), 0, st, p);
     Q3_LAUNCH_CHECK();
   }

@@ -105,96 +105,89 @@ struct QKNormRopeArgs {
   int64_t st[18];  // (b, s, h) strides of q_in, k_in, v_in, q_out, k_out, v_out
 };
 
-// One group of G = D/8 lanes per (b, s, head) row; lane j holds elements
-// [8j, 8j+8). The rotate-half partner of lane j is lane j ^ (G/2).
+// One block per (b, s) token. The D/2 rotary angles of the token (pos[axis]
+// * inv_freq[i], fp32, sincosf) are computed once into LDS and shared by all
+// of its q, k (and v) head rows. A group of G = D/8 lanes handles one head
+// row, lane j holding elements [8j, 8j+8); the rotate-half partner of lane j
+// is lane j ^ (G/2).
 template <typename T, int G>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const QKNormRopeArgs a) {
   constexpr int D = G * 8;
-  const int lane = threadIdx.x & 63;
-  const int j = lane % G;
-  const int64_t grow = ((blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6) * (64 / G) + lane / G;
-  const int64_t rq = (int64_t)a.B * a.S * a.Hq;
-  const int64_t rk = (int64_t)a.B * a.S * a.Hkv;
-  const int64_t rv = a.v_out ? rk : 0;
-  if (grow >= rq + rk + rv) return;
-  int kind;  // 0 = q, 1 = k, 2 = v
-  int64_t r;
-  if (grow < rq) {
-    kind = 0;
-    r = grow;
-  } else if (grow < rq + rk) {
-    kind = 1;
-    r = grow - rq;
-  } else {
-    kind = 2;
-    r = grow - rq - rk;
+  constexpr int HALF = D / 2;
+  __shared__ float s_cos[HALF], s_sin[HALF];
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x / a.S, s = blockIdx.x % a.S;
+  for (int i = tid; i < HALF; i += blockDim.x) {
+    const int axis = (i < a.s0) ? 0 : (i < a.s0 + a.s1 ? 1 : 2);
+    const float ang = (float)a.pos[((int64_t)axis * a.B + b) * a.S + s] * a.inv_freq[i];
+    float sn, c;
+    sincosf(ang, &sn, &c);
+    s_cos[i] = c;
+    s_sin[i] = sn;
   }
-  const int H = kind == 0 ? a.Hq : a.Hkv;
-  const int h = (int)(r % H);
-  const int64_t bs = r / H;
-  const int s = (int)(bs % a.S);
-  const int b = (int)(bs / a.S);
-  const int64_t* sin_ = a.st + 3 * kind;
-  const int64_t* sout = a.st + 9 + 3 * kind;
-  const T* in = static_cast<const T*>(kind == 0 ? a.q_in : (kind == 1 ? a.k_in : a.v_in)) + b * sin_[0] +
-                s * sin_[1] + h * sin_[2];
-  const int so = (kind > 0 && a.dst_seq_off) ? a.dst_seq_off[b] : 0;
-  const bool skip_store = kind > 0 && (s + (int64_t)so >= a.dst_seq_cap || s + so < 0);
-  T* out = static_cast<T*>(kind == 0 ? a.q_out : (kind == 1 ? a.k_out : a.v_out)) + b * sout[0] +
-           (int64_t)(s + so) * sout[1] + h * sout[2];
-
-  float v[8];
+  __syncthreads();
+  const int j = tid % G;
+  const int nrows = a.Hq + a.Hkv + (a.v_out ? a.Hkv : 0);
+  const bool lo = j < G / 2;
+  for (int row = tid / G; row < nrows; row += blockDim.x / G) {  // uniform per G-lane group
+    const int kind = row < a.Hq ? 0 : (row < a.Hq + a.Hkv ? 1 : 2);  // 0 = q, 1 = k, 2 = v
+    const int h = kind == 0 ? row : (kind == 1 ? row - a.Hq : row - a.Hq - a.Hkv);
+    const int64_t* sin_ = a.st + 3 * kind;
+    const int64_t* sout = a.st + 9 + 3 * kind;
+    const T* in = static_cast<const T*>(kind == 0 ? a.q_in : (kind == 1 ? a.k_in : a.v_in)) + b * sin_[0] +
+                  s * sin_[1] + h * sin_[2];
+    const int so = (kind > 0 && a.dst_seq_off) ? a.dst_seq_off[b] : 0;
+    const bool skip_store = kind > 0 && (s + (int64_t)so >= a.dst_seq_cap || s + so < 0);
+    T* out = static_cast<T*>(kind == 0 ? a.q_out : (kind == 1 ? a.k_out : a.v_out)) + b * sout[0] +
+             (int64_t)(s + so) * sout[1] + h * sout[2];
+    float v[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) v[e] = to_f<T>(in[8 * j + e]);
-  if (kind < 2) {
-    // RMSNorm over the head (skipped when no weights are given).
-    if (a.q_w) {
-      float ss = 0.f;
+    for (int e = 0; e < 8; ++e) v[e] = to_f<T>(in[8 * j + e]);
+    if (kind < 2) {
+      // RMSNorm over the head (skipped when no weights are given).
+      if (a.q_w) {
+        float ss = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
-      ss = group_sum<G>(ss);
-      const float rstd = rsqrtf(ss / (float)D + a.eps);
-      const T* w = static_cast<const T*>(kind == 0 ? a.q_w : a.k_w);
+        for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+        ss = group_sum<G>(ss);
+        const float rstd = rsqrtf(ss / (float)D + a.eps);
+        const T* w = static_cast<const T*>(kind == 0 ? a.q_w : a.k_w);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = v[e] * rstd * to_f<T>(w[8 * j + e]);
+        for (int e = 0; e < 8; ++e) v[e] = v[e] * rstd * to_f<T>(w[8 * j + e]);
+      }
+      // mRoPE.
+      float p[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) p[e] = __shfl_xor(v[e], G / 2, 64);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int i = (8 * j + e) % HALF;
+        const float c = s_cos[i], sn = s_sin[i];
+        // lo half: x1*c - x2*s  (partner holds x2); hi half: x2*c + x1*s (partner holds x1).
+        v[e] = lo ? (v[e] * c - p[e] * sn) : (v[e] * c + p[e] * sn);
+      }
     }
-    // mRoPE.
-    float p[8];
+    if (skip_store) continue;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) p[e] = __shfl_xor(v[e], G / 2, 64);
-    const bool lo = j < G / 2;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int i = (8 * j + e) % (D / 2);
-      const int axis = (i < a.s0) ? 0 : (i < a.s0 + a.s1 ? 1 : 2);
-      const float ang = (float)a.pos[((int64_t)axis * a.B + b) * a.S + s] * a.inv_freq[i];
-      float sn, c;
-      sincosf(ang, &sn, &c);
-      // lo half: x1*c - x2*s  (partner holds x2); hi half: x2*c + x1*s (partner holds x1).
-      v[e] = lo ? (v[e] * c - p[e] * sn) : (v[e] * c + p[e] * sn);
-    }
+    for (int e = 0; e < 8; ++e) out[8 * j + e] = from_f<T>(v[e]);
   }
-  if (skip_store) return;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) out[8 * j + e] = from_f<T>(v[e]);
 }
 
 template <typename T>
 int launch_qk(const QKNormRopeArgs& a, hipStream_t st) {
-  const int64_t rows = (int64_t)a.B * a.S * (a.Hq + (a.v_out ? 2 : 1) * a.Hkv);
-  if (rows == 0) return Q3_OK;
+  const int64_t tokens = (int64_t)a.B * a.S;
+  if (tokens == 0) return Q3_OK;
+  Q3_REQUIRE(tokens < (1ll << 31), Q3_ERR_SHAPE);
   const int G = a.D / 8;
-  const int64_t rows_per_block = 4 * (64 / G);
-  const unsigned blocks = (unsigned)q3_cdiv(rows, rows_per_block);
   switch (G) {
     case 8:
-      hipLaunchKernelGGL((qk_norm_rope_kernel<T, 8>), dim3(blocks), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<T, 8>), dim3((unsigned)tokens), dim3(256), 0, st, a);
       break;
     case 16:
-      hipLaunchKernelGGL((qk_norm_rope_kernel<T, 16>), dim3(blocks), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<T, 16>), dim3((unsigned)tokens), dim3(256), 0, st, a);
       break;
     case 32:
-      hipLaunchKernelGGL((qk_norm_rope_kernel<T, 32>), dim3(blocks), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<T, 32>), dim3((unsigned)tokens), dim3(256), 0, st, a);
       break;
     default:
       return Q3_ERR_UNSUPPORTED;

@@ -76,6 +76,8 @@ def test_matmul_swiglu(M):
 @pytest.mark.parametrize("M,ns,bias", [
     (600, (1024, 256, 256), False),   # tiled, one launch (starts are multiples of 256)
     (600, (512, 256, 256), True),     # tiled with per-segment bias
+    (4096, (4096, 1024, 1024), True), # the q/k/v shape: 256x192 tiles straddle segment starts
+    (2048, (1040, 512, 48), True),    # starts on 16-row (not tile) boundaries, one launch
     (300, (200, 72, 72), True),       # unaligned starts: one launch per segment
     (32, (1024, 256, 256), False),    # skinny, one launch
     (5, (96, 32, 32), True),          # skinny with bias
