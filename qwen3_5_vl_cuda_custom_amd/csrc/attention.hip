@@ -629,6 +629,235 @@ __global__ __launch_bounds__(256) void flash_decode_combine(const AttnParams p) 
   }
 }
 
+// ----------------------------------------------------------------- prefill, pipelined (D = 128)
+// Prefill kernel for head_dim 128 and GQA groups that are a multiple of 4
+// (the text layers): one block = 4 waves = 4 query heads of one KV head over
+// the same 64 queries; each wave owns 64 queries of its head (two 32-column
+// MFMA sub-tiles), so every K/V fragment read from LDS feeds two MFMAs.
+//  * 32-key K and V tiles go global -> LDS by direct-to-LDS loads into a ring
+//    of kPipeStages tiles, issued kPipeStages - 2 tiles ahead. K rows: chunk
+//    c of row r at slot c ^ (r & 15); V rows: chunk c at slot c ^ ((r & 3) << 2),
+//    read transposed by ds_read_b64_tr_b16 (the decode kernel's V^T scheme).
+//  * Per tile: S^T = K Q^T (16 MFMAs), online softmax (exp2 on log2e-scaled
+//    scores; the running max rises only by more than kRescale), O^T += V^T P^T
+//    (16 MFMAs) with P^T straight from the S^T accumulators.
+//  * Two S^T buffers: tile t + 1's S^T MFMAs are issued before tile t's
+//    softmax, so that VALU work overlaps MFMAs still in the matrix pipe.
+namespace fwdp {
+constexpr int kQ = 64;           // queries per wave
+constexpr int kKeys = 32;        // keys per tile
+constexpr int kPipeStages = 8;   // K/V tile ring depth
+constexpr int kTile = kKeys * kRowK;
+}  // namespace fwdp
+
+__global__ __launch_bounds__(256) void flash_fwd_pipe_kernel(const AttnParams p) {
+  using namespace fwdp;
+  constexpr int D = 128;
+  constexpr int KSTEPS = D / 16;
+  constexpr int OT = D / 32;
+  constexpr int PERW = 4;                 // DMA instructions per wave per tile (2 K + 2 V)
+  constexpr int AHEAD = kPipeStages - 2;  // tiles issued ahead of the one being read
+  __shared__ __attribute__((aligned(1024))) bf16 ring[kPipeStages * 2 * kTile];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31;
+  const int h = lane >> 5;
+
+  const int Sq = p.Sq, Sk = p.Sk;
+  const bool causal = p.causal != 0;
+  const int n_qt = (Sq + kQ - 1) / kQ;
+  const int qt = causal ? (n_qt - 1 - (int)blockIdx.y) : (int)blockIdx.y;  // heaviest first
+  const int hgroups = p.groups / 4;
+  int yb = blockIdx.x;
+  const int hg = yb % hgroups;
+  yb /= hgroups;
+  const int kvh = yb % p.Hkv;
+  const int b = yb / p.Hkv;
+  const int hq = kvh * p.groups + hg * 4 + wave;
+  const int q0 = qt * kQ;
+  const int klimit = causal ? min(Sk, q0 + kQ) : Sk;
+  const int nkt = (klimit + kKeys - 1) / kKeys;
+
+  const bf16* kbase = p.k + (int64_t)b * p.kb + (int64_t)kvh * p.kh;
+  const bf16* vbase = p.v + (int64_t)b * p.vb + (int64_t)kvh * p.vh;
+  const int ks2 = (int)p.ks * 2, vs2 = (int)p.vs * 2;  // host guarantees Sk * stride * 2 < 2^31
+  const __amdgpu_buffer_rsrc_t krs = q3::make_rsrc(kbase, (int64_t)(Sk - 1) * ks2 + D * 2);
+  const __amdgpu_buffer_rsrc_t vrs = q3::make_rsrc(vbase, (int64_t)(Sk - 1) * vs2 + D * 2);
+  const uint32_t lbase = q3::lds_addr(ring);
+
+  // Wave w loads rows 8w .. 8w + 7 of tile t's K and V (4 rows per instruction).
+  const int cs = lane & 15;
+  const int r0 = 8 * wave + (lane >> 4), r1 = r0 + 4;
+  const uint32_t kc0 = (uint32_t)((cs ^ (r0 & 15)) << 4), kc1 = (uint32_t)((cs ^ (r1 & 15)) << 4);
+  const uint32_t vc0 = (uint32_t)((cs ^ ((r0 & 3) << 2)) << 4), vc1 = (uint32_t)((cs ^ ((r1 & 3) << 2)) << 4);
+  auto issue = [&](int t) {
+    const uint32_t lk = lbase + (uint32_t)((t % kPipeStages) * 2 * kTile * 2) + (uint32_t)(8 * wave * kRowK * 2);
+    const uint32_t lv = lk + kTile * 2;
+    const bool live = t < nkt;
+    const int row = t * kKeys;
+    q3::dma16(krs, live ? (uint32_t)((row + r0) * ks2) + kc0 : q3::kOOB, lk);
+    q3::dma16(krs, live ? (uint32_t)((row + r1) * ks2) + kc1 : q3::kOOB, lk + 4 * kRowK * 2);
+    q3::dma16(vrs, live ? (uint32_t)((row + r0) * vs2) + vc0 : q3::kOOB, lv);
+    q3::dma16(vrs, live ? (uint32_t)((row + r1) * vs2) + vc1 : q3::kOOB, lv + 4 * kRowK * 2);
+  };
+
+  // Q fragments (B operand): lane supplies Q[q0 + 32 qs + l32][16 ks + 8 h .. + 7].
+  bf16x8 qf[2][KSTEPS];
+#pragma unroll
+  for (int qs = 0; qs < 2; ++qs) {
+    const int qi = q0 + 32 * qs + l32;
+    const bf16* qrow = p.q + (int64_t)b * p.qb + (int64_t)hq * p.qh + (int64_t)qi * p.qs;
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks)
+      qf[qs][ks] = qi < Sq ? *reinterpret_cast<const bf16x8*>(qrow + ks * 16 + 8 * h) : bf16x8{};
+  }
+
+  floatx16 o[2][OT];
+#pragma unroll
+  for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+    for (int t = 0; t < OT; ++t) o[qs][t] = floatx16{};
+  float m[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f};
+  const float c = p.scale_log2;
+
+  // LDS element offsets of this lane's fragments within a tile: K row l32 at
+  // chunk 2 ks + h; V^T reads at V[4 h + rr (+ 16 j, + 8)][32 dt + 16 g16 + 4 qq].
+  int koff[KSTEPS];
+#pragma unroll
+  for (int ks = 0; ks < KSTEPS; ++ks) koff[ks] = fwd::k_off(l32, 2 * ks + h);
+  const int g16 = (lane >> 4) & 1, rr = (lane & 15) >> 2, qq = lane & 3;
+  int voff[OT];
+#pragma unroll
+  for (int dt = 0; dt < OT; ++dt) {
+    const int d = 32 * dt + 16 * g16 + 4 * qq;
+    voff[dt] = dec_v_off(4 * h + rr, d >> 3) + (d & 7);
+  }
+
+  // S^T (32 keys x 32 queries) of tile t for query sub-tiles 0 and 1.
+  auto qk = [&](floatx16 (&s)[2], int t) {
+    const bf16* sK = ring + (t % kPipeStages) * 2 * kTile;
+    s[0] = floatx16{};
+    s[1] = floatx16{};
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(sK + koff[ks]);
+      s[0] = mfma32x32x16(a, qf[0][ks], s[0]);
+      s[1] = mfma32x32x16(a, qf[1][ks], s[1]);
+    }
+  };
+  // Softmax of tile t, first part: masking and the running max.
+  auto softmax_max = [&](floatx16 (&s)[2], int t) {
+    const int k0 = t * kKeys;
+    if ((causal && k0 + kKeys - 1 > q0) || k0 + kKeys > Sk) {  // uniform
+#pragma unroll
+      for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (key >= Sk || (causal && key > q0 + 32 * qs + l32)) s[qs][r] = -INFINITY;
+        }
+    }
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+      float mx = s[qs][0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[qs][r]);
+      const float mloc = fwd::half_max(mx) * c;  // finite: key t * 32 <= q0 <= every query of the block
+      const bool raise = mloc > m[qs] + fwd::kRescale;
+      if (__builtin_amdgcn_ballot_w64(raise) != 0) {
+        const float mnew = raise ? mloc : m[qs];
+        const float alpha = fast_exp2(m[qs] - mnew);
+        lsum[qs] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < OT; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[qs][dt][r] *= alpha;
+        m[qs] = mnew;
+      }
+    }
+  };
+  // Second part: exponentials into the P^T fragments (straight-line code).
+  auto softmax_exp = [&](const floatx16 (&s)[2], bf16x8 (&pb)[2][2]) {
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+      const float nm = -m[qs];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pr = fast_exp2(fmaf(s[qs][r], c, nm));
+        lsum[qs] += pr;
+        pb[qs][r >> 3][r & 7] = f2bf(pr);
+      }
+    }
+  };
+  // O^T += V^T P^T of tile t (V^T fragments by transposed reads).
+  auto pv = [&](int t, const bf16x8 (&pb)[2][2]) {
+    const bf16* sV = ring + (t % kPipeStages) * 2 * kTile + kTile;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int dt = 0; dt < OT; ++dt) {
+        const short4v lo = lds_read_tr16(sV + voff[dt] + 16 * j * kRowK);
+        const short4v hi = lds_read_tr16(sV + voff[dt] + (16 * j + 8) * kRowK);
+        const short8v a8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        const bf16x8 av = __builtin_bit_cast(bf16x8, a8);
+        o[0][dt] = mfma32x32x16(av, pb[0][j], o[0][dt]);
+        o[1][dt] = mfma32x32x16(av, pb[1][j], o[1][dt]);
+      }
+    }
+  };
+
+  // One tile step: S of tile t is in `cur`; S of tile t + 1 goes to `nxt`
+  // (past the last tile it is computed on the zero-filled slot and unused).
+  auto step = [&](int t, floatx16 (&cur)[2], floatx16 (&nxt)[2]) {
+    q3::vm_wait<(AHEAD - 1) * PERW>();  // this wave's part of tile t + 1 has landed
+    __syncthreads();                     // every wave's; tile t - 1's slot is free
+    issue(t + AHEAD + 1);
+    qk(nxt, t + 1);
+    softmax_max(cur, t);
+    bf16x8 pb[2][2];
+    softmax_exp(cur, pb);
+    pv(t, pb);
+  };
+
+  if (nkt > 0) {
+#pragma unroll
+    for (int s = 0; s <= AHEAD; ++s) issue(s);
+    q3::vm_wait<AHEAD * PERW>();  // tile 0 has landed (this wave's part)
+    __syncthreads();
+    floatx16 sa[2], sb[2];
+    qk(sa, 0);
+    int t = 0;
+    for (; t + 1 < nkt; t += 2) {
+      step(t, sa, sb);
+      step(t + 1, sb, sa);
+    }
+    if (t < nkt) step(t, sa, sb);
+  }
+  q3::vm_wait<0>();  // the trailing zero-fill DMAs must land before the block's LDS is reused
+
+#pragma unroll
+  for (int qs = 0; qs < 2; ++qs) {
+    const int qi = q0 + 32 * qs + l32;
+    const float l = lsum[qs] + __shfl_xor(lsum[qs], 32, 64);
+    if (qi >= Sq) continue;
+    const float inv_l = l > 0.f ? 1.0f / l : 0.f;
+    bf16* orow = p.o + (int64_t)b * p.ob + (int64_t)hq * p.oh + (int64_t)qi * p.os;
+#pragma unroll
+    for (int dt = 0; dt < OT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = dt * 32 + 8 * g + 4 * h;
+        bf16x4 v4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v4[e] = f2bf(o[qs][dt][4 * g + e] * inv_l);
+        *reinterpret_cast<bf16x4*>(orow + d) = v4;
+      }
+    if (p.lse && h == 0) p.lse[((int64_t)b * p.Hq + hq) * Sq + qi] = (m[qs] + log2f(l)) * 0.6931471805599453f;
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(128) void flash_generic_kernel(const AttnParams p, int D, const int* kv_lens) {
   const int64_t row = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
@@ -667,6 +896,15 @@ __global__ __launch_bounds__(128) void flash_generic_kernel(const AttnParams p, 
 }
 
 bool mfma_head_dim(int64_t D) { return D == 64 || D == 72 || D == 80 || D == 96 || D == 128; }
+
+int launch_fwd_pipe(const AttnParams& p, hipStream_t st) {
+  const int n_qt = (int)q3_cdiv(p.Sq, fwdp::kQ);
+  Q3_REQUIRE(n_qt <= 65535, Q3_ERR_UNSUPPORTED);
+  dim3 grid((unsigned)(p.B * p.Hkv * (p.groups / 4)), (unsigned)n_qt);
+  hipLaunchKernelGGL(flash_fwd_pipe_kernel, grid, dim3(256), 0, st, p);
+  Q3_LAUNCH_CHECK();
+  return Q3_OK;
+}
 
 template <int D>
 int launch_fwd(const AttnParams& p, hipStream_t st) {
@@ -753,6 +991,7 @@ int q3_flash_attention(const void* q, const void* k, const void* v, void* o, flo
       case 96:
         return launch_fwd<96>(p, st);
       default:
+        if (p.groups % 4 == 0) return launch_fwd_pipe(p, st);
         return launch_fwd<128>(p, st);
     }
   }
