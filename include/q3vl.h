@@ -160,6 +160,16 @@ int q3_decode_attention(const void* q, const void* k_cache, const void* v_cache,
                         int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len, const int64_t* strides,
                         float scale, int dtype, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* The decode step of CudaFullAttention.forward with a KV cache
+ * (modules/attention.py:89-96: cache concat, then attention of the new token):
+ * the new token's K/V row is already at cache row kv_lens[b]; sequence b
+ * attends to rows [0, kv_lens[b] + 1) and kv_lens[b] is then incremented in
+ * place (the reference's torch.cat growth of the cache). Same arguments and
+ * workspace as q3_decode_attention; max_len >= every kv_lens[b] + 1. */
+int q3_decode_attention_step(const void* q, const void* k_cache, const void* v_cache, int* kv_lens, void* o,
+                             int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len, const int64_t* strides,
+                             float scale, int dtype, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------- MoE
  * Router of CudaSparseMoE.forward (modules/moe.py:60-65): softmax over the
  * (bf16) logits (softmax_forward, csrc/softmax_op.cpp:7), top-k

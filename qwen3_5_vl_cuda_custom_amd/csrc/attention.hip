@@ -45,6 +45,9 @@ struct AttnParams {
   int groups;
   // decode
   const int* kv_lens;
+  int len_add;      // decode: sequence b attends to kv_lens[b] + len_add cache rows
+  int* lens_inc;    // decode: if set, lens_inc[b] += 1 once the step has read the lengths
+  int* dec_hdr;     // decode workspace header: unit prefix over sequences (B + 1 ints)
   float* partial;  // decode workspace
 };
 
@@ -335,7 +338,7 @@ __device__ void dec_prefix(const AttnParams& p, int* s_pre, int* s_len) {
   for (int i = 0; i < per; ++i) {
     const int b = tid * per + i;
     if (b < B) {
-      const int L = min(max(p.kv_lens[b], 0), p.Sk);
+      const int L = min(max(p.kv_lens[b] + p.len_add, 0), p.Sk);
       s_len[b] = L;
       local += (L + kDecUnit - 1) / kDecUnit;
     }
@@ -382,6 +385,8 @@ __global__ __launch_bounds__(64 * kDecBlockWaves) void flash_decode_kernel(const
   __shared__ __attribute__((aligned(1024))) bf16 ring[kDecBlockWaves * NSLOT * SLOT];
 
   dec_prefix(p, s_pre, s_len);  // block-wide, before the waves part ways
+  if (blockIdx.x == 0)           // for the combine kernel, which must not read the lengths
+    for (int i = threadIdx.x; i <= p.B; i += blockDim.x) p.dec_hdr[i] = s_pre[i];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -597,12 +602,13 @@ __global__ __launch_bounds__(64 * kDecBlockWaves) void flash_decode_kernel(const
 // per pair, one thread per (head, d) output.
 template <int D>
 __global__ __launch_bounds__(256) void flash_decode_combine(const AttnParams p) {
-  __shared__ int s_pre[kDecMaxBatch + 1];
-  __shared__ int s_len[kDecMaxBatch];
-  dec_prefix(p, s_pre, s_len);
+  const int* s_pre = p.dec_hdr;  // written by the main kernel
   const int pair = blockIdx.x;
   const int Hkv = p.Hkv, G = p.groups;
   const int b = pair / Hkv, kvh = pair % Hkv;
+  // Advance the sequence's cache length (one block per sequence; nothing in
+  // this launch reads the lengths).
+  if (p.lens_inc && kvh == 0 && threadIdx.x == 0) p.lens_inc[b] += 1;
   const int nb = s_pre[b + 1] - s_pre[b];
   bf16* obase = p.o + (int64_t)b * p.ob + (int64_t)kvh * G * p.oh;
   if (nb == 0) {  // empty sequence: zeros
@@ -870,7 +876,7 @@ __global__ __launch_bounds__(128) void flash_generic_kernel(const AttnParams p, 
   const T* q = reinterpret_cast<const T*>(p.q) + (int64_t)b * p.qb + (int64_t)hq * p.qh + (int64_t)i * p.qs;
   const T* kb = reinterpret_cast<const T*>(p.k) + (int64_t)b * p.kb + (int64_t)kvh * p.kh;
   const T* vb = reinterpret_cast<const T*>(p.v) + (int64_t)b * p.vb + (int64_t)kvh * p.vh;
-  int nk = kv_lens ? min(kv_lens[b], p.Sk) : p.Sk;
+  int nk = kv_lens ? min(kv_lens[b] + p.len_add, p.Sk) : p.Sk;
   if (p.causal) nk = min(nk, i + 1);
   float acc[256];
   for (int d = 0; d < D; ++d) acc[d] = 0.f;
@@ -929,11 +935,20 @@ bool strides_aligned8(const int64_t* s, int n) {
   return true;
 }
 
+constexpr int64_t kDecHdrBytes = (kDecMaxBatch + 1 + 63) / 64 * 256;  // unit prefix, 256-byte aligned
+
 int64_t decode_ws_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t D) {
   (void)max_len;
-  // one record per (wave, pair) piece: at most one per pair plus one per wave boundary
-  return (kDecWavesTotal + B * Hkv) * (int64_t)dec_partial_floats((int)(Hq / std::max<int64_t>(Hkv, 1)), (int)D) *
-         (int64_t)sizeof(float);
+  // header, then one record per (wave, pair) piece: at most one per pair plus
+  // one per boundary between waves
+  return kDecHdrBytes + (kDecWavesTotal + B * Hkv) *
+                            (int64_t)dec_partial_floats((int)(Hq / std::max<int64_t>(Hkv, 1)), (int)D) *
+                            (int64_t)sizeof(float);
+}
+
+__global__ void lens_inc_kernel(int* lens, int B) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < B) lens[i] += 1;
 }
 
 }  // namespace
@@ -1018,9 +1033,14 @@ int64_t q3_decode_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, 
 // o: (B, Hq, D) strides [ob, oh]; kv_lens (B) int32 on device: sequence b
 // attends to cache positions [0, kv_lens[b]); max_len >= max(kv_lens).
 // strides = [qb, qh, kb, kh, ks, vb, vh, vs, ob, oh].
-int q3_decode_attention(const void* q, const void* k_cache, const void* v_cache, const int* kv_lens, void* o,
-                        int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len, const int64_t* strides,
-                        float scale, int dtype, void* workspace, int64_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int decode_impl(const void* q, const void* k_cache, const void* v_cache, const int* kv_lens, int len_add,
+                int* lens_inc, void* o, int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len,
+                const int64_t* strides, float scale, int dtype, void* workspace, int64_t workspace_bytes,
+                void* stream) {
   Q3_REQUIRE(q && k_cache && v_cache && kv_lens && o && strides, Q3_ERR_NULL);
   Q3_REQUIRE(B >= 0 && Hq >= 1 && Hkv >= 1 && Hq % Hkv == 0 && D >= 1 && max_len >= 1, Q3_ERR_SHAPE);
   if (B == 0) return Q3_OK;
@@ -1050,6 +1070,7 @@ int q3_decode_attention(const void* q, const void* k_cache, const void* v_cache,
   p.causal = 0;
   p.groups = (int)(Hq / Hkv);
   p.kv_lens = kv_lens;
+  p.len_add = len_add;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool aligned = q3_aligned(q, 16) && q3_aligned(k_cache, 16) && q3_aligned(v_cache, 16) &&
                        strides_aligned8(strides, 8);
@@ -1057,7 +1078,10 @@ int q3_decode_attention(const void* q, const void* k_cache, const void* v_cache,
   if (dtype == Q3_BF16 && D == 128 && p.groups <= 32 && B <= kDecMaxBatch && aligned &&
       (max_len + 1) * strides[4] * 2 < 0x7fffffffLL && (max_len + 1) * strides[7] * 2 < 0x7fffffffLL) {
     Q3_REQUIRE(workspace != nullptr && workspace_bytes >= decode_ws_bytes(B, Hq, Hkv, max_len, D), Q3_ERR_WORKSPACE);
-    p.partial = static_cast<float*>(workspace);
+    Q3_REQUIRE(q3_aligned(workspace, 16), Q3_ERR_ALIGN);
+    p.dec_hdr = static_cast<int*>(workspace);
+    p.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + kDecHdrBytes);
+    p.lens_inc = lens_inc;
     const dim3 grid(kDecBlocks), block(64 * kDecBlockWaves);
     if (p.groups <= 4)
       hipLaunchKernelGGL((flash_decode_kernel<1, 4>), grid, block, 0, st, p);
@@ -1080,7 +1104,29 @@ int q3_decode_attention(const void* q, const void* k_cache, const void* v_cache,
   else
     return Q3_ERR_DTYPE;
   Q3_LAUNCH_CHECK();
+  if (lens_inc) {
+    hipLaunchKernelGGL(lens_inc_kernel, dim3((unsigned)q3_cdiv(B, 256)), dim3(256), 0, st, lens_inc, (int)B);
+    Q3_LAUNCH_CHECK();
+  }
   return Q3_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int q3_decode_attention(const void* q, const void* k_cache, const void* v_cache, const int* kv_lens, void* o,
+                        int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len, const int64_t* strides,
+                        float scale, int dtype, void* workspace, int64_t workspace_bytes, void* stream) {
+  return decode_impl(q, k_cache, v_cache, kv_lens, 0, nullptr, o, B, Hq, Hkv, D, max_len, strides, scale, dtype,
+                     workspace, workspace_bytes, stream);
+}
+
+int q3_decode_attention_step(const void* q, const void* k_cache, const void* v_cache, int* kv_lens, void* o,
+                             int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len, const int64_t* strides,
+                             float scale, int dtype, void* workspace, int64_t workspace_bytes, void* stream) {
+  return decode_impl(q, k_cache, v_cache, kv_lens, 1, kv_lens, o, B, Hq, Hkv, D, max_len, strides, scale, dtype,
+                     workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

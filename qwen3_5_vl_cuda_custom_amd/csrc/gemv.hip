@@ -206,6 +206,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
   };
 
   // Sum of a split tile's pieces (in piece order) and its epilogue.
+  constexpr int kBatch = 8;
   auto reduce_tile = [&](int t, int npieces) {
     const __amdgpu_buffer_rsrc_t rp =
         make_rsrc(p.partial + (int64_t)t * p.max_pieces * kGvPiece, (int64_t)p.max_pieces * kGvPiece * 4);
@@ -213,13 +214,27 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
     if constexpr (SWIGLU) {
       const int cc0 = (tid & 7) * 8;
       const int nng = (cc0 >> 5) * 64 + (cc0 & 31);
+      // Pieces in batches of kBatch with all their loads in flight (pieces past
+      // the count load as zeros), summed in piece order.
       floatx4 g0 = {}, g1 = {}, v0 = {}, v1 = {};
-      for (int pc = 0; pc < npieces; ++pc) {
-        const uint32_t o = (uint32_t)((pc * kGvPiece + m * kGvBN + nng) * 4);
-        g0 += __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o, 0, 16));
-        g1 += __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o + 16, 0, 16));
-        v0 += __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o + 128, 0, 16));
-        v1 += __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o + 144, 0, 16));
+      for (int pc0 = 0; pc0 < npieces; pc0 += kBatch) {
+        floatx4 ld[kBatch][4];
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+          const uint32_t o =
+              pc0 + i < npieces ? (uint32_t)(((pc0 + i) * kGvPiece + m * kGvBN + nng) * 4) : kOOB - 256;
+          ld[i][0] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o, 0, 16));
+          ld[i][1] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o + 16, 0, 16));
+          ld[i][2] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o + 128, 0, 16));
+          ld[i][3] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o + 144, 0, 16));
+        }
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+          g0 += ld[i][0];
+          g1 += ld[i][1];
+          v0 += ld[i][2];
+          v1 += ld[i][3];
+        }
       }
       if (m >= M) return;
       const int n0 = t * 64 + cc0;
@@ -240,11 +255,20 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
     } else {
       const int nn0 = (tid & 7) * 16;
       floatx4 s[4] = {};
-      for (int pc = 0; pc < npieces; ++pc) {
-        const uint32_t o = (uint32_t)((pc * kGvPiece + m * kGvBN + nn0) * 4);
+      for (int pc0 = 0; pc0 < npieces; pc0 += kBatch) {
+        floatx4 ld[kBatch][4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          s[q] += __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o + 16 * q, 0, 16));
+        for (int i = 0; i < kBatch; ++i) {
+          const uint32_t o =
+              pc0 + i < npieces ? (uint32_t)(((pc0 + i) * kGvPiece + m * kGvBN + nn0) * 4) : kOOB - 256;
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            ld[i][q] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o + 16 * q, 0, 16));
+        }
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) s[q] += ld[i][q];
       }
       if (m >= M) return;
       const int n0 = t * kGvBN + nn0;

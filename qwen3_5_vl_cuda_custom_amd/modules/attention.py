@@ -97,10 +97,9 @@ class CudaFullAttention(nn.Module):
                          rope.mrope_section, self.q_norm.eps, dst_seq_offset=kv_cache.lens,
                          dst_seq_cap=kv_cache.capacity)
             if S == 1:
-                lens = kv_cache.lens + 1
-                decode_attention(q[:, 0], kv_cache.k, kv_cache.v, lens, self.scale, out=o[:, 0],
-                                 max_len=kv_cache.capacity)
-                kv_cache.lens.copy_(lens)
+                # attends to lens + 1 rows (the new token's included), then lens += 1
+                decode_attention(q[:, 0], kv_cache.k, kv_cache.v, kv_cache.lens, self.scale, out=o[:, 0],
+                                 max_len=kv_cache.capacity, append=True)
             else:
                 # Prefill of an empty cache: causal attention over the rows just written.
                 flash_attention(q.transpose(1, 2), kv_cache.k[:, :, :S], kv_cache.v[:, :, :S], self.scale, True,

@@ -211,6 +211,19 @@ def test_decode_attention_ragged(groups):
     assert_bf16_close(o, ref, what=f"decode groups={groups}")
 
 
+def test_decode_attention_append_step():
+    # the new token's row is already at cache row lens[b]: attend to lens + 1 rows, then lens += 1
+    B, Hkv, G, D, cap = 5, 2, 4, 128, 300
+    lens = torch.tensor([0, 3, 64, 100, 299], dtype=torch.int32)
+    q = rnd(B, Hkv * G, D, seed=35)
+    kc, vc = rnd(B, Hkv, cap, D, seed=36), rnd(B, Hkv, cap, D, seed=37)
+    lens_d = gpu(lens)
+    o = K.decode_attention(gpu(q), gpu(kc), gpu(vc), lens_d, D ** -0.5, append=True)
+    assert torch.equal(lens_d.cpu(), lens + 1)
+    ref = O.decode_attention(f32(q)[:, :, None], f32(kc), f32(vc), lens + 1, D ** -0.5, G)[:, :, 0]
+    assert_bf16_close(o, ref, what="decode append step")
+
+
 def test_decode_attention_c3_lengths():
     # the C3 decode shape: 32 sequences x 8 KV heads, lengths U[1024, 8192] (a work split where
     # pairs straddle waves), plus a second call with most sequences short (pairs inside one wave)
