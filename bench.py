@@ -27,6 +27,15 @@ sys.path.insert(0, str(ROOT))
 PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 
+# Bytes the dominant kernel (gate/up + SwiGLU GEMM, S=4096) moves between L2
+# and memory per launch, from two rocprofv3 --pmc passes over `bench.py
+# --traffic-probe` (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled
+# by what the same counter reads for a plain 512 MiB device copy in the same
+# run (FETCH_SIZE 262157.5 KiB -> x2.000; WRITE_SIZE 524288 KiB -> x1.000).
+# GEMM: FETCH_SIZE 591346.9, WRITE_SIZE 98319.2 KiB. Re-measure when the kernel
+# changes; the command and per-dispatch counts are in profiles/.
+GATE_UP_TRAFFIC_BYTES = int((591_346.9 * (524_288 / 262_157.5) + 98_319.2 * 1.0) * 1024)
+
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
@@ -81,6 +90,72 @@ def cpu_baseline(cfg, seq: int, layer, budget_s: float = 20.0) -> dict:
                       f"run(s), {med:.2f} s/layer"}
 
 
+def other_configs(torch, W, dev: str, warmup: int) -> dict:
+    """The other BASELINE configurations, one GPU each: C2 at S=1024 and 16384,
+    the C4 MoE layer (4096 tokens) and the C5 patch embed + vision block."""
+    out = {}
+    for S in (1024, 16384):
+        cfg = W.C2
+        layer = W.make_text_layer(cfg, torch.bfloat16, dev, seed=0)
+        x, pos = W.text_inputs(cfg, 1, S, torch.bfloat16, dev, seed=0)
+        b = W.make_rope(cfg, dev).bind(pos)
+        ms = time_gpu(lambda: layer(x, b), 5, max(2, warmup // 2))
+        fl = cfg.gemm_flops_per_token() * S + cfg.causal_attn_flops(S)
+        out[f"c2_prefill_s{S}"] = {"ms": round(ms, 4), "tok_s": round(S / (ms / 1e3), 1),
+                                   "tflops": round(fl / (ms / 1e3) / 1e12, 1),
+                                   "mfma_frac": round(fl / (ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+        log(f"C2 prefill S={S}: {out[f'c2_prefill_s{S}']}")
+        del layer, x
+    cfg = W.C4
+    layer = W.make_text_layer(cfg, torch.bfloat16, dev, seed=0)
+    x, pos = W.text_inputs(cfg, 1, 4096, torch.bfloat16, dev, seed=0)
+    b = W.make_rope(cfg, dev).bind(pos)
+    ms = time_gpu(lambda: layer(x, b), 10, warmup)
+    fl = cfg.gemm_flops_per_token() * 4096 + cfg.causal_attn_flops(4096)
+    out["c4_moe_layer_t4096"] = {"ms": round(ms, 4), "tok_s": round(4096 / (ms / 1e3), 1),
+                                 "tflops": round(fl / (ms / 1e3) / 1e12, 1),
+                                 "mfma_frac": round(fl / (ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+    log(f"C4 MoE layer: {out['c4_moe_layer_t4096']}")
+    del layer, x
+    v = W.C5
+    blk = W.make_vision_block(v, torch.bfloat16, dev, seed=0)
+    pe = W.make_patch_embed(v, torch.bfloat16, dev, seed=0)
+    patches = W.vision_inputs(v, torch.bfloat16, dev, seed=0)
+    cos, sin = W.vision_rope_cos_sin(v, dev)
+
+    def vis():
+        h = pe(patches)
+        return blk(h.view(v.images, v.patches_per_image, v.hidden), cos, sin)
+
+    ms = time_gpu(vis, 10, warmup)
+    fl = v.flops()
+    n = v.images * v.patches_per_image
+    out["c5_vision_patch_embed_block"] = {"ms": round(ms, 4), "patches_s": round(n / (ms / 1e3), 1),
+                                          "tflops": round(fl / (ms / 1e3) / 1e12, 1),
+                                          "mfma_frac": round(fl / (ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+    log(f"C5 vision: {out['c5_vision_patch_embed_block']}")
+    return out
+
+
+def traffic_probe(torch, K, W, cfg, S: int, dev: str) -> int:
+    """Launch the dominant kernel and a plain copy of known size, nothing else
+    timed: the workload for the FETCH_SIZE / WRITE_SIZE counter passes."""
+    with torch.inference_mode():
+        layer = W.make_text_layer(cfg, torch.bfloat16, dev, seed=0)
+        x, _ = W.text_inputs(cfg, 1, S, torch.bfloat16, dev, seed=0)
+        h = layer.post_attention_layernorm(x)
+        wg, wu = layer.mlp.gate_proj.weight, layer.mlp.up_proj.weight
+        for _ in range(3):
+            K.matmul_swiglu(h, wg, wu)
+        src = torch.empty(256 << 20, dtype=torch.bfloat16, device=dev).normal_()  # 512 MiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+    log("traffic probe done: 3 gate/up GEMMs, 3 copies of 512 MiB")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -89,6 +164,9 @@ def main() -> int:
     ap.add_argument("--seq", type=int, default=4096)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the C2 S=1024/16384, C4 and C5 measurements")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run only the gate/up GEMM (3x) and a 512 MiB device copy (3x), for PMC counter passes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build runs on a single GPU (no multi-GPU path); "
@@ -105,6 +183,8 @@ def main() -> int:
     torch.cuda.set_device(0)
     cfg = W.C2
     S = args.seq
+    if args.traffic_probe:
+        return traffic_probe(torch, K, W, cfg, S, dev)
     with torch.inference_mode():
         layer = W.make_text_layer(cfg, torch.bfloat16, dev, seed=0)
         x, pos = W.text_inputs(cfg, 1, S, torch.bfloat16, dev, seed=0)
@@ -189,6 +269,11 @@ def main() -> int:
                 f"({gbs / PEAK_HBM_GBS:.1%} of HBM)")
             del case
 
+    extra = None
+    if not args.no_extra:
+        with torch.inference_mode():
+            extra = other_configs(torch, W, dev, args.warmup)
+
     cpu = None
     if not args.no_cpu_baseline:
         with torch.inference_mode():
@@ -215,9 +300,11 @@ def main() -> int:
         "layer_mfma_frac": round(layer_tflops / PEAK_BF16_TFLOPS, 4),
         "roofline": {"bound": "mfma", "kernel": "gemm_bf16 gate/up+SwiGLU (M=S, N=2x12288, K=4096)",
                      "achieved": round(gemm_tflops, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(gemm_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None},
+                     "frac": round(gemm_tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": GATE_UP_TRAFFIC_BYTES if S == 4096 else None},
         "kernel_tflops": detail,
         "decode": decode,
+        "other_configs": extra,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -81,6 +81,15 @@ class VisionConfig:
         t, h, w = self.grid
         return t * h * w
 
+    def flops(self) -> int:
+        """Patch-embed GEMM + one block (qkv, proj, fc1, fc2, full attention per image)."""
+        n = self.images * self.patches_per_image
+        k_in = self.channels * self.temporal * self.patch * self.patch
+        h = self.hidden
+        gemm = 2 * n * (k_in * h + 4 * h * h + 2 * h * self.intermediate)
+        attn = 4 * self.head_dim * self.heads * self.patches_per_image ** 2 * self.images
+        return gemm + attn
+
 
 C5 = VisionConfig()
 
