@@ -156,6 +156,57 @@ def traffic_probe(torch, K, W, cfg, S: int, dev: str) -> int:
     return 0
 
 
+def counter_probe(torch, K, W, dev: str) -> int:
+    """Launch every kernel of the path, nothing timed: C2 prefill layer at
+    S=4096 (2x), C3 decode step (eager, 2x), C4 MoE layer, C5 patch embed +
+    vision block, and the op-level elementwise / norm kernels at layer sizes
+    (2x each). The workload for per-kernel MFMA and HBM counter passes."""
+    with torch.inference_mode():
+        cfg = W.C2
+        layer = W.make_text_layer(cfg, torch.bfloat16, dev, seed=0)
+        x, pos = W.text_inputs(cfg, 1, 4096, torch.bfloat16, dev, seed=0)
+        b = W.make_rope(cfg, dev).bind(pos)
+        for _ in range(2):
+            layer(x, b)
+        del x
+        case = W.make_decode_case(cfg, batch=32, capacity=8193 + 4, device=dev, seed=0, layer=layer)
+        dbind = case.rope.bind(case.positions.to(torch.int32))
+        for _ in range(2):
+            case.layer(case.x, dbind, kv_cache=case.cache)
+        torch.cuda.synchronize()
+        del case, layer
+        c4 = W.C4
+        moe = W.make_text_layer(c4, torch.bfloat16, dev, seed=0)
+        x, pos = W.text_inputs(c4, 1, 4096, torch.bfloat16, dev, seed=0)
+        moe(x, W.make_rope(c4, dev).bind(pos))
+        del moe, x
+        v = W.C5
+        blk = W.make_vision_block(v, torch.bfloat16, dev, seed=0)
+        pe = W.make_patch_embed(v, torch.bfloat16, dev, seed=0)
+        patches = W.vision_inputs(v, torch.bfloat16, dev, seed=0)
+        cos, sin = W.vision_rope_cos_sin(v, dev)
+        blk(pe(patches).view(v.images, v.patches_per_image, v.hidden), cos, sin)
+        g = torch.Generator(device=dev)
+        g.manual_seed(0)
+
+        def rnd(*shape):
+            return torch.randn(*shape, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+
+        a, c = rnd(4096, 4096), rnd(4096, 4096)
+        gate, up = rnd(4096, 12288), rnd(4096, 12288)
+        hv, wv, bv = rnd(3136, 1152), rnd(1152), rnd(1152)
+        act = rnd(3136, 4304)
+        for _ in range(2):
+            K.rmsnorm(a, c[0], 1e-6)
+            K.layernorm(hv, wv, bv, 1e-6)
+            K.swiglu(gate, up)
+            K.residual_add(a, c)
+            K.gelu_tanh(act)
+        torch.cuda.synchronize()
+    log("counter probe done")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -165,6 +216,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the C2 S=1024/16384, C4 and C5 measurements")
+    ap.add_argument("--counter-probe", action="store_true",
+                    help="run every kernel of the path a few times and exit, for PMC counter passes")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run only the gate/up GEMM (3x) and a 512 MiB device copy (3x), for PMC counter passes")
     args = ap.parse_args()
@@ -185,6 +238,8 @@ def main() -> int:
     S = args.seq
     if args.traffic_probe:
         return traffic_probe(torch, K, W, cfg, S, dev)
+    if args.counter_probe:
+        return counter_probe(torch, K, W, dev)
     with torch.inference_mode():
         layer = W.make_text_layer(cfg, torch.bfloat16, dev, seed=0)
         x, pos = W.text_inputs(cfg, 1, S, torch.bfloat16, dev, seed=0)

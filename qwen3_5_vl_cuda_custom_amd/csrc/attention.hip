@@ -19,8 +19,10 @@
 // KV head) pairs, one wave-private DMA ring per wave; the MFMA query columns
 // are the GQA group's heads (see the decode section below).
 #include <algorithm>
+#include <type_traits>
 
 #include "gemm_tile.h"
+
 #include "q3_common.h"
 
 namespace {
@@ -641,19 +643,39 @@ __global__ __launch_bounds__(256) void flash_decode_combine(const AttnParams p) 
 // the same 64 queries; each wave owns 64 queries of its head (two 32-column
 // MFMA sub-tiles), so every K/V fragment read from LDS feeds two MFMAs.
 //  * 32-key K and V tiles go global -> LDS by direct-to-LDS loads into a ring
-//    of kPipeStages tiles, issued kPipeStages - 2 tiles ahead. K rows: chunk
-//    c of row r at slot c ^ (r & 15); V rows: chunk c at slot c ^ ((r & 3) << 2),
-//    read transposed by ds_read_b64_tr_b16 (the decode kernel's V^T scheme).
+//    of kPipeStages tiles, kAhead tiles ahead. K rows: chunk c of row r at
+//    slot c ^ (r & 15); V rows: chunk c at slot c ^ ((r & 3) << 2), read
+//    transposed by ds_read_b64_tr_b16 (the decode kernel's V^T scheme).
 //  * Per tile: S^T = K Q^T (16 MFMAs), online softmax (exp2 on log2e-scaled
 //    scores; the running max rises only by more than kRescale), O^T += V^T P^T
 //    (16 MFMAs) with P^T straight from the S^T accumulators.
-//  * Two S^T buffers: tile t + 1's S^T MFMAs are issued before tile t's
-//    softmax, so that VALU work overlaps MFMAs still in the matrix pipe.
+//  * Software pipeline: step t runs O += V(t-1) P(t-1) and S(t+1) = K(t+1) Q^T
+//    (32 MFMAs, neither depends on step t's softmax) and the softmax of S(t),
+//    so the VALU work of the softmax runs under MFMAs already issued.
+//  * O lives in AGPRs (MFMA accumulators); the rare rescale reads, scales and
+//    writes them back in place, so the common path never copies them.
 namespace fwdp {
 constexpr int kQ = 64;           // queries per wave
 constexpr int kKeys = 32;        // keys per tile
 constexpr int kPipeStages = 8;   // K/V tile ring depth
+constexpr int kAhead = 6;        // step t issues tile t + kAhead (its slot held tile t - 2)
 constexpr int kTile = kKeys * kRowK;
+
+// acc *= alpha for an accumulator held in AGPRs. The leading s_nops give the
+// 18 wait states a 16-pass MFMA result needs before a VALU-side read; the
+// trailing ones cover the VALU write -> MFMA source-C read.
+__device__ __forceinline__ void scale_acc(floatx16& acc, float alpha) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    float x = acc[r], tmp;
+    asm volatile("v_accvgpr_read_b32 %1, %0\n\tv_mul_f32 %1, %2, %1\n\tv_accvgpr_write_b32 %0, %1"
+                 : "+a"(x), "=&v"(tmp)
+                 : "v"(alpha));
+    acc[r] = x;
+  }
+  asm volatile("s_nop 4" ::: "memory");
+}
 }  // namespace fwdp
 
 __global__ __launch_bounds__(256) void flash_fwd_pipe_kernel(const AttnParams p) {
@@ -661,8 +683,8 @@ __global__ __launch_bounds__(256) void flash_fwd_pipe_kernel(const AttnParams p)
   constexpr int D = 128;
   constexpr int KSTEPS = D / 16;
   constexpr int OT = D / 32;
-  constexpr int PERW = 4;                 // DMA instructions per wave per tile (2 K + 2 V)
-  constexpr int AHEAD = kPipeStages - 2;  // tiles issued ahead of the one being read
+  constexpr int PERW = 4;  // DMA instructions per wave per tile (2 K + 2 V)
+  static_assert(kAhead + 2 == kPipeStages, "step t reuses the slot of tile t - 2");
   __shared__ __attribute__((aligned(1024))) bf16 ring[kPipeStages * 2 * kTile];
 
   const int tid = threadIdx.x;
@@ -753,23 +775,32 @@ __global__ __launch_bounds__(256) void flash_fwd_pipe_kernel(const AttnParams p)
       s[1] = mfma32x32x16(a, qf[1][ks], s[1]);
     }
   };
-  // Softmax of tile t, first part: masking and the running max.
-  auto softmax_max = [&](floatx16 (&s)[2], int t) {
+  // Keys of tile t this lane must drop (MASK: the tile may hold keys past Sk
+  // or above the causal diagonal): bit r of the result is register r of
+  // query sub-tile qs. Uniformly 0 for tiles that need no mask.
+  auto tile_mask = [&](auto mask, int t, int qs) -> uint32_t {
+    uint32_t bits = 0;
     const int k0 = t * kKeys;
-    if ((causal && k0 + kKeys - 1 > q0) || k0 + kKeys > Sk) {  // uniform
+    if (decltype(mask)::value && ((causal && k0 + kKeys - 1 > q0) || k0 + kKeys > Sk)) {  // uniform
+      const int qi = q0 + 32 * qs + l32;
 #pragma unroll
-      for (int qs = 0; qs < 2; ++qs)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = k0 + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (key >= Sk || (causal && key > q0 + 32 * qs + l32)) s[qs][r] = -INFINITY;
-        }
+      for (int r = 0; r < 16; ++r) {
+        const int key = k0 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (key >= Sk || (causal && key > qi)) bits |= 1u << r;
+      }
     }
+    return bits;
+  };
+  // Softmax of tile t, first part: the running max over the kept keys. When it
+  // rises by more than kRescale, O, the row sums and the not yet applied
+  // P(t - 1) fragments `pp` move to the new reference (P(t - 1) is rounded to
+  // bf16 once more; this happens a few times per row at most).
+  auto softmax_max = [&](const floatx16 (&s)[2], const uint32_t (&drop)[2], bf16x8 (&pp)[2][2]) {
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) {
-      float mx = s[qs][0];
+      float mx = -INFINITY;
 #pragma unroll
-      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[qs][r]);
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, (drop[qs] >> r) & 1 ? -INFINITY : s[qs][r]);
       const float mloc = fwd::half_max(mx) * c;  // finite: key t * 32 <= q0 <= every query of the block
       const bool raise = mloc > m[qs] + fwd::kRescale;
       if (__builtin_amdgcn_ballot_w64(raise) != 0) {
@@ -777,21 +808,23 @@ __global__ __launch_bounds__(256) void flash_fwd_pipe_kernel(const AttnParams p)
         const float alpha = fast_exp2(m[qs] - mnew);
         lsum[qs] *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < OT; ++dt)
+        for (int dt = 0; dt < OT; ++dt) scale_acc(o[qs][dt], alpha);
 #pragma unroll
-          for (int r = 0; r < 16; ++r) o[qs][dt][r] *= alpha;
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) pp[qs][j][e] = f2bf(bf2f(pp[qs][j][e]) * alpha);
         m[qs] = mnew;
       }
     }
   };
-  // Second part: exponentials into the P^T fragments (straight-line code).
-  auto softmax_exp = [&](const floatx16 (&s)[2], bf16x8 (&pb)[2][2]) {
+  // Second part: exponentials into the P^T fragments (dropped keys give 0).
+  auto softmax_exp = [&](const floatx16 (&s)[2], const uint32_t (&drop)[2], bf16x8 (&pb)[2][2]) {
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) {
       const float nm = -m[qs];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float pr = fast_exp2(fmaf(s[qs][r], c, nm));
+        const float pr = (drop[qs] >> r) & 1 ? 0.f : fast_exp2(fmaf(s[qs][r], c, nm));
         lsum[qs] += pr;
         pb[qs][r >> 3][r & 7] = f2bf(pr);
       }
@@ -814,32 +847,56 @@ __global__ __launch_bounds__(256) void flash_fwd_pipe_kernel(const AttnParams p)
     }
   };
 
-  // One tile step: S of tile t is in `cur`; S of tile t + 1 goes to `nxt`
-  // (past the last tile it is computed on the zero-filled slot and unused).
-  auto step = [&](int t, floatx16 (&cur)[2], floatx16 (&nxt)[2]) {
-    q3::vm_wait<(AHEAD - 1) * PERW>();  // this wave's part of tile t + 1 has landed
-    __syncthreads();                     // every wave's; tile t - 1's slot is free
-    issue(t + AHEAD + 1);
+  // Step t (1 <= t < nkt): S(t) is in `cur`, P(t - 1) in `pp`. Runs
+  // O += V(t-1) P(t-1), S(t+1) into `nxt` (past the last tile on a
+  // zero-filled slot, unused) and the softmax of S(t) into `pc`.
+  auto step = [&](auto mask, int t, const floatx16 (&cur)[2], floatx16 (&nxt)[2], bf16x8 (&pp)[2][2],
+                  bf16x8 (&pc)[2][2]) {
+    q3::vm_wait<(kAhead - 2) * PERW>();  // this wave's part of tile t + 1 has landed
+    __syncthreads();                      // every wave's; step t - 1 is done with tile t - 2
+    issue(t + kAhead);
+    const uint32_t drop[2] = {tile_mask(mask, t, 0), tile_mask(mask, t, 1)};
+    softmax_max(cur, drop, pp);
+    // 32 MFMAs and the exponentials, none depending on another.
+    pv(t - 1, pp);
     qk(nxt, t + 1);
-    softmax_max(cur, t);
-    bf16x8 pb[2][2];
-    softmax_exp(cur, pb);
-    pv(t, pb);
+    softmax_exp(cur, drop, pc);
   };
+  constexpr std::true_type kMasked{};
+  constexpr std::false_type kUnmasked{};
 
   if (nkt > 0) {
 #pragma unroll
-    for (int s = 0; s <= AHEAD; ++s) issue(s);
-    q3::vm_wait<AHEAD * PERW>();  // tile 0 has landed (this wave's part)
+    for (int s = 0; s <= kAhead; ++s) issue(s);
+    q3::vm_wait<(kAhead - 1) * PERW>();  // tiles 0 and 1 have landed (this wave's part)
     __syncthreads();
     floatx16 sa[2], sb[2];
+    bf16x8 pa[2][2] = {}, pb[2][2] = {};
     qk(sa, 0);
-    int t = 0;
-    for (; t + 1 < nkt; t += 2) {
-      step(t, sa, sb);
-      step(t + 1, sb, sa);
+    qk(sb, 1);
+    {
+      const uint32_t drop[2] = {tile_mask(kMasked, 0, 0), tile_mask(kMasked, 0, 1)};
+      softmax_max(sa, drop, pb);  // pb holds no P yet: nothing in O either
+      softmax_exp(sa, drop, pa);
     }
-    if (t < nkt) step(t, sa, sb);
+    // Tiles below nfull hold only keys < Sk at or below every query of the
+    // block: no masking.
+    const int nfull = min(causal ? q0 / kKeys : nkt, Sk / kKeys);
+    int t = 1;
+    for (; t + 1 < nfull; t += 2) {
+      step(kUnmasked, t, sb, sa, pa, pb);
+      step(kUnmasked, t + 1, sa, sb, pb, pa);
+    }
+    for (; t + 1 < nkt; t += 2) {
+      step(kMasked, t, sb, sa, pa, pb);
+      step(kMasked, t + 1, sa, sb, pb, pa);
+    }
+    if (t < nkt) {
+      step(kMasked, t, sb, sa, pa, pb);
+      pv(t, pb);
+    } else {
+      pv(t - 1, pa);
+    }
   }
   q3::vm_wait<0>();  // the trailing zero-fill DMAs must land before the block's LDS is reused
 

@@ -138,6 +138,8 @@ def test_conv3d_patch():
     (1, 8, 2, 300, 128, True),
     (2, 4, 1, 130, 128, True),
     (1, 32, 8, 512, 128, True),
+    (1, 8, 2, 1100, 128, False),  # odd number of key tiles, ragged last tile
+    (1, 4, 1, 1000, 128, True),
     (1, 4, 4, 200, 128, False),  # one head per KV head: 4 query tiles per block
     (1, 4, 2, 100, 128, True),   # groups 2
     (2, 4, 4, 200, 64, False),
