@@ -108,8 +108,9 @@ int launch_tiled_cfg(GemmParams p, int64_t batch, hipStream_t st) {
 
 // Tile configuration by estimated time: full waves of blocks over 256 CUs,
 // times the block's work over its relative MFMA efficiency (measured on
-// MI355X): 256x256 (8 waves; 1 block per CU) 1.0, 256x192 (8 waves, 64-wide
-// K stages; plain epilogue only) 0.95, 128x128 (4 waves; 2 blocks per CU) 0.75.
+// MI355X): 256x256 (8 waves, 64-wide K stages x 2; 1 block per CU) 1.0,
+// 256x192 (8 waves, 64-wide K stages; plain epilogue only) 0.95, 128x128
+// (4 waves; 2 blocks per CU) 0.75.
 template <int EPI>
 int launch_tiled(GemmParams p, int64_t batch, hipStream_t st) {
   constexpr int kCUs = 256;
@@ -125,7 +126,7 @@ int launch_tiled(GemmParams p, int64_t batch, hipStream_t st) {
     const double cost_b = waves(q3_cdiv(p.M, 256) * q3_cdiv(p.N, 192) * batch, kCUs) * 256.0 * 192.0 / 0.95;
     if (cost_c < cost_a && cost_c < cost_b) return launch_tiled_cfg<128, 128, 2, 2, EPI, 4, 32>(p, batch, st);
     if (cost_b < cost_a) return launch_tiled_cfg<256, 192, 4, 2, EPI, 2, 64>(p, batch, st);
-    return launch_tiled_cfg<256, 256, 2, 4, EPI, 4, 32>(p, batch, st);
+    return launch_tiled_cfg<256, 256, 2, 4, EPI, 2, 64>(p, batch, st);
   }
 }
 
