@@ -23,6 +23,8 @@
 //                   source order in fp32 and rounds once.
 #include <algorithm>
 
+#include <climits>
+
 #include "gemm_kernels.h"
 
 using namespace q3;
@@ -103,9 +105,12 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const bf16* __restrict__
 
 // ------------------------------------------------------------------ permute
 // Workspace carve-out (all int32 unless noted):
-//   counts[E], offsets[E + 1], tile_table[max_tiles], n_tiles[1],
+//   hist[chunks][E], cstart[chunks][E], counts[E], offsets[E + 1],
+//   tile_table[max_tiles], n_tiles[1],
 //   sorted_token[P], sorted_w (bf16)[P], pos_of[P]   (P = T * k)
 struct MoeWs {
+  int* hist;    // (chunks, E) entries per chunk and expert
+  int* cstart;  // (chunks, E) first row of the chunk's entries in each expert's block
   int* counts;
   int* offsets;
   int* tile_table;
@@ -117,78 +122,178 @@ struct MoeWs {
   bf16* y_perm;  // (P, H)
 };
 
-__device__ __forceinline__ int block_excl_scan_flags(int flag, int* s_wave, int* total) {
-  // 256 threads = 4 waves; returns the exclusive prefix of `flag` in thread order.
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const unsigned long long m = __ballot(flag);
-  const int before = __popcll(m & ((1ull << lane) - 1ull));
-  if (lane == 0) s_wave[wave] = __popcll(m);
+constexpr int kMoeChunk = 64;  // tokens per dispatch chunk (one wave)
+
+// Wave per 64-token chunk: number of (token, slot) entries of the chunk per
+// expert (ids outside [0, E) are never dispatched).
+__global__ __launch_bounds__(64) void moe_hist_kernel(const int* __restrict__ top_idx, int T, int k, int E,
+                                                      int* __restrict__ hist) {
+  extern __shared__ int s_cnt[];  // E counters
+  const int c = blockIdx.x, lane = threadIdx.x;
+  for (int e = lane; e < E; e += 64) s_cnt[e] = 0;
   __syncthreads();
-  int base = 0;
-  for (int w = 0; w < wave; ++w) base += s_wave[w];
-  *total = s_wave[0] + s_wave[1] + s_wave[2] + s_wave[3];
-  __syncthreads();
-  return base + before;
-}
-
-// Block per expert: number of tokens routed to it.
-__global__ __launch_bounds__(256) void moe_count_kernel(const int* __restrict__ top_idx, int T, int k,
-                                                        int* __restrict__ counts) {
-  __shared__ int s_wave[4];
-  const int e = blockIdx.x;
-  int count = 0;
-  for (int t0 = 0; t0 < T; t0 += 256) {
-    const int t = t0 + threadIdx.x;
-    int flag = 0;
-    if (t < T)
-      for (int s = 0; s < k; ++s) flag |= (top_idx[(int64_t)t * k + s] == e);
-    int tot;
-    block_excl_scan_flags(flag, s_wave, &tot);
-    count += tot;
-  }
-  if (threadIdx.x == 0) counts[e] = count;
-}
-
-// One block: offsets = exclusive scan of counts; m-tile table for the grouped GEMM.
-__global__ __launch_bounds__(256) void moe_scan_kernel(const int* __restrict__ counts, int E, int* __restrict__ offsets,
-                                                       int* __restrict__ tile_table, int* __restrict__ n_tiles) {
-  if (threadIdx.x != 0) return;
-  int off = 0, nt = 0;
-  for (int e = 0; e < E; ++e) {
-    offsets[e] = off;
-    const int c = counts[e];
-    for (int m = 0; m < c; m += kMoeBM) tile_table[nt++] = (e << 20) | (off + m);
-    off += c;
-  }
-  offsets[E] = off;
-  *n_tiles = nt;
-}
-
-// Block per expert: write its pairs in ascending token order.
-__global__ __launch_bounds__(256) void moe_scatter_kernel(const int* __restrict__ top_idx,
-                                                          const bf16* __restrict__ top_w, int T, int k,
-                                                          const int* __restrict__ offsets,
-                                                          int* __restrict__ sorted_token, bf16* __restrict__ sorted_w,
-                                                          int* __restrict__ pos_of) {
-  __shared__ int s_wave[4];
-  const int e = blockIdx.x;
-  int base = offsets[e];
-  for (int t0 = 0; t0 < T; t0 += 256) {
-    const int t = t0 + threadIdx.x;
-    int slot = -1;
-    if (t < T)
-      for (int s = 0; s < k; ++s)
-        if (top_idx[(int64_t)t * k + s] == e) slot = s;
-    int tot;
-    const int rank = block_excl_scan_flags(slot >= 0, s_wave, &tot);
-    if (slot >= 0) {
-      const int pos = base + rank;
-      sorted_token[pos] = t;
-      sorted_w[pos] = top_w[(int64_t)t * k + slot];
-      pos_of[(int64_t)t * k + slot] = pos;
+  const int t = c * kMoeChunk + lane;
+  if (t < T)
+    for (int s = 0; s < k; ++s) {
+      const int e = top_idx[(int64_t)t * k + s];
+      if (e >= 0 && e < E) atomicAdd(&s_cnt[e], 1);
     }
-    base += tot;
+  __syncthreads();
+  for (int e = lane; e < E; e += 64) hist[(int64_t)c * E + e] = s_cnt[e];
+}
+
+// In-place exclusive scan of a[0, n) in LDS, n <= 2 * blockDim.x; tmp holds
+// blockDim.x ints. Returns the total. Every thread of the block calls it.
+__device__ int lds_excl_scan(int* a, int n, int* tmp) {
+  const int t = threadIdx.x, B = blockDim.x;
+  const int a0 = 2 * t < n ? a[2 * t] : 0, a1 = 2 * t + 1 < n ? a[2 * t + 1] : 0;
+  tmp[t] = a0 + a1;
+  __syncthreads();
+  for (int o = 1; o < B; o <<= 1) {
+    const int v = t >= o ? tmp[t - o] : 0;
+    __syncthreads();
+    tmp[t] += v;
+    __syncthreads();
   }
+  const int excl = tmp[t] - (a0 + a1);
+  const int total = tmp[B - 1];
+  __syncthreads();
+  if (2 * t < n) a[2 * t] = excl;
+  if (2 * t + 1 < n) a[2 * t + 1] = excl + a0;
+  __syncthreads();
+  return total;
+}
+
+// One block of 1024 threads: per-expert counts and offsets (exclusive scan),
+// each chunk's first position per expert, and the m-tile table of the grouped
+// GEMMs (tiles of kMoeBM rows, expert-major). Thread (g, e) sums the chunk
+// range g of expert e (G = 1024 / E ranges; independent loads), so the chunk
+// prefix per expert is a short scan over the ranges.
+__global__ __launch_bounds__(1024) void moe_plan_kernel(const int* __restrict__ hist, int NC, int E,
+                                                        int* __restrict__ counts, int* __restrict__ offsets,
+                                                        int* __restrict__ cstart, int* __restrict__ tile_table,
+                                                        int* __restrict__ n_tiles) {
+  __shared__ int s_off[2048], s_til[2048], s_tmp[1024], s_part[1024];
+  const int tid = threadIdx.x;
+  const int G = E <= 1024 ? 1024 / E : 1;  // chunk ranges per expert
+  // Partial sums (for E > 1024 one range per expert, thread strides over experts).
+  for (int e0 = 0; e0 < E; e0 += 1024 / G) {
+    const int e = e0 + tid % (1024 / G), g = tid / (1024 / G);
+    const bool act = e < E && g < G;
+    int sum = 0;
+    if (act) {
+      const int c0 = (int)((int64_t)g * NC / G), c1 = (int)((int64_t)(g + 1) * NC / G);
+#pragma unroll 8
+      for (int ci = c0; ci < c1; ++ci) sum += hist[(int64_t)ci * E + e];
+    }
+    if (G > 1) {
+      if (act) s_part[g * E + e] = sum;
+    } else if (act) {
+      s_off[e] = sum;
+    }
+  }
+  __syncthreads();
+  if (G > 1) {
+    for (int e = tid; e < E; e += 1024) {
+      int run = 0;
+      for (int g = 0; g < G; ++g) {
+        const int v = s_part[g * E + e];
+        s_part[g * E + e] = run;  // exclusive prefix over ranges
+        run += v;
+      }
+      s_off[e] = run;
+    }
+    __syncthreads();
+  }
+  for (int e = tid; e < E; e += 1024) {
+    counts[e] = s_off[e];
+    s_til[e] = (s_off[e] + kMoeBM - 1) / kMoeBM;
+  }
+  __syncthreads();
+  const int rows = lds_excl_scan(s_off, E, s_tmp);
+  const int tiles = lds_excl_scan(s_til, E, s_tmp);
+  for (int e = tid; e < E; e += 1024) {
+    const int off = s_off[e];
+    offsets[e] = off;
+    const int end = e + 1 < E ? s_off[e + 1] : rows;
+    int tt = s_til[e];
+    for (int m = off; m < end; m += kMoeBM) tile_table[tt++] = (e << 20) | m;
+  }
+  // Chunk starts: range g of expert e begins at off_e + (rows of ranges < g).
+  for (int e0 = 0; e0 < E; e0 += 1024 / G) {
+    const int e = e0 + tid % (1024 / G), g = tid / (1024 / G);
+    if (e >= E || g >= G) continue;
+    int run = s_off[e] + (G > 1 ? s_part[g * E + e] : 0);
+    const int c0 = (int)((int64_t)g * NC / G), c1 = (int)((int64_t)(g + 1) * NC / G);
+    for (int ci = c0; ci < c1; ++ci) {
+      cstart[(int64_t)ci * E + e] = run;
+      run += hist[(int64_t)ci * E + e];
+    }
+  }
+  if (tid == 0) {
+    offsets[E] = rows;
+    *n_tiles = tiles;
+  }
+}
+
+// Wave per chunk: every (token, slot) entry of an expert gets the next row of
+// that expert's block, in (token, slot) order: the order of nonzero() on the
+// (T, k) routing matrix. Lane l of every wave holds token l's k expert ids in
+// registers and the chunk's histogram and start rows sit in LDS; the block's
+// waves split the experts, and per expert present in the chunk one ballot per
+// slot counts the entries of the lanes below.
+constexpr int kPlaceWaves = 8;  // waves per chunk; wave w places experts e = w (mod 8)
+
+template <int KMAX>
+__global__ __launch_bounds__(kPlaceWaves * 64) void moe_place_kernel(const int* __restrict__ top_idx,
+                                                       const bf16* __restrict__ top_w, int T, int k, int E,
+                                                       const int* __restrict__ hist, const int* __restrict__ cstart,
+                                                       int* __restrict__ sorted_token, bf16* __restrict__ sorted_w,
+                                                       int* __restrict__ pos_of) {
+  extern __shared__ int s_row[];  // [0, E): the chunk's counts, [E, 2E): its start rows
+  const int c = blockIdx.x, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  for (int e = threadIdx.x; e < E; e += kPlaceWaves * 64) {
+    s_row[e] = hist[(int64_t)c * E + e];
+    s_row[E + e] = cstart[(int64_t)c * E + e];
+  }
+  const int t = c * kMoeChunk + lane;
+  int ex[KMAX];
+  bf16 wv[KMAX];
+#pragma unroll
+  for (int s = 0; s < KMAX; ++s) {
+    const bool ok = t < T && s < k;
+    ex[s] = ok ? top_idx[(int64_t)t * k + s] : -1;
+    wv[s] = ok ? top_w[(int64_t)t * k + s] : bf16{};
+  }
+  __syncthreads();
+  int dst[KMAX];  // row of each slot's entry (-1: not dispatched)
+#pragma unroll
+  for (int s = 0; s < KMAX; ++s) dst[s] = -1;
+  for (int e = wave; e < E; e += kPlaceWaves) {
+    if (s_row[e] == 0) continue;  // uniform
+    // Entries of lower lanes (earlier tokens) with expert e: per slot, the
+    // ballot's set bits below this lane.
+    int below = 0;
+#pragma unroll
+    for (int s = 0; s < KMAX; ++s) {
+      const uint64_t m = __ballot(ex[s] == e);
+      below += __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+    }
+    int pos = s_row[E + e] + below;
+#pragma unroll
+    for (int s = 0; s < KMAX; ++s)
+      if (ex[s] == e) dst[s] = pos++;
+  }
+  // One store per slot and array, all lanes together (a slot's row was set
+  // by the wave that owns its expert).
+#pragma unroll
+  for (int s = 0; s < KMAX; ++s)
+    if (dst[s] >= 0) {
+      sorted_token[dst[s]] = t;
+      sorted_w[dst[s]] = wv[s];
+      pos_of[(int64_t)t * k + s] = dst[s];
+    }
 }
 
 // One wave per token: add its k expert rows in ascending expert order.
@@ -248,6 +353,68 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const int* __restrict_
   }
 }
 
+// Combine, wide form (k <= 8, H = 8 * blockDim.x): one block per token,
+// thread j owns columns [8j, 8j + 8). The token's valid slots are ranked by
+// expert id in registers (ties by slot), every thread issues its k row loads
+// at once, then adds them in rank order with the same per-add bf16 rounding.
+template <int KMAX>
+__global__ __launch_bounds__(1024) void moe_combine_wide_kernel(const int* __restrict__ top_idx,
+                                                                const int* __restrict__ pos_of,
+                                                                const bf16* __restrict__ y_perm,
+                                                                const bf16* __restrict__ residual,
+                                                                bf16* __restrict__ out, int T, int k, int H, int E) {
+  const int t = blockIdx.x;
+  const int j = threadIdx.x;
+  int e[KMAX], p[KMAX];
+#pragma unroll
+  for (int s = 0; s < KMAX; ++s) {
+    int ee = INT_MAX, pp = -1;
+    if (s < k) {
+      ee = top_idx[(int64_t)t * k + s];
+      pp = pos_of[(int64_t)t * k + s];
+      if (ee < 0 || ee >= E || pp < 0 || pp >= T * k) {  // never dispatched
+        ee = INT_MAX;
+        pp = -1;
+      }
+    }
+    e[s] = ee;
+    p[s] = pp;
+  }
+  // rank[s]: slots before s in (expert, slot) order; invalid slots rank last
+  int ps[KMAX];
+#pragma unroll
+  for (int r = 0; r < KMAX; ++r) ps[r] = -1;
+#pragma unroll
+  for (int s = 0; s < KMAX; ++s) {
+    int rank = 0;
+#pragma unroll
+    for (int q = 0; q < KMAX; ++q) rank += (e[q] < e[s]) || (e[q] == e[s] && q < s);
+#pragma unroll
+    for (int r = 0; r < KMAX; ++r)
+      if (rank == r) ps[r] = p[s];
+  }
+  bf16x8 yv[KMAX];
+#pragma unroll
+  for (int r = 0; r < KMAX; ++r)
+    yv[r] = ps[r] >= 0 ? reinterpret_cast<const bf16x8*>(y_perm + (int64_t)ps[r] * H)[j] : bf16x8{};
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int r = 0; r < KMAX; ++r)
+    if (ps[r] >= 0)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) acc[q] = bf2f(f2bf(acc[q] + bf2f(yv[r][q])));
+  bf16x8 o;
+  if (residual) {
+    const bf16x8 rv = reinterpret_cast<const bf16x8*>(residual + (int64_t)t * H)[j];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) o[q] = f2bf(acc[q] + bf2f(rv[q]));
+  } else {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) o[q] = f2bf(acc[q]);
+  }
+  reinterpret_cast<bf16x8*>(out + (int64_t)t * H)[j] = o;
+}
+
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
 int64_t moe_ws_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, MoeWs* ws, char* base) {
@@ -260,6 +427,9 @@ int64_t moe_ws_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, Moe
     return p;
   };
   MoeWs w{};
+  const int64_t NC = q3_cdiv(T, kMoeChunk);
+  w.hist = reinterpret_cast<int*>(take(NC * E * 4));
+  w.cstart = reinterpret_cast<int*>(take(NC * E * 4));
   w.counts = reinterpret_cast<int*>(take(E * 4));
   w.offsets = reinterpret_cast<int*>(take((E + 1) * 4));
   w.tile_table = reinterpret_cast<int*>(take(max_tiles * 4));
@@ -462,12 +632,21 @@ int q3_moe_experts(const void* x, const void* gate_up, const void* down, const i
   const int64_t P = T * k;
   const int64_t max_tiles = q3_cdiv(P, kMoeBM) + E;
 
-  hipLaunchKernelGGL(moe_count_kernel, dim3((unsigned)E), dim3(256), 0, st, top_idx, (int)T, (int)k, w.counts);
-  hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(64), 0, st, w.counts, (int)E, w.offsets, w.tile_table,
-                     w.n_tiles);
-  hipLaunchKernelGGL(moe_scatter_kernel, dim3((unsigned)E), dim3(256), 0, st, top_idx,
-                     static_cast<const bf16*>(top_w), (int)T, (int)k, w.offsets, w.sorted_token, w.sorted_w,
-                     w.pos_of);
+  const int NC = (int)q3_cdiv(T, kMoeChunk);
+  hipLaunchKernelGGL(moe_hist_kernel, dim3((unsigned)NC), dim3(64), E * sizeof(int), st, top_idx, (int)T, (int)k,
+                     (int)E, w.hist);
+  hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(1024), 0, st, w.hist, NC, (int)E, w.counts, w.offsets, w.cstart,
+                     w.tile_table, w.n_tiles);
+  const dim3 place_blk(kPlaceWaves * 64);
+  const size_t place_lds = 2 * E * sizeof(int);
+  if (k <= 8)
+    hipLaunchKernelGGL(moe_place_kernel<8>, dim3((unsigned)NC), place_blk, place_lds, st, top_idx,
+                       static_cast<const bf16*>(top_w), (int)T, (int)k, (int)E, w.hist, w.cstart, w.sorted_token,
+                       w.sorted_w, w.pos_of);
+  else
+    hipLaunchKernelGGL(moe_place_kernel<32>, dim3((unsigned)NC), place_blk, place_lds, st, top_idx,
+                       static_cast<const bf16*>(top_w), (int)T, (int)k, (int)E, w.hist, w.cstart, w.sorted_token,
+                       w.sorted_w, w.pos_of);
   Q3_LAUNCH_CHECK();
 
   // GEMM 1: act[pos] = swiglu(x[token(pos)] . gate_up[e]^T)
@@ -521,7 +700,10 @@ int q3_moe_experts(const void* x, const void* gate_up, const void* down, const i
   const unsigned cb = (unsigned)q3_cdiv(T, 4);
   const bf16* res = static_cast<const bf16*>(residual);
   bf16* o = static_cast<bf16*>(out);
-  if (vpl <= 4)
+  if (k <= 8 && H % 8 == 0 && H / 8 <= 1024) {
+    hipLaunchKernelGGL(moe_combine_wide_kernel<8>, dim3((unsigned)T), dim3((unsigned)(H / 8)), 0, st, top_idx,
+                       w.pos_of, w.y_perm, res, o, (int)T, (int)k, (int)H, (int)E);
+  } else if (vpl <= 4)
     hipLaunchKernelGGL(moe_combine_kernel<4>, dim3(cb), dim3(256), 0, st, top_idx, w.pos_of, w.y_perm, res, o, (int)T,
                        (int)k, (int)H, (int)E);
   else if (vpl <= 8)

@@ -11,7 +11,7 @@ import torch
 
 from oracle import ops as O
 from qwen3_5_vl_cuda_custom_amd import kernels as K
-from tests.parity import assert_bf16_close, assert_close, assert_within_ulp
+from tests.parity import assert_bf16_close, assert_close, assert_layer_parity, assert_within_ulp, bf16_round
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -97,6 +97,32 @@ def test_matmul_segments(M, ns, bias):
         single = K.matmul(gpu(x), gpu(w), gpu(b) if b is not None else None)
         assert torch.equal(y[:, col:col + w.shape[0]].cpu(), single.cpu()), f"segment at column {col}"
         col += w.shape[0]
+
+
+@pytest.mark.parametrize("M", [1, 17, 32])
+def test_decode_gemv_shapes(M):
+    """The C3 decode projections (M <= 32 rows): q/k/v as three segments, o and
+    down with the residual fused, gate/up with SwiGLU, at the layer's N and K."""
+    H, I = 4096, 12288
+    x, xi = rnd(M, H, seed=70), rnd(M, I, seed=71)
+    wq, wk, wv = rnd(4096, H, seed=72, std=0.02), rnd(1024, H, seed=73, std=0.02), rnd(1024, H, seed=74, std=0.02)
+    y = K.matmul_segments(gpu(x), [gpu(wq), gpu(wk), gpu(wv)])
+    ref = torch.cat([O.linear(f32(x), f32(w)) for w in (wq, wk, wv)], dim=-1)
+    assert_bf16_close(y, ref, what=f"decode qkv M={M}")
+    wo, r = rnd(H, H, seed=75, std=0.02), rnd(M, H, seed=76)
+    assert_bf16_close(K.matmul(gpu(x), gpu(wo), residual=gpu(r)), O.linear(f32(x), f32(wo)) + f32(r),
+                      what=f"decode o+residual M={M}")
+    # gate/up values reach |4..8| here, where half a bf16 ulp of the output
+    # alone exceeds 2e-2: bound the worst element by the reference's own bf16
+    # path (bf16 gate and up, then swiglu, rounded), as the layer tests do.
+    wg, wu = rnd(I, H, seed=77, std=0.02), rnd(I, H, seed=78, std=0.02)
+    g32, u32 = O.linear(f32(x), f32(wg)), O.linear(f32(x), f32(wu))
+    assert_layer_parity(K.matmul_swiglu(gpu(x), gpu(wg), gpu(wu)), O.swiglu(g32, u32),
+                        bf16_round(O.swiglu(bf16_round(g32), bf16_round(u32))), what=f"decode gate/up M={M}")
+    wd = rnd(H, I, seed=79, std=0.02)  # K = 12288: outputs reach |10|, same bound as gate/up
+    d32 = O.linear(f32(xi), f32(wd))
+    assert_layer_parity(K.matmul(gpu(xi), gpu(wd), residual=gpu(r)), d32 + f32(r),
+                        bf16_round(bf16_round(d32) + f32(r)), what=f"decode down+residual M={M}")
 
 
 def test_matmul_fp32_reference_style():
