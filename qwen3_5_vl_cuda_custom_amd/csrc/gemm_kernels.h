@@ -90,9 +90,19 @@ __device__ __forceinline__ bool tile_ctx(const GemmParams& p, TileCtx& t) {
   bf16* C = p.C;
 
   if constexpr (GROUPED) {
-    const int tt = blockIdx.x / n_tiles_n;
-    tile_n = blockIdx.x % n_tiles_n;
-    if (tt >= *p.n_tiles_total) return false;
+    // XCD-aware over the valid tiles (known on the device only): blocks are
+    // dealt round-robin over the 8 XCDs, so XCD x takes the contiguous range
+    // [x * per, (x + 1) * per) of the (m-tile, n-tile) order; the blocks that
+    // share an expert's weight panels and its rows' activations then run on
+    // one XCD at the same time. Surplus blocks exit.
+    const int total = *p.n_tiles_total * n_tiles_n;
+    const int per = (total + 7) / 8;
+    const int b = blockIdx.x;
+    if (b / 8 >= per) return false;
+    const int L = (b % 8) * per + b / 8;
+    if (L >= total) return false;
+    const int tt = L / n_tiles_n;
+    tile_n = L % n_tiles_n;
     const int entry = p.tile_table[tt];
     const int expert = entry >> 20;
     m_begin = entry & 0xFFFFF;

@@ -32,7 +32,7 @@ using namespace q3;
 namespace {
 
 constexpr int kMoeBM = 128;
-constexpr int kMoeBN = 128;
+constexpr int kMoeBN = 256;  // weight rows per tile (SwiGLU: 128 gate/up output columns)
 
 // ------------------------------------------------------------------ routing
 template <int MAXV>
@@ -669,8 +669,10 @@ int q3_moe_experts(const void* x, const void* gate_up, const void* down, const i
     p.n_tiles_total = w.n_tiles;
     p.expert_stride_w = 2 * I * H;
     const int64_t ntn = q3_cdiv(I, kMoeBN / 2);
-    hipLaunchKernelGGL((gemm_bf16_dma_kernel<kMoeBM, kMoeBN, 2, 2, kEpiSwiGLU, true, kStages, kBK>), dim3((unsigned)(max_tiles * ntn)),
-                       dim3(256), 0, st, p);
+    // Grid: a multiple of 8 (the kernel deals the valid tiles out per XCD).
+    hipLaunchKernelGGL((gemm_bf16_dma_kernel<kMoeBM, kMoeBN, 2, 4, kEpiSwiGLU, true, 2, 64>),
+                       dim3((unsigned)(q3_cdiv(max_tiles * ntn, 8) * 8)),
+                       dim3(512), 0, st, p);
     Q3_LAUNCH_CHECK();
   }
   // GEMM 2: y_perm[pos] = bf16(bf16(act[pos] . down[e]^T) * w[pos])
@@ -692,8 +694,8 @@ int q3_moe_experts(const void* x, const void* gate_up, const void* down, const i
     p.n_tiles_total = w.n_tiles;
     p.expert_stride_w = H * I;
     const int64_t ntn = q3_cdiv(H, kMoeBN);
-    hipLaunchKernelGGL((gemm_bf16_dma_kernel<kMoeBM, kMoeBN, 2, 2, kEpiRowScale, true, kStages, kBK>),
-                       dim3((unsigned)(max_tiles * ntn)), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((gemm_bf16_dma_kernel<kMoeBM, kMoeBN, 2, 4, kEpiRowScale, true, 2, 64>),
+                       dim3((unsigned)(q3_cdiv(max_tiles * ntn, 8) * 8)), dim3(512), 0, st, p);
     Q3_LAUNCH_CHECK();
   }
   const int vpl = (int)q3_cdiv(H / 8, 64);
