@@ -32,9 +32,9 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # --traffic-probe` (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled
 # by what the same counter reads for a plain 512 MiB device copy in the same
 # run (FETCH_SIZE 262157.5 KiB -> x2.000; WRITE_SIZE 524288 KiB -> x1.000).
-# GEMM: FETCH_SIZE 591346.9, WRITE_SIZE 98319.2 KiB. Re-measure when the kernel
+# GEMM: FETCH_SIZE 591715.6, WRITE_SIZE 98322.4 KiB. Re-measure when the kernel
 # changes; the command and per-dispatch counts are in profiles/.
-GATE_UP_TRAFFIC_BYTES = int((591_346.9 * (524_288 / 262_157.5) + 98_319.2 * 1.0) * 1024)
+GATE_UP_TRAFFIC_BYTES = int((591715.6 * (524_288 / 262157.5) + 98322.4 * 1.0) * 1024)
 
 
 def log(*a):
