@@ -416,6 +416,45 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
 #pragma unroll
       for (int j = 0; j < TM; ++j) acc.c[i][j] = mfma32x32x16(fa[buf][i], fb[buf][j], acc.c[i][j]);
   };
+  // The stage's last k16 step with the next DMAs spread between its MFMAs
+  // (one DMA after each MFMA, order pinned), so the matrix core is not idle
+  // while a burst of DMA instructions issues after the barrier.
+  auto last_step = [&](int buf, int kn) {
+    constexpr int ND = PX + PW;
+    const int k0 = kn * BKT;
+    const uint32_t sb = lbase + (uint32_t)((kn % NST) * kStage * 2);
+    uint32_t doff[ND], dlds[ND];
+#pragma unroll
+    for (int i = 0; i < PX; ++i) {
+      const int k = k0 + xc[i] * 8;
+      doff[i] = (k < K && xoff[i] != kOOB) ? xoff[i] + (uint32_t)k * 2u : kOOB;
+      dlds[i] = sb + (uint32_t)((wave + NW * i) * 1024);
+    }
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+      const int k = k0 + wc[i] * 8;
+      doff[PX + i] = (k < K && woff[i] != kOOB) ? woff[i] + (uint32_t)k * 2u : kOOB;
+      dlds[PX + i] = sb + (uint32_t)(BM * BKT * 2 + (wave + NW * i) * 1024);
+    }
+    auto dma = [&](int d) {
+      if (d < PX)
+        dma16(rx, doff[d], dlds[d]);
+      else
+        dma16(make_rsrc(wsrc[d - PX], (int64_t)wrows[d - PX] * ldw * 2), doff[d], dlds[d]);
+    };
+    __builtin_amdgcn_sched_barrier(0);
+    int d = 0;
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+      for (int j = 0; j < TM; ++j) {
+        acc.c[i][j] = mfma32x32x16(fa[buf][i], fb[buf][j], acc.c[i][j]);
+        if (d < ND) dma(d++);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+    for (; d < ND; ++d) dma(d);
+  };
   auto interleave = [&]() {
     constexpr int NR = TN + TM, NM = TN * TM;
 #pragma unroll
@@ -437,14 +476,14 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
     for (int ks = 0; ks < KS; ++ks) {
       if (ks + 1 < KS) {
         read((ks + 1) & 1, kt, ks + 1);
+        mma(ks & 1);
+        interleave();
       } else {
         vm_wait<(NST - 2) * (PX + PW)>();  // this wave's part of stage kt + 1 has landed
         __syncthreads();                    // every wave's; nobody reads stage kt any more
-        issue(kt + NST);                    // into stage kt's slot (zeros past the end of K)
         read((ks + 1) & 1, kt + 1, 0);
+        last_step(ks & 1, kt + NST);        // MFMAs with the DMAs of stage kt + NST (into stage kt's slot) between them
       }
-      mma(ks & 1);
-      interleave();
     }
   }
   vm_wait<0>();  // the trailing zero-fill DMAs must land before the block's LDS is reused
