@@ -50,6 +50,7 @@ struct AttnParams {
   int len_add;      // decode: sequence b attends to kv_lens[b] + len_add cache rows
   int* lens_inc;    // decode: if set, lens_inc[b] += 1 once the step has read the lengths
   int* dec_hdr;     // decode workspace header: unit prefix over sequences (B + 1 ints)
+  int dec_waves;    // decode: waves in the main kernel's grid
   float* partial;  // decode workspace
 };
 
@@ -282,13 +283,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 //
 //  * Work units are 32-key tiles of a (sequence b, KV head) pair, listed
 //    pair-major (pair p = b * Hkv + kvh has n_b = ceil(L_b / 32) units). The
-//    grid has one block of kDecBlockWaves waves per CU; of its
-//    W = min(U, kDecWavesTotal) first waves, wave w takes units
+//    grid has one block of BW waves per CU (4 for groups <= 8, one per SIMD,
+//    so the MFMA/softmax work of one wave runs beside the others' streams);
+//    of its NW = 256 * BW waves the first W = min(U, NW) take units
 //    [w * U / W, (w + 1) * U / W) of the U in all (at least one each).
 //  * Each wave owns a ring of kDecSlots LDS slots. A unit's slot holds its K
 //    tile, its V tile and the group's query rows, all filled by direct-to-LDS
-//    loads (buffer_load ... lds), issued kDecSlots - 1 units ahead, so the
-//    wave's stream never stops between units or pairs.
+//    loads (buffer_load ... lds, non-temporal for K and V, which are read
+//    once), issued NSLOT - 1 units ahead, so the wave's stream never stops
+//    between units or pairs.
 //      K tile: 32 rows x 128, chunk c of row r at slot c ^ (r & 15).
 //      V tile: 32 rows x 128, chunk c of row r at slot c ^ ((r & 3) << 2).
 //    The PV A operand (V^T fragments) is read with ds_read_b64_tr_b16, which
@@ -304,9 +307,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 //    workspace (record w + p, unique and increasing in (w, p)), merged by
 //    flash_decode_combine.
 constexpr int kDecUnit = 32;                                   // keys per unit
-constexpr int kDecBlockWaves = 2;                              // waves per block (one block per CU)
-constexpr int kDecBlocks = 256;
-constexpr int kDecWavesTotal = kDecBlocks * kDecBlockWaves;
+constexpr int kDecBlocks = 256;                                // one block per CU
+constexpr int kDecWavesMax = kDecBlocks * 4;                   // waves of the widest variant
 constexpr int kDecMaxBatch = 1024;                             // sequences the fast path takes
 constexpr int kDecTile = kDecUnit * kRowK;                     // elements of a K or V tile
 
@@ -323,12 +325,12 @@ __device__ __forceinline__ short4v lds_read_tr16(const bf16* p) {
 
 __device__ __forceinline__ int dec_v_off(int r, int c) { return r * kRowK + ((c ^ ((r & 3) << 2)) << 3); }
 
-// Waves that get work: min(U, kDecWavesTotal), so every one of them has at
-// least one unit; wave w takes units [w * U / nw, (w + 1) * U / nw).
-__device__ __forceinline__ int dec_active_waves(int64_t U) { return (int)min<int64_t>(U, kDecWavesTotal); }
+// Waves that get work: min(U, NW) of the grid's NW, so every one of them has
+// at least one unit; wave w takes units [w * U / nw, (w + 1) * U / nw).
+__device__ __forceinline__ int dec_active_waves(int64_t U, int NW) { return (int)min<int64_t>(U, NW); }
 // Active wave whose unit range contains unit u.
-__device__ __forceinline__ int dec_wave_of(int64_t u, int64_t U) {
-  return (int)(((u + 1) * dec_active_waves(U) - 1) / U);
+__device__ __forceinline__ int dec_wave_of(int64_t u, int64_t U, int NW) {
+  return (int)(((u + 1) * dec_active_waves(U, NW) - 1) / U);
 }
 
 // Exclusive prefix over sequences of their unit counts, into s_pre[0..B]
@@ -375,8 +377,8 @@ struct DecCursor {
   int b, kvh, tile, nb;
 };
 
-template <int QI, int NSLOT>
-__global__ __launch_bounds__(64 * kDecBlockWaves) void flash_decode_kernel(const AttnParams p) {
+template <int QI, int NSLOT, int BW>
+__global__ __launch_bounds__(64 * BW) void flash_decode_kernel(const AttnParams p) {
   constexpr int D = 128;
   constexpr int KSTEPS = D / 16;
   constexpr int OT = D / 32;
@@ -384,7 +386,7 @@ __global__ __launch_bounds__(64 * kDecBlockWaves) void flash_decode_kernel(const
   constexpr int PER_UNIT = 2 * (kDecUnit / 4) + QI;     // DMA instructions per unit
   __shared__ int s_pre[kDecMaxBatch + 1];
   __shared__ int s_len[kDecMaxBatch];
-  __shared__ __attribute__((aligned(1024))) bf16 ring[kDecBlockWaves * NSLOT * SLOT];
+  __shared__ __attribute__((aligned(1024))) bf16 ring[BW * NSLOT * SLOT];
 
   dec_prefix(p, s_pre, s_len);  // block-wide, before the waves part ways
   if (blockIdx.x == 0)           // for the combine kernel, which must not read the lengths
@@ -395,8 +397,8 @@ __global__ __launch_bounds__(64 * kDecBlockWaves) void flash_decode_kernel(const
   const int l32 = lane & 31, h = lane >> 5;
   const int B = p.B, Hkv = p.Hkv, G = p.groups;
   const int64_t U = (int64_t)Hkv * s_pre[B];
-  const int w = blockIdx.x * kDecBlockWaves + wave;
-  const int nw = dec_active_waves(U);
+  const int w = blockIdx.x * BW + wave;
+  const int nw = dec_active_waves(U, kDecBlocks * BW);
   if (w >= nw) return;
   const int64_t u0 = (int64_t)w * U / nw, u1 = (int64_t)(w + 1) * U / nw;
 
@@ -448,8 +450,8 @@ __global__ __launch_bounds__(64 * kDecBlockWaves) void flash_decode_kernel(const
       const int r = 4 * i + (lane >> 4);
       const uint32_t ko = live ? (uint32_t)((k0 + r) * ks2 + ((cs ^ (r & 15)) << 4)) : q3::kOOB;
       const uint32_t vo = live ? (uint32_t)((k0 + r) * vs2 + ((cs ^ ((r & 3) << 2)) << 4)) : q3::kOOB;
-      q3::dma16(krs, ko, lk + i * 1024);
-      q3::dma16(vrs, vo, lv + i * 1024);
+      q3::dma16_nt(krs, ko, lk + i * 1024);
+      q3::dma16_nt(vrs, vo, lv + i * 1024);
     }
 #pragma unroll
     for (int i = 0; i < QI; ++i) {
@@ -619,7 +621,7 @@ __global__ __launch_bounds__(256) void flash_decode_combine(const AttnParams p) 
   }
   const int64_t U = (int64_t)Hkv * s_pre[p.B];
   const int64_t pu0 = (int64_t)Hkv * s_pre[b] + (int64_t)kvh * nb;
-  const int wf = dec_wave_of(pu0, U), wl = dec_wave_of(pu0 + nb - 1, U);
+  const int wf = dec_wave_of(pu0, U, p.dec_waves), wl = dec_wave_of(pu0 + nb - 1, U, p.dec_waves);
   if (wf == wl) return;  // finished by its wave
   const int PF = dec_partial_floats(G, D);
   for (int e = threadIdx.x; e < G * D; e += blockDim.x) {
@@ -998,7 +1000,7 @@ int64_t decode_ws_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int
   (void)max_len;
   // header, then one record per (wave, pair) piece: at most one per pair plus
   // one per boundary between waves
-  return kDecHdrBytes + (kDecWavesTotal + B * Hkv) *
+  return kDecHdrBytes + (kDecWavesMax + B * Hkv) *
                             (int64_t)dec_partial_floats((int)(Hq / std::max<int64_t>(Hkv, 1)), (int)D) *
                             (int64_t)sizeof(float);
 }
@@ -1139,13 +1141,16 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
     p.dec_hdr = static_cast<int*>(workspace);
     p.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + kDecHdrBytes);
     p.lens_inc = lens_inc;
-    const dim3 grid(kDecBlocks), block(64 * kDecBlockWaves);
+    // Four waves per CU with two ring slots each where a slot fits (groups
+    // <= 8), else two waves with three slots (the LDS holds ~150 KB of ring).
+    const dim3 grid(kDecBlocks);
+    p.dec_waves = kDecBlocks * (p.groups <= 8 ? 4 : 2);
     if (p.groups <= 4)
-      hipLaunchKernelGGL((flash_decode_kernel<1, 4>), grid, block, 0, st, p);
+      hipLaunchKernelGGL((flash_decode_kernel<1, 2, 4>), grid, dim3(256), 0, st, p);
     else if (p.groups <= 8)
-      hipLaunchKernelGGL((flash_decode_kernel<2, 4>), grid, block, 0, st, p);
+      hipLaunchKernelGGL((flash_decode_kernel<2, 2, 4>), grid, dim3(256), 0, st, p);
     else
-      hipLaunchKernelGGL((flash_decode_kernel<8, 3>), grid, block, 0, st, p);
+      hipLaunchKernelGGL((flash_decode_kernel<8, 3, 2>), grid, dim3(128), 0, st, p);
     Q3_LAUNCH_CHECK();
     hipLaunchKernelGGL(flash_decode_combine<128>, dim3((unsigned)(B * Hkv)), dim3(256), 0, st, p);
     Q3_LAUNCH_CHECK();

@@ -36,6 +36,12 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, u
   asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds" ::"v"(voff), "s"(lds_byte), "s"(r)
                : "memory");
 }
+// dma16 with the non-temporal hint, for data read exactly once (the KV cache
+// in decode): streaming it past the caches keeps HBM reads near their peak.
+__device__ __forceinline__ void dma16_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t lds_byte) {
+  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen nt lds" ::"v"(voff), "s"(lds_byte), "s"(r)
+               : "memory");
+}
 template <int N>
 __device__ __forceinline__ void vm_wait() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");

@@ -127,10 +127,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
           const int grp = j >> 2;
           const int n = t * 64 + (grp >> 1) * 32 + (r & 31);
           const uint32_t off = (live && n < N && k < K) ? (uint32_t)(((int64_t)n * a.ldw + k) * 2) : kOOB;
-          dma16((grp & 1) ? ru : rg, off, dst);
+          dma16_nt((grp & 1) ? ru : rg, off, dst);
         } else {
           const uint32_t off = (live && r < lim && k < K) ? (uint32_t)(((int64_t)(rowbase + r) * a.ldw + k) * 2) : kOOB;
-          dma16(rw, off, dst);
+          dma16_nt(rw, off, dst);
         }
       } else {  // X rows
         const int m = r - kGvBN;

@@ -102,9 +102,9 @@ def test_attention_validation():
     d = _lib.i64s(8 * 128, 128, 2 * 100 * 128, 100 * 128, 128, 2 * 100 * 128, 100 * 128, 128, 8 * 128, 128)
     assert L.q3_decode_attention(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 8, 2, 128, 100, d, 0.1, 1, None, 0, None) == -6
     # one (m, l, O) record of the group's 4 heads per piece of a (sequence, KV head) pair: at most one
-    # per pair plus one per boundary between the 512 waves of the grid
+    # per pair plus one per boundary between the (at most 1024) waves of the grid
     # (after a 4352-byte header holding the work split)
-    assert L.q3_decode_attention_workspace_bytes(32, 32, 8, 8193, 128) == 4352 + (512 + 32 * 8) * 4 * 130 * 4
+    assert L.q3_decode_attention_workspace_bytes(32, 32, 8, 8193, 128) == 4352 + (1024 + 32 * 8) * 4 * 130 * 4
     assert L.q3_decode_attention_step(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 8, 2, 128, 100, d, 0.1, 1, None, 0, None) == -6
     assert L.q3_decode_attention_step(FAKE, FAKE, FAKE, None, FAKE, 2, 8, 2, 128, 100, d, 0.1, 1, None, 0, None) == -1
 
