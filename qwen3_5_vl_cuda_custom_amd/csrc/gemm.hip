@@ -280,9 +280,9 @@ int64_t q3_matmul_segments_workspace_bytes(int64_t M, const int64_t* n, int64_t 
   for (int64_t i = 0; i < nseg; ++i) {
     if (n[i] <= 0) continue;
     N += n[i];
-    need = std::max(need, gemv_workspace_bytes(n[i], K, false));
+    need = std::max(need, gemv_workspace_bytes(M, n[i], K, false));
   }
-  return N > 0 ? std::max(need, gemv_workspace_bytes(N, K, false)) : 0;
+  return N > 0 ? std::max(need, gemv_workspace_bytes(M, N, K, false)) : 0;
 }
 
 int q3_matmul_segments(const void* x, const void* const* w, const void* const* bias, const int64_t* n, int64_t nseg,
@@ -294,7 +294,7 @@ int q3_matmul_segments(const void* x, const void* const* w, const void* const* b
 
 int64_t q3_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int dtype, int swiglu) {
   if (dtype != Q3_BF16 || M > kGemvMaxRows || M <= 0 || N <= 0 || K <= 0) return 0;
-  return gemv_workspace_bytes(N, K, swiglu != 0);
+  return gemv_workspace_bytes(M, N, K, swiglu != 0);
 }
 
 int q3_matmul(const void* x, const void* w, const void* bias, const void* residual, void* y, int64_t M, int64_t N,

@@ -26,6 +26,25 @@
 //    stage's DMA covers them); the counter's return values are read after the
 //    loop, and the block that completes a count sums the pieces in piece
 //    order (deterministic) and resets the counter to zero.
+//
+// The split-K reduction above costs a few microseconds of dependent memory
+// round trips at the end of every call (piece stores, counter atomics, the
+// last block's piece loads). Where that outweighs what split-K saves, the
+// row-owned kernel (gemv_rows_kernel) runs instead: each block owns r
+// consecutive weight rows of one segment over all of K, so nothing leaves the
+// block before the epilogue:
+//  * r is the smallest row count that gives every CU at most one block; the
+//    rows form 16-row groups of v_mfma_f32_16x16x32_bf16 (W as A, X as B),
+//    rows past r load as zeros (out-of-range offsets: no memory traffic).
+//  * W goes straight into VGPRs D k-steps (of 32) ahead of its MFMAs.
+//  * X, M <= 8: straight into VGPRs like W. Larger M: staged per 512-k chunk
+//    through LDS. Each wave loads whole 1 KB row pieces (contiguous reads,
+//    which the L2 serves ~3x faster per CU than 16-row fragment reads) and
+//    writes them to LDS; one barrier per chunk; the next chunk's loads are in
+//    flight while the current one is consumed.
+//  * The 4 waves take the k-steps round robin and sum their fp32 partials
+//    through LDS in wave order (deterministic); the epilogue adds bias and
+//    residual or applies SwiGLU and rounds once.
 #include "gemv.h"
 
 namespace q3 {
@@ -396,6 +415,320 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
   }
 }
 
+
+// ------------------------------------------------------------ row-owned GEMV
+constexpr int kRowsDirectMaxM = 8;   // X straight into VGPRs up to this many rows
+constexpr int kRowsMaxK = 8192;      // staged-X kernel beats stream-K up to here (M > 8)
+constexpr int kRowsMaxRG = 4;        // at most 64 weight rows per block
+constexpr int kRowsKC = 512;         // staged X: k per LDS chunk (1 KB of each X row)
+
+struct RowsParams {
+  GemvArgs a;
+  int r;          // weight rows per block
+  int bstart[5];  // first block of each segment; bstart[seg.n] = grid
+  int vec4;       // C (and R, bias) allow 8-byte access at 4-aligned columns
+};
+
+template <int RG, int MT, bool SW, bool STAGED, int D>
+__global__ __launch_bounds__(256) void gemv_rows_kernel(const RowsParams p) {
+  constexpr int NW = 4;
+  constexpr int RGT = SW ? 2 * RG : RG;
+  constexpr int XR = 16 * MT;              // X rows of the MFMA B operand
+  constexpr int XPW = XR / NW;             // staged X rows loaded per wave
+  constexpr int SPC = kRowsKC / 32;        // k-steps per chunk
+  constexpr int SPW = SPC / NW;            // k-steps per wave per chunk
+  __shared__ __attribute__((aligned(1024))) bf16 xs[STAGED ? 2 : 1][STAGED ? XR * kRowsKC : 8];
+  __shared__ floatx4 red[NW][RGT][MT][64];
+  const GemvArgs& a = p.a;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int i = lane & 15, g = lane >> 4;
+  const int b = blockIdx.x;
+  int s = 0;
+#pragma unroll
+  for (int j = 1; j < 4; ++j)
+    if (j < a.seg.n && b >= p.bstart[j]) s = j;
+  const int n0 = (b - p.bstart[s]) * p.r;  // first row of the block within segment s
+  const int seg_start = pick4(s, a.seg.start[0], a.seg.start[1], a.seg.start[2], a.seg.start[3]);
+  const int seg_end = s + 1 < a.seg.n ? pick4(s, a.seg.start[1], a.seg.start[2], a.seg.start[3], a.N) : a.N;
+  const int rows = min(p.r, seg_end - seg_start - n0);
+  const int K = a.K, M = a.M;
+  const bf16* wb = uniform_ptr(pick4(s, a.seg.w[0], a.seg.w[1], a.seg.w[2], a.seg.w[3]) + (int64_t)n0 * a.ldw);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(wb, (int64_t)rows * a.ldw * 2);
+  const __amdgpu_buffer_rsrc_t ru =
+      SW ? make_rsrc(uniform_ptr(a.W2 + (int64_t)n0 * a.ldw), (int64_t)rows * a.ldw * 2) : rw;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.X, (int64_t)M * a.ldx * 2);
+  uint32_t woff[RG];
+#pragma unroll
+  for (int q = 0; q < RG; ++q) woff[q] = 16 * q + i < rows ? (uint32_t)((16 * q + i) * a.ldw * 2) : kOOB;
+  uint32_t xoff[MT];  // direct X: lane's row
+#pragma unroll
+  for (int t = 0; t < MT; ++t) xoff[t] = 16 * t + i < M ? (uint32_t)((16 * t + i) * a.ldx * 2) : kOOB;
+
+  const int S = (K + 31) / 32;              // k-steps of 32
+  const int NC = (K + kRowsKC - 1) / kRowsKC;
+  // Wave step j -> k-step: staged, chunk j / SPW, in-chunk step wave + NW * (j % SPW)
+  // (every wave has NC * SPW steps; those past K load zeros); direct, wave + NW * j.
+  const int nsw = STAGED ? NC * SPW : (S - wave + NW - 1) / NW;
+  auto kstep = [&](int j) { return STAGED ? (j / SPW) * SPC + wave + NW * (j % SPW) : wave + NW * j; };
+
+  bf16x8 wf[D][RGT];
+  bf16x8 xd[STAGED ? 1 : D][MT];
+  floatx4 acc[RGT][MT];
+#pragma unroll
+  for (int q = 0; q < RGT; ++q)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[q][t] = floatx4{};
+
+  // Operands of wave step j into ring slot `slot`; k >= K loads zeros.
+  auto load = [&](int j, int slot) {
+    const int kk = 32 * kstep(j) + 8 * g;
+    const uint32_t kmask = (uint32_t)((K - 1 - kk) >> 31) << 31;
+#pragma unroll
+    for (int q = 0; q < RG; ++q) {
+      const uint32_t o = (woff[q] + (uint32_t)kk * 2u) | kmask;
+      wf[slot][q] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rw, o, 0, 0));
+      if constexpr (SW)
+        wf[slot][RG + q] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(ru, o, 0, 0));
+    }
+    if constexpr (!STAGED) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const uint32_t o = (xoff[t] + (uint32_t)kk * 2u) | kmask;
+        xd[slot][t] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0));
+      }
+    }
+  };
+  // Staged X, chunk c: wave loads rows wave * XPW .. + XPW, 16 B per lane of each
+  // row's 1 KB piece; lane l lands at slot l and fetches chunk l ^ (row & 15), so
+  // the fragment reads (16 rows, one chunk) hit 16 different bank groups.
+  // Two register buffers: chunk c's rows sit in xr[c & 1] from two chunks
+  // before their LDS store, so the W loads issued in between stay in flight.
+  bf16x8 xr[2][STAGED ? XPW : 1];
+  auto xload = [&](int c, int rb) {
+#pragma unroll
+    for (int e = 0; e < XPW; ++e) {
+      const int m = wave * XPW + e;
+      const int kk = c * kRowsKC + 8 * (lane ^ (m & 15));
+      const uint32_t o = (m < M && kk < K) ? (uint32_t)((m * a.ldx + kk) * 2) : kOOB;
+      xr[rb][e] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0));
+    }
+  };
+  auto xstore = [&](int buf) {
+#pragma unroll
+    for (int e = 0; e < XPW; ++e)
+      *reinterpret_cast<bf16x8*>(&xs[buf][(wave * XPW + e) * kRowsKC + 8 * lane]) = xr[buf][e];
+  };
+  auto comp = [&](int j, int slot) {
+    bf16x8 xf[MT];
+    if constexpr (STAGED) {
+      const bf16* xb = xs[(j / SPW) & 1];
+      const int ch = 4 * (wave + NW * (j % SPW)) + g;  // 16-byte chunk of the row piece
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const int m = 16 * t + i;
+        xf[t] = *reinterpret_cast<const bf16x8*>(xb + m * kRowsKC + 8 * (ch ^ (m & 15)));
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < MT; ++t) xf[t] = xd[slot][t];
+    }
+#pragma unroll
+    for (int q = 0; q < RGT; ++q)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) acc[q][t] = mfma16x16x32(wf[slot][q], xf[t], acc[q][t]);
+  };
+
+  // Chunk c (in registers xr[c & 1] since two chunks ago) goes to LDS buffer
+  // c & 1, which last held chunk c - 2 (finished by every wave before the
+  // barrier of chunk c - 1); chunk c + 2 is loaded into the freed registers
+  // (zeros past K). `cb` = c & 1, static in the unrolled loops below.
+  auto chunk = [&](int c, int cb) {
+    xstore(cb);
+    xload(c + 2, cb);
+    __syncthreads();
+  };
+  if constexpr (STAGED) {
+    xload(0, 0);
+    xstore(0);
+    xload(1, 1);
+    xload(2, 0);
+  }
+  // Loads sit outside any branch (only loop back-edges), so the compiler's
+  // per-register waits keep D steps of loads in flight. The unrolled block is
+  // U steps (two chunks when staged, so chunk parities are static); the first
+  // and last blocks are peeled.
+  constexpr int U = STAGED ? 2 * SPW : D;
+  static_assert(U % D == 0, "the unrolled block holds whole register rings");
+  const int nfull = nsw / U;
+  if (nfull >= 2) {
+#pragma unroll
+    for (int jj = 0; jj < D; ++jj) load(jj, jj);
+    if constexpr (STAGED) __syncthreads();
+#pragma unroll
+    for (int jj = 0; jj < U; ++jj) {
+      if (STAGED && jj % SPW == 0 && jj > 0) chunk(jj / SPW, (jj / SPW) & 1);
+      comp(jj, jj % D);
+      load(D + jj, jj % D);
+      __builtin_amdgcn_sched_barrier(0);  // keep each step's loads beside its MFMAs
+    }
+    for (int j0 = U; j0 < (nfull - 1) * U; j0 += U) {
+#pragma unroll
+      for (int jj = 0; jj < U; ++jj) {
+        if (STAGED && jj % SPW == 0) chunk((j0 + jj) / SPW, (jj / SPW) & 1);
+        comp(j0 + jj, jj % D);
+        load(j0 + D + jj, jj % D);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    const int jl = (nfull - 1) * U;
+#pragma unroll
+    for (int jj = 0; jj < U; ++jj) {
+      if (STAGED && jj % SPW == 0) chunk((jl + jj) / SPW, (jj / SPW) & 1);
+      comp(jl + jj, jj % D);
+      if (jj + D < U) load(jl + D + jj, (jj + D) % D);  // jj static: no runtime branch
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else if constexpr (STAGED) {
+    __syncthreads();
+  }
+  // Steps past the last full block (all of them for short K), unpipelined.
+  for (int j = nfull >= 2 ? nfull * U : 0; j < nsw; ++j) {
+    if (STAGED && j % SPW == 0 && j > 0) {
+      const int c = j / SPW;
+      if (c & 1) chunk(c, 1);
+      else chunk(c, 0);
+    }
+    load(j, 0);
+    comp(j, 0);
+  }
+
+  // Cross-wave sum in wave order, then the epilogue. Accumulator register e of
+  // lane l in group (q, t) holds row 16 q + 4 (l / 16) + e, X row 16 t + l % 16.
+#pragma unroll
+  for (int q = 0; q < RGT; ++q)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) red[wave][q][t][lane] = acc[q][t];
+  __syncthreads();
+  const bf16* bias = SW ? nullptr : pick4(s, a.seg.b[0], a.seg.b[1], a.seg.b[2], a.seg.b[3]);
+  const int cbase = seg_start + n0;
+  for (int it = tid; it < RG * MT * 64; it += 64 * NW) {
+    const int q = it / (MT * 64), t = (it / 64) % MT, l = it & 63;
+    const int m = 16 * t + (l & 15);
+    const int row = 16 * q + 4 * (l >> 4);
+    if (m >= M || row >= rows) continue;
+    floatx4 v = red[0][q][t][l];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) v += red[w][q][t][l];
+    float o[4];
+    if constexpr (SW) {
+      floatx4 u = red[0][RG + q][t][l];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) u += red[w][RG + q][t][l];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = silu_mul(v[e], u[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = v[e];
+    }
+    const int n = cbase + row;  // output column
+    bf16* crow = a.C + (int64_t)m * a.ldc;
+    const bf16* rrow = a.R ? a.R + (int64_t)m * a.ldr : nullptr;
+    if (p.vec4 && row + 3 < rows && (n & 3) == 0) {
+      if (bias) {
+        const bf16x4 bv = *reinterpret_cast<const bf16x4*>(bias + n0 + row);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] += bf2f(bv[e]);
+      }
+      if (rrow) {
+        const bf16x4 rv = *reinterpret_cast<const bf16x4*>(rrow + n);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] += bf2f(rv[e]);
+      }
+      *reinterpret_cast<bf16x4*>(crow + n) = bf16x4{f2bf(o[0]), f2bf(o[1]), f2bf(o[2]), f2bf(o[3])};
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (row + e >= rows) continue;
+        float v2 = o[e];
+        if (bias) v2 += bf2f(bias[n0 + row + e]);
+        if (rrow) v2 += bf2f(rrow[n + e]);
+        crow[n + e] = f2bf(v2);
+      }
+    }
+  }
+}
+
+bool rows_selected(int64_t M, int64_t K) { return M <= kRowsDirectMaxM || K <= kRowsMaxK; }
+
+int device_cus() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+template <int RG, int MT, bool SW, bool STAGED>
+void rows_launch_d(const RowsParams& p, int grid, hipStream_t st) {
+  constexpr int RGT = SW ? 2 * RG : RG;
+  constexpr int D = RGT <= 4 ? 8 : 4;  // register ring: ~32-48 KB of W in flight per CU
+  hipLaunchKernelGGL((gemv_rows_kernel<RG, MT, SW, STAGED, D>), dim3(grid), dim3(256), 0, st, p);
+}
+template <int RG, int MT, bool SW>
+void rows_launch_x(const RowsParams& p, int grid, hipStream_t st) {
+  if (p.a.M <= kRowsDirectMaxM) rows_launch_d<RG, 1, SW, false>(p, grid, st);
+  else rows_launch_d<RG, MT, SW, true>(p, grid, st);
+}
+template <bool SW>
+void rows_launch_rg(const RowsParams& p, int rg, int grid, hipStream_t st) {
+  const bool mt2 = p.a.M > 16;
+  switch (rg) {
+    case 1: mt2 ? rows_launch_x<1, 2, SW>(p, grid, st) : rows_launch_x<1, 1, SW>(p, grid, st); break;
+    case 2: mt2 ? rows_launch_x<2, 2, SW>(p, grid, st) : rows_launch_x<2, 1, SW>(p, grid, st); break;
+    case 3: mt2 ? rows_launch_x<3, 2, SW>(p, grid, st) : rows_launch_x<3, 1, SW>(p, grid, st); break;
+    default: mt2 ? rows_launch_x<4, 2, SW>(p, grid, st) : rows_launch_x<4, 1, SW>(p, grid, st); break;
+  }
+}
+
+int rows_launch(const GemvArgs& a, hipStream_t st) {
+  RowsParams p{};
+  p.a = a;
+  const int nseg = a.seg.n;
+  int64_t len[4] = {};
+  for (int i = 0; i < nseg; ++i) len[i] = (i + 1 < nseg ? a.seg.start[i + 1] : a.N) - a.seg.start[i];
+  const int cus = device_cus();
+  auto blocks_for = [&](int64_t r) {
+    int64_t n = 0;
+    for (int i = 0; i < nseg; ++i) n += q3_cdiv(len[i], r);
+    return n;
+  };
+  // Smallest r that gives every CU at most one block, at most 64 (beyond
+  // 64 * CUs rows the grid takes several blocks per CU).
+  int64_t r = std::min<int64_t>(16 * kRowsMaxRG, std::max<int64_t>(1, q3_cdiv(a.N, cus)));
+  while (r < 16 * kRowsMaxRG && blocks_for(r) > cus) ++r;
+  p.r = (int)r;
+  int64_t acc = 0;
+  for (int i = 0; i < nseg; ++i) {
+    p.bstart[i] = (int)acc;
+    acc += q3_cdiv(len[i], r);
+  }
+  for (int i = nseg; i < 5; ++i) p.bstart[i] = (int)acc;
+  const bool r_ok = a.R == nullptr || (q3_aligned(a.R, 8) && a.ldr % 4 == 0);
+  bool b_ok = true;
+  for (int i = 0; i < nseg; ++i) b_ok = b_ok && (!a.seg.b[i] || q3_aligned(a.seg.b[i], 8));
+  p.vec4 = q3_aligned(a.C, 8) && a.ldc % 4 == 0 && r_ok && b_ok;
+  const int rg = (int)q3_cdiv(r, 16);
+  if (a.W2) rows_launch_rg<true>(p, rg, (int)acc, st);
+  else rows_launch_rg<false>(p, rg, (int)acc, st);
+  Q3_LAUNCH_CHECK();
+  return Q3_OK;
+}
+
 struct GemvPlan {
   int n_tiles, k_stages, total, grid, max_pieces;
   int64_t counter_bytes, bytes;
@@ -442,12 +775,13 @@ bool gemv_eligible(const GemvArgs& a) {
   return true;
 }
 
-int64_t gemv_workspace_bytes(int64_t N, int64_t K, bool swiglu) {
-  if (N <= 0 || K <= 0) return 0;
+int64_t gemv_workspace_bytes(int64_t M, int64_t N, int64_t K, bool swiglu) {
+  if (M <= 0 || N <= 0 || K <= 0 || rows_selected(M, K)) return 0;
   return gemv_plan(N, K, swiglu).bytes;
 }
 
 int gemv_launch(const GemvArgs& a, void* ws, int64_t ws_bytes, hipStream_t st) {
+  if (rows_selected(a.M, a.K)) return rows_launch(a, st);
   const bool swiglu = a.W2 != nullptr;
   const GemvPlan pl = gemv_plan(a.N, a.K, swiglu);
   Q3_REQUIRE(ws != nullptr && ws_bytes >= pl.bytes, Q3_ERR_WORKSPACE);
