@@ -623,17 +623,35 @@ __global__ __launch_bounds__(256) void flash_decode_combine(const AttnParams p) 
   const int64_t pu0 = (int64_t)Hkv * s_pre[b] + (int64_t)kvh * nb;
   const int wf = dec_wave_of(pu0, U, p.dec_waves), wl = dec_wave_of(pu0 + nb - 1, U, p.dec_waves);
   if (wf == wl) return;  // finished by its wave
+  // Records in batches of kB with all their loads (m, l and the output
+  // element) in flight together, merged into a running (max, sum, acc).
+  constexpr int kB = 8;
   const int PF = dec_partial_floats(G, D);
   for (int e = threadIdx.x; e < G * D; e += blockDim.x) {
     const int qc = e / D, d = e % D;
-    float mm = -INFINITY;
-    for (int w = wf; w <= wl; ++w) mm = fmaxf(mm, p.partial[(int64_t)(w + pair) * PF + qc]);
-    float l = 0.f, acc = 0.f;
-    for (int w = wf; w <= wl; ++w) {
-      const float* rec = p.partial + (int64_t)(w + pair) * PF;
-      const float wt = fast_exp2(rec[qc] - mm);
-      l += rec[G + qc] * wt;
-      acc += rec[2 * G + qc * D + d] * wt;
+    float mm = -INFINITY, l = 0.f, acc = 0.f;
+    for (int w0 = wf; w0 <= wl; w0 += kB) {
+      float mv[kB], lv[kB], ov[kB];
+#pragma unroll
+      for (int u = 0; u < kB; ++u) {
+        const float* rec = p.partial + (int64_t)(min(w0 + u, wl) + pair) * PF;
+        mv[u] = w0 + u <= wl ? rec[qc] : -INFINITY;
+        lv[u] = rec[G + qc];
+        ov[u] = rec[2 * G + qc * D + d];
+      }
+      float mb = mm;
+#pragma unroll
+      for (int u = 0; u < kB; ++u) mb = fmaxf(mb, mv[u]);
+      const float sc = fast_exp2(mm - mb);  // 0 on the first batch (mm = -inf)
+      l *= sc;
+      acc *= sc;
+#pragma unroll
+      for (int u = 0; u < kB; ++u) {
+        const float wt = fast_exp2(mv[u] - mb);  // 0 for the padding records
+        l += lv[u] * wt;
+        acc += ov[u] * wt;
+      }
+      mm = mb;
     }
     obase[(int64_t)qc * p.oh + d] = f2bf(l > 0.f ? acc / l : 0.f);
   }

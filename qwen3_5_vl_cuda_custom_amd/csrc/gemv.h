@@ -24,7 +24,7 @@ struct GemvArgs {
 // True when the GEMV path takes the problem (bf16 rows 16-byte aligned,
 // segment starts on 128-column tiles, 32-bit buffer offsets).
 bool gemv_eligible(const GemvArgs& a);
-// Workspace: none where the row-owned kernel runs (M <= 8 or K <= 8192);
+// Workspace: none where the row-owned kernel runs (M <= 8 or K <= 16384);
 // else a fixed 16 KiB region of tile counters (zero before the first call;
 // every call leaves it zero) followed by fp32 split-K partials.
 int64_t gemv_workspace_bytes(int64_t M, int64_t N, int64_t K, bool swiglu);

@@ -418,7 +418,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
 
 // ------------------------------------------------------------ row-owned GEMV
 constexpr int kRowsDirectMaxM = 8;   // X straight into VGPRs up to this many rows
-constexpr int kRowsMaxK = 8192;      // staged-X kernel beats stream-K up to here (M > 8)
+constexpr int kRowsMaxK = 16384;     // staged-X kernel beats stream-K up to here (M > 8)
 constexpr int kRowsMaxRG = 4;        // at most 64 weight rows per block
 constexpr int kRowsKC = 512;         // staged X: k per LDS chunk (1 KB of each X row)
 

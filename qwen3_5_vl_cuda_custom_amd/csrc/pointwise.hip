@@ -102,10 +102,15 @@ __global__ __launch_bounds__(256) void norm_kernel(const T* __restrict__ x, cons
   const bool valid = row < rows;
   const T* xr = x + (valid ? row : 0) * (int64_t)cols;
 
+  // The weight (and bias) vectors load with the row, so one memory round trip
+  // covers every operand (small-row calls are latency-bound).
   float v[VPT][V];
+  VT wv[VPT], bv[VPT];
 #pragma unroll
   for (int t = 0; t < VPT; ++t) {
     const VT u = valid ? reinterpret_cast<const VT*>(xr)[j + t * G] : VT{};
+    wv[t] = reinterpret_cast<const VT*>(w)[j + t * G];
+    bv[t] = (KIND == kLayer && bias) ? reinterpret_cast<const VT*>(bias)[j + t * G] : VT{};
 #pragma unroll
     for (int e = 0; e < V; ++e) v[t][e] = to_f<T>(u[e]);
   }
@@ -134,14 +139,11 @@ __global__ __launch_bounds__(256) void norm_kernel(const T* __restrict__ x, cons
 #pragma unroll
   for (int t = 0; t < VPT; ++t) {
     const int vi = j + t * G;
-    const VT wv = reinterpret_cast<const VT*>(w)[vi];
-    VT bv{};
-    if (KIND == kLayer && bias) bv = reinterpret_cast<const VT*>(bias)[vi];
     VT out;
 #pragma unroll
     for (int e = 0; e < V; ++e) {
-      float o = (v[t][e] - mean) * rstd * to_f<T>(wv[e]);
-      if (KIND == kLayer && bias) o += to_f<T>(bv[e]);
+      float o = (v[t][e] - mean) * rstd * to_f<T>(wv[t][e]);
+      if (KIND == kLayer && bias) o += to_f<T>(bv[t][e]);
       out[e] = from_f<T>(o);
     }
     reinterpret_cast<VT*>(yr)[vi] = out;

@@ -13,6 +13,8 @@
 // Rotate-half on pairs (i, i + Dr/2) with c = cos[i], s = sin[i], i < Dr/2:
 //   y[i] = x[i] c - x[i + Dr/2] s,   y[i + Dr/2] = x[i + Dr/2] c + x[i] s
 // and dims >= Dr pass through.
+#include <type_traits>
+
 #include "q3_common.h"
 
 namespace {
@@ -109,67 +111,151 @@ struct QKNormRopeArgs {
 // * inv_freq[i], fp32, sincosf) are computed once into LDS and shared by all
 // of its q, k (and v) head rows. A group of G = D/8 lanes handles one head
 // row, lane j holding elements [8j, 8j+8); the rotate-half partner of lane j
-// is lane j ^ (G/2).
-template <typename T, int G>
+// is lane j ^ (G/2). Every load of a batch of up to kQKBatch rows per lane
+// group (the rows, both norm weights, the positions and frequencies) is issued
+// before the first use, so a decode call (one batch) costs one memory round
+// trip before its stores.
+constexpr int kQKBatch = 4;
+
+// One of three kernel arguments by a per-lane index, as selects (indexing the
+// argument array with a lane-varying index would load it from memory).
+__device__ __forceinline__ int64_t pick3(int k, int64_t x0, int64_t x1, int64_t x2) {
+  return k == 0 ? x0 : (k == 1 ? x1 : x2);
+}
+
+// Eight consecutive elements at p (16-byte vectors when VEC: p 16-byte aligned).
+template <typename T, bool VEC>
+__device__ __forceinline__ void load8(const T* p, float (&v)[8]) {
+  if constexpr (VEC) {
+    typedef typename Vec16<T>::type VT;
+    constexpr int N = Vec16<T>::N;
+#pragma unroll
+    for (int c = 0; c < 8 / N; ++c) {
+      const VT u = reinterpret_cast<const VT*>(p)[c];
+#pragma unroll
+      for (int e = 0; e < N; ++e) v[c * N + e] = to_f<T>(u[e]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = to_f<T>(p[e]);
+  }
+}
+template <typename T, bool VEC>
+__device__ __forceinline__ void store8(T* p, const float (&v)[8]) {
+  if constexpr (VEC) {
+    typedef typename Vec16<T>::type VT;
+    constexpr int N = Vec16<T>::N;
+#pragma unroll
+    for (int c = 0; c < 8 / N; ++c) {
+      VT u;
+#pragma unroll
+      for (int e = 0; e < N; ++e) u[e] = from_f<T>(v[c * N + e]);
+      reinterpret_cast<VT*>(p)[c] = u;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) p[e] = from_f<T>(v[e]);
+  }
+}
+
+template <typename T, int G, bool VEC>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const QKNormRopeArgs a) {
   constexpr int D = G * 8;
   constexpr int HALF = D / 2;
+  constexpr int RPP = 256 / G;  // rows per pass of the block
   __shared__ float s_cos[HALF], s_sin[HALF];
   const int tid = threadIdx.x;
   const int b = blockIdx.x / a.S, s = blockIdx.x % a.S;
-  for (int i = tid; i < HALF; i += blockDim.x) {
-    const int axis = (i < a.s0) ? 0 : (i < a.s0 + a.s1 ? 1 : 2);
-    const float ang = (float)a.pos[((int64_t)axis * a.B + b) * a.S + s] * a.inv_freq[i];
-    float sn, c;
-    sincosf(ang, &sn, &c);
-    s_cos[i] = c;
-    s_sin[i] = sn;
-  }
-  __syncthreads();
   const int j = tid % G;
   const int nrows = a.Hq + a.Hkv + (a.v_out ? a.Hkv : 0);
   const bool lo = j < G / 2;
-  for (int row = tid / G; row < nrows; row += blockDim.x / G) {  // uniform per G-lane group
-    const int kind = row < a.Hq ? 0 : (row < a.Hq + a.Hkv ? 1 : 2);  // 0 = q, 1 = k, 2 = v
-    const int h = kind == 0 ? row : (kind == 1 ? row - a.Hq : row - a.Hq - a.Hkv);
-    const int64_t* sin_ = a.st + 3 * kind;
-    const int64_t* sout = a.st + 9 + 3 * kind;
-    const T* in = static_cast<const T*>(kind == 0 ? a.q_in : (kind == 1 ? a.k_in : a.v_in)) + b * sin_[0] +
-                  s * sin_[1] + h * sin_[2];
-    const int so = (kind > 0 && a.dst_seq_off) ? a.dst_seq_off[b] : 0;
-    const bool skip_store = kind > 0 && (s + (int64_t)so >= a.dst_seq_cap || s + so < 0);
-    T* out = static_cast<T*>(kind == 0 ? a.q_out : (kind == 1 ? a.k_out : a.v_out)) + b * sout[0] +
-             (int64_t)(s + so) * sout[1] + h * sout[2];
-    float v[8];
+
+  // The token's angles: thread i < HALF loads its position and frequency.
+  int posv = 0;
+  float fr = 0.f;
+  if (tid < HALF) {
+    const int axis = (tid < a.s0) ? 0 : (tid < a.s0 + a.s1 ? 1 : 2);
+    posv = a.pos[((int64_t)axis * a.B + b) * a.S + s];
+    fr = a.inv_freq[tid];
+  }
+  // Norm weights of lane j (read from q_in when there are none: never used).
+  const bool has_w = a.q_w != nullptr;
+  float wq[8], wk[8];
+  load8<T, VEC>(static_cast<const T*>(has_w ? a.q_w : a.q_in) + 8 * j, wq);
+  load8<T, VEC>(static_cast<const T*>(has_w ? a.k_w : a.q_in) + 8 * j, wk);
+  auto row_kind = [&](int row, int& kind, int& h) {
+    kind = row < a.Hq ? 0 : (row < a.Hq + a.Hkv ? 1 : 2);  // 0 = q, 1 = k, 2 = v
+    h = kind == 0 ? row : (kind == 1 ? row - a.Hq : row - a.Hq - a.Hkv);
+  };
+  // Rows past the end load row nrows - 1 again (no branch around the loads).
+  float v[kQKBatch][8];
+  auto load_batch = [&](int r0) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = to_f<T>(in[8 * j + e]);
-    if (kind < 2) {
-      // RMSNorm over the head (skipped when no weights are given).
-      if (a.q_w) {
-        float ss = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
-        ss = group_sum<G>(ss);
-        const float rstd = rsqrtf(ss / (float)D + a.eps);
-        const T* w = static_cast<const T*>(kind == 0 ? a.q_w : a.k_w);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = v[e] * rstd * to_f<T>(w[8 * j + e]);
-      }
-      // mRoPE.
-      float p[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) p[e] = __shfl_xor(v[e], G / 2, 64);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int i = (8 * j + e) % HALF;
-        const float c = s_cos[i], sn = s_sin[i];
-        // lo half: x1*c - x2*s  (partner holds x2); hi half: x2*c + x1*s (partner holds x1).
-        v[e] = lo ? (v[e] * c - p[e] * sn) : (v[e] * c + p[e] * sn);
-      }
+    for (int u = 0; u < kQKBatch; ++u) {
+      int kind, h;
+      row_kind(min(r0 + u * RPP, nrows - 1), kind, h);
+      const T* in = static_cast<const T*>(kind == 0 ? a.q_in : (kind == 1 ? a.k_in : a.v_in)) +
+                    b * pick3(kind, a.st[0], a.st[3], a.st[6]) + s * pick3(kind, a.st[1], a.st[4], a.st[7]) +
+                    h * pick3(kind, a.st[2], a.st[5], a.st[8]);
+      load8<T, VEC>(in + 8 * j, v[u]);
     }
-    if (skip_store) continue;
+  };
+  const int first = tid / G;
+  load_batch(first);
+  const int so_b = a.dst_seq_off ? a.dst_seq_off[b] : 0;
+  if (tid < HALF) {
+    float sn, c;
+    sincosf((float)posv * fr, &sn, &c);
+    s_cos[tid] = c;
+    s_sin[tid] = sn;
+  }
+  __syncthreads();
+  float cs[8], sn[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) out[8 * j + e] = from_f<T>(v[e]);
+  for (int e = 0; e < 8; ++e) {
+    const int i = (8 * j + e) % HALF;
+    cs[e] = s_cos[i];
+    sn[e] = s_sin[i];
+  }
+  for (int r0 = first; r0 < nrows; r0 += kQKBatch * RPP) {  // uniform per lane group
+    if (r0 != first) load_batch(r0);
+#pragma unroll
+    for (int u = 0; u < kQKBatch; ++u) {
+      const int row = r0 + u * RPP;
+      if (row >= nrows) break;
+      int kind, h;
+      row_kind(row, kind, h);
+      const int so = kind > 0 ? so_b : 0;
+      const bool skip_store = kind > 0 && (s + (int64_t)so >= a.dst_seq_cap || s + so < 0);
+      T* out = static_cast<T*>(kind == 0 ? a.q_out : (kind == 1 ? a.k_out : a.v_out)) +
+               b * pick3(kind, a.st[9], a.st[12], a.st[15]) + (int64_t)(s + so) * pick3(kind, a.st[10], a.st[13], a.st[16]) +
+               h * pick3(kind, a.st[11], a.st[14], a.st[17]);
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = v[u][e];
+      if (kind < 2) {
+        // RMSNorm over the head (skipped when no weights are given).
+        if (has_w) {
+          float ss = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+          ss = group_sum<G>(ss);
+          const float rstd = rsqrtf(ss / (float)D + a.eps);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = x[e] * rstd * (kind == 0 ? wq[e] : wk[e]);
+        }
+        // mRoPE.
+        float p[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) p[e] = __shfl_xor(x[e], G / 2, 64);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          // lo half: x1*c - x2*s  (partner holds x2); hi half: x2*c + x1*s (partner holds x1).
+          x[e] = lo ? (x[e] * cs[e] - p[e] * sn[e]) : (x[e] * cs[e] + p[e] * sn[e]);
+      }
+      if (skip_store) continue;
+      store8<T, VEC>(out + 8 * j, x);
+    }
   }
 }
 
@@ -179,15 +265,26 @@ int launch_qk(const QKNormRopeArgs& a, hipStream_t st) {
   if (tokens == 0) return Q3_OK;
   Q3_REQUIRE(tokens < (1ll << 31), Q3_ERR_SHAPE);
   const int G = a.D / 8;
+  // 16-byte vector access when every row start is 16-byte aligned.
+  bool vec = q3_aligned(a.q_in, 16) && q3_aligned(a.k_in, 16) && q3_aligned(a.q_out, 16) &&
+             q3_aligned(a.k_out, 16) && (!a.v_in || (q3_aligned(a.v_in, 16) && q3_aligned(a.v_out, 16))) &&
+             (!a.q_w || (q3_aligned(a.q_w, 16) && q3_aligned(a.k_w, 16)));
+  for (int i = 0; i < 18; ++i) vec = vec && (a.st[i] * (int64_t)sizeof(T)) % 16 == 0;
+  auto go = [&](auto g, auto v) {
+    hipLaunchKernelGGL((qk_norm_rope_kernel<T, decltype(g)::value, decltype(v)::value>), dim3((unsigned)tokens),
+                       dim3(256), 0, st, a);
+  };
+  using VT = std::true_type;
+  using VF = std::false_type;
   switch (G) {
     case 8:
-      hipLaunchKernelGGL((qk_norm_rope_kernel<T, 8>), dim3((unsigned)tokens), dim3(256), 0, st, a);
+      vec ? go(std::integral_constant<int, 8>{}, VT{}) : go(std::integral_constant<int, 8>{}, VF{});
       break;
     case 16:
-      hipLaunchKernelGGL((qk_norm_rope_kernel<T, 16>), dim3((unsigned)tokens), dim3(256), 0, st, a);
+      vec ? go(std::integral_constant<int, 16>{}, VT{}) : go(std::integral_constant<int, 16>{}, VF{});
       break;
     case 32:
-      hipLaunchKernelGGL((qk_norm_rope_kernel<T, 32>), dim3((unsigned)tokens), dim3(256), 0, st, a);
+      vec ? go(std::integral_constant<int, 32>{}, VT{}) : go(std::integral_constant<int, 32>{}, VF{});
       break;
     default:
       return Q3_ERR_UNSUPPORTED;
