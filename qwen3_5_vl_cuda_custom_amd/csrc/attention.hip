@@ -659,9 +659,12 @@ __global__ __launch_bounds__(256) void flash_decode_combine(const AttnParams p) 
 
 // ----------------------------------------------------------------- prefill, pipelined (D = 128)
 // Prefill kernel for head_dim 128 and GQA groups that are a multiple of 4
-// (the text layers): one block = 4 waves = 4 query heads of one KV head over
-// the same 64 queries; each wave owns 64 queries of its head (two 32-column
-// MFMA sub-tiles), so every K/V fragment read from LDS feeds two MFMAs.
+// (the text layers): one block = 8 waves = 4 query heads of one KV head x 2
+// halves of the same 64 queries; each wave owns 32 queries of its head. All
+// 8 waves share one K/V tile ring, and a wave's state (O, two S tiles, Q)
+// fits 256 registers, so two waves run per SIMD: the MFMAs of one overlap
+// the softmax of the other (with 64 queries per wave, one wave per SIMD, the
+// same block ran ~12% slower at S=4096).
 //  * 32-key K and V tiles go global -> LDS by direct-to-LDS loads into a ring
 //    of kPipeStages tiles, kAhead tiles ahead. K rows: chunk c of row r at
 //    slot c ^ (r & 15); V rows: chunk c at slot c ^ ((r & 3) << 2), read
@@ -675,7 +678,7 @@ __global__ __launch_bounds__(256) void flash_decode_combine(const AttnParams p) 
 //  * O lives in AGPRs (MFMA accumulators); the rare rescale reads, scales and
 //    writes them back in place, so the common path never copies them.
 namespace fwdp {
-constexpr int kQ = 64;           // queries per wave
+constexpr int kQ = 64;           // queries per block (32 per wave)
 constexpr int kKeys = 32;        // keys per tile
 constexpr int kPipeStages = 8;   // K/V tile ring depth
 constexpr int kAhead = 6;        // step t issues tile t + kAhead (its slot held tile t - 2)
@@ -698,12 +701,12 @@ __device__ __forceinline__ void scale_acc(floatx16& acc, float alpha) {
 }
 }  // namespace fwdp
 
-__global__ __launch_bounds__(256) void flash_fwd_pipe_kernel(const AttnParams p) {
+__global__ __launch_bounds__(512) void flash_fwd_pipe_kernel(const AttnParams p) {
   using namespace fwdp;
   constexpr int D = 128;
   constexpr int KSTEPS = D / 16;
   constexpr int OT = D / 32;
-  constexpr int PERW = 4;  // DMA instructions per wave per tile (2 K + 2 V)
+  constexpr int PERW = 2;  // DMA instructions per wave per tile (1 K + 1 V)
   static_assert(kAhead + 2 == kPipeStages, "step t reuses the slot of tile t - 2");
   __shared__ __attribute__((aligned(1024))) bf16 ring[kPipeStages * 2 * kTile];
 
@@ -712,6 +715,7 @@ __global__ __launch_bounds__(256) void flash_fwd_pipe_kernel(const AttnParams p)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31;
   const int h = lane >> 5;
+  const int hw = wave & 3, qh = wave >> 2;  // head of the group's 4, query half
 
   const int Sq = p.Sq, Sk = p.Sk;
   const bool causal = p.causal != 0;
@@ -723,55 +727,49 @@ __global__ __launch_bounds__(256) void flash_fwd_pipe_kernel(const AttnParams p)
   yb /= hgroups;
   const int kvh = yb % p.Hkv;
   const int b = yb / p.Hkv;
-  const int hq = kvh * p.groups + hg * 4 + wave;
+  const int hq = kvh * p.groups + hg * 4 + hw;
   const int q0 = qt * kQ;
+  const int qw0 = q0 + 32 * qh;  // this wave's first query
   const int klimit = causal ? min(Sk, q0 + kQ) : Sk;
   const int nkt = (klimit + kKeys - 1) / kKeys;
 
   const bf16* kbase = p.k + (int64_t)b * p.kb + (int64_t)kvh * p.kh;
   const bf16* vbase = p.v + (int64_t)b * p.vb + (int64_t)kvh * p.vh;
-  const int ks2 = (int)p.ks * 2, vs2 = (int)p.vs * 2;  // host guarantees Sk * stride * 2 < 2^31
+  const int ks2 = (int)p.ks * 2, vs2 = (int)p.vs * 2;
   const __amdgpu_buffer_rsrc_t krs = q3::make_rsrc(kbase, (int64_t)(Sk - 1) * ks2 + D * 2);
   const __amdgpu_buffer_rsrc_t vrs = q3::make_rsrc(vbase, (int64_t)(Sk - 1) * vs2 + D * 2);
   const uint32_t lbase = q3::lds_addr(ring);
 
-  // Wave w loads rows 8w .. 8w + 7 of tile t's K and V (4 rows per instruction).
+  // Wave w loads rows 4w .. 4w + 3 of tile t's K and V (one instruction each).
   const int cs = lane & 15;
-  const int r0 = 8 * wave + (lane >> 4), r1 = r0 + 4;
-  const uint32_t kc0 = (uint32_t)((cs ^ (r0 & 15)) << 4), kc1 = (uint32_t)((cs ^ (r1 & 15)) << 4);
-  const uint32_t vc0 = (uint32_t)((cs ^ ((r0 & 3) << 2)) << 4), vc1 = (uint32_t)((cs ^ ((r1 & 3) << 2)) << 4);
+  const int r0 = 4 * wave + (lane >> 4);
+  const uint32_t kc0 = (uint32_t)((cs ^ (r0 & 15)) << 4);
+  const uint32_t vc0 = (uint32_t)((cs ^ ((r0 & 3) << 2)) << 4);
   auto issue = [&](int t) {
-    const uint32_t lk = lbase + (uint32_t)((t % kPipeStages) * 2 * kTile * 2) + (uint32_t)(8 * wave * kRowK * 2);
+    const uint32_t lk = lbase + (uint32_t)((t % kPipeStages) * 2 * kTile * 2) + (uint32_t)(4 * wave * kRowK * 2);
     const uint32_t lv = lk + kTile * 2;
     const bool live = t < nkt;
     const int row = t * kKeys;
     q3::dma16(krs, live ? (uint32_t)((row + r0) * ks2) + kc0 : q3::kOOB, lk);
-    q3::dma16(krs, live ? (uint32_t)((row + r1) * ks2) + kc1 : q3::kOOB, lk + 4 * kRowK * 2);
     q3::dma16(vrs, live ? (uint32_t)((row + r0) * vs2) + vc0 : q3::kOOB, lv);
-    q3::dma16(vrs, live ? (uint32_t)((row + r1) * vs2) + vc1 : q3::kOOB, lv + 4 * kRowK * 2);
   };
 
-  // Q fragments (B operand): lane supplies Q[q0 + 32 qs + l32][16 ks + 8 h .. + 7].
-  bf16x8 qf[2][KSTEPS];
-#pragma unroll
-  for (int qs = 0; qs < 2; ++qs) {
-    const int qi = q0 + 32 * qs + l32;
+  // Q fragments (B operand): lane supplies Q[qw0 + l32][16 ks + 8 h .. + 7].
+  bf16x8 qf[KSTEPS];
+  {
+    const int qi = qw0 + l32;
     const bf16* qrow = p.q + (int64_t)b * p.qb + (int64_t)hq * p.qh + (int64_t)qi * p.qs;
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks)
-      qf[qs][ks] = qi < Sq ? *reinterpret_cast<const bf16x8*>(qrow + ks * 16 + 8 * h) : bf16x8{};
+      qf[ks] = qi < Sq ? *reinterpret_cast<const bf16x8*>(qrow + ks * 16 + 8 * h) : bf16x8{};
   }
 
-  floatx16 o[2][OT];
+  floatx16 o[OT];
 #pragma unroll
-  for (int qs = 0; qs < 2; ++qs)
-#pragma unroll
-    for (int t = 0; t < OT; ++t) o[qs][t] = floatx16{};
-  float m[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f};
+  for (int t = 0; t < OT; ++t) o[t] = floatx16{};
+  float m = -INFINITY, lsum = 0.f;
   const float c = p.scale_log2;
 
-  // LDS element offsets of this lane's fragments within a tile: K row l32 at
-  // chunk 2 ks + h; V^T reads at V[4 h + rr (+ 16 j, + 8)][32 dt + 16 g16 + 4 qq].
   int koff[KSTEPS];
 #pragma unroll
   for (int ks = 0; ks < KSTEPS; ++ks) koff[ks] = fwd::k_off(l32, 2 * ks + h);
@@ -783,26 +781,20 @@ __global__ __launch_bounds__(256) void flash_fwd_pipe_kernel(const AttnParams p)
     voff[dt] = dec_v_off(4 * h + rr, d >> 3) + (d & 7);
   }
 
-  // S^T (32 keys x 32 queries) of tile t for query sub-tiles 0 and 1.
-  auto qk = [&](floatx16 (&s)[2], int t) {
+  auto qk = [&](floatx16& s, int t) {
     const bf16* sK = ring + (t % kPipeStages) * 2 * kTile;
-    s[0] = floatx16{};
-    s[1] = floatx16{};
+    s = floatx16{};
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
       const bf16x8 a = *reinterpret_cast<const bf16x8*>(sK + koff[ks]);
-      s[0] = mfma32x32x16(a, qf[0][ks], s[0]);
-      s[1] = mfma32x32x16(a, qf[1][ks], s[1]);
+      s = mfma32x32x16(a, qf[ks], s);
     }
   };
-  // Keys of tile t this lane must drop (MASK: the tile may hold keys past Sk
-  // or above the causal diagonal): bit r of the result is register r of
-  // query sub-tile qs. Uniformly 0 for tiles that need no mask.
-  auto tile_mask = [&](auto mask, int t, int qs) -> uint32_t {
+  auto tile_mask = [&](auto mask, int t) -> uint32_t {
     uint32_t bits = 0;
     const int k0 = t * kKeys;
-    if (decltype(mask)::value && ((causal && k0 + kKeys - 1 > q0) || k0 + kKeys > Sk)) {  // uniform
-      const int qi = q0 + 32 * qs + l32;
+    if (decltype(mask)::value && ((causal && k0 + kKeys - 1 > qw0) || k0 + kKeys > Sk)) {  // uniform
+      const int qi = qw0 + l32;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = k0 + 8 * (r >> 2) + 4 * h + (r & 3);
@@ -811,47 +803,35 @@ __global__ __launch_bounds__(256) void flash_fwd_pipe_kernel(const AttnParams p)
     }
     return bits;
   };
-  // Softmax of tile t, first part: the running max over the kept keys. When it
-  // rises by more than kRescale, O, the row sums and the not yet applied
-  // P(t - 1) fragments `pp` move to the new reference (P(t - 1) is rounded to
-  // bf16 once more; this happens a few times per row at most).
-  auto softmax_max = [&](const floatx16 (&s)[2], const uint32_t (&drop)[2], bf16x8 (&pp)[2][2]) {
+  auto softmax_max = [&](const floatx16& s, uint32_t drop, bf16x8 (&pp)[2]) {
+    float mx = -INFINITY;
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
-      float mx = -INFINITY;
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, (drop >> r) & 1 ? -INFINITY : s[r]);
+    const float mloc = fwd::half_max(mx) * c;  // -inf only for a tile wholly above this wave's queries
+    const bool raise = mloc > m + fwd::kRescale;
+    if (__builtin_amdgcn_ballot_w64(raise) != 0) {
+      const float mnew = raise ? mloc : m;
+      const float alpha = fast_exp2(m - mnew);
+      lsum *= alpha;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, (drop[qs] >> r) & 1 ? -INFINITY : s[qs][r]);
-      const float mloc = fwd::half_max(mx) * c;  // finite: key t * 32 <= q0 <= every query of the block
-      const bool raise = mloc > m[qs] + fwd::kRescale;
-      if (__builtin_amdgcn_ballot_w64(raise) != 0) {
-        const float mnew = raise ? mloc : m[qs];
-        const float alpha = fast_exp2(m[qs] - mnew);
-        lsum[qs] *= alpha;
+      for (int dt = 0; dt < OT; ++dt) scale_acc(o[dt], alpha);
 #pragma unroll
-        for (int dt = 0; dt < OT; ++dt) scale_acc(o[qs][dt], alpha);
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) pp[qs][j][e] = f2bf(bf2f(pp[qs][j][e]) * alpha);
-        m[qs] = mnew;
-      }
+        for (int e = 0; e < 8; ++e) pp[j][e] = f2bf(bf2f(pp[j][e]) * alpha);
+      m = mnew;
     }
   };
-  // Second part: exponentials into the P^T fragments (dropped keys give 0).
-  auto softmax_exp = [&](const floatx16 (&s)[2], const uint32_t (&drop)[2], bf16x8 (&pb)[2][2]) {
+  auto softmax_exp = [&](const floatx16& s, uint32_t drop, bf16x8 (&pb)[2]) {
+    const float nm = -m;
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
-      const float nm = -m[qs];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float pr = (drop[qs] >> r) & 1 ? 0.f : fast_exp2(fmaf(s[qs][r], c, nm));
-        lsum[qs] += pr;
-        pb[qs][r >> 3][r & 7] = f2bf(pr);
-      }
+    for (int r = 0; r < 16; ++r) {
+      const float pr = (drop >> r) & 1 ? 0.f : fast_exp2(fmaf(s[r], c, nm));
+      lsum += pr;
+      pb[r >> 3][r & 7] = f2bf(pr);
     }
   };
-  // O^T += V^T P^T of tile t (V^T fragments by transposed reads).
-  auto pv = [&](int t, const bf16x8 (&pb)[2][2]) {
+  auto pv = [&](int t, const bf16x8 (&pb)[2]) {
     const bf16* sV = ring + (t % kPipeStages) * 2 * kTile + kTile;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -860,24 +840,16 @@ __global__ __launch_bounds__(256) void flash_fwd_pipe_kernel(const AttnParams p)
         const short4v lo = lds_read_tr16(sV + voff[dt] + 16 * j * kRowK);
         const short4v hi = lds_read_tr16(sV + voff[dt] + (16 * j + 8) * kRowK);
         const short8v a8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        const bf16x8 av = __builtin_bit_cast(bf16x8, a8);
-        o[0][dt] = mfma32x32x16(av, pb[0][j], o[0][dt]);
-        o[1][dt] = mfma32x32x16(av, pb[1][j], o[1][dt]);
+        o[dt] = mfma32x32x16(__builtin_bit_cast(bf16x8, a8), pb[j], o[dt]);
       }
     }
   };
-
-  // Step t (1 <= t < nkt): S(t) is in `cur`, P(t - 1) in `pp`. Runs
-  // O += V(t-1) P(t-1), S(t+1) into `nxt` (past the last tile on a
-  // zero-filled slot, unused) and the softmax of S(t) into `pc`.
-  auto step = [&](auto mask, int t, const floatx16 (&cur)[2], floatx16 (&nxt)[2], bf16x8 (&pp)[2][2],
-                  bf16x8 (&pc)[2][2]) {
+  auto step = [&](auto mask, int t, const floatx16& cur, floatx16& nxt, bf16x8 (&pp)[2], bf16x8 (&pc)[2]) {
     q3::vm_wait<(kAhead - 2) * PERW>();  // this wave's part of tile t + 1 has landed
     __syncthreads();                      // every wave's; step t - 1 is done with tile t - 2
     issue(t + kAhead);
-    const uint32_t drop[2] = {tile_mask(mask, t, 0), tile_mask(mask, t, 1)};
+    const uint32_t drop = tile_mask(mask, t);
     softmax_max(cur, drop, pp);
-    // 32 MFMAs and the exponentials, none depending on another.
     pv(t - 1, pp);
     qk(nxt, t + 1);
     softmax_exp(cur, drop, pc);
@@ -888,19 +860,17 @@ __global__ __launch_bounds__(256) void flash_fwd_pipe_kernel(const AttnParams p)
   if (nkt > 0) {
 #pragma unroll
     for (int s = 0; s <= kAhead; ++s) issue(s);
-    q3::vm_wait<(kAhead - 1) * PERW>();  // tiles 0 and 1 have landed (this wave's part)
+    q3::vm_wait<(kAhead - 1) * PERW>();
     __syncthreads();
-    floatx16 sa[2], sb[2];
-    bf16x8 pa[2][2] = {}, pb[2][2] = {};
+    floatx16 sa, sb;
+    bf16x8 pa[2] = {}, pb[2] = {};
     qk(sa, 0);
     qk(sb, 1);
     {
-      const uint32_t drop[2] = {tile_mask(kMasked, 0, 0), tile_mask(kMasked, 0, 1)};
-      softmax_max(sa, drop, pb);  // pb holds no P yet: nothing in O either
+      const uint32_t drop = tile_mask(kMasked, 0);
+      softmax_max(sa, drop, pb);
       softmax_exp(sa, drop, pa);
     }
-    // Tiles below nfull hold only keys < Sk at or below every query of the
-    // block: no masking.
     const int nfull = min(causal ? q0 / kKeys : nkt, Sk / kKeys);
     int t = 1;
     for (; t + 1 < nfull; t += 2) {
@@ -918,26 +888,26 @@ __global__ __launch_bounds__(256) void flash_fwd_pipe_kernel(const AttnParams p)
       pv(t - 1, pa);
     }
   }
-  q3::vm_wait<0>();  // the trailing zero-fill DMAs must land before the block's LDS is reused
+  q3::vm_wait<0>();
 
+  {
+    const int qi = qw0 + l32;
+    const float l = lsum + __shfl_xor(lsum, 32, 64);
+    if (qi < Sq) {
+      const float inv_l = l > 0.f ? 1.0f / l : 0.f;
+      bf16* orow = p.o + (int64_t)b * p.ob + (int64_t)hq * p.oh + (int64_t)qi * p.os;
 #pragma unroll
-  for (int qs = 0; qs < 2; ++qs) {
-    const int qi = q0 + 32 * qs + l32;
-    const float l = lsum[qs] + __shfl_xor(lsum[qs], 32, 64);
-    if (qi >= Sq) continue;
-    const float inv_l = l > 0.f ? 1.0f / l : 0.f;
-    bf16* orow = p.o + (int64_t)b * p.ob + (int64_t)hq * p.oh + (int64_t)qi * p.os;
+      for (int dt = 0; dt < OT; ++dt)
 #pragma unroll
-    for (int dt = 0; dt < OT; ++dt)
+        for (int g = 0; g < 4; ++g) {
+          const int d = dt * 32 + 8 * g + 4 * h;
+          bf16x4 v4;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d = dt * 32 + 8 * g + 4 * h;
-        bf16x4 v4;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v4[e] = f2bf(o[qs][dt][4 * g + e] * inv_l);
-        *reinterpret_cast<bf16x4*>(orow + d) = v4;
-      }
-    if (p.lse && h == 0) p.lse[((int64_t)b * p.Hq + hq) * Sq + qi] = (m[qs] + log2f(l)) * 0.6931471805599453f;
+          for (int e = 0; e < 4; ++e) v4[e] = f2bf(o[dt][4 * g + e] * inv_l);
+          *reinterpret_cast<bf16x4*>(orow + d) = v4;
+        }
+      if (p.lse && h == 0) p.lse[((int64_t)b * p.Hq + hq) * Sq + qi] = (m + log2f(l)) * 0.6931471805599453f;
+    }
   }
 }
 
@@ -984,7 +954,7 @@ int launch_fwd_pipe(const AttnParams& p, hipStream_t st) {
   const int n_qt = (int)q3_cdiv(p.Sq, fwdp::kQ);
   Q3_REQUIRE(n_qt <= 65535, Q3_ERR_UNSUPPORTED);
   dim3 grid((unsigned)(p.B * p.Hkv * (p.groups / 4)), (unsigned)n_qt);
-  hipLaunchKernelGGL(flash_fwd_pipe_kernel, grid, dim3(256), 0, st, p);
+  hipLaunchKernelGGL(flash_fwd_pipe_kernel, grid, dim3(512), 0, st, p);
   Q3_LAUNCH_CHECK();
   return Q3_OK;
 }
