@@ -2,8 +2,6 @@
 // tile core in gemm_tile.h. Host launchers live in gemm.hip and moe.hip.
 #pragma once
 
-#include <type_traits>
-
 #include "gemm_tile.h"
 
 namespace q3 {
@@ -489,220 +487,6 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
     }
   }
   vm_wait<0>();  // the trailing zero-fill DMAs must land before the block's LDS is reused
-
-  store_tile<WTM, WTN, TN, TM, EPI>(p, tc, acc.c, wm, wn, lane);
-}
-
-
-// Register-staged variant of the kernel above (same tiles, fragment reads,
-// MFMAs and epilogue): operands go global -> VGPRs -> LDS instead of by
-// direct-to-LDS loads, so the loads in flight are not bounded by the LDS
-// ring. Two LDS stages (double buffer) and two register sets: stage s is
-// loaded into set s & 1 two stages before it is computed, written to LDS at
-// the start of stage s - 1 (into the slot stage s - 2 just left), and read
-// in stage s; each wave therefore keeps two stages of loads in flight, and
-// the write plus the next load are spread over the first k16 step's MFMAs.
-// One barrier per stage, before its last k16 step.
-template <int BM, int BN, int WM, int WN, int EPI, bool GROUPED, int BKT>
-__global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_rs_kernel(const GemmParams p) {
-  constexpr int NW = WM * WN;
-  constexpr int WTM = BM / WM;
-  constexpr int WTN = BN / WN;
-  constexpr int TM = WTM / 32;
-  constexpr int TN = WTN / 32;
-  static_assert(TM >= 1 && TN >= 1, "wave tile too small");
-  static_assert(EPI != kEpiSwiGLU || (TN % 2 == 0), "SwiGLU pairs gate/up tiles");
-  static_assert(BKT == 32 || BKT == 64, "stage width");
-  constexpr int BN_OUT = (EPI == kEpiSwiGLU) ? BN / 2 : BN;
-  constexpr int CH = BKT / 8;              // 16-byte chunks per LDS row
-  constexpr int KS = BKT / 16;             // MFMA K steps per stage
-  constexpr int kStage = (BM + BN) * BKT;  // elements per LDS slot
-  constexpr int RPI = 64 / CH;             // rows per load instruction
-  constexpr int DX = BM / RPI, DW = BN / RPI;
-  static_assert(DX % NW == 0 && DW % NW == 0, "loads must split evenly over the waves");
-  constexpr int PX = DX / NW, PW = DW / NW;  // per wave and stage
-  constexpr int ND = PX + PW;
-  static_assert(KS >= 2, "the first step carries the stage's writes and loads, the last its barrier");
-
-  __shared__ __attribute__((aligned(1024))) bf16 smem[2 * kStage];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave % WM;
-  const int wn = wave / WM;
-
-  TileCtx tc;
-  if (!tile_ctx<BM, BN_OUT, EPI, GROUPED>(p, tc)) return;
-  const int m_begin = tc.m_begin, rows_m = tc.rows_m, n0_out = tc.n0_out, n_lim = tc.n_lim;
-  const int K = p.K;
-  const int nk = (K + BKT - 1) / BKT;
-  const int64_t ldx = p.ldx, ldw = p.ldw;
-
-  // Load d of this wave: global row offset (kOOB past the tile's rows), and
-  // its LDS byte offset within a slot. The lane reads chunk `lslot` of the
-  // row (contiguous row pieces) and stores it at slot lslot ^ swz(row).
-  const int lrow = lane / CH, lslot = lane % CH;
-  uint32_t goff[ND], loff[ND];
-  const bf16* wsrc[PW];
-  int wrows[PW];
-#pragma unroll
-  for (int i = 0; i < PX; ++i) {
-    const int r = (wave + NW * i) * RPI + lrow;
-    loff[i] = (uint32_t)((r * BKT + ((lslot ^ dma_swz<BKT>(r)) << 3)) * 2);
-    if (r < rows_m) {
-      const int lr = m_begin + r;
-      const int64_t pr = p.gather ? (int64_t)p.gather[lr] : (int64_t)lr;
-      goff[i] = (uint32_t)(pr * ldx * 2);
-    } else {
-      goff[i] = kOOB;
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < PW; ++i) {
-    const int r = (wave + NW * i) * RPI + lrow;
-    loff[PX + i] = (uint32_t)(((BM + r) * BKT + ((lslot ^ dma_swz<BKT>(r)) << 3)) * 2);
-    int n, rbase = 0, rlim;
-    const bf16* wb;
-    if constexpr (EPI == kEpiSwiGLU) {
-      n = n0_out + (r >> 6) * 32 + (r & 31);  // 32-row groups alternate gate / up
-      const bool up = (((wave + NW * i) * RPI) >> 5) & 1;
-      wb = up ? tc.W2 : tc.W;
-      rlim = p.N;
-    } else {
-      n = n0_out + r;
-      wb = tc.W;
-      rlim = n_lim;
-      if (!GROUPED && p.seg.n > 1) {
-        const int n_first = n0_out + (wave + NW * i) * RPI;
-        const int sgi = __builtin_amdgcn_readfirstlane(segment_of(p.seg, n_first));
-        wb = pick4(sgi, p.seg.w[0], p.seg.w[1], p.seg.w[2], p.seg.w[3]);
-        rbase = pick4(sgi, p.seg.start[0], p.seg.start[1], p.seg.start[2], p.seg.start[3]);
-        const int end = sgi + 1 < p.seg.n ? pick4(sgi, p.seg.start[1], p.seg.start[2], p.seg.start[3], p.N) : p.N;
-        rlim = end - rbase;
-      }
-    }
-    wb = uniform_ptr(wb);
-    rbase = __builtin_amdgcn_readfirstlane(rbase);
-    rlim = __builtin_amdgcn_readfirstlane(rlim);
-    wsrc[i] = wb;
-    wrows[i] = rlim;
-    goff[PX + i] = (n - rbase < rlim) ? (uint32_t)((int64_t)(n - rbase) * ldw * 2) : kOOB;
-  }
-  const __amdgpu_buffer_rsrc_t rx =
-      make_rsrc(tc.X, p.gather ? (int64_t)p.M_src * ldx * 2 : (int64_t)(m_begin + rows_m) * ldx * 2);
-  char* const lds_bytes = reinterpret_cast<char*>(smem);
-
-  bf16x8 R[2][ND];
-  // Stage kt's loads into register set `set` (zeros past K).
-  auto gload_one = [&](int kt, int set, int d) {
-    const int k = kt * BKT + lslot * 8;
-    const uint32_t off = (k < K && goff[d] != kOOB) ? goff[d] + (uint32_t)k * 2u : kOOB;
-    if (d < PX)
-      R[set][d] = buffer_load16(rx, off);
-    else
-      R[set][d] = buffer_load16(make_rsrc(wsrc[d - PX], (int64_t)wrows[d - PX] * ldw * 2), off);
-  };
-  auto lwrite_one = [&](int set, int slot, int d) {
-    *reinterpret_cast<bf16x8*>(lds_bytes + slot * kStage * 2 + loff[d]) = R[set][d];
-  };
-
-  WaveAcc<TN, TM> acc;
-  acc.zero();
-  const int l32 = lane & 31, h = lane >> 5;
-  const int rn = wn * WTN, rm = wm * WTM;
-  bf16x8 fa[2][TN], fb[2][TM];
-  auto read = [&](int buf, int slot, int ks) {
-    const bf16* sx = smem + slot * kStage;
-    const bf16* sw = sx + BM * BKT;
-    const int c = ks * 2 + h;
-#pragma unroll
-    for (int i = 0; i < TN; ++i) {
-      const int r = rn + i * 32 + l32;
-      fa[buf][i] = *reinterpret_cast<const bf16x8*>(sw + r * BKT + ((c ^ dma_swz<BKT>(r)) << 3));
-    }
-#pragma unroll
-    for (int j = 0; j < TM; ++j) {
-      const int r = rm + j * 32 + l32;
-      fb[buf][j] = *reinterpret_cast<const bf16x8*>(sx + r * BKT + ((c ^ dma_swz<BKT>(r)) << 3));
-    }
-  };
-  auto mma = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < TN; ++i)
-#pragma unroll
-      for (int j = 0; j < TM; ++j) acc.c[i][j] = mfma32x32x16(fa[buf][i], fb[buf][j], acc.c[i][j]);
-  };
-  auto interleave = [&]() {
-    constexpr int NR = TN + TM, NM = TN * TM;
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, NM - NR, 0);
-  };
-  // First k16 step of stage kt: its MFMAs with the next step's fragment reads,
-  // the LDS writes of stage kt + 1 (set `ns`, into slot ns) and the loads of
-  // stage kt + 3 (into the same set) spread between them, order pinned.
-  auto first_step = [&](int kt, int slot, int ns) {
-    read(1, slot, 1);
-    __builtin_amdgcn_sched_barrier(0);
-    int d = 0;
-#pragma unroll
-    for (int i = 0; i < TN; ++i)
-#pragma unroll
-      for (int j = 0; j < TM; ++j) {
-        acc.c[i][j] = mfma32x32x16(fa[0][i], fb[0][j], acc.c[i][j]);
-        if (d < ND) {
-          lwrite_one(ns, ns, d);
-          gload_one(kt + 3, ns, d);
-          ++d;
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-#pragma unroll
-    for (; d < ND; ++d) {
-      lwrite_one(ns, ns, d);
-      gload_one(kt + 3, ns, d);
-    }
-  };
-  // Stage kt from LDS slot `slot` (= kt & 1, static); set ns = slot ^ 1.
-  auto stage = [&](int kt, auto slot_c) {
-    constexpr int slot = decltype(slot_c)::value;
-    constexpr int ns = slot ^ 1;
-    first_step(kt, slot, ns);
-#pragma unroll
-    for (int ks = 1; ks < KS; ++ks) {
-      if (ks + 1 < KS) {
-        read((ks + 1) & 1, slot, ks + 1);
-        mma(ks & 1);
-        interleave();
-      } else {
-        __syncthreads();  // stage kt + 1 is in slot ns for everyone; nobody reads slot `slot` any more
-        read((ks + 1) & 1, ns, 0);
-        mma(ks & 1);
-        interleave();
-      }
-    }
-  };
-
-#pragma unroll
-  for (int d = 0; d < ND; ++d) gload_one(0, 0, d);
-#pragma unroll
-  for (int d = 0; d < ND; ++d) gload_one(1, 1, d);
-#pragma unroll
-  for (int d = 0; d < ND; ++d) lwrite_one(0, 0, d);
-#pragma unroll
-  for (int d = 0; d < ND; ++d) gload_one(2, 0, d);
-  __syncthreads();
-  read(0, 0, 0);
-  int kt = 0;
-  for (; kt + 1 < nk; kt += 2) {
-    stage(kt, std::integral_constant<int, 0>{});
-    stage(kt + 1, std::integral_constant<int, 1>{});
-  }
-  if (kt < nk) stage(kt, std::integral_constant<int, 0>{});
 
   store_tile<WTM, WTN, TN, TM, EPI>(p, tc, acc.c, wm, wn, lane);
 }

@@ -55,13 +55,13 @@ def test_matmul_validation():
     assert L.q3_matmul(FAKE, FAKE, None, None, FAKE, -1, 4, 4, 4, 4, 0, 4, 1, None, 0, None) == -2
     assert L.q3_matmul(FAKE, FAKE, None, None, FAKE, 4, 4, 8, 4, 8, 0, 4, 1, None, 0, None) == -2  # ldx < K
     assert L.q3_matmul(FAKE, FAKE, None, None, FAKE, 4, 4, 4, 4, 4, 0, 4, 7, None, 0, None) == -3
-    # decode-shaped bf16 GEMM: the row-owned kernel (M <= 8 or K <= 8192) needs no
-    # workspace; the stream-K kernel (M > 8, K > 8192) needs its split-K workspace
-    assert L.q3_matmul_workspace_bytes(32, 4096, 4096, 1, 0) == 0
-    assert L.q3_matmul_workspace_bytes(8, 4096, 12288, 1, 0) == 0
-    ws = L.q3_matmul_workspace_bytes(32, 4096, 12288, 1, 0)
+    # decode-shaped bf16 GEMM: the row-owned kernel (M <= 8 or K <= 16384) needs no
+    # workspace; the stream-K kernel (M > 8, K > 16384) needs its split-K workspace
+    assert L.q3_matmul_workspace_bytes(32, 4096, 12288, 1, 0) == 0
+    assert L.q3_matmul_workspace_bytes(8, 4096, 20480, 1, 0) == 0
+    ws = L.q3_matmul_workspace_bytes(32, 4096, 20480, 1, 0)
     assert ws > 0
-    assert L.q3_matmul(FAKE, FAKE, None, None, FAKE, 32, 4096, 12288, 12288, 12288, 0, 4096, 1, None, 0, None) == -6
+    assert L.q3_matmul(FAKE, FAKE, None, None, FAKE, 32, 4096, 20480, 20480, 20480, 0, 4096, 1, None, 0, None) == -6
     assert L.q3_matmul_workspace_bytes(4096, 4096, 4096, 1, 0) == 0
     assert L.q3_matmul(FAKE, FAKE, None, None, FAKE, 0, 4, 4, 4, 4, 0, 4, 1, None, 0, None) == 0  # empty: no-op
 
@@ -78,9 +78,9 @@ def test_matmul_segments_validation():
     assert L.q3_matmul_segments(FAKE, ws3, None, ns, 3, FAKE, 8, 4096, 4096, 4096, 6000, 1, None, 0, None) == -2
     assert L.q3_matmul_segments(FAKE, ws3, None, ns, 3, FAKE, 8, 4096, 4096, 4096, 6144, 7, None, 0, None) == -3
     assert L.q3_matmul_segments_workspace_bytes(8, ns, 3, 4096, 1) == 0  # row-owned kernel
-    need = L.q3_matmul_segments_workspace_bytes(32, ns, 3, 12288, 1)
+    need = L.q3_matmul_segments_workspace_bytes(32, ns, 3, 20480, 1)
     assert need > 0
-    assert L.q3_matmul_segments(FAKE, ws3, None, ns, 3, FAKE, 32, 12288, 12288, 12288, 6144, 1, None, 0, None) == -6
+    assert L.q3_matmul_segments(FAKE, ws3, None, ns, 3, FAKE, 32, 20480, 20480, 20480, 6144, 1, None, 0, None) == -6
     assert L.q3_matmul_segments_workspace_bytes(4096, ns, 3, 4096, 1) == 0
     assert L.q3_matmul_segments(FAKE, ws3, None, ns, 3, FAKE, 0, 4096, 4096, 4096, 6144, 1, None, 0, None) == 0
 

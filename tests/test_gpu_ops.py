@@ -132,35 +132,38 @@ def test_decode_gemv_shapes(M):
     (12, (700,), 1000, "swiglu"),          # SwiGLU, X staged, ragged K chunk
     (8, (4096,), 2048, "residual"),        # last M of the direct-X kernel
     (32, (128,), 2048, "plain"),           # router-sized: 8 rows per block, 16 blocks
+    (17, (1024,), 16400, "residual"),      # M > 8, K > 16384: the stream-K kernel
+    (17, (512,), 16384, "swiglu"),         # last K of the row-owned kernel
 ])
-def test_gemv_row_owned_edges(M, ns, Kd, kind):
-    """Decode shapes on the row-owned GEMV (M <= 8, or K <= 8192): ragged rows,
-    K tails, segments with bias, residual, SwiGLU; and run-to-run identity.
-    Weights ~N(0, 0.015^2) keep the outputs near unit scale, where half a bf16
-    ulp stays inside the 2e-2 bound."""
+def test_gemv_edges(M, ns, Kd, kind):
+    """Decode shapes (M <= 32) on the row-owned GEMV (M <= 8, or K <= 16384) and
+    the stream-K one: ragged rows, K tails, segments with bias, residual,
+    SwiGLU; and run-to-run identity. Weights ~N(0, 1/K) keep the outputs near
+    unit scale, where half a bf16 ulp stays inside the 2e-2 bound."""
+    sd = Kd ** -0.5
     x = rnd(M, Kd, seed=90)
     if kind == "swiglu":
-        wg, wu = rnd(ns[0], Kd, seed=91, std=0.015), rnd(ns[0], Kd, seed=92, std=0.015)
+        wg, wu = rnd(ns[0], Kd, seed=91, std=sd), rnd(ns[0], Kd, seed=92, std=sd)
         y = K.matmul_swiglu(gpu(x), gpu(wg), gpu(wu))
         ref = O.swiglu(O.linear(f32(x), f32(wg)), O.linear(f32(x), f32(wu)))
         again = K.matmul_swiglu(gpu(x), gpu(wg), gpu(wu))
     elif len(ns) > 1:
-        ws = [rnd(n, Kd, seed=93 + i, std=0.015) for i, n in enumerate(ns)]
-        bs = [rnd(n, seed=97 + i, std=0.015) for i, n in enumerate(ns)]
+        ws = [rnd(n, Kd, seed=93 + i, std=sd) for i, n in enumerate(ns)]
+        bs = [rnd(n, seed=97 + i, std=sd) for i, n in enumerate(ns)]
         y = K.matmul_segments(gpu(x), [gpu(w) for w in ws], [gpu(b) for b in bs])
         ref = torch.cat([O.linear(f32(x), f32(w), f32(b)) for w, b in zip(ws, bs)], dim=-1)
         again = K.matmul_segments(gpu(x), [gpu(w) for w in ws], [gpu(b) for b in bs])
     else:
-        w = rnd(ns[0], Kd, seed=94, std=0.015)
-        b = rnd(ns[0], seed=95, std=0.015) if kind == "bias" else None
+        w = rnd(ns[0], Kd, seed=94, std=sd)
+        b = rnd(ns[0], seed=95, std=sd) if kind == "bias" else None
         r = rnd(M, ns[0], seed=96) if kind == "residual" else None
         y = K.matmul(gpu(x), gpu(w), gpu(b) if b is not None else None,
                      residual=gpu(r) if r is not None else None)
         ref = O.linear(f32(x), f32(w), f32(b) if b is not None else None) + (f32(r) if r is not None else 0)
         again = K.matmul(gpu(x), gpu(w), gpu(b) if b is not None else None,
                          residual=gpu(r) if r is not None else None)
-    assert_bf16_close(y, ref, what=f"row-owned gemv M={M} N={ns} K={Kd} {kind}")
-    assert torch.equal(y.cpu(), again.cpu()), "the row-owned GEMV must be deterministic"
+    assert_bf16_close(y, ref, what=f"gemv M={M} N={ns} K={Kd} {kind}")
+    assert torch.equal(y.cpu(), again.cpu()), "the GEMV must be deterministic"
 
 
 def test_matmul_fp32_reference_style():
