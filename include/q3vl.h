@@ -79,6 +79,25 @@ int q3_matmul_swiglu(const void* x, const void* w_gate, const void* w_up, void* 
                      int64_t ldx, int64_t ldw, int64_t ldc, int dtype, void* workspace, int64_t workspace_bytes,
                      void* stream);
 
+/* Decode-shaped (1 <= M <= 32 rows, bf16) RMSNorm fused into the projection
+ * that consumes it: y = rmsnorm(x; norm_w, eps) . w^T, per segment (+ bias),
+ * or silu(. w_gate) * (. w_up). The rows are normalised as X is staged into
+ * the weight-streaming kernel (x * norm_w rounded to bf16 once, rows scaled
+ * by rsqrt(mean(x^2) + eps) in fp32 after the dot products), so the
+ * normalised rows never go to memory. Equals q3_rmsnorm followed by
+ * q3_matmul_segments / q3_matmul_swiglu to bf16 rounding. No counterpart in
+ * the reference (CudaTextDecoderLayer.forward, modules/text_decoder.py:56-58,
+ * runs the RMSNorm and then the projections); used by this library's
+ * decoder-layer composition for decode steps. Needs x,
+ * norm_w and each weight 16-byte aligned, ldx, ldw and K multiples of 8
+ * (else Q3_ERR_ALIGN); M > 32 gives Q3_ERR_UNSUPPORTED. No workspace. */
+int q3_rmsnorm_matmul_segments(const void* x, const void* norm_w, float eps, const void* const* w,
+                               const void* const* bias, const int64_t* n, int64_t nseg, void* y, int64_t M, int64_t K,
+                               int64_t ldx, int64_t ldw, int64_t ldc, int dtype, void* stream);
+int q3_rmsnorm_matmul_swiglu(const void* x, const void* norm_w, float eps, const void* w_gate, const void* w_up,
+                             void* y, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw, int64_t ldc,
+                             int dtype, void* stream);
+
 /* y[e] = x[e] . w[e]^T for x (E, M, K), w (E, N, K), y (E, M, N), contiguous.
  * Replaces batched_gemm_forward(Tensor x, Tensor weight)
  * (csrc/moe_routing_op.cpp:12, kernels/moe_routing.py:126-181). */

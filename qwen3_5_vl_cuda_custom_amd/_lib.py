@@ -32,6 +32,8 @@ _SIGS: dict[str, tuple] = {
     "q3_matmul_swiglu": (c_int, [_V, _V, _V, _V, _I, _I, _I, _I, _I, _I, c_int, _V, _I, _V]),
     "q3_matmul_segments_workspace_bytes": (c_int64, [_I, _i64p, _I, _I, c_int]),
     "q3_matmul_segments": (c_int, [_V, _V, _V, _i64p, _I, _V, _I, _I, _I, _I, _I, c_int, _V, _I, _V]),
+    "q3_rmsnorm_matmul_segments": (c_int, [_V, _V, c_float, _V, _V, _i64p, _I, _V, _I, _I, _I, _I, _I, c_int, _V]),
+    "q3_rmsnorm_matmul_swiglu": (c_int, [_V, _V, c_float, _V, _V, _V, _I, _I, _I, _I, _I, _I, c_int, _V]),
     "q3_batched_gemm": (c_int, [_V, _V, _V, _I, _I, _I, _I, c_int, _V]),
     "q3_residual_add": (c_int, [_V, _V, _V, _I, c_int, _V]),
     "q3_swiglu": (c_int, [_V, _V, _V, _I, c_int, _V]),

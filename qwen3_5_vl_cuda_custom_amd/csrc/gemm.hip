@@ -1,4 +1,5 @@
-// GEMM entry points of the C-ABI: q3_matmul, q3_matmul_swiglu, q3_batched_gemm.
+// GEMM entry points of the C-ABI: q3_matmul, q3_matmul_swiglu, q3_matmul_segments,
+// q3_rmsnorm_matmul_segments, q3_rmsnorm_matmul_swiglu, q3_batched_gemm.
 //
 //   Y[m, n] = sum_k X[m, k] * W[n, k] (+ bias[n]) (+ R[m, n])   (nn.Linear layout)
 //
@@ -269,6 +270,36 @@ int segments_impl(const void* x, const void* const* w, const void* const* bias, 
   return launch_tiled<kEpiStore>(p, 1, st);
 }
 
+// Decode-shaped RMSNorm fused into the projection that consumes it (row-owned
+// GEMV, staged X path). Only bf16, 1 <= M <= 32; no workspace.
+int rmsnorm_gemv_impl(const void* x, const void* norm_w, float eps, WeightSegments seg, const void* w_up, void* y,
+                      int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw, int64_t ldc, int dtype,
+                      hipStream_t st) {
+  Q3_REQUIRE(x && norm_w && y, Q3_ERR_NULL);
+  Q3_REQUIRE(M >= 0 && N >= 0 && K >= 0 && ldx >= K && ldw >= K && ldc >= N && N < (1ll << 31), Q3_ERR_SHAPE);
+  Q3_REQUIRE(M <= kGemvMaxRows, Q3_ERR_UNSUPPORTED);
+  Q3_REQUIRE(dtype == Q3_BF16, Q3_ERR_DTYPE);
+  Q3_REQUIRE(eps >= 0.f, Q3_ERR_SHAPE);
+  if (M == 0 || N == 0) return Q3_OK;
+  Q3_REQUIRE(K > 0, Q3_ERR_SHAPE);
+  Q3_REQUIRE(q3_aligned(norm_w, 16), Q3_ERR_ALIGN);
+  GemvArgs ga{};
+  ga.X = static_cast<const bf16*>(x);
+  ga.ldx = ldx;
+  ga.seg = seg;
+  ga.W2 = static_cast<const bf16*>(w_up);
+  ga.C = static_cast<bf16*>(y);
+  ga.ldc = ldc;
+  ga.M = (int)M;
+  ga.N = (int)N;
+  ga.K = (int)K;
+  ga.ldw = ldw;
+  ga.nw = static_cast<const bf16*>(norm_w);
+  ga.eps = eps;
+  Q3_REQUIRE(gemv_eligible(ga), Q3_ERR_ALIGN);
+  return gemv_launch(ga, nullptr, 0, st);
+}
+
 }  // namespace
 
 extern "C" {
@@ -309,6 +340,37 @@ int q3_matmul_swiglu(const void* x, const void* w_gate, const void* w_up, void* 
                      void* stream) {
   return matmul_impl(x, w_gate, w_up, nullptr, nullptr, y, M, N, K, 1, ldx, ldw, 0, ldc, 0, 0, 0, dtype, true,
                      workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int q3_rmsnorm_matmul_segments(const void* x, const void* norm_w, float eps, const void* const* w,
+                               const void* const* bias, const int64_t* n, int64_t nseg, void* y, int64_t M, int64_t K,
+                               int64_t ldx, int64_t ldw, int64_t ldc, int dtype, void* stream) {
+  Q3_REQUIRE(w && n, Q3_ERR_NULL);
+  Q3_REQUIRE(nseg >= 1 && nseg <= 4, Q3_ERR_SHAPE);
+  WeightSegments seg{};
+  seg.n = (int)nseg;
+  int64_t N = 0;
+  for (int64_t i = 0; i < nseg; ++i) {
+    Q3_REQUIRE(w[i], Q3_ERR_NULL);
+    Q3_REQUIRE(n[i] >= 0, Q3_ERR_SHAPE);
+    seg.start[i] = (int)N;
+    seg.w[i] = static_cast<const bf16*>(w[i]);
+    seg.b[i] = bias ? static_cast<const bf16*>(bias[i]) : nullptr;
+    N += n[i];
+  }
+  return rmsnorm_gemv_impl(x, norm_w, eps, seg, nullptr, y, M, N, K, ldx, ldw, ldc, dtype,
+                           static_cast<hipStream_t>(stream));
+}
+
+int q3_rmsnorm_matmul_swiglu(const void* x, const void* norm_w, float eps, const void* w_gate, const void* w_up,
+                             void* y, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw, int64_t ldc,
+                             int dtype, void* stream) {
+  Q3_REQUIRE(w_gate && w_up, Q3_ERR_NULL);
+  WeightSegments seg{};
+  seg.n = 1;
+  seg.w[0] = static_cast<const bf16*>(w_gate);
+  return rmsnorm_gemv_impl(x, norm_w, eps, seg, w_up, y, M, N, K, ldx, ldw, ldc, dtype,
+                           static_cast<hipStream_t>(stream));
 }
 
 int q3_batched_gemm(const void* x, const void* w, void* y, int64_t E, int64_t M, int64_t N, int64_t K, int dtype,

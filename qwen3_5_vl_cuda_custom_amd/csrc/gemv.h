@@ -19,6 +19,8 @@ struct GemvArgs {
   int64_t ldc;
   int M, N, K;
   int64_t ldw;
+  const bf16* nw;  // RMSNorm weight (K) applied to the X rows first (row-owned kernel), or null
+  float eps;       // RMSNorm epsilon when nw is set
 };
 
 // True when the GEMV path takes the problem (bf16 rows 16-byte aligned,

@@ -429,8 +429,13 @@ struct RowsParams {
   int vec4;       // C (and R, bias) allow 8-byte access at 4-aligned columns
 };
 
-template <int RG, int MT, bool SW, bool STAGED, int D>
+// NORM (staged X only): the X rows are RMS-normalised on their way in. The LDS
+// copy holds bf16(x * w_norm); each staging lane keeps its rows' partial sums
+// of x^2 over the K it loads; the epilogue scales each row's dot products by
+// rsqrt(sum / K + eps), which equals projecting the normalised rows.
+template <int RG, int MT, bool SW, bool STAGED, int D, bool NORM>
 __global__ __launch_bounds__(256) void gemv_rows_kernel(const RowsParams p) {
+  static_assert(!NORM || STAGED, "the fused norm runs on the staged X path");
   constexpr int NW = 4;
   constexpr int RGT = SW ? 2 * RG : RG;
   constexpr int XR = 16 * MT;              // X rows of the MFMA B operand
@@ -439,6 +444,7 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const RowsParams p) {
   constexpr int SPW = SPC / NW;            // k-steps per wave per chunk
   __shared__ __attribute__((aligned(1024))) bf16 xs[STAGED ? 2 : 1][STAGED ? XR * kRowsKC : 8];
   __shared__ floatx4 red[NW][RGT][MT][64];
+  __shared__ float rsum[NORM ? XR : 1];  // NORM: sum of x^2 of each X row
   const GemvArgs& a = p.a;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -470,7 +476,7 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const RowsParams p) {
   // Wave step j -> k-step: staged, chunk j / SPW, in-chunk step wave + NW * (j % SPW)
   // (every wave has NC * SPW steps; those past K load zeros); direct, wave + NW * j.
   const int nsw = STAGED ? NC * SPW : (S - wave + NW - 1) / NW;
-  auto kstep = [&](int j) { return STAGED ? (j / SPW) * SPC + wave + NW * (j % SPW) : wave + NW * j; };
+  auto kstep = [&](int j) __attribute__((always_inline)) { return STAGED ? (j / SPW) * SPC + wave + NW * (j % SPW) : wave + NW * j; };
 
   bf16x8 wf[D][RGT];
   bf16x8 xd[STAGED ? 1 : D][MT];
@@ -481,7 +487,7 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const RowsParams p) {
     for (int t = 0; t < MT; ++t) acc[q][t] = floatx4{};
 
   // Operands of wave step j into ring slot `slot`; k >= K loads zeros.
-  auto load = [&](int j, int slot) {
+  auto load = [&](int j, int slot) __attribute__((always_inline)) {
     const int kk = 32 * kstep(j) + 8 * g;
     const uint32_t kmask = (uint32_t)((K - 1 - kk) >> 31) << 31;
 #pragma unroll
@@ -504,22 +510,47 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const RowsParams p) {
   // the fragment reads (16 rows, one chunk) hit 16 different bank groups.
   // Two register buffers: chunk c's rows sit in xr[c & 1] from two chunks
   // before their LDS store, so the W loads issued in between stay in flight.
+  // NORM: lane l loads chunk l of every row instead and stores it at slot
+  // l ^ (row & 15) (the same LDS layout), so one norm-weight piece per lane and
+  // chunk (wn) serves all of the lane's rows.
   bf16x8 xr[2][STAGED ? XPW : 1];
-  auto xload = [&](int c, int rb) {
+  bf16x8 wn[NORM ? 2 : 1];
+  float ss[NORM ? XPW : 1];
+#pragma unroll
+  for (int e = 0; e < (NORM ? XPW : 1); ++e) ss[e] = 0.f;
+  const __amdgpu_buffer_rsrc_t rn = make_rsrc(NORM ? a.nw : a.X, NORM ? (int64_t)K * 2 : 0);
+  auto xload = [&](int c, int rb) __attribute__((always_inline)) {
 #pragma unroll
     for (int e = 0; e < XPW; ++e) {
       const int m = wave * XPW + e;
-      const int kk = c * kRowsKC + 8 * (lane ^ (m & 15));
+      const int kk = c * kRowsKC + 8 * (NORM ? lane : (lane ^ (m & 15)));
       const uint32_t o = (m < M && kk < K) ? (uint32_t)((m * a.ldx + kk) * 2) : kOOB;
       xr[rb][e] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0));
     }
+    if constexpr (NORM) {
+      const int kk = c * kRowsKC + 8 * lane;
+      wn[rb] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rn, kk < K ? (uint32_t)kk * 2u : kOOB, 0, 0));
+    }
   };
-  auto xstore = [&](int buf) {
+  auto xstore = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
-    for (int e = 0; e < XPW; ++e)
-      *reinterpret_cast<bf16x8*>(&xs[buf][(wave * XPW + e) * kRowsKC + 8 * lane]) = xr[buf][e];
+    for (int e = 0; e < XPW; ++e) {
+      const int m = wave * XPW + e;
+      if constexpr (NORM) {
+        bf16x8 y;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const float f = bf2f(xr[buf][e][q]);
+          ss[e] += f * f;
+          y[q] = f2bf(f * bf2f(wn[buf][q]));
+        }
+        *reinterpret_cast<bf16x8*>(&xs[buf][m * kRowsKC + 8 * (lane ^ (m & 15))]) = y;
+      } else {
+        *reinterpret_cast<bf16x8*>(&xs[buf][m * kRowsKC + 8 * lane]) = xr[buf][e];
+      }
+    }
   };
-  auto comp = [&](int j, int slot) {
+  auto comp = [&](int j, int slot) __attribute__((always_inline)) {
     bf16x8 xf[MT];
     if constexpr (STAGED) {
       const bf16* xb = xs[(j / SPW) & 1];
@@ -543,7 +574,7 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const RowsParams p) {
   // c & 1, which last held chunk c - 2 (finished by every wave before the
   // barrier of chunk c - 1); chunk c + 2 is loaded into the freed registers
   // (zeros past K). `cb` = c & 1, static in the unrolled loops below.
-  auto chunk = [&](int c, int cb) {
+  auto chunk = [&](int c, int cb) __attribute__((always_inline)) {
     xstore(cb);
     xload(c + 2, cb);
     __syncthreads();
@@ -609,6 +640,17 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const RowsParams p) {
   for (int q = 0; q < RGT; ++q)
 #pragma unroll
     for (int t = 0; t < MT; ++t) red[wave][q][t][lane] = acc[q][t];
+  if constexpr (NORM) {
+    // The wave's rows: partial sums over its 64 lanes (each lane saw 8 of
+    // every 512 k of the row).
+#pragma unroll
+    for (int e = 0; e < XPW; ++e) {
+      float v = ss[e];
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+      if (lane == 0) rsum[wave * XPW + e] = v;
+    }
+  }
   __syncthreads();
   const bf16* bias = SW ? nullptr : pick4(s, a.seg.b[0], a.seg.b[1], a.seg.b[2], a.seg.b[3]);
   const int cbase = seg_start + n0;
@@ -620,11 +662,15 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const RowsParams p) {
     floatx4 v = red[0][q][t][l];
 #pragma unroll
     for (int w = 1; w < NW; ++w) v += red[w][q][t][l];
+    float rstd = 1.f;
+    if constexpr (NORM) rstd = rsqrtf(rsum[m] / (float)K + a.eps);
+    if constexpr (NORM) v *= rstd;
     float o[4];
     if constexpr (SW) {
       floatx4 u = red[0][RG + q][t][l];
 #pragma unroll
       for (int w = 1; w < NW; ++w) u += red[w][RG + q][t][l];
+      if constexpr (NORM) u *= rstd;
 #pragma unroll
       for (int e = 0; e < 4; ++e) o[e] = silu_mul(v[e], u[e]);
     } else {
@@ -673,16 +719,17 @@ int device_cus() {
   return cached[dev];
 }
 
-template <int RG, int MT, bool SW, bool STAGED>
+template <int RG, int MT, bool SW, bool STAGED, bool NORM>
 void rows_launch_d(const RowsParams& p, int grid, hipStream_t st) {
   constexpr int RGT = SW ? 2 * RG : RG;
   constexpr int D = RGT <= 4 ? 8 : 4;  // register ring: ~32-48 KB of W in flight per CU
-  hipLaunchKernelGGL((gemv_rows_kernel<RG, MT, SW, STAGED, D>), dim3(grid), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((gemv_rows_kernel<RG, MT, SW, STAGED, D, NORM>), dim3(grid), dim3(256), 0, st, p);
 }
 template <int RG, int MT, bool SW>
 void rows_launch_x(const RowsParams& p, int grid, hipStream_t st) {
-  if (p.a.M <= kRowsDirectMaxM) rows_launch_d<RG, 1, SW, false>(p, grid, st);
-  else rows_launch_d<RG, MT, SW, true>(p, grid, st);
+  if (p.a.nw) rows_launch_d<RG, MT, SW, true, true>(p, grid, st);  // the fused norm stages X
+  else if (p.a.M <= kRowsDirectMaxM) rows_launch_d<RG, 1, SW, false, false>(p, grid, st);
+  else rows_launch_d<RG, MT, SW, true, false>(p, grid, st);
 }
 template <bool SW>
 void rows_launch_rg(const RowsParams& p, int rg, int grid, hipStream_t st) {
@@ -757,7 +804,10 @@ GemvPlan gemv_plan(int64_t N, int64_t K, bool swiglu) {
 
 bool gemv_eligible(const GemvArgs& a) {
   if (a.M < 1 || a.M > kGemvMaxRows || a.N < 1 || a.K < 8 || (a.K % 8) != 0) return false;
-  if (q3_cdiv(a.N, a.W2 ? 64 : kGvBN) > kGvMaxTiles) return false;
+  // Tile count and segment alignment bound the stream-K kernel only; a fused
+  // norm always runs the row-owned one.
+  const bool sk = a.nw == nullptr && !rows_selected(a.M, a.K);
+  if (sk && q3_cdiv(a.N, a.W2 ? 64 : kGvBN) > kGvMaxTiles) return false;
   if (a.seg.n < 1 || a.seg.n > 4) return false;
   if (!q3_aligned(a.X, 16) || (a.ldx % 8) != 0 || (a.ldw % 8) != 0) return false;
   if ((int64_t)a.M * a.ldx * 2 >= 0x7fffffffLL) return false;
@@ -769,7 +819,7 @@ bool gemv_eligible(const GemvArgs& a) {
   }
   for (int i = 0; i < a.seg.n; ++i) {
     const int64_t end = i + 1 < a.seg.n ? a.seg.start[i + 1] : a.N;
-    if (!a.seg.w[i] || !q3_aligned(a.seg.w[i], 16) || (a.seg.start[i] % kGvBN) != 0) return false;
+    if (!a.seg.w[i] || !q3_aligned(a.seg.w[i], 16) || (sk && (a.seg.start[i] % kGvBN) != 0)) return false;
     if ((end - a.seg.start[i]) * a.ldw * 2 >= 0x7fffffffLL) return false;
   }
   return true;
@@ -781,7 +831,7 @@ int64_t gemv_workspace_bytes(int64_t M, int64_t N, int64_t K, bool swiglu) {
 }
 
 int gemv_launch(const GemvArgs& a, void* ws, int64_t ws_bytes, hipStream_t st) {
-  if (rows_selected(a.M, a.K)) return rows_launch(a, st);
+  if (a.nw || rows_selected(a.M, a.K)) return rows_launch(a, st);
   const bool swiglu = a.W2 != nullptr;
   const GemvPlan pl = gemv_plan(a.N, a.K, swiglu);
   Q3_REQUIRE(ws != nullptr && ws_bytes >= pl.bytes, Q3_ERR_WORKSPACE);

@@ -4,7 +4,8 @@ from ._loader import FALLBACK_LOG, record_fallback, strict_mode, summarize_fallb
 from .conv3d_patch import conv3d_patch
 from .elementwise import gelu_tanh, residual_add, swiglu
 from .flash_attention import decode_attention, flash_attention
-from .matmul import matmul, matmul_segments, matmul_swiglu
+from .matmul import (RMSNORM_MATMUL_MAX_ROWS, matmul, matmul_segments, matmul_swiglu, rmsnorm_matmul_segments,
+                     rmsnorm_matmul_swiglu)
 from .moe_routing import cuda_batched_gemm, cuda_index_add, cuda_topk, moe_experts, moe_route
 from .norms import layernorm, rmsnorm, softmax
 from .rotary import apply_mrope, apply_rope, qk_norm_rope
@@ -32,6 +33,9 @@ __all__ = [
     "decode_attention",
     "matmul_segments",
     "matmul_swiglu",
+    "rmsnorm_matmul_segments",
+    "rmsnorm_matmul_swiglu",
+    "RMSNORM_MATMUL_MAX_ROWS",
     "moe_experts",
     "moe_route",
     "qk_norm_rope",

@@ -100,3 +100,70 @@ def matmul_segments(x: torch.Tensor, weights, biases=None, *, out: torch.Tensor 
               _lib.ptrs(*bs) if any(b is not None for b in bs) else None, n_arr, len(ns), y2.data_ptr(), M, K,
               x2.stride(0), K, y2.stride(0), dt, _lib.ptr(ws), nws, _lib.stream())
     return y
+
+
+# Largest row count (tokens) of the fused RMSNorm projections: the
+# weight-streaming kernel's decode shapes.
+RMSNORM_MATMUL_MAX_ROWS = 32
+
+
+def _norm_args(name: str, x: torch.Tensor, norm_weight: torch.Tensor, K: int):
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"{name}: bfloat16 only")
+    if norm_weight.shape != (K,) or norm_weight.dtype != x.dtype:
+        raise ValueError(f"{name}: norm weight must be ({K},) {x.dtype}")
+    x2 = x.reshape(-1, K)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    if x2.shape[0] > RMSNORM_MATMUL_MAX_ROWS:
+        raise ValueError(f"{name}: at most {RMSNORM_MATMUL_MAX_ROWS} rows (decode shapes)")
+    return x2, norm_weight.contiguous()
+
+
+def rmsnorm_matmul_segments(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, weights,
+                            biases=None) -> torch.Tensor:
+    """matmul_segments(rmsnorm(x, norm_weight, eps), weights, biases) for decode
+    shapes (at most 32 rows) in one launch: the rows are normalised as the
+    weight-streaming kernel stages them (q3_rmsnorm_matmul_segments). Equals
+    the two-op composition of modules/text_decoder.py:56 + attention.py:82-84
+    to bf16 rounding."""
+    weights = list(weights)
+    biases = list(biases) if biases is not None else [None] * len(weights)
+    if not 1 <= len(weights) <= 4 or len(biases) != len(weights):
+        raise ValueError("rmsnorm_matmul_segments: 1 to 4 weights, one bias (or None) each")
+    check("rmsnorm_matmul_segments", x, norm_weight, *weights, *biases)
+    K = x.shape[-1]
+    x2, nw = _norm_args("rmsnorm_matmul_segments", x, norm_weight, K)
+    ws_ = [w if w.stride(-1) == 1 and w.stride(0) == K else w.contiguous() for w in weights]
+    for w, b in zip(ws_, biases):
+        if w.dim() != 2 or w.shape[1] != K:
+            raise ValueError(f"rmsnorm_matmul_segments: weight {tuple(w.shape)} does not match x (..., {K})")
+        if b is not None and b.shape != (w.shape[0],):
+            raise ValueError(f"rmsnorm_matmul_segments: bias {tuple(b.shape)} != ({w.shape[0]},)")
+    bs = [b.contiguous() if b is not None else None for b in biases]
+    ns = [w.shape[0] for w in ws_]
+    N = sum(ns)
+    M = x2.shape[0]
+    y = torch.empty((*x.shape[:-1], N), dtype=x.dtype, device=x.device)
+    _lib.call("q3_rmsnorm_matmul_segments", x2.data_ptr(), nw.data_ptr(), float(eps), _lib.ptrs(*ws_),
+              _lib.ptrs(*bs) if any(b is not None for b in bs) else None, _lib.i64s(*ns), len(ns),
+              y.data_ptr(), M, K, x2.stride(0), K, N, _lib.dtype_code(x.dtype), _lib.stream())
+    return y
+
+
+def rmsnorm_matmul_swiglu(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, w_gate: torch.Tensor,
+                          w_up: torch.Tensor) -> torch.Tensor:
+    """matmul_swiglu(rmsnorm(x, norm_weight, eps), w_gate, w_up) for decode shapes
+    (at most 32 rows) in one launch (q3_rmsnorm_matmul_swiglu)."""
+    check("rmsnorm_matmul_swiglu", x, norm_weight, w_gate, w_up)
+    K = x.shape[-1]
+    N = w_gate.shape[0]
+    if w_gate.shape != w_up.shape or w_gate.shape[1] != K:
+        raise ValueError("rmsnorm_matmul_swiglu: gate/up weights must both be (N, K)")
+    x2, nw = _norm_args("rmsnorm_matmul_swiglu", x, norm_weight, K)
+    wg, wu = w_gate.contiguous(), w_up.contiguous()
+    M = x2.shape[0]
+    y = torch.empty((*x.shape[:-1], N), dtype=x.dtype, device=x.device)
+    _lib.call("q3_rmsnorm_matmul_swiglu", x2.data_ptr(), nw.data_ptr(), float(eps), wg.data_ptr(), wu.data_ptr(),
+              y.data_ptr(), M, N, K, x2.stride(0), wg.stride(0), N, _lib.dtype_code(x.dtype), _lib.stream())
+    return y

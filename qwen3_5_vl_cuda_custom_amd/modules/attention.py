@@ -4,10 +4,11 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from ..kernels import apply_rope, decode_attention, flash_attention, matmul_segments, qk_norm_rope
+from ..kernels import (apply_rope, decode_attention, flash_attention, matmul_segments, qk_norm_rope,
+                       rmsnorm_matmul_segments)
 from .kv_cache import StaticKVCache
 from .linear import CudaLinear
-from .norms import CudaRMSNorm
+from .norms import CudaRMSNorm, fused_norm_ok
 from .rotary import MRoPEBinding
 
 
@@ -49,6 +50,9 @@ class CudaFullAttention(nn.Module):
                               sequence's length and attention runs over the
                               ragged cache (decode when S == 1)
       residual=tensor         added to o_proj's output in the GEMM epilogue
+      input_norm=CudaRMSNorm  x is the layer input before this RMSNorm; for
+                              decode shapes (at most 32 tokens, bf16) the norm
+                              runs inside the q/k/v projection, else first
     When `mrope_apply` is a TextMRoPE.bind(...) binding, q/k normalisation and
     rotation run as one fused kernel on the projection outputs.
     """
@@ -73,13 +77,20 @@ class CudaFullAttention(nn.Module):
                 and self.head_dim % 16 == 0 and self.head_dim <= 256 and x.is_cuda)
 
     def forward(self, x: torch.Tensor, mrope_apply, past_kv: tuple[torch.Tensor, torch.Tensor] | None = None, *,
-                kv_cache: StaticKVCache | None = None, residual: torch.Tensor | None = None):
+                kv_cache: StaticKVCache | None = None, residual: torch.Tensor | None = None,
+                input_norm: CudaRMSNorm | None = None):
         B, S, _ = x.shape
         Hq, Hkv, D = self.num_heads, self.num_kv_heads, self.head_dim
         # q/k/v projections in one GEMM over the three weights (no concatenated
         # copy); q, k, v are column views of its output.
-        qkv = matmul_segments(x, (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight),
-                              (self.q_proj.bias, self.k_proj.bias, self.v_proj.bias))
+        weights = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight)
+        biases = (self.q_proj.bias, self.k_proj.bias, self.v_proj.bias)
+        if input_norm is not None and fused_norm_ok(x, input_norm):
+            qkv = rmsnorm_matmul_segments(x, input_norm.weight, input_norm.eps, weights, biases)
+        else:
+            if input_norm is not None:
+                x = input_norm(x)
+            qkv = matmul_segments(x, weights, biases)
         q = qkv[..., :Hq * D].view(B, S, Hq, D)
         k = qkv[..., Hq * D:(Hq + Hkv) * D].view(B, S, Hkv, D)
         v = qkv[..., (Hq + Hkv) * D:].view(B, S, Hkv, D)

@@ -4,8 +4,9 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from ..kernels import gelu_tanh, matmul_swiglu, swiglu
+from ..kernels import gelu_tanh, matmul_swiglu, rmsnorm_matmul_swiglu, swiglu
 from .linear import CudaLinear
+from .norms import CudaRMSNorm, fused_norm_ok
 
 
 class CudaSwiGLUMLP(nn.Module):
@@ -17,8 +18,18 @@ class CudaSwiGLUMLP(nn.Module):
         self.up_proj = CudaLinear(hidden_size, intermediate_size, bias=bias)
         self.down_proj = CudaLinear(intermediate_size, hidden_size, bias=bias)
 
-    def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None) -> torch.Tensor:
-        if self.gate_proj.bias is None and self.up_proj.bias is None:
+    def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None,
+                input_norm: CudaRMSNorm | None = None) -> torch.Tensor:
+        """`input_norm`: x is taken before this RMSNorm; for decode shapes (at
+        most 32 bf16 tokens) it runs inside the gate/up GEMM, else first."""
+        no_bias = self.gate_proj.bias is None and self.up_proj.bias is None
+        if input_norm is not None and no_bias and fused_norm_ok(x, input_norm):
+            act = rmsnorm_matmul_swiglu(x, input_norm.weight, input_norm.eps, self.gate_proj.weight,
+                                        self.up_proj.weight)
+            return self.down_proj(act, residual=residual)
+        if input_norm is not None:
+            x = input_norm(x)
+        if no_bias:
             act = matmul_swiglu(x, self.gate_proj.weight, self.up_proj.weight)  # gate, up and swiglu in one GEMM
         else:
             act = swiglu(self.gate_proj(x), self.up_proj(x))

@@ -4,7 +4,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from ..kernels import layernorm, rmsnorm
+from ..kernels import RMSNORM_MATMUL_MAX_ROWS, layernorm, rmsnorm
 
 
 class CudaRMSNorm(nn.Module):
@@ -21,6 +21,16 @@ class CudaRMSNorm(nn.Module):
 
     def extra_repr(self) -> str:
         return f"{self.dim}, eps={self.eps}"
+
+
+def fused_norm_ok(x: torch.Tensor, norm: CudaRMSNorm) -> bool:
+    """Whether `norm` can run inside the projection that consumes x
+    (rmsnorm_matmul_segments / rmsnorm_matmul_swiglu): decode shapes of at most
+    32 bf16 rows, 16-byte aligned rows of a multiple of 8 elements."""
+    K = x.shape[-1]
+    return (x.is_cuda and x.dtype == torch.bfloat16 and norm.weight.dtype == torch.bfloat16 and K == norm.dim
+            and K % 8 == 0 and x.is_contiguous() and x.data_ptr() % 16 == 0
+            and 0 < x.numel() // K <= RMSNORM_MATMUL_MAX_ROWS)
 
 
 class CudaLayerNorm(nn.Module):

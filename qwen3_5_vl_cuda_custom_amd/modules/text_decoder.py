@@ -36,11 +36,12 @@ class CudaTextDecoderLayer(nn.Module):
 
     def forward(self, x: torch.Tensor, mrope_apply, past_kv: tuple[torch.Tensor, torch.Tensor] | None = None, *,
                 kv_cache: StaticKVCache | None = None):
-        h, new_kv = self.self_attn(self.input_layernorm(x), mrope_apply, past_kv=past_kv, kv_cache=kv_cache,
-                                   residual=x)
-        mlp_in = self.post_attention_layernorm(h)
+        # Each RMSNorm is handed to the module that consumes it: at decode
+        # shapes it runs inside the q/k/v (resp. gate/up) projection.
+        h, new_kv = self.self_attn(x, mrope_apply, past_kv=past_kv, kv_cache=kv_cache, residual=x,
+                                   input_norm=self.input_layernorm)
         if self.use_moe:
-            y, router_logits = self.mlp(mlp_in, residual=h)
+            y, router_logits = self.mlp(self.post_attention_layernorm(h), residual=h)
         else:
-            y, router_logits = self.mlp(mlp_in, residual=h), None
+            y, router_logits = self.mlp(h, residual=h, input_norm=self.post_attention_layernorm), None
         return y, router_logits, new_kv

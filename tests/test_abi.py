@@ -66,6 +66,32 @@ def test_matmul_validation():
     assert L.q3_matmul(FAKE, FAKE, None, None, FAKE, 0, 4, 4, 4, 4, 0, 4, 1, None, 0, None) == 0  # empty: no-op
 
 
+def test_rmsnorm_matmul_validation():
+    L = _lib.lib()
+    ws3 = (ctypes.c_void_p * 3)(FAKE, FAKE, FAKE)
+    ns = _lib.i64s(4096, 1024, 1024)
+    seg = lambda x, nw, w, M, K, ldx, dt: L.q3_rmsnorm_matmul_segments(x, nw, 1e-6, w, None, ns, 3, FAKE, M, K, ldx, K,
+                                                                      6144, dt, None)
+    assert seg(FAKE, None, ws3, 32, 4096, 4096, 1) == -1                  # no norm weight
+    assert seg(None, FAKE, ws3, 32, 4096, 4096, 1) == -1
+    assert seg(FAKE, FAKE, ws3, 32, 4096, 4000, 1) == -2                  # ldx < K
+    assert seg(FAKE, FAKE, ws3, 33, 4096, 4096, 1) == -5                  # prefill rows: not fused
+    assert seg(FAKE, FAKE, ws3, 32, 4096, 4096, 0) == -3                  # fp32
+    assert seg(FAKE, FAKE, ws3, 0, 4096, 4096, 1) == 0                    # empty: no-op
+    assert seg(FAKE, FAKE + 8, ws3, 32, 4096, 4096, 1) == -4              # misaligned norm weight
+    assert L.q3_rmsnorm_matmul_segments(FAKE, FAKE, 1e-6, ws3, None, ns, 5, FAKE, 32, 4096, 4096, 4096, 6144, 1,
+                                        None) == -2                       # > 4 segments
+    sw = lambda M, K, ldx, dt, nw=FAKE: L.q3_rmsnorm_matmul_swiglu(FAKE, nw, 1e-6, FAKE, FAKE, FAKE, M, 12288, K, ldx,
+                                                                   K, 12288, dt, None)
+    assert sw(32, 4096, 4096, 1, nw=None) == -1
+    assert sw(64, 4096, 4096, 1) == -5
+    assert sw(32, 4096, 4096, 0) == -3
+    assert sw(32, 4100, 4104, 1) == -4                                    # K not a multiple of 8
+    assert sw(0, 4096, 4096, 1) == 0
+    assert L.q3_rmsnorm_matmul_swiglu(FAKE, FAKE, -1.0, FAKE, FAKE, FAKE, 32, 12288, 4096, 4096, 4096, 12288, 1,
+                                      None) == -2                         # negative eps
+
+
 def test_matmul_segments_validation():
     import ctypes
     ns = _lib.i64s(4096, 1024, 1024)

@@ -166,6 +166,58 @@ def test_gemv_edges(M, ns, Kd, kind):
     assert torch.equal(y.cpu(), again.cpu()), "the GEMV must be deterministic"
 
 
+@pytest.mark.parametrize("M,ns,Kd,kind", [
+    (32, (4096, 1024, 1024), 4096, "plain"),  # the decode q/k/v shape (B=32)
+    (1, (256,), 520, "bias"),                  # one row, K tail inside a chunk
+    (9, (1000, 24), 1032, "bias"),             # ragged segments, K tail
+    (17, (384,), 2048, "swiglu"),
+    (32, (12288,), 4096, "swiglu"),            # the decode gate/up shape (B=32)
+    (5, (200,), 4104, "swiglu"),               # M <= 8 also stages X when fused
+    (32, (512,), 20480, "plain"),              # K past the row-owned limit: still row-owned
+])
+def test_rmsnorm_matmul_fused(M, ns, Kd, kind):
+    """RMSNorm fused into the decode projection (q3_rmsnorm_matmul_segments /
+    q3_rmsnorm_matmul_swiglu) against the fp32 oracle's rmsnorm -> linear
+    (-> swiglu), with the worst element bounded as in the layer tests by the
+    reference's own bf16 path (norm output, projections and swiglu each
+    rounded to bf16); against the two-launch library path; run-to-run
+    identity. Inputs at 3x unit scale make the norm's 1/rms factor matter."""
+    eps = 1e-6
+    sd = Kd ** -0.5
+    x = rnd(M, Kd, seed=100, std=3.0)
+    nw = (1.0 + rnd(Kd, seed=101, std=0.2, dtype=torch.float32)).to(torch.bfloat16)
+    xn = O.rmsnorm(f32(x), f32(nw), eps)
+    xb = bf16_round(xn)
+    if kind == "swiglu":
+        wg, wu = rnd(ns[0], Kd, seed=102, std=sd), rnd(ns[0], Kd, seed=103, std=sd)
+        call = lambda: K.rmsnorm_matmul_swiglu(gpu(x), gpu(nw), eps, gpu(wg), gpu(wu))
+        ref = O.swiglu(O.linear(xn, f32(wg)), O.linear(xn, f32(wu)))
+        ref_bf16 = bf16_round(O.swiglu(bf16_round(O.linear(xb, f32(wg))), bf16_round(O.linear(xb, f32(wu)))))
+        two = K.matmul_swiglu(K.rmsnorm(gpu(x), gpu(nw), eps), gpu(wg), gpu(wu))
+    else:
+        ws = [rnd(n, Kd, seed=104 + i, std=sd) for i, n in enumerate(ns)]
+        bs = [rnd(n, seed=108 + i, std=sd) if kind == "bias" else None for i, n in enumerate(ns)]
+        gb = [gpu(b) if b is not None else None for b in bs]
+        call = lambda: K.rmsnorm_matmul_segments(gpu(x), gpu(nw), eps, [gpu(w) for w in ws], gb)
+        fb = [f32(b) if b is not None else None for b in bs]
+        ref = torch.cat([O.linear(xn, f32(w), b) for w, b in zip(ws, fb)], dim=-1)
+        ref_bf16 = bf16_round(torch.cat([O.linear(xb, f32(w), b) for w, b in zip(ws, fb)], dim=-1))
+        two = K.matmul_segments(K.rmsnorm(gpu(x), gpu(nw), eps), [gpu(w) for w in ws], gb)
+    y = call()
+    assert y.shape == ref.shape and y.dtype == torch.bfloat16
+    assert_layer_parity(y, ref, ref_bf16, what=f"rmsnorm+{kind} M={M} K={Kd}")
+    # Two bf16 results, each within the bound of the fp32 result, may lie twice
+    # the bound apart.
+    assert_layer_parity(y, f32(two), ref_bf16, what=f"fused vs two launches M={M} K={Kd}", slack=2.5)
+    assert torch.equal(y, call()), "fused norm projection must be deterministic"
+
+
+def test_rmsnorm_matmul_fused_rejects_prefill_rows():
+    x = gpu(rnd(33, 64))
+    with pytest.raises(ValueError):
+        K.rmsnorm_matmul_segments(x, gpu(rnd(64)), 1e-6, [gpu(rnd(16, 64))])
+
+
 def test_matmul_fp32_reference_style():
     torch.manual_seed(0)
     x, w, b = torch.randn(8, 64), torch.randn(32, 64), torch.randn(32)
