@@ -77,6 +77,7 @@ def test_matmul_swiglu(M):
     (600, (1024, 256, 256), False),   # tiled, one launch (starts are multiples of 256)
     (600, (512, 256, 256), True),     # tiled with per-segment bias
     (4096, (4096, 1024, 1024), True), # the q/k/v shape: 256x192 tiles straddle segment starts
+    (4096, (4096, 2048), True),       # two segments, both with bias
     (2048, (1040, 512, 48), True),    # starts on 16-row (not tile) boundaries, one launch
     (300, (200, 72, 72), True),       # unaligned starts: one launch per segment
     (32, (1024, 256, 256), False),    # skinny, one launch
@@ -87,7 +88,7 @@ def test_matmul_segments(M, ns, bias):
     Kd = 512
     x = rnd(M, Kd, seed=40)
     ws = [rnd(n, Kd, seed=41 + i, std=0.02) for i, n in enumerate(ns)]
-    bs = [rnd(n, seed=50 + i, std=0.02) if bias and i != 1 else None for i, n in enumerate(ns)]
+    bs = [rnd(n, seed=50 + i, std=0.02) if bias and (i != 1 or len(ns) == 2) else None for i, n in enumerate(ns)]
     y = K.matmul_segments(gpu(x), [gpu(w) for w in ws], [gpu(b) if b is not None else None for b in bs])
     ref = torch.cat([O.linear(f32(x), f32(w), f32(b) if b is not None else None) for w, b in zip(ws, bs)], dim=-1)
     assert_bf16_close(y, ref, what=f"matmul_segments M={M} {ns}")
