@@ -850,9 +850,51 @@ __global__ __launch_bounds__(512) void flash_fwd_pipe_kernel(const AttnParams p)
     issue(t + kAhead);
     const uint32_t drop = tile_mask(mask, t);
     softmax_max(cur, drop, pp);
-    pv(t - 1, pp);
-    qk(nxt, t + 1);
-    softmax_exp(cur, drop, pc);
+    // The step as 16 fenced chunks, each one MFMA (slots 0-7: O += V(t-1) P(t-1)
+    // for the (j, dt) pairs; slots 8-15: S(t+1) = K(t+1) Q^T k-steps), the LDS
+    // fragment reads of the slot three ahead, and one exponential of S(t), so
+    // every MFMA has its operands in registers and an independent slice of the
+    // softmax to hide behind.
+    const bf16* sV = ring + ((t - 1) % kPipeStages) * 2 * kTile + kTile;
+    const bf16* sK = ring + ((t + 1) % kPipeStages) * 2 * kTile;
+    short4v vlo[8], vhi[8];
+    bf16x8 kf[KSTEPS];
+    auto read_u = [&](int u) {  // u: 16 MFMA slots; PV slots 0-7 (j, dt), QK slots 8-15 (ks)
+      if (u < 8) {
+        const int j = u / OT, dt = u % OT;
+        vlo[u] = lds_read_tr16(sV + voff[dt] + 16 * j * kRowK);
+        vhi[u] = lds_read_tr16(sV + voff[dt] + (16 * j + 8) * kRowK);
+      } else {
+        kf[u - 8] = *reinterpret_cast<const bf16x8*>(sK + koff[u - 8]);
+      }
+    };
+    auto mma_u = [&](int u) {
+      if (u < 8) {
+        const int j = u / OT, dt = u % OT;
+        const short8v a8 = {vlo[u][0], vlo[u][1], vlo[u][2], vlo[u][3], vhi[u][0], vhi[u][1], vhi[u][2], vhi[u][3]};
+        o[dt] = mfma32x32x16(__builtin_bit_cast(bf16x8, a8), pp[j], o[dt]);
+      } else {
+        const int ks = u - 8;
+        nxt = mfma32x32x16(kf[ks], qf[ks], ks == 0 ? floatx16{} : nxt);
+      }
+    };
+    const float nm = -m;
+    auto exp_i = [&](int r) {
+      const float pr = (drop >> r) & 1 ? 0.f : fast_exp2(fmaf(cur[r], c, nm));
+      lsum += pr;
+      pc[r >> 3][r & 7] = f2bf(pr);
+    };
+    __builtin_amdgcn_sched_barrier(0);
+    read_u(0);
+    read_u(1);
+    read_u(2);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      if (u + 3 < 16) read_u(u + 3);
+      mma_u(u);
+      exp_i(u);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   };
   constexpr std::true_type kMasked{};
   constexpr std::false_type kUnmasked{};
