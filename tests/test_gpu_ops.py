@@ -213,6 +213,32 @@ def test_rmsnorm_matmul_fused(M, ns, Kd, kind):
     assert torch.equal(y, call()), "fused norm projection must be deterministic"
 
 
+def test_rmsnorm_matmul_fused_closed_forms():
+    """Pins that do not go through the oracle: a constant row c*1 with eps = 0
+    normalises to sign(c)*w exactly, so the projection equals (sign(c)*w).W^T
+    (one bf16 rounding of w*x per element, here exact: x is a power of two);
+    K = 8 (one 16-byte piece) and a single row."""
+    Kd, N = 1024, 384
+    nw = (1.0 + rnd(Kd, seed=120, std=0.2, dtype=torch.float32)).to(torch.bfloat16)
+    w = rnd(N, Kd, seed=121, std=Kd ** -0.5)
+    x = torch.full((3, Kd), 4.0).to(torch.bfloat16)
+    x[1] = -0.5
+    x[2] = 2.0 ** -6
+    y = K.rmsnorm_matmul_segments(gpu(x), gpu(nw), 0.0, [gpu(w)])
+    sign = torch.tensor([1.0, -1.0, 1.0]).unsqueeze(1)
+    ref = sign * O.linear(f32(nw).unsqueeze(0), f32(w))
+    assert_bf16_close(y, ref, what="constant rows, eps=0")
+    # The row scale enters only through rsqrt(mean(x^2)) (hardware reciprocal
+    # square root): outputs agree to a bf16 ulp across scales and signs.
+    assert_within_ulp(y[2], y[0].float(), ulps=1, what="constant row: scale invariance")
+    assert_within_ulp(y[1], -y[0].float(), ulps=1, what="constant row: sign")
+    # K = 8: one piece of one chunk, one row
+    x8, nw8, w8 = rnd(1, 8, seed=122), rnd(8, seed=123, std=0.1) + 1, rnd(40, 8, seed=124)
+    y8 = K.rmsnorm_matmul_segments(gpu(x8), gpu(nw8.to(torch.bfloat16)), 1e-6, [gpu(w8)])
+    ref8 = O.linear(O.rmsnorm(f32(x8), f32(nw8.to(torch.bfloat16)), 1e-6), f32(w8))
+    assert_bf16_close(y8, ref8, what="K=8")
+
+
 def test_rmsnorm_matmul_fused_rejects_prefill_rows():
     x = gpu(rnd(33, 64))
     with pytest.raises(ValueError):
