@@ -18,7 +18,7 @@ class CudaSwiGLUMLP(nn.Module):
         self.up_proj = CudaLinear(hidden_size, intermediate_size, bias=bias)
         self.down_proj = CudaLinear(intermediate_size, hidden_size, bias=bias)
 
-    def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None,
+    def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None, *,
                 input_norm: CudaRMSNorm | None = None) -> torch.Tensor:
         """`input_norm`: x is taken before this RMSNorm; for decode shapes (at
         most 32 bf16 tokens) it runs inside the gate/up GEMM, else first."""
