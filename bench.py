@@ -56,13 +56,45 @@ def time_gpu(fn, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
+def usable_cpus() -> int:
+    """CPUs this process may run on: its affinity set, capped by a cgroup CPU quota if one is set."""
+    n = len(os.sched_getaffinity(0))
+    try:
+        quota, period = Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        if quota != "max":
+            n = min(n, max(1, -(-int(quota) // int(period))))
+    except (OSError, ValueError):
+        pass
+    return n
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(cfg, seq: int, layer, budget_s: float = 20.0) -> dict:
-    """The oracle's decoder layer on CPU tensors (bf16), 1 warm-up + timed runs within the budget."""
+    """The oracle's decoder layer on CPU tensors (bf16), 1 warm-up + timed runs within the budget,
+    with torch's intra-op threads set to every CPU the process may use."""
     import torch
 
     from oracle import layers as L
     from oracle import ops as O
-    threads = torch.get_num_threads()
+    prev = torch.get_num_threads()
+    threads = usable_cpus()
+    torch.set_num_threads(threads)
+    try:
+        return _cpu_baseline(torch, L, O, cfg, seq, layer, budget_s, threads)
+    finally:
+        torch.set_num_threads(prev)
+
+
+def _cpu_baseline(torch, L, O, cfg, seq, layer, budget_s, threads) -> dict:
     p = {n: t.detach().to("cpu") for n, t in layer.state_dict().items()}
     g = torch.Generator().manual_seed(1)
     x = torch.randn(1, seq, cfg.hidden, generator=g).to(torch.bfloat16)
@@ -86,11 +118,91 @@ def cpu_baseline(cfg, seq: int, layer, budget_s: float = 20.0) -> dict:
     times.sort()
     med = times[len(times) // 2]
     return {"value": round(seq / med, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(),
+            "threads": f"torch.set_num_threads({threads}): the CPUs the process may use (affinity, cgroup quota)",
             "sample": f"oracle decoder layer (torch CPU, bf16) at S={seq}, 1 warm-up + median of {len(times)} "
                       f"run(s), {med:.2f} s/layer"}
 
 
-def other_configs(torch, W, dev: str, warmup: int) -> dict:
+def parity_leg(cases: dict) -> dict:
+    """Per configuration: the GPU output against the fp32 oracle and the reference's bf16
+    path (the oracle with every op output rounded to bf16), both on CPU, on the same
+    seeded inputs. Runs after every timed region; the oracle is only the checker here."""
+    import torch
+
+    from oracle import layers as L
+    from oracle import ops as O
+    prev = torch.get_num_threads()
+    torch.set_num_threads(usable_cpus())
+    ident = lambda t: t  # noqa: E731
+
+    def metrics(out, ref):
+        d = (out.float() - ref).abs()
+        return float(d.max()), float(d.mean() / ref.abs().mean().clamp_min(1e-30))
+
+    def ulp_at_worst(out, ref):
+        import math
+        w = float(ref.reshape(-1)[int((out.float() - ref).abs().argmax())])
+        return 2.0 ** (math.frexp(abs(w))[1] - 8) if w else 0.0
+
+    res = {}
+    try:
+        for name, (gpu_out, run) in cases.items():
+            t0 = time.perf_counter()
+            ref = run(L, O, ident)
+            emu = run(L, O, O.round_bf16)
+            ma, mr = metrics(gpu_out, ref)
+            ema, emr = metrics(emu, ref)
+            res[name] = {"max_abs": round(ma, 5), "mean_rel": round(mr, 6), "ref_bf16_max_abs": round(ema, 5),
+                         "ref_bf16_mean_rel": round(emr, 6), "bar_max_abs": 2e-2, "bar_mean_rel": 5e-3,
+                         "within_2e-2": ma <= 2e-2,
+                         # the test bar: no worse than the reference bf16 path, up to
+                         # equal-rounding ties (2% of mean-rel, one bf16 ulp of the worst element)
+                         "within_ref_bf16": (ma <= max(2e-2, ema + ulp_at_worst(gpu_out, ref))
+                                             and mr <= emr * 1.02 and mr <= 5e-3)}
+            log(f"parity {name}: {res[name]} ({time.perf_counter() - t0:.1f} s)")
+    finally:
+        torch.set_num_threads(prev)
+    return res
+
+
+def _params_cpu(module) -> dict:
+    return {n: t.detach().float().cpu() for n, t in module.state_dict().items()}
+
+
+def text_layer_case(cfg, layer, x, pos, y, router_logits=None):
+    """(GPU output, oracle closure) for a prefill layer, everything on the CPU."""
+    p, xc, posc = _params_cpu(layer), x.detach().float().cpu(), pos.detach().cpu()
+    rl = router_logits.detach().float().cpu() if router_logits is not None else None
+
+    def run(L, O, rd):
+        cos3, sin3 = O.mrope_cos_sin(posc, cfg.head_dim, cfg.theta)
+        return L.text_decoder_layer(xc, p, num_heads=cfg.heads, num_kv_heads=cfg.kv_heads, head_dim=cfg.head_dim,
+                                    eps=cfg.eps, cos_3d=cos3, sin_3d=sin3, mrope_section=list(cfg.mrope_section),
+                                    use_moe=cfg.use_moe, top_k=cfg.top_k, router_logits=rl, rd=rd)[0]
+    return y.detach().float().cpu(), run
+
+
+def decode_case(cfg, layer, x, pos, lens, k_cache, v_cache, y):
+    """(GPU output, oracle closure) for one decode step: each sequence attends to its cache rows
+    [0, L_b) plus the new token (the reference's past_kv form, one sequence at a time)."""
+    p, xc, posc = _params_cpu(layer), x.detach().float().cpu(), pos.detach().cpu()
+    kc, vc, lc = k_cache.detach().cpu(), v_cache.detach().cpu(), [int(v) for v in lens]
+
+    def run(L, O, rd):
+        import torch
+        outs = []
+        for b, Lb in enumerate(lc):
+            cos3, sin3 = O.mrope_cos_sin(posc[:, b:b + 1], cfg.head_dim, cfg.theta)
+            past = (kc[b:b + 1, :, :Lb].float(), vc[b:b + 1, :, :Lb].float())
+            outs.append(L.text_decoder_layer(xc[b:b + 1], p, num_heads=cfg.heads, num_kv_heads=cfg.kv_heads,
+                                             head_dim=cfg.head_dim, eps=cfg.eps, cos_3d=cos3, sin_3d=sin3,
+                                             mrope_section=list(cfg.mrope_section), past_kv=past, rd=rd)[0])
+        return torch.cat(outs)
+    return y.detach().float().cpu(), run
+
+
+def other_configs(torch, W, dev: str, warmup: int, cases: dict) -> dict:
     """The other BASELINE configurations, one GPU each: C2 at S=1024 and 16384,
     the C4 MoE layer (4096 tokens) and the C5 patch embed + vision block."""
     out = {}
@@ -110,11 +222,22 @@ def other_configs(torch, W, dev: str, warmup: int) -> dict:
     layer = W.make_text_layer(cfg, torch.bfloat16, dev, seed=0)
     x, pos = W.text_inputs(cfg, 1, 4096, torch.bfloat16, dev, seed=0)
     b = W.make_rope(cfg, dev).bind(pos)
+    y, logits, _ = layer(x, b)
+    cases["c4_moe_layer_t4096"] = text_layer_case(cfg, layer, x, pos, y, router_logits=logits)
     ms = time_gpu(lambda: layer(x, b), 10, warmup)
     fl = cfg.gemm_flops_per_token() * 4096 + cfg.causal_attn_flops(4096)
+    # Both bounds: MFMA on the layer's FLOPs, HBM on the bytes it must move at
+    # least once (every weight, the token activations in and out).
+    wbytes = sum(t.numel() * t.element_size() for t in layer.parameters())
+    abytes = 2 * 4096 * cfg.hidden * 2
     out["c4_moe_layer_t4096"] = {"ms": round(ms, 4), "tok_s": round(4096 / (ms / 1e3), 1),
                                  "tflops": round(fl / (ms / 1e3) / 1e12, 1),
-                                 "mfma_frac": round(fl / (ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+                                 "mfma_frac": round(fl / (ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                                 "min_bytes": wbytes + abytes,
+                                 "hbm_gbs": round((wbytes + abytes) / (ms / 1e3) / 1e9, 1),
+                                 "hbm_frac": round((wbytes + abytes) / (ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
+                                 "floor_ms": {"mfma": round(fl / PEAK_BF16_TFLOPS / 1e9, 4),
+                                              "hbm": round((wbytes + abytes) / PEAK_HBM_GBS / 1e6, 4)}}
     log(f"C4 MoE layer: {out['c4_moe_layer_t4096']}")
     del layer, x
     v = W.C5
@@ -126,6 +249,16 @@ def other_configs(torch, W, dev: str, warmup: int) -> dict:
     def vis():
         h = pe(patches)
         return blk(h.view(v.images, v.patches_per_image, v.hidden), cos, sin)
+
+    yv = vis()
+    pp, pb = _params_cpu(pe), _params_cpu(blk)
+    pc, cc, sc = patches.detach().float().cpu(), cos.detach().float().cpu(), sin.detach().float().cpu()
+
+    def run_vis(L, O, rd):
+        h = rd(L.patch_embed(pc, pp["weight"], pp["bias"], v.channels, v.temporal, v.patch))
+        return L.vision_block(h.view(v.images, v.patches_per_image, v.hidden), pb, num_heads=v.heads, cos=cc,
+                              sin=sc, eps=v.eps, rd=rd)
+    cases["c5_vision_patch_embed_block"] = (yv.detach().float().cpu(), run_vis)
 
     ms = time_gpu(vis, 10, warmup)
     fl = v.flops()
@@ -249,6 +382,9 @@ def main() -> int:
         def step():
             return layer(x, binding)
 
+        cases = {}
+        if not args.no_cpu_baseline:
+            cases[f"c2_prefill_s{S}"] = text_layer_case(cfg, layer, x, pos, step()[0])
         for _ in range(args.warmup):
             step()
         torch.cuda.synchronize()
@@ -301,9 +437,13 @@ def main() -> int:
             def dstep():
                 return case.layer(case.x, dbind, kv_cache=case.cache)[0]
 
+            if not args.no_cpu_baseline:
+                # one step from the initial cache, for the parity check (rows [0, L_b) stay as they are)
+                cases["c3_decode_b32"] = decode_case(cfg, layer, case.x, case.positions, case.lens, case.cache.k,
+                                                     case.cache.v, dstep())
             eager_ms = time_gpu(dstep, max(args.steps, 20), args.warmup)
             # The step as a serving loop runs it: one HIP graph launch per token.
-            graph = StepGraph(dstep)
+            graph = StepGraph(dstep, caches=[case.cache])
             for _ in range(args.warmup):
                 graph.replay()
             torch.cuda.synchronize()
@@ -327,13 +467,14 @@ def main() -> int:
     extra = None
     if not args.no_extra:
         with torch.inference_mode():
-            extra = other_configs(torch, W, dev, args.warmup)
+            extra = other_configs(torch, W, dev, args.warmup, cases if not args.no_cpu_baseline else {})
 
-    cpu = None
+    cpu = parity = None
     if not args.no_cpu_baseline:
         with torch.inference_mode():
             cpu = cpu_baseline(cfg, S, layer)
-        log(f"cpu baseline: {cpu}")
+            log(f"cpu baseline: {cpu}")
+            parity = parity_leg(cases)
 
     out = {
         "metric": "decoder-layer prefill tokens/s (8B, S=4096) + decode tok/s; % MFMA/HBM roofline",
@@ -361,6 +502,7 @@ def main() -> int:
         "decode": decode,
         "other_configs": extra,
         "cpu_baseline": cpu,
+        "parity": parity,
     }
     print(json.dumps(out), flush=True)
     return 0

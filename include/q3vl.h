@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define Q3VL_ABI_VERSION 1
+#define Q3VL_ABI_VERSION 2
 
 typedef enum { Q3_F32 = 0, Q3_BF16 = 1 } q3_dtype;
 
@@ -168,6 +168,20 @@ int q3_flash_attention(const void* q, const void* k, const void* v, void* o, flo
                        int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D, const int64_t* strides, float scale,
                        int is_causal, int dtype, void* stream);
 
+/* A prefill chunk of Sq tokens per sequence over a ragged KV cache: the
+ * S > 1 case of CudaFullAttention.forward with a cache
+ * (modules/attention.py:89-96) without the torch.cat growth. k/v cache
+ * (B, Hkv, cap, D) whose rows [kv_lens[b], kv_lens[b] + Sq) already hold the
+ * chunk's keys/values; query i of sequence b is the token at position
+ * kv_lens[b] + i and attends to rows [0, kv_lens[b] + i] (causal over the
+ * whole sequence). kv_lens[b] += Sq afterwards when `advance` is non-zero.
+ * strides as q3_flash_attention's (k/v = the caches). Keys past cap are never
+ * read. The reference's past_kv form runs such a chunk non-causally
+ * (is_causal = Sq == Sk); this entry point is for the in-place cache. */
+int q3_flash_attention_cache(const void* q, const void* k_cache, const void* v_cache, int* kv_lens, void* o,
+                             int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t cap, int64_t D,
+                             const int64_t* strides, float scale, int advance, int dtype, void* stream);
+
 /* Decode step over a ragged KV cache: the Sq = 1 case of the same op
  * (modules/attention.py:89-96) without the torch.cat cache growth. q (B, Hq, D)
  * strides [qb, qh]; k/v cache (B, Hkv, cap, D) strides [b, h, s]; o (B, Hq, D)
@@ -208,15 +222,32 @@ int q3_moe_experts(const void* x, const void* gate_up, const void* down, const i
                    const void* residual, void* out, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
                    void* workspace, int64_t workspace_bytes, void* stream);
 
+/* The dispatch step of q3_moe_experts on its own: the per-expert token
+ * lists that CudaSparseMoE.forward builds with `(top_idx == e).nonzero()` for
+ * each expert e (modules/moe.py:70-76). Rows of expert e are
+ * [offsets[e], offsets[e + 1]) (offsets (E + 1) int32, offsets[0] = 0); within
+ * them the (token, slot) entries routed to e in ascending (token, slot) order:
+ * sorted_token (T * k) int32 and sorted_w (T * k) bf16 (the entry's routing
+ * weight). pos_of (T, k) int32 is the inverse (the row of each entry). Ids
+ * outside [0, E) are not dispatched (their pos_of entry is left unwritten).
+ * Workspace: q3_moe_permute_workspace_bytes. */
+int64_t q3_moe_permute_workspace_bytes(int64_t T, int64_t E, int64_t k);
+int q3_moe_permute(const int* top_idx, const void* top_w, int* offsets, int* sorted_token, void* sorted_w,
+                   int* pos_of, int64_t T, int64_t E, int64_t k, void* workspace, int64_t workspace_bytes,
+                   void* stream);
+
 /* Deterministic target[idx[i]] += src[i] (in place): replaces
  * index_add_forward(Tensor(a!) target, Tensor source, Tensor index)
  * (csrc/moe_routing_op.cpp:11). Each target row adds its sources in ascending
  * i in fp32, starting from the target value, and rounds to dtype once (the
  * semantics of torch's index_add_, kernels/moe_routing.py:111-115).
- * idx int64 in [0, n_target). */
+ * idx int64; entries outside [0, n_target) are skipped and set bit 0 of
+ * *status (a device int32, or null), which the call never clears: the index
+ * check needs no host synchronisation (the reference's kernel,
+ * csrc/moe_routing_op.cu:90-102, writes out of bounds instead). */
 int64_t q3_index_add_workspace_bytes(int64_t n_src, int64_t n_target);
 int q3_index_add(void* target, const void* src, const int64_t* idx, int64_t n_src, int64_t n_target, int64_t D,
-                 int dtype, void* workspace, int64_t workspace_bytes, void* stream);
+                 int dtype, void* workspace, int64_t workspace_bytes, int* status, void* stream);
 
 #ifdef __cplusplus
 }

@@ -15,6 +15,8 @@ no CPU fallback.
 Pinning (how each function is checked independently of its own formula):
   ops.linear / batched_gemm / conv3d_patch   numpy float64 brute force (tests/test_oracle_pins.py)
   ops.flash_attention (+ decode form)        numpy float64 per-row softmax loop; causal row 0 == v0
+  ops.chunk_attention                        numpy float64 masked loop; equals the last rows of causal
+                                             ops.flash_attention over the whole sequence; offset 0 is causal
   ops.interleave_cos_sin / mrope_cos_sin     per-element closed form with distinct T/H/W positions;
                                              HF Qwen3-VL rotary for identical axes
   ops.rotate_half_apply                      identity at theta=0, per-pair norm preservation, numpy loop

@@ -12,7 +12,7 @@ import torch
 import torch.nn.functional as F
 
 __all__ = [
-    "linear", "batched_gemm", "conv3d_patch", "flash_attention", "decode_attention",
+    "linear", "batched_gemm", "conv3d_patch", "flash_attention", "decode_attention", "chunk_attention",
     "interleave_cos_sin", "rotate_half_apply", "mrope_inv_freq", "mrope_cos_sin",
     "apply_mrope", "apply_rope", "rmsnorm", "layernorm", "swiglu", "residual_add",
     "gelu_tanh", "softmax", "topk", "index_add", "round_bf16",
@@ -76,6 +76,34 @@ def decode_attention(q, k_cache, v_cache, kv_lens, scale: float, num_kv_groups: 
         L = int(kv_lens[b])
         outs.append(flash_attention(q[b:b + 1], k_cache[b:b + 1, :, :L], v_cache[b:b + 1, :, :L],
                                     scale, False, num_kv_groups))
+    return torch.cat(outs, dim=0)
+
+
+def chunk_attention(q, k_cache, v_cache, kv_lens, scale: float, num_kv_groups: int):
+    """Causal attention of a prefill chunk over a ragged per-sequence KV cache.
+
+    The chunk's Sq tokens of sequence b sit at cache rows kv_lens[b] + i; query
+    i attends to rows [0, kv_lens[b] + i] of that sequence, i.e. the causal mask
+    of the whole sequence restricted to the chunk's rows. The reference has no
+    such form: its cache concat runs a chunk non-causally (is_causal = Sq == Sk,
+    modules/attention.py:89-96). This is the attention of
+    `flash_attention(..., is_causal=True)` (kernels/flash_attention.py:13-18,
+    SDPA) over the whole sequence, kept for the chunk's rows, computed with an
+    explicit boolean mask per sequence.
+    q (B,Hq,Sq,D); k_cache/v_cache (B,Hkv,cap,D); kv_lens (B,) int.
+    """
+    B, Hq, Sq, D = q.shape
+    outs = []
+    for b in range(B):
+        L = int(kv_lens[b])
+        k = k_cache[b:b + 1, :, :L + Sq]
+        v = v_cache[b:b + 1, :, :L + Sq]
+        if num_kv_groups > 1:
+            nkv = k.shape[1]
+            k = k[:, :, None].expand(1, nkv, num_kv_groups, L + Sq, D).reshape(1, Hq, L + Sq, D)
+            v = v[:, :, None].expand(1, nkv, num_kv_groups, L + Sq, D).reshape(1, Hq, L + Sq, D)
+        keep = torch.arange(L + Sq)[None, :] <= (L + torch.arange(Sq))[:, None]
+        outs.append(F.scaled_dot_product_attention(q[b:b + 1], k, v, attn_mask=keep.to(q.device), scale=scale))
     return torch.cat(outs, dim=0)
 
 

@@ -48,6 +48,8 @@ _SIGS: dict[str, tuple] = {
                                 _i64p, c_float, _i64p, c_int, _V]),
     "q3_flash_attention": (c_int, [_V, _V, _V, _V, _f32p, _I, _I, _I, _I, _I, _I, _i64p, c_float, c_int, c_int,
                                    _V]),
+    "q3_flash_attention_cache": (c_int, [_V, _V, _V, _i32p, _V, _I, _I, _I, _I, _I, _I, _i64p, c_float, c_int,
+                                         c_int, _V]),
     "q3_decode_attention_workspace_bytes": (c_int64, [_I, _I, _I, _I, _I]),
     "q3_decode_attention": (c_int, [_V, _V, _V, _i32p, _V, _I, _I, _I, _I, _I, _i64p, c_float, c_int, _V, _I, _V]),
     "q3_decode_attention_step": (c_int, [_V, _V, _V, _i32p, _V, _I, _I, _I, _I, _I, _i64p, c_float, c_int, _V, _I,
@@ -55,8 +57,10 @@ _SIGS: dict[str, tuple] = {
     "q3_moe_route": (c_int, [_V, _i32p, _V, _f32p, _I, _I, _I, c_int, _V]),
     "q3_moe_experts_workspace_bytes": (c_int64, [_I, _I, _I, _I, _I]),
     "q3_moe_experts": (c_int, [_V, _V, _V, _i32p, _V, _V, _V, _I, _I, _I, _I, _I, _V, _I, _V]),
+    "q3_moe_permute_workspace_bytes": (c_int64, [_I, _I, _I]),
+    "q3_moe_permute": (c_int, [_i32p, _V, _i32p, _i32p, _V, _i32p, _I, _I, _I, _V, _I, _V]),
     "q3_index_add_workspace_bytes": (c_int64, [_I, _I]),
-    "q3_index_add": (c_int, [_V, _V, _V, _I, _I, _I, c_int, _V, _I, _V]),
+    "q3_index_add": (c_int, [_V, _V, _V, _I, _I, _I, c_int, _V, _I, _i32p, _V]),
 }
 
 EXPORTED = tuple(_SIGS)
@@ -155,3 +159,35 @@ def gemm_workspace(nbytes: int, device: torch.device) -> tuple[torch.Tensor | No
         bufs.append(torch.zeros(size, dtype=torch.uint8, device=dev))
     buf = bufs[-1]
     return buf, buf.numel()
+
+
+# Per-device sticky status words (one int32 each, zero-initialised): kernels
+# that validate device-side data (index_add's indices) set bits here instead
+# of synchronising with the host. `device_status` reads and clears them.
+_status: dict[int, torch.Tensor] = {}
+
+STATUS_INDEX_OUT_OF_RANGE = 1
+
+
+def status_word(device: torch.device) -> torch.Tensor:
+    dev = torch.device(device)
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    t = _status.get(idx)
+    if t is None:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("status_word: first use on this device inside HIP-graph capture; run the op once "
+                               "eagerly before capturing it")
+        t = _status[idx] = torch.zeros(1, dtype=torch.int32, device=dev)
+    return t
+
+
+def device_status(device: torch.device | str | None = None, clear: bool = True) -> int:
+    """The bits set on `device` since the last clear (synchronises with the device)."""
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    t = _status.get(dev.index if dev.index is not None else torch.cuda.current_device())
+    if t is None:
+        return 0
+    v = int(t.item())
+    if clear and v:
+        t.zero_()
+    return v

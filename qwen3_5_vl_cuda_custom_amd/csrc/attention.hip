@@ -48,6 +48,10 @@ struct AttnParams {
   // decode
   const int* kv_lens;
   int len_add;      // decode: sequence b attends to kv_lens[b] + len_add cache rows
+  // prefill into a KV cache: sequence b's query i is token q_off[b] + i; it
+  // sees keys [0, q_off[b] + i] (causal) and the sequence has q_off[b] + Sq
+  // keys (clamped to Sk). Null: offset 0, Sk keys.
+  const int* q_off;
   int* lens_inc;    // decode: if set, lens_inc[b] += 1 once the step has read the lengths
   int* dec_hdr;     // decode workspace header: unit prefix over sequences (B + 1 ints)
   int dec_waves;    // decode: waves in the main kernel's grid
@@ -118,7 +122,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int q0 = qt * QB + wq * 32;
   const int qidx = q0 + l32;
   const int qend_block = min(p.Sq, qt * QB + QB);
-  const int klimit = p.causal ? min(p.Sk, qend_block) : p.Sk;
+  const int off = p.q_off ? __builtin_amdgcn_readfirstlane(max(p.q_off[b], 0)) : 0;
+  const int Skb = p.q_off ? min(p.Sk, off + p.Sq) : p.Sk;  // keys of this sequence
+  const int klimit = p.causal ? min(Skb, qend_block + off) : Skb;
   const int nkt = (klimit + kKT - 1) / kKT;
 
   const bf16* kbase = p.k + (int64_t)b * p.kb + (int64_t)kvh * p.kh;
@@ -160,7 +166,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const int key = kt * kKT + 4 * vu + kk;
-      vreg[kk] = (vlive && key < p.Sk) ? *reinterpret_cast<const bf16x8*>(vbase + (int64_t)key * p.vs + vcd * 8)
+      vreg[kk] = (vlive && key < Skb) ? *reinterpret_cast<const bf16x8*>(vbase + (int64_t)key * p.vs + vcd * 8)
                                        : bf16x8{};
     }
   };
@@ -197,7 +203,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       load_v(kt + 1);
     }
     const int k0 = kt * kKT;
-    if (q0 < p.Sq && (!p.causal || k0 <= wave_last_q)) {
+    if (q0 < p.Sq && (!p.causal || k0 <= wave_last_q + off)) {
       const bf16* sKc = sK[cur];
       const bf16* sVc = sV[cur];
       floatx16 s0 = floatx16{}, s1 = floatx16{};
@@ -209,13 +215,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         s1 = mfma32x32x16(a1, qf[ks], s1);
       }
       // Wave-uniform: does any key of this tile need masking for this wave?
-      const bool need_mask = (p.causal && k0 + kKT - 1 > q0) || (k0 + kKT > p.Sk);
+      const bool need_mask = (p.causal && k0 + kKT - 1 > q0 + off) || (k0 + kKT > Skb);
       if (need_mask) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = k0 + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (key >= p.Sk || (p.causal && key > qidx)) s0[r] = -INFINITY;
-          if (key + 32 >= p.Sk || (p.causal && key + 32 > qidx)) s1[r] = -INFINITY;
+          if (key >= Skb || (p.causal && key > qidx + off)) s0[r] = -INFINITY;
+          if (key + 32 >= Skb || (p.causal && key + 32 > qidx + off)) s1[r] = -INFINITY;
         }
       }
       float mloc = fmaxf(s0[0], s1[0]);
@@ -730,7 +736,9 @@ __global__ __launch_bounds__(512) void flash_fwd_pipe_kernel(const AttnParams p)
   const int hq = kvh * p.groups + hg * 4 + hw;
   const int q0 = qt * kQ;
   const int qw0 = q0 + 32 * qh;  // this wave's first query
-  const int klimit = causal ? min(Sk, q0 + kQ) : Sk;
+  const int off = p.q_off ? __builtin_amdgcn_readfirstlane(max(p.q_off[b], 0)) : 0;
+  const int Skb = p.q_off ? min(Sk, off + Sq) : Sk;  // keys of this sequence
+  const int klimit = causal ? min(Skb, q0 + kQ + off) : Skb;
   const int nkt = (klimit + kKeys - 1) / kKeys;
 
   const bf16* kbase = p.k + (int64_t)b * p.kb + (int64_t)kvh * p.kh;
@@ -793,12 +801,12 @@ __global__ __launch_bounds__(512) void flash_fwd_pipe_kernel(const AttnParams p)
   auto tile_mask = [&](auto mask, int t) -> uint32_t {
     uint32_t bits = 0;
     const int k0 = t * kKeys;
-    if (decltype(mask)::value && ((causal && k0 + kKeys - 1 > qw0) || k0 + kKeys > Sk)) {  // uniform
-      const int qi = qw0 + l32;
+    if (decltype(mask)::value && ((causal && k0 + kKeys - 1 > qw0 + off) || k0 + kKeys > Skb)) {  // uniform
+      const int qi = qw0 + l32 + off;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = k0 + 8 * (r >> 2) + 4 * h + (r & 3);
-        if (key >= Sk || (causal && key > qi)) bits |= 1u << r;
+        if (key >= Skb || (causal && key > qi)) bits |= 1u << r;
       }
     }
     return bits;
@@ -913,7 +921,7 @@ __global__ __launch_bounds__(512) void flash_fwd_pipe_kernel(const AttnParams p)
       softmax_max(sa, drop, pb);
       softmax_exp(sa, drop, pa);
     }
-    const int nfull = min(causal ? q0 / kKeys : nkt, Sk / kKeys);
+    const int nfull = min(causal ? (q0 + off) / kKeys : nkt, Skb / kKeys);
     int t = 1;
     for (; t + 1 < nfull; t += 2) {
       step(kUnmasked, t, sb, sa, pa, pb);
@@ -965,8 +973,9 @@ __global__ __launch_bounds__(128) void flash_generic_kernel(const AttnParams p, 
   const T* q = reinterpret_cast<const T*>(p.q) + (int64_t)b * p.qb + (int64_t)hq * p.qh + (int64_t)i * p.qs;
   const T* kb = reinterpret_cast<const T*>(p.k) + (int64_t)b * p.kb + (int64_t)kvh * p.kh;
   const T* vb = reinterpret_cast<const T*>(p.v) + (int64_t)b * p.vb + (int64_t)kvh * p.vh;
-  int nk = kv_lens ? min(kv_lens[b] + p.len_add, p.Sk) : p.Sk;
-  if (p.causal) nk = min(nk, i + 1);
+  const int off = p.q_off ? max(p.q_off[b], 0) : 0;
+  int nk = kv_lens ? min(kv_lens[b] + p.len_add, p.Sk) : (p.q_off ? min(p.Sk, off + p.Sq) : p.Sk);
+  if (p.causal) nk = min(nk, i + off + 1);
   float acc[256];
   for (int d = 0; d < D; ++d) acc[d] = 0.f;
   float m = -INFINITY, l = 0.f;
@@ -1035,20 +1044,18 @@ int64_t decode_ws_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int
                             (int64_t)sizeof(float);
 }
 
-__global__ void lens_inc_kernel(int* lens, int B) {
+__global__ void lens_inc_kernel(int* lens, int B, int add) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < B) lens[i] += 1;
+  if (i < B) lens[i] += add;
 }
-
-}  // namespace
-
-extern "C" {
 
 // q, k, v, o: (B, H, S, D) with element strides (b, h, s) given in `strides`
 // as [qb, qh, qs, kb, kh, ks, vb, vh, vs, ob, oh, os]; the head dim is contiguous.
-int q3_flash_attention(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t Hq,
-                       int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D, const int64_t* strides, float scale,
-                       int is_causal, int dtype, void* stream) {
+// q_off (B) int32 on the device or null: per-sequence query offset (see
+// AttnParams::q_off). lens_add: if set, lens_add[b] += Sq after the attention.
+int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t Hq, int64_t Hkv,
+             int64_t Sq, int64_t Sk, int64_t D, const int64_t* strides, float scale, int is_causal, int dtype,
+             const int* q_off, int* lens_add, void* stream) {
   Q3_REQUIRE(q && k && v && o && strides, Q3_ERR_NULL);
   Q3_REQUIRE(B >= 0 && Hq >= 1 && Hkv >= 1 && Sq >= 0 && Sk >= 0 && D >= 1, Q3_ERR_SHAPE);
   Q3_REQUIRE(Hq % Hkv == 0, Q3_ERR_SHAPE);
@@ -1080,36 +1087,72 @@ int q3_flash_attention(const void* q, const void* k, const void* v, void* o, flo
   p.scale_log2 = scale * kLog2e;
   p.causal = is_causal ? 1 : 0;
   p.groups = (int)(Hq / Hkv);
+  p.q_off = q_off;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool aligned = q3_aligned(q, 16) && q3_aligned(k, 16) && q3_aligned(v, 16) && q3_aligned(o, 8) &&
                        strides_aligned8(strides, 12);
+  int rc = Q3_OK;
   // The MFMA path addresses K with 32-bit buffer offsets.
   if (dtype == Q3_BF16 && mfma_head_dim(D) && aligned && Sk > 0 && (Sk + 1) * strides[5] * 2 < 0x7fffffffLL) {
     switch (D) {
       case 64:
-        return launch_fwd<64>(p, st);
+        rc = launch_fwd<64>(p, st);
+        break;
       case 72:
-        return launch_fwd<72>(p, st);
+        rc = launch_fwd<72>(p, st);
+        break;
       case 80:
-        return launch_fwd<80>(p, st);
+        rc = launch_fwd<80>(p, st);
+        break;
       case 96:
-        return launch_fwd<96>(p, st);
+        rc = launch_fwd<96>(p, st);
+        break;
       default:
-        if (p.groups % 4 == 0) return launch_fwd_pipe(p, st);
-        return launch_fwd<128>(p, st);
+        rc = p.groups % 4 == 0 ? launch_fwd_pipe(p, st) : launch_fwd<128>(p, st);
     }
+  } else {
+    const int64_t rows = B * Hq * Sq;
+    if (dtype == Q3_F32)
+      hipLaunchKernelGGL(flash_generic_kernel<float>, dim3((unsigned)q3_cdiv(rows, 128)), dim3(128), 0, st, p,
+                         (int)D, nullptr);
+    else if (dtype == Q3_BF16)
+      hipLaunchKernelGGL(flash_generic_kernel<bf16>, dim3((unsigned)q3_cdiv(rows, 128)), dim3(128), 0, st, p,
+                         (int)D, nullptr);
+    else
+      return Q3_ERR_DTYPE;
+    Q3_LAUNCH_CHECK();
   }
-  const int64_t rows = B * Hq * Sq;
-  if (dtype == Q3_F32)
-    hipLaunchKernelGGL(flash_generic_kernel<float>, dim3((unsigned)q3_cdiv(rows, 128)), dim3(128), 0, st, p, (int)D,
-                       nullptr);
-  else if (dtype == Q3_BF16)
-    hipLaunchKernelGGL(flash_generic_kernel<bf16>, dim3((unsigned)q3_cdiv(rows, 128)), dim3(128), 0, st, p, (int)D,
-                       nullptr);
-  else
-    return Q3_ERR_DTYPE;
-  Q3_LAUNCH_CHECK();
+  if (rc != Q3_OK) return rc;
+  if (lens_add) {
+    hipLaunchKernelGGL(lens_inc_kernel, dim3((unsigned)q3_cdiv(B, 256)), dim3(256), 0, st, lens_add, (int)B, (int)Sq);
+    Q3_LAUNCH_CHECK();
+  }
   return Q3_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int q3_flash_attention(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t Hq,
+                       int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D, const int64_t* strides, float scale,
+                       int is_causal, int dtype, void* stream) {
+  return fwd_impl(q, k, v, o, lse, B, Hq, Hkv, Sq, Sk, D, strides, scale, is_causal, dtype, nullptr, nullptr,
+                  stream);
+}
+
+// Prefill of Sq new tokens per sequence over a ragged KV cache whose rows
+// [kv_lens[b], kv_lens[b] + Sq) already hold the new tokens' K/V: query i of
+// sequence b attends causally to rows [0, kv_lens[b] + i]; kv_lens[b] += Sq
+// afterwards when `advance` is non-zero. strides as q3_flash_attention's with
+// k/v the (B, Hkv, cap, D) caches.
+int q3_flash_attention_cache(const void* q, const void* k_cache, const void* v_cache, int* kv_lens, void* o,
+                             int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t cap, int64_t D,
+                             const int64_t* strides, float scale, int advance, int dtype, void* stream) {
+  Q3_REQUIRE(kv_lens, Q3_ERR_NULL);
+  Q3_REQUIRE(Sq <= cap, Q3_ERR_SHAPE);
+  return fwd_impl(q, k_cache, v_cache, o, nullptr, B, Hq, Hkv, Sq, cap, D, strides, scale, 1, dtype, kv_lens,
+                  advance ? kv_lens : nullptr, stream);
 }
 
 int64_t q3_decode_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t D) {
@@ -1197,7 +1240,7 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
     return Q3_ERR_DTYPE;
   Q3_LAUNCH_CHECK();
   if (lens_inc) {
-    hipLaunchKernelGGL(lens_inc_kernel, dim3((unsigned)q3_cdiv(B, 256)), dim3(256), 0, st, lens_inc, (int)B);
+    hipLaunchKernelGGL(lens_inc_kernel, dim3((unsigned)q3_cdiv(B, 256)), dim3(256), 0, st, lens_inc, (int)B, 1);
     Q3_LAUNCH_CHECK();
   }
   return Q3_OK;

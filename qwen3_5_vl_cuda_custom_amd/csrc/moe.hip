@@ -443,6 +443,51 @@ int64_t moe_ws_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, Moe
   return off;
 }
 
+// Workspace of the dispatch alone (q3_moe_permute): the per-chunk tables,
+// counts and the m-tile table; the sorted list, weights and positions go to
+// the caller's buffers.
+int64_t moe_permute_ws_layout(int64_t T, int64_t E, int64_t k, MoeWs* ws, char* base) {
+  const int64_t P = T * k;
+  const int64_t max_tiles = q3_cdiv(P, kMoeBM) + E;
+  int64_t off = 0;
+  auto take = [&](int64_t bytes) {
+    char* p = base ? base + off : nullptr;
+    off += align256(bytes);
+    return p;
+  };
+  MoeWs w{};
+  const int64_t NC = q3_cdiv(T, kMoeChunk);
+  w.hist = reinterpret_cast<int*>(take(NC * E * 4));
+  w.cstart = reinterpret_cast<int*>(take(NC * E * 4));
+  w.counts = reinterpret_cast<int*>(take(E * 4));
+  w.tile_table = reinterpret_cast<int*>(take(max_tiles * 4));
+  w.n_tiles = reinterpret_cast<int*>(take(4));
+  if (ws) *ws = w;
+  return off;
+}
+
+// Dispatch: per-expert counts and offsets, the m-tile table, and every
+// (token, slot) entry's row in expert-major, (token, slot)-ascending order
+// (the order of the reference's per-expert nonzero(), modules/moe.py:75).
+int moe_dispatch(const int* top_idx, const bf16* top_w, int64_t T, int64_t k, int64_t E, const MoeWs& w,
+                 hipStream_t st) {
+  const int NC = (int)q3_cdiv(T, kMoeChunk);
+  hipLaunchKernelGGL(moe_hist_kernel, dim3((unsigned)NC), dim3(64), E * sizeof(int), st, top_idx, (int)T, (int)k,
+                     (int)E, w.hist);
+  hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(1024), 0, st, w.hist, NC, (int)E, w.counts, w.offsets, w.cstart,
+                     w.tile_table, w.n_tiles);
+  const dim3 place_blk(kPlaceWaves * 64);
+  const size_t place_lds = 2 * E * sizeof(int);
+  if (k <= 8)
+    hipLaunchKernelGGL(moe_place_kernel<8>, dim3((unsigned)NC), place_blk, place_lds, st, top_idx, top_w, (int)T,
+                       (int)k, (int)E, w.hist, w.cstart, w.sorted_token, w.sorted_w, w.pos_of);
+  else
+    hipLaunchKernelGGL(moe_place_kernel<32>, dim3((unsigned)NC), place_blk, place_lds, st, top_idx, top_w, (int)T,
+                       (int)k, (int)E, w.hist, w.cstart, w.sorted_token, w.sorted_w, w.pos_of);
+  Q3_LAUNCH_CHECK();
+  return Q3_OK;
+}
+
 // ------------------------------------------------------------------ index_add
 __global__ void fill_int_kernel(int* p, int64_t n, int v) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
@@ -556,15 +601,15 @@ __global__ __launch_bounds__(256) void ia_accumulate_kernel(T* __restrict__ targ
 
 template <typename T>
 int index_add_t(void* target, const void* src, const int64_t* idx, int64_t ns, int64_t nt, int64_t D, char* ws,
-                hipStream_t st) {
+                int* status, hipStream_t st) {
   int* counts = reinterpret_cast<int*>(ws);
   int* fill = counts + nt;
   int* starts = fill + nt;
   int* bucket = starts + nt + 1;
-  int* bad = bucket + ns;
+  int* bad = status ? status : bucket + ns;  // the caller's status word is sticky: never cleared here
   const unsigned fb = (unsigned)std::min<int64_t>(q3_cdiv(2 * nt + 1, 256), 1024);
   hipLaunchKernelGGL(fill_int_kernel, dim3(fb), dim3(256), 0, st, counts, 2 * nt, 0);
-  hipLaunchKernelGGL(fill_int_kernel, dim3(1), dim3(64), 0, st, bad, (int64_t)1, 0);
+  if (!status) hipLaunchKernelGGL(fill_int_kernel, dim3(1), dim3(64), 0, st, bad, (int64_t)1, 0);
   const unsigned sb = (unsigned)std::max<int64_t>(1, std::min<int64_t>(q3_cdiv(ns, 256), 1024));
   hipLaunchKernelGGL(ia_count_kernel, dim3(sb), dim3(256), 0, st, idx, ns, nt, counts, bad);
   hipLaunchKernelGGL(ia_scan_kernel, dim3(1), dim3(256), 0, st, counts, nt, starts);
@@ -631,23 +676,10 @@ int q3_moe_experts(const void* x, const void* gate_up, const void* down, const i
   moe_ws_layout(T, H, I, E, k, &w, static_cast<char*>(workspace));
   const int64_t P = T * k;
   const int64_t max_tiles = q3_cdiv(P, kMoeBM) + E;
-
-  const int NC = (int)q3_cdiv(T, kMoeChunk);
-  hipLaunchKernelGGL(moe_hist_kernel, dim3((unsigned)NC), dim3(64), E * sizeof(int), st, top_idx, (int)T, (int)k,
-                     (int)E, w.hist);
-  hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(1024), 0, st, w.hist, NC, (int)E, w.counts, w.offsets, w.cstart,
-                     w.tile_table, w.n_tiles);
-  const dim3 place_blk(kPlaceWaves * 64);
-  const size_t place_lds = 2 * E * sizeof(int);
-  if (k <= 8)
-    hipLaunchKernelGGL(moe_place_kernel<8>, dim3((unsigned)NC), place_blk, place_lds, st, top_idx,
-                       static_cast<const bf16*>(top_w), (int)T, (int)k, (int)E, w.hist, w.cstart, w.sorted_token,
-                       w.sorted_w, w.pos_of);
-  else
-    hipLaunchKernelGGL(moe_place_kernel<32>, dim3((unsigned)NC), place_blk, place_lds, st, top_idx,
-                       static_cast<const bf16*>(top_w), (int)T, (int)k, (int)E, w.hist, w.cstart, w.sorted_token,
-                       w.sorted_w, w.pos_of);
-  Q3_LAUNCH_CHECK();
+  {
+    const int rc = moe_dispatch(top_idx, static_cast<const bf16*>(top_w), T, k, E, w, st);
+    if (rc != Q3_OK) return rc;
+  }
 
   // GEMM 1: act[pos] = swiglu(x[token(pos)] . gate_up[e]^T)
   {
@@ -718,16 +750,40 @@ int q3_moe_experts(const void* x, const void* gate_up, const void* down, const i
   return Q3_OK;
 }
 
+int64_t q3_moe_permute_workspace_bytes(int64_t T, int64_t E, int64_t k) {
+  if (T <= 0 || E <= 0 || k <= 0) return 0;
+  return moe_permute_ws_layout(T, E, k, nullptr, nullptr);
+}
+
+// The dispatch of q3_moe_experts on its own: offsets (E + 1) int32,
+// sorted_token / sorted_w (T * k) (int32 / bf16) and pos_of (T, k) int32.
+int q3_moe_permute(const int* top_idx, const void* top_w, int* offsets, int* sorted_token, void* sorted_w,
+                   int* pos_of, int64_t T, int64_t E, int64_t k, void* workspace, int64_t workspace_bytes,
+                   void* stream) {
+  Q3_REQUIRE(top_idx && top_w && offsets && sorted_token && sorted_w && pos_of, Q3_ERR_NULL);
+  Q3_REQUIRE(T >= 0 && E >= 1 && k >= 1 && k <= E, Q3_ERR_SHAPE);
+  Q3_REQUIRE(k <= 32 && E < 2048 && T * k < (1 << 20), Q3_ERR_UNSUPPORTED);
+  if (T == 0) return Q3_OK;
+  Q3_REQUIRE(workspace && workspace_bytes >= q3_moe_permute_workspace_bytes(T, E, k), Q3_ERR_WORKSPACE);
+  MoeWs w{};
+  moe_permute_ws_layout(T, E, k, &w, static_cast<char*>(workspace));
+  w.offsets = offsets;
+  w.sorted_token = sorted_token;
+  w.sorted_w = static_cast<bf16*>(sorted_w);
+  w.pos_of = pos_of;
+  return moe_dispatch(top_idx, static_cast<const bf16*>(top_w), T, k, E, w, static_cast<hipStream_t>(stream));
+}
+
 int64_t q3_index_add_workspace_bytes(int64_t n_src, int64_t n_target) {
   if (n_src < 0 || n_target < 0) return 0;
   return (3 * n_target + 1 + n_src + 1) * (int64_t)sizeof(int);
 }
 
 // target (n_target, D) += rows of src (n_src, D) at idx (n_src) int64, in place.
-// Returns Q3_ERR_SHAPE (after the fact, via `status` on the device) ... indices
-// out of range are skipped; the host-side wrapper validates them.
+// Source rows whose index is outside [0, n_target) are skipped, and bit 0 of
+// *status (a device int, when given) is set: the check costs the host nothing.
 int q3_index_add(void* target, const void* src, const int64_t* idx, int64_t n_src, int64_t n_target, int64_t D,
-                 int dtype, void* workspace, int64_t workspace_bytes, void* stream) {
+                 int dtype, void* workspace, int64_t workspace_bytes, int* status, void* stream) {
   Q3_REQUIRE(target && (src || n_src == 0) && (idx || n_src == 0), Q3_ERR_NULL);
   Q3_REQUIRE(n_src >= 0 && n_target >= 0 && D >= 0, Q3_ERR_SHAPE);
   Q3_REQUIRE(n_src < (1ll << 31) && n_target < (1ll << 31), Q3_ERR_UNSUPPORTED);
@@ -735,8 +791,8 @@ int q3_index_add(void* target, const void* src, const int64_t* idx, int64_t n_sr
   Q3_REQUIRE(workspace && workspace_bytes >= q3_index_add_workspace_bytes(n_src, n_target), Q3_ERR_WORKSPACE);
   hipStream_t st = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
-  if (dtype == Q3_BF16) return index_add_t<bf16>(target, src, idx, n_src, n_target, D, ws, st);
-  if (dtype == Q3_F32) return index_add_t<float>(target, src, idx, n_src, n_target, D, ws, st);
+  if (dtype == Q3_BF16) return index_add_t<bf16>(target, src, idx, n_src, n_target, D, ws, status, st);
+  if (dtype == Q3_F32) return index_add_t<float>(target, src, idx, n_src, n_target, D, ws, status, st);
   return Q3_ERR_DTYPE;
 }
 

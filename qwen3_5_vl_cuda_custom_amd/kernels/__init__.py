@@ -3,10 +3,11 @@ each backed by a hand-written gfx950 HIP kernel of libq3vl.so. GPU tensors only;
 from ._loader import FALLBACK_LOG, record_fallback, strict_mode, summarize_fallbacks
 from .conv3d_patch import conv3d_patch
 from .elementwise import gelu_tanh, residual_add, swiglu
-from .flash_attention import decode_attention, flash_attention
+from .flash_attention import decode_attention, flash_attention, flash_attention_cache
 from .matmul import (RMSNORM_MATMUL_MAX_ROWS, matmul, matmul_segments, matmul_swiglu, rmsnorm_matmul_segments,
                      rmsnorm_matmul_swiglu)
-from .moe_routing import cuda_batched_gemm, cuda_index_add, cuda_topk, moe_experts, moe_route
+from .moe_routing import (cuda_batched_gemm, cuda_index_add, cuda_topk, moe_experts, moe_permute, moe_route,
+                          raise_device_errors)
 from .norms import layernorm, rmsnorm, softmax
 from .rotary import apply_mrope, apply_rope, qk_norm_rope
 
@@ -31,6 +32,7 @@ __all__ = [
     "swiglu",
     # additions beyond the reference API (fused / decode / MoE dispatch paths)
     "decode_attention",
+    "flash_attention_cache",
     "matmul_segments",
     "matmul_swiglu",
     "rmsnorm_matmul_segments",
@@ -38,5 +40,7 @@ __all__ = [
     "RMSNORM_MATMUL_MAX_ROWS",
     "moe_experts",
     "moe_route",
+    "moe_permute",
+    "raise_device_errors",
     "qk_norm_rope",
 ]

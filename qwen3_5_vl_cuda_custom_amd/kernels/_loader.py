@@ -32,3 +32,21 @@ def record_fallback(op_name: str, reason: str = "not_implemented") -> None:
 def strict_mode() -> bool:
     """Reference env switch; the HIP ops always behave strictly (they raise)."""
     return os.environ.get("CUDA_QWEN3_VL_STRICT") == "1"
+
+
+def load_op(name: str, sources: list[str] | None = None, verbose: bool = False) -> bool:
+    """Reference name (kernels/_loader.py:190). Every op of this package lives in the
+    prebuilt libq3vl.so: True when it loads, else the load error propagates."""
+    from .. import _lib
+    _lib.lib()
+    return True
+
+
+def get_load_error(name: str) -> Exception | None:
+    """Reference name (kernels/_loader.py:250): ops are never loaded per name, so there is none."""
+    return None
+
+
+def maybe_strict_raise(op_name: str, exc: Exception) -> None:
+    """Reference name (kernels/_loader.py:258). No op here falls back, so an error always propagates."""
+    raise exc

@@ -66,3 +66,38 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
               _lib.i64s(q.stride(0), q.stride(1), *_s4(k_cache), *_s4(v_cache), o.stride(0), o.stride(1)),
               float(scale), _lib.dtype_code(q.dtype), _lib.ptr(ws), nws, _lib.stream())
     return o
+
+
+def flash_attention_cache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, kv_lens: torch.Tensor,
+                          scale: float, num_kv_groups: int = 1, *, out: torch.Tensor | None = None,
+                          advance: bool = False) -> torch.Tensor:
+    """Causal attention of a prefill chunk over a ragged KV cache.
+
+    q (B, Hq, Sq, D); k_cache/v_cache (B, Hkv, cap, D) whose rows
+    [kv_lens[b], kv_lens[b] + Sq) already hold the chunk's keys/values;
+    kv_lens (B,) int32 on the device. Query i of sequence b is the token at
+    position kv_lens[b] + i and attends to cache rows [0, kv_lens[b] + i]
+    (the causal mask of the whole sequence, bottom-right aligned for the
+    chunk). advance=True adds Sq to kv_lens afterwards, in stream order.
+    Returns (B, Hq, Sq, D).
+    """
+    check("flash_attention_cache", q, k_cache, v_cache)
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    B, Hq, Sq, D = q.shape
+    Hkv, cap = k_cache.shape[1], k_cache.shape[2]
+    if k_cache.shape != v_cache.shape or k_cache.shape[0] != B or k_cache.shape[3] != D:
+        raise ValueError(f"flash_attention_cache: q {tuple(q.shape)}, caches {tuple(k_cache.shape)}")
+    if k_cache.stride(-1) != 1 or v_cache.stride(-1) != 1:
+        raise ValueError("flash_attention_cache: the caches' head dim must be contiguous")
+    if Hkv * num_kv_groups != Hq:
+        raise ValueError(f"flash_attention_cache: Hq={Hq} != Hkv={Hkv} * num_kv_groups={num_kv_groups}")
+    if kv_lens.dtype != torch.int32 or not kv_lens.is_cuda or kv_lens.shape != (B,) or kv_lens.stride(0) != 1:
+        raise ValueError("flash_attention_cache: kv_lens must be a contiguous int32 (B,) device tensor")
+    o = out if out is not None else torch.empty((B, Hq, Sq, D), dtype=q.dtype, device=q.device)
+    if o.shape != (B, Hq, Sq, D) or o.stride(-1) != 1:
+        raise ValueError("flash_attention_cache: out must be (B, Hq, Sq, D) with a contiguous head dim")
+    _lib.call("q3_flash_attention_cache", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), kv_lens.data_ptr(),
+              o.data_ptr(), B, Hq, Hkv, Sq, cap, D, _lib.i64s(*_s4(q), *_s4(k_cache), *_s4(v_cache), *_s4(o)),
+              float(scale), int(bool(advance)), _lib.dtype_code(q.dtype), _lib.stream())
+    return o

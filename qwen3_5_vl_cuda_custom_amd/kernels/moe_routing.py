@@ -28,7 +28,9 @@ def cuda_index_add(target: torch.Tensor, source: torch.Tensor, index: torch.Tens
 
     Deterministic: each target row adds its sources in ascending i in fp32,
     starting from its own value, and rounds once (torch's index_add_
-    semantics). Indices must lie in [0, target.shape[0]).
+    semantics). Indices must lie in [0, target.shape[0]): the kernel skips any
+    other and records it on the device (see raise_device_errors); the call
+    itself never synchronises with the host.
     """
     check("cuda_index_add", target, source)
     if index.dim() != 1 or index.shape[0] != source.shape[0] or not index.is_cuda:
@@ -41,15 +43,25 @@ def cuda_index_add(target: torch.Tensor, source: torch.Tensor, index: torch.Tens
     if n_src == 0:
         return target
     idx = index.to(torch.int64).contiguous()
-    lo, hi = int(idx.min()), int(idx.max())
-    if lo < 0 or hi >= n_t:
-        raise IndexError(f"cuda_index_add: index out of range [0, {n_t})")
     src = source.contiguous()
     D = src[0].numel()
     ws, nws = _lib.workspace(_lib.lib().q3_index_add_workspace_bytes(n_src, n_t), target.device)
     _lib.call("q3_index_add", target.data_ptr(), src.data_ptr(), idx.data_ptr(), n_src, n_t, D,
-              _lib.dtype_code(target.dtype), _lib.ptr(ws), nws, _lib.stream())
+              _lib.dtype_code(target.dtype), _lib.ptr(ws), nws, _lib.status_word(target.device).data_ptr(),
+              _lib.stream())
     return target
+
+
+def raise_device_errors(device=None) -> None:
+    """Raise for errors that device-side validation recorded since the last check (synchronises).
+
+    cuda_index_add checks its indices on the device: a source row whose index
+    lies outside [0, target rows) is skipped and flagged, with no host
+    synchronisation in the op itself (so it can be captured in a HIP graph).
+    """
+    bits = _lib.device_status(device)
+    if bits & _lib.STATUS_INDEX_OUT_OF_RANGE:
+        raise IndexError("cuda_index_add: an index was out of range; its source row was skipped")
 
 
 def cuda_batched_gemm(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
@@ -91,10 +103,22 @@ def moe_experts(x: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor, top_
     top_w (T, k) bf16. Returns (T, H) (+ residual).
     """
     check("moe_experts", x, gate_up, down, top_w, residual)
+    if x.dim() != 2 or gate_up.dim() != 3 or down.dim() != 3:
+        raise ValueError("moe_experts: x (T, H), gate_up (E, 2I, H), down (E, H, I)")
     T, H = x.shape
     E, I2, _ = gate_up.shape
     I = I2 // 2
+    if gate_up.shape[2] != H or tuple(down.shape) != (E, H, I) or I2 % 2:
+        raise ValueError(f"moe_experts: gate_up {tuple(gate_up.shape)} / down {tuple(down.shape)} do not match "
+                         f"H={H}")
+    if top_idx.dtype != torch.int32 or not top_idx.is_cuda or top_idx.dim() != 2 or top_idx.shape[0] != T:
+        raise ValueError(f"moe_experts: top_idx must be an int32 (T={T}, k) device tensor, got {top_idx.dtype} "
+                         f"{tuple(top_idx.shape)}")
     k = top_idx.shape[1]
+    if tuple(top_w.shape) != (T, k):
+        raise ValueError(f"moe_experts: top_w must be ({T}, {k}), got {tuple(top_w.shape)}")
+    if residual is not None and tuple(residual.shape) != (T, H):
+        raise ValueError(f"moe_experts: residual must be ({T}, {H})")
     x = x.contiguous()
     out = torch.empty_like(x)
     nbytes = _lib.lib().q3_moe_experts_workspace_bytes(T, H, I, E, k)
@@ -104,3 +128,29 @@ def moe_experts(x: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor, top_
               top_idx.contiguous().data_ptr(), top_w.contiguous().data_ptr(), _lib.ptr(r), out.data_ptr(), T, H, I,
               E, k, _lib.ptr(ws), nws, _lib.stream())
     return out
+
+
+def moe_permute(top_idx: torch.Tensor, top_w: torch.Tensor, num_experts: int):
+    """The expert dispatch of CudaSparseMoE (modules/moe.py:70-76) as tables.
+
+    top_idx (T, k) int32, top_w (T, k) bf16. Returns (offsets (E+1,) int32,
+    sorted_token (T*k,) int32, sorted_w (T*k,) bf16, pos_of (T, k) int32):
+    expert e's entries are rows [offsets[e], offsets[e+1]) in ascending
+    (token, slot) order, the order of `(top_idx == e).nonzero()`.
+    """
+    check("moe_permute", top_w)
+    if top_idx.dtype != torch.int32 or not top_idx.is_cuda or top_idx.dim() != 2:
+        raise ValueError("moe_permute: top_idx must be an int32 (T, k) device tensor")
+    if top_w.dtype != torch.bfloat16 or tuple(top_w.shape) != tuple(top_idx.shape):
+        raise ValueError("moe_permute: top_w must be bf16 with top_idx's shape")
+    T, k = top_idx.shape
+    dev = top_idx.device
+    offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
+    sorted_token = torch.empty(T * k, dtype=torch.int32, device=dev)
+    sorted_w = torch.empty(T * k, dtype=torch.bfloat16, device=dev)
+    pos_of = torch.full((T, k), -1, dtype=torch.int32, device=dev)
+    ws, nws = _lib.workspace(_lib.lib().q3_moe_permute_workspace_bytes(T, num_experts, k), dev)
+    _lib.call("q3_moe_permute", top_idx.contiguous().data_ptr(), top_w.contiguous().data_ptr(), offsets.data_ptr(),
+              sorted_token.data_ptr(), sorted_w.data_ptr(), pos_of.data_ptr(), T, num_experts, k, _lib.ptr(ws), nws,
+              _lib.stream())
+    return offsets, sorted_token, sorted_w, pos_of

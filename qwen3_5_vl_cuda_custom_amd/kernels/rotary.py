@@ -83,6 +83,21 @@ def qk_norm_rope(q_in, k_in, v_in, q_out, k_out, v_out, q_weight, k_weight, posi
     """
     B, S, Hq, D = q_in.shape
     Hkv = k_in.shape[2]
+    # The kernel reads positions[(axis * B + b) * S + s] and inv_freq[0, D/2):
+    # anything else would be read out of bounds on the device.
+    if (positions.dtype != torch.int32 or not positions.is_cuda or tuple(positions.shape) != (3, B, S)
+            or not positions.is_contiguous()):
+        raise ValueError(f"qk_norm_rope: positions must be a contiguous int32 (3, {B}, {S}) device tensor, got "
+                         f"{positions.dtype} {tuple(positions.shape)}")
+    if inv_freq.dtype != torch.float32 or not inv_freq.is_cuda or inv_freq.numel() != D // 2:
+        raise ValueError(f"qk_norm_rope: inv_freq must be a float32 ({D // 2},) device tensor")
+    if dst_seq_offset is not None and (dst_seq_offset.dtype != torch.int32 or not dst_seq_offset.is_cuda
+                                       or tuple(dst_seq_offset.shape) != (B,) or not dst_seq_offset.is_contiguous()):
+        raise ValueError(f"qk_norm_rope: dst_seq_offset must be a contiguous int32 ({B},) device tensor")
+    if tuple(k_in.shape) != (B, S, Hkv, D) or tuple(q_out.shape) != (B, S, Hq, D):
+        raise ValueError("qk_norm_rope: q/k views must be (B, S, H, D) with matching B, S and D")
+    if sum(mrope_section) * 2 != D:
+        raise ValueError(f"qk_norm_rope: mrope_section {list(mrope_section)} must sum to D/2 = {D // 2}")
     ts = [q_in, k_in, v_in, q_out, k_out, v_out]
     strides = []
     for t in ts:

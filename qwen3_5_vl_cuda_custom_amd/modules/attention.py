@@ -4,8 +4,8 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from ..kernels import (apply_rope, decode_attention, flash_attention, matmul_segments, qk_norm_rope,
-                       rmsnorm_matmul_segments)
+from ..kernels import (apply_rope, decode_attention, flash_attention, flash_attention_cache, matmul_segments,
+                       qk_norm_rope, rmsnorm_matmul_segments)
 from .kv_cache import StaticKVCache
 from .linear import CudaLinear
 from .norms import CudaRMSNorm, fused_norm_ok
@@ -48,7 +48,9 @@ class CudaFullAttention(nn.Module):
     returns (out, (k, v)) with k/v (B, Hkv, S_total, D). Additions:
       kv_cache=StaticKVCache  rotated k/v are written in place at each
                               sequence's length and attention runs over the
-                              ragged cache (decode when S == 1)
+                              ragged cache: decode when S == 1, else a
+                              prefill chunk whose token i attends causally to
+                              the cache rows up to its own (lens[b] + i)
       residual=tensor         added to o_proj's output in the GEMM epilogue
       input_norm=CudaRMSNorm  x is the layer input before this RMSNorm; for
                               decode shapes (at most 32 tokens, bf16) the norm
@@ -101,9 +103,13 @@ class CudaFullAttention(nn.Module):
                 raise ValueError("pass either past_kv or kv_cache, not both")
             if not self._fusable(mrope_apply, x):
                 raise ValueError("kv_cache decoding needs mrope_apply = TextMRoPE.bind(position_ids)")
+            if kv_cache.batch != B:
+                raise ValueError(f"kv_cache holds {kv_cache.batch} sequences, the input has {B}")
             rope = mrope_apply.rope
-            pos = mrope_apply.positions_int32(x.device)
+            pos = mrope_apply.positions_int32(x.device, B, S)
+            kv_cache.reserve(S)  # raises, before any launch, if a sequence would overflow the cache
             kc, vc = kv_cache.k.transpose(1, 2), kv_cache.v.transpose(1, 2)  # (B, cap, Hkv, D) views
+            # The new tokens' K/V rows go to cache rows [lens[b], lens[b] + S).
             qk_norm_rope(q, k, v, q, kc, vc, self.q_norm.weight, self.k_norm.weight, pos, rope.inv_freq,
                          rope.mrope_section, self.q_norm.eps, dst_seq_offset=kv_cache.lens,
                          dst_seq_cap=kv_cache.capacity)
@@ -112,15 +118,15 @@ class CudaFullAttention(nn.Module):
                 decode_attention(q[:, 0], kv_cache.k, kv_cache.v, kv_cache.lens, self.scale, out=o[:, 0],
                                  max_len=kv_cache.capacity, append=True)
             else:
-                # Prefill of an empty cache: causal attention over the rows just written.
-                flash_attention(q.transpose(1, 2), kv_cache.k[:, :, :S], kv_cache.v[:, :, :S], self.scale, True,
-                                self.num_kv_groups, out=o.transpose(1, 2))
-                kv_cache.lens.add_(S)
+                # Prefill chunk: token i of sequence b sits at row lens[b] + i and
+                # attends causally to rows [0, lens[b] + i]; then lens += S.
+                flash_attention_cache(q.transpose(1, 2), kv_cache.k, kv_cache.v, kv_cache.lens, self.scale,
+                                      self.num_kv_groups, out=o.transpose(1, 2), advance=True)
             return self.o_proj(o.view(B, S, Hq * D), residual=residual), (kv_cache.k, kv_cache.v)
 
         if self._fusable(mrope_apply, x):
             rope = mrope_apply.rope
-            pos = mrope_apply.positions_int32(x.device)
+            pos = mrope_apply.positions_int32(x.device, B, S)
             qk_norm_rope(q, k, None, q, k, None, self.q_norm.weight, self.k_norm.weight, pos, rope.inv_freq,
                          rope.mrope_section, self.q_norm.eps)
             qh, kh, vh = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)

@@ -16,18 +16,27 @@ Rules for a captured step:
 """
 from __future__ import annotations
 
-from typing import Any, Callable
+from typing import Any, Callable, Sequence
 
 import torch
 
 
 class StepGraph:
-    """Capture `fn()` (after `warmup` eager runs on a side stream) and replay it."""
+    """Capture `fn()` (after `warmup` eager runs on a side stream) and replay it.
 
-    def __init__(self, fn: Callable[[], Any], warmup: int = 2) -> None:
+    `caches`: the StaticKVCaches the step appends to, `tokens` rows per
+    sequence each replay; replay() accounts for the rows on the host first
+    (StaticKVCache.reserve), so a replay that would overflow a cache raises
+    instead of launching.
+    """
+
+    def __init__(self, fn: Callable[[], Any], warmup: int = 2, *, caches: Sequence[Any] = (),
+                 tokens: int = 1) -> None:
         if not torch.cuda.is_available():
             raise RuntimeError("StepGraph needs a GPU")
         self.fn = fn
+        self.caches = list(caches)
+        self.tokens = tokens
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
@@ -40,5 +49,10 @@ class StepGraph:
 
     def replay(self) -> Any:
         """Launch the captured step on the current stream; returns the static outputs."""
+        for c in self.caches:
+            if c.max_len + self.tokens > c.capacity:
+                c.reserve(self.tokens)  # raises, before any cache has been advanced
+        for c in self.caches:
+            c.reserve(self.tokens)
         self.graph.replay()
         return self.out

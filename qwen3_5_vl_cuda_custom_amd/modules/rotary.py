@@ -41,13 +41,29 @@ class MRoPEBinding:
         self.position_ids = position_ids
         self._pos32: torch.Tensor | None = None
 
-    def positions_int32(self, device: torch.device) -> torch.Tensor:
-        """(3, B, S) int32 positions on `device`. An int32 contiguous device tensor
-        passed at construction is used as is, so in-place updates of it reach
-        the kernels (a captured decode step reads its positions from there)."""
-        if self._pos32 is None or self._pos32.device != device:
-            self._pos32 = self.position_ids.to(device=device, dtype=torch.int32).contiguous()
-        return self._pos32
+    def positions_int32(self, device: torch.device, batch: int | None = None, seq: int | None = None) -> torch.Tensor:
+        """(3, B, S) int32 positions on `device`, checked against the batch and
+        sequence length of the tokens they rotate. (3, 1, S) positions are
+        broadcast over the batch (a copy), as TextMRoPE.apply and the
+        reference's cos/sin tables do; any other shape raises. An int32
+        contiguous (3, B, S) device tensor passed at construction is used as is,
+        so in-place updates of it reach the kernels (a captured decode step
+        reads its positions from there)."""
+        pid = self.position_ids
+        if pid.dim() != 3 or pid.shape[0] != 3:
+            raise ValueError(f"mRoPE positions must be (3, B, S), got {tuple(pid.shape)}")
+        if seq is not None and pid.shape[2] != seq:
+            raise ValueError(f"mRoPE positions cover {pid.shape[2]} tokens, the input has {seq}")
+        if batch is not None and pid.shape[1] not in (1, batch):
+            raise ValueError(f"mRoPE positions have batch {pid.shape[1]}, the input has {batch}")
+        want_b = batch if batch is not None else pid.shape[1]
+        p = self._pos32
+        if p is None or p.device != torch.device(device) or p.shape[1] != want_b:
+            p = pid.to(device=device, dtype=torch.int32)
+            if p.shape[1] != want_b:
+                p = p.expand(3, want_b, p.shape[2])
+            self._pos32 = p = p.contiguous()
+        return p
 
     def __call__(self, q: torch.Tensor, k: torch.Tensor):
         return self.rope.apply(q, k, self.position_ids)

@@ -52,22 +52,43 @@ def assert_within_ulp(out: torch.Tensor, ref: torch.Tensor, ulps: float = 1.0, w
     assert not bad.any(), f"{what}: {int(bad.sum())} elements beyond {ulps} ulp (max err {float(err.max()):.3e})"
 
 
-def assert_layer_parity(out, ref32, ref_bf16, what="", slack=1.25):
+# Equal-rounding ties. Where our output and the reference bf16 path end in the
+# same bf16 rounding of the same value (v = bf16(x.Wv) in both), their errors
+# differ only where a different fp32 summation order flips that rounding: the
+# v projections measure identical to 4 digits (GPU run). The bar allows that
+# noise and no more: mean-rel within TIE_REL of the reference path's, and the
+# worst element within one bf16 ulp (of the reference value there) of the
+# reference path's worst.
+TIE_REL = 0.02
+
+
+def _ulp_bf16(x: float) -> float:
+    import math
+    return 2.0 ** (math.frexp(abs(x))[1] - 8) if x != 0 else 2.0 ** -133
+
+
+def assert_layer_parity(out, ref32, ref_bf16, what=""):
     """Module-level bar.
 
     `ref32` is the fp32 oracle; `ref_bf16` the same oracle with the reference's
     bf16 rounding after every op (the reference's own bf16 path). A bf16 layer
     carries the quantisation error of its bf16 GEMM operands, so its worst
-    element vs fp32 can exceed max-abs 2e-2 whatever the kernels do. The test
-    requires: mean-rel <= 5e-3 vs fp32, and max-abs vs
-    fp32 within 2e-2 or, where the reference's own bf16 path is further than
-    that, no more than `slack` times the reference path's max-abs.
+    element vs fp32 can exceed max-abs 2e-2 whatever the kernels do. Asserted:
+      * mean-rel vs fp32 <= 5e-3, and no larger than the
+        reference bf16 path's mean-rel (up to the equal-rounding tie TIE_REL);
+      * max-abs vs fp32 <= 2e-2, or, where the reference bf16 path's own
+        max-abs is larger, no larger than that (up to one bf16 ulp of the
+        reference value at our worst element).
     """
-    ma, mr = metrics(out, ref32)
-    ma_r, mr_r = metrics(ref_bf16, ref32)
+    o = out.detach().float().cpu()
+    r = ref32.detach().float().cpu()
+    ma, mr = metrics(o, r)
+    ma_r, mr_r = metrics(ref_bf16, r)
+    worst = float(r.reshape(-1)[int((o - r).abs().argmax())])
     msg = (f"{what}: ours max-abs {ma:.3e} mean-rel {mr:.3e} | reference bf16 path max-abs {ma_r:.3e} "
            f"mean-rel {mr_r:.3e}")
     print(msg)
     assert mr <= BF16_MEAN_REL, msg
-    assert ma <= max(BF16_MAX_ABS, slack * ma_r), msg
+    assert mr <= mr_r * (1 + TIE_REL), msg
+    assert ma <= max(BF16_MAX_ABS, ma_r + _ulp_bf16(worst)), msg
     return ma, mr, ma_r, mr_r

@@ -20,7 +20,7 @@ def header_functions():
 
 def test_library_loads_and_reports_version():
     lib = _lib.lib()
-    assert lib.q3_abi_version() == 1
+    assert lib.q3_abi_version() == 2
     assert _lib.error_string(0) == "ok"
     assert "pointer" in _lib.error_string(-1)
 
@@ -137,6 +137,14 @@ def test_attention_validation():
     assert L.q3_decode_attention_workspace_bytes(32, 32, 8, 8193, 128) == 4352 + (1024 + 32 * 8) * 4 * 130 * 4
     assert L.q3_decode_attention_step(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 8, 2, 128, 100, d, 0.1, 1, None, 0, None) == -6
     assert L.q3_decode_attention_step(FAKE, FAKE, FAKE, None, FAKE, 2, 8, 2, 128, 100, d, 0.1, 1, None, 0, None) == -1
+    # prefill chunk over a cache: lengths are required, and the chunk must fit the capacity
+    assert L.q3_flash_attention_cache(FAKE, FAKE, FAKE, None, FAKE, 2, 8, 2, 16, 100, 128, st, 0.1, 1, 1, None) == -1
+    assert L.q3_flash_attention_cache(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 8, 2, 101, 100, 128, st, 0.1, 1, 1,
+                                      None) == -2
+    assert L.q3_flash_attention_cache(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 6, 4, 16, 100, 128, st, 0.1, 1, 1,
+                                      None) == -2  # Hq % Hkv
+    assert L.q3_flash_attention_cache(FAKE, FAKE, FAKE, FAKE, FAKE, 0, 8, 2, 16, 100, 128, st, 0.1, 1, 1,
+                                      None) == 0  # empty batch: no-op
 
 
 def test_rope_validation():
@@ -159,5 +167,12 @@ def test_moe_validation():
     ws = L.q3_moe_experts_workspace_bytes(4096, 2048, 768, 128, 8)
     assert ws > 4096 * 8 * (2048 + 768) * 2
     assert L.q3_moe_experts(FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE, 16, 64, 32, 4, 2, None, 0, None) == -6
-    assert L.q3_index_add(FAKE, FAKE, FAKE, 5, 3, 4, 1, None, 0, None) == -6
-    assert L.q3_index_add(FAKE, None, FAKE, 5, 3, 4, 1, None, 0, None) == -1
+    assert L.q3_index_add(FAKE, FAKE, FAKE, 5, 3, 4, 1, None, 0, None, None) == -6
+    assert L.q3_index_add(FAKE, None, FAKE, 5, 3, 4, 1, None, 0, None, None) == -1
+    assert L.q3_index_add(FAKE, FAKE, FAKE, 0, 3, 4, 1, None, 0, None, None) == 0  # no sources: no-op
+    # dispatch tables on their own
+    assert L.q3_moe_permute(FAKE, FAKE, FAKE, FAKE, FAKE, None, 16, 8, 2, FAKE, 1 << 20, None) == -1
+    assert L.q3_moe_permute(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 16, 8, 9, FAKE, 1 << 20, None) == -2  # k > E
+    assert L.q3_moe_permute(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 16, 8, 2, None, 0, None) == -6
+    assert 0 < L.q3_moe_permute_workspace_bytes(4096, 128, 8) < ws
+    assert L.q3_moe_permute(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 0, 8, 2, None, 0, None) == 0

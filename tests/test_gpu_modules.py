@@ -76,6 +76,97 @@ def test_c2_layer_bf16_full_seq4096():
     assert torch.equal(y, y2)
 
 
+@pytest.mark.slow
+def test_c2_layer_bf16_full_seq16384():
+    """The third C2 length: the fp32 oracle on the GPU (its attention in fp32)."""
+    cfg = W.C2
+    layer = W.make_text_layer(cfg, torch.bfloat16, DEV, seed=0)
+    x, pos = W.text_inputs(cfg, 1, 16384, torch.bfloat16, DEV, seed=0)
+    y, _, (k, v) = layer(x, W.make_rope(cfg, DEV).bind(pos))
+    ref, _, (rk, rv) = oracle_text_layer(layer, cfg, x, pos, DEV)
+    emu, _, (ek, ev) = oracle_text_layer(layer, cfg, x, pos, DEV, bf16_path=True)
+    assert_layer_parity(k, rk, ek, what="C2 k S=16384")
+    assert_layer_parity(v, rv, ev, what="C2 v S=16384")
+    del rk, rv, ek, ev
+    assert_layer_parity(y, ref, emu, what="C2 layer S=16384")
+
+
+def _positions(starts, seq):
+    """(3, B, seq) int64 text positions starts[b] + 0..seq-1 on every axis."""
+    p = torch.tensor(starts).view(-1, 1) + torch.arange(seq).view(1, -1)
+    return p.unsqueeze(0).expand(3, -1, -1).contiguous().to(DEV)
+
+
+@pytest.mark.parametrize("cfg", [
+    W.TextLayerConfig(hidden=1024, heads=8, kv_heads=2, head_dim=128, intermediate=2048),
+    W.TextLayerConfig(hidden=512, heads=8, kv_heads=4, head_dim=64, intermediate=1024, mrope_section=(12, 10, 10)),
+])
+def test_kv_cache_chunked_prefill_ragged_then_decode(cfg):
+    """Prefill in two chunks into a StaticKVCache, with ragged lengths between them
+    (sequence 1 keeps only its first 57 tokens), then one decode step. Chunked
+    causal attention equals attention over the whole sequence at once, so every
+    output and cache row must match the fp32 oracle's layer over each sequence's
+    full token list."""
+    layer = W.make_text_layer(cfg, torch.bfloat16, DEV, seed=11)
+    rope = W.make_rope(cfg, DEV)
+    B, S1, S2, keep, cap = 2, 100, 60, 57, 256
+    g = torch.Generator(device=DEV).manual_seed(12)
+    xs = torch.randn(B, S1 + S2 + 1, cfg.hidden, generator=g, device=DEV).to(torch.bfloat16)
+    cache = W.StaticKVCache(B, cfg.kv_heads, cap, cfg.head_dim, dtype=torch.bfloat16, device=DEV)
+    y1, _, _ = layer(xs[:, :S1], rope.bind(_positions([0, 0], S1)), kv_cache=cache)
+    cache.set_lens([S1, keep])
+    y2, _, _ = layer(xs[:, S1:S1 + S2], rope.bind(_positions([S1, keep], S2)), kv_cache=cache)
+    y3, _, _ = layer(xs[:, S1 + S2:], rope.bind(_positions([S1 + S2, keep + S2], 1)), kv_cache=cache)
+    assert cache.lens.cpu().tolist() == [S1 + S2 + 1, keep + S2 + 1]
+    seqs = [xs[0:1], torch.cat([xs[1:2, :keep], xs[1:2, S1:]], dim=1)]
+    outs = [torch.cat([y1[0:1], y2[0:1], y3[0:1]], dim=1), torch.cat([y1[1:2, :keep], y2[1:2], y3[1:2]], dim=1)]
+    for b in range(B):
+        n = seqs[b].shape[1]
+        pos = _positions([0], n)
+        ref, _, (rk, rv) = oracle_text_layer(layer, cfg, seqs[b], pos, DEV)
+        emu, _, (ek, ev) = oracle_text_layer(layer, cfg, seqs[b], pos, DEV, bf16_path=True)
+        assert_layer_parity(outs[b], ref, emu, what=f"chunked prefill + decode, sequence {b}")
+        assert_layer_parity(cache.k[b:b + 1, :, :n], rk, ek, what=f"cache k, sequence {b}")
+        assert_layer_parity(cache.v[b:b + 1, :, :n], rv, ev, what=f"cache v, sequence {b}")
+
+
+def test_past_kv_reference_contract():
+    """The reference's cache form (modules/attention.py:89-96): past_kv=(k, v) tensors grown
+    by torch.cat, attention causal only when Sq == Sk, so a one-token step attends to the
+    whole cache and a multi-token step attends non-causally to everything."""
+    cfg = W.TextLayerConfig(hidden=1024, heads=8, kv_heads=2, head_dim=128, intermediate=2048)
+    layer = W.make_text_layer(cfg, torch.bfloat16, DEV, seed=21)
+    rope = W.make_rope(cfg, DEV)
+    g = torch.Generator(device=DEV).manual_seed(22)
+    x = torch.randn(1, 54, cfg.hidden, generator=g, device=DEV).to(torch.bfloat16)
+    y0, _, kv0 = layer(x[:, :48], rope.bind(_positions([0], 48)))
+    y1, _, kv1 = layer(x[:, 48:49], rope.bind(_positions([48], 1)), past_kv=kv0)
+    y2, _, kv2 = layer(x[:, 49:], rope.bind(_positions([49], 5)), past_kv=kv1)
+    assert kv1[0].shape == (1, cfg.kv_heads, 49, cfg.head_dim) and kv2[1].shape == (1, cfg.kv_heads, 54, cfg.head_dim)
+    assert torch.equal(kv2[0][:, :, :48], kv0[0]), "the cache prefix is carried unchanged"
+    for xs, start, past, y, kv in [(x[:, 48:49], 48, kv0, y1, kv1), (x[:, 49:], 49, kv1, y2, kv2)]:
+        past32 = (past[0].float(), past[1].float())
+        pos = _positions([start], xs.shape[1])
+        ref, _, (rk, _) = oracle_text_layer(layer, cfg, xs, pos, DEV, past_kv=past32)
+        emu, _, (ek, _) = oracle_text_layer(layer, cfg, xs, pos, DEV, past_kv=past32, bf16_path=True)
+        assert_layer_parity(y, ref, emu, what=f"past_kv step of {xs.shape[1]} token(s)")
+        assert_layer_parity(kv[0], rk, ek, what=f"past_kv grown k ({xs.shape[1]} token(s))")
+
+
+def test_batch_one_positions_broadcast():
+    """(3, 1, S) positions rotate every sequence of a batch alike (TextMRoPE.apply's
+    broadcast), identical to the explicit (3, B, S) form."""
+    cfg = W.TextLayerConfig(hidden=1024, heads=8, kv_heads=2, head_dim=128, intermediate=2048)
+    layer = W.make_text_layer(cfg, torch.bfloat16, DEV, seed=23)
+    rope = W.make_rope(cfg, DEV)
+    x, pos = W.text_inputs(cfg, 2, 40, torch.bfloat16, DEV, seed=24)
+    a, _, _ = layer(x, rope.bind(pos[:, :1]))
+    b, _, _ = layer(x, rope.bind(pos))
+    assert torch.equal(a, b)
+    with pytest.raises(ValueError):
+        layer(x, rope.bind(pos[:, :, :39]))
+
+
 def test_c3_decode_layer_against_per_sequence_oracle():
     cfg = W.C2
     case = W.make_decode_case(cfg, batch=32, capacity=8193, device=DEV, seed=0)
@@ -138,9 +229,9 @@ def test_decode_step_graph_replays_match_eager():
     lens_saved = cache.lens.clone()
     x_in.copy_(xs[0])
     pos32.copy_(lens0.to(DEV).view(1, B, 1).expand(3, B, 1))
-    graph = StepGraph(lambda: layer(x_in, binding, kv_cache=cache)[0], warmup=1)
+    graph = StepGraph(lambda: layer(x_in, binding, kv_cache=cache)[0], warmup=1, caches=[cache])
     # warm-up and capture advanced the lengths and wrote rows: start over
-    cache.lens.copy_(lens_saved)
+    cache.set_lens(lens_saved)
     junk = torch.randn(1 << 20, device=DEV)
     for t in range(steps):
         x_in.copy_(xs[t])
@@ -150,6 +241,7 @@ def test_decode_step_graph_replays_match_eager():
         assert torch.equal(out, eager[t]), f"replay {t} differs from the eager step"
         float(junk.sum())  # eager work between replays
     assert torch.equal(cache.lens.cpu(), lens0 + steps)
+    assert cache.max_len == int(lens0.max()) + steps  # replays accounted on the host
     for b in range(B):
         n = int(lens0[b]) + steps
         assert torch.equal(cache.k[b, :, :n], k_ref[b, :, :n]) and torch.equal(cache.v[b, :, :n], v_ref[b, :, :n])
@@ -166,6 +258,19 @@ def test_c4_moe_layer_reduced_tokens():
     ref, _, _ = oracle_text_layer(layer, cfg, x, pos, DEV, router_logits=logits.float())
     emu, _, _ = oracle_text_layer(layer, cfg, x, pos, DEV, router_logits=logits.float(), bf16_path=True)
     assert_layer_parity(y, ref, emu, what="C4 MoE layer")
+
+
+@pytest.mark.slow
+def test_c4_moe_layer_full_tokens():
+    """The benchmarked C4 size (4096 tokens, ~256 rows per expert: the 128x256 grouped
+    tiles and their XCD deal), routed with the device's logits as above."""
+    cfg = W.C4
+    layer = W.make_text_layer(cfg, torch.bfloat16, DEV, seed=0)
+    x, pos = W.text_inputs(cfg, 1, 4096, torch.bfloat16, DEV, seed=0)
+    y, logits, _ = layer(x, W.make_rope(cfg, DEV).bind(pos))
+    ref, _, _ = oracle_text_layer(layer, cfg, x, pos, DEV, router_logits=logits.float())
+    emu, _, _ = oracle_text_layer(layer, cfg, x, pos, DEV, router_logits=logits.float(), bf16_path=True)
+    assert_layer_parity(y, ref, emu, what="C4 MoE layer T=4096")
 
 
 def test_c4_router_indices_bit_exact_full():

@@ -207,9 +207,8 @@ def test_rmsnorm_matmul_fused(M, ns, Kd, kind):
     y = call()
     assert y.shape == ref.shape and y.dtype == torch.bfloat16
     assert_layer_parity(y, ref, ref_bf16, what=f"rmsnorm+{kind} M={M} K={Kd}")
-    # Two bf16 results, each within the bound of the fp32 result, may lie twice
-    # the bound apart.
-    assert_layer_parity(y, f32(two), ref_bf16, what=f"fused vs two launches M={M} K={Kd}", slack=2.5)
+    # The two-launch library path meets the same bar against fp32.
+    assert_layer_parity(two, ref, ref_bf16, what=f"two launches M={M} K={Kd}")
     assert torch.equal(y, call()), "fused norm projection must be deterministic"
 
 
@@ -550,3 +549,80 @@ def test_moe_experts_against_oracle_loop():
     pf = {n: f32(t) for n, t in p.items()}
     ref, _ = sparse_moe(f32(x), pf, top_k=k, router_logits=logits.float().cpu())
     assert_bf16_close(out, ref[0], what="moe_experts")
+
+
+# ------------------------------------------------------------------ prefill chunk over a KV cache
+@pytest.mark.parametrize("Hq,Hkv,D,dtype", [
+    (8, 2, 128, torch.bfloat16),   # groups 4: the eight-wave pipelined kernel
+    (8, 4, 64, torch.bfloat16),    # groups 2: the four-wave kernel family
+    (4, 2, 72, torch.bfloat16),    # vision head dim through the same kernel family
+    (4, 2, 32, torch.float32),     # fp32: the SIMT kernel
+])
+def test_flash_attention_cache_ragged(Hq, Hkv, D, dtype):
+    """Chunk of Sq tokens per sequence over cache rows [0, lens[b] + i] (causal over the
+    whole sequence), ragged lens incl. 0 and lens + Sq == cap; advance adds Sq in place."""
+    B, Sq, cap = 4, 77, 300
+    lens = torch.tensor([0, 5, 150, cap - Sq], dtype=torch.int32)
+    q = rnd(B, Hq, Sq, D, seed=200, dtype=dtype)
+    kc = rnd(B, Hkv, cap, D, seed=201, dtype=dtype)
+    vc = rnd(B, Hkv, cap, D, seed=202, dtype=dtype)
+    dl = gpu(lens)
+    out = K.flash_attention_cache(gpu(q), gpu(kc), gpu(vc), dl, D ** -0.5, Hq // Hkv, advance=True)
+    assert torch.equal(dl.cpu(), lens + Sq), "advance must add Sq to every length"
+    ref = O.chunk_attention(f32(q), f32(kc), f32(vc), lens.tolist(), D ** -0.5, Hq // Hkv)
+    if dtype == torch.float32:
+        assert_close(out, ref, atol=2e-5, what="chunk attention fp32")
+    else:
+        assert_bf16_close(out, ref, what=f"chunk attention D={D} groups={Hq // Hkv}")
+    # Empty cache: identical to plain causal attention over the chunk's own rows.
+    z = torch.zeros(B, dtype=torch.int32, device=DEV)
+    a = K.flash_attention_cache(gpu(q), gpu(kc), gpu(vc), z, D ** -0.5, Hq // Hkv)
+    b = K.flash_attention(gpu(q), gpu(kc)[:, :, :Sq], gpu(vc)[:, :, :Sq], D ** -0.5, True, Hq // Hkv)
+    assert torch.equal(a, b), "an empty cache must give causal attention bit for bit"
+    assert torch.equal(z.cpu(), torch.zeros(B, dtype=torch.int32)), "advance=False leaves the lengths"
+
+
+# ------------------------------------------------------------------ MoE dispatch tables
+@pytest.mark.parametrize("T,E,k", [(4096, 128, 8), (300, 16, 4), (70, 64, 1)])
+def test_moe_permute_matches_nonzero_order(T, E, k):
+    """The dispatch tables against the reference loop's per-expert `(top_idx == e).nonzero()`
+    (modules/moe.py:70-76), bit-exact: offsets, the (token) order, routing weights, inverse."""
+    g = torch.Generator().manual_seed(210 + T)
+    # random distinct experts per token, skewed so some experts get nothing
+    scores = torch.rand(T, E, generator=g) * torch.linspace(1.0, 0.05, E)
+    top_idx = scores.topk(k, dim=-1).indices.to(torch.int32)
+    top_w = torch.rand(T, k, generator=g).to(torch.bfloat16)
+    offsets, st, sw, pos_of = K.moe_permute(gpu(top_idx), gpu(top_w), E)
+    offsets, st, sw, pos_of = offsets.cpu(), st.cpu(), sw.cpu(), pos_of.cpu()
+    row = 0
+    for e in range(E):
+        tok, slot = (top_idx.long() == e).nonzero(as_tuple=True)
+        assert int(offsets[e]) == row, f"offset of expert {e}"
+        n = tok.numel()
+        assert torch.equal(st[row:row + n].long(), tok), f"token order of expert {e}"
+        assert torch.equal(sw[row:row + n], top_w[tok, slot]), f"routing weights of expert {e}"
+        assert torch.equal(pos_of[tok, slot].long(), torch.arange(row, row + n)), f"inverse of expert {e}"
+        row += n
+    assert int(offsets[E]) == row == T * k
+
+
+def test_index_add_out_of_range_is_skipped_and_flagged():
+    """Indices outside [0, rows) are skipped on the device and reported through the status
+    word (no host synchronisation in the op); valid rows match the CPU index_add_."""
+    from qwen3_5_vl_cuda_custom_amd import _lib
+    _lib.device_status(DEV)  # clear anything earlier tests left
+    g = torch.Generator().manual_seed(64)
+    target = torch.randn(20, 64, generator=g).to(torch.bfloat16)
+    src = torch.randn(40, 64, generator=g).to(torch.bfloat16)
+    idx = torch.randint(0, 20, (40,), generator=g)
+    K.cuda_index_add(gpu(target.clone()), gpu(src), gpu(idx))
+    K.raise_device_errors(DEV)  # all in range: nothing recorded
+    bad = idx.clone()
+    bad[3], bad[17] = 20, -1
+    out = K.cuda_index_add(gpu(target.clone()), gpu(src), gpu(bad))
+    keep = (bad >= 0) & (bad < 20)
+    ref = O.index_add(target.clone(), src[keep], bad[keep])
+    assert torch.equal(out.cpu(), ref), "valid rows must be added exactly as before"
+    with pytest.raises(IndexError):
+        K.raise_device_errors(DEV)
+    K.raise_device_errors(DEV)  # the check clears the word

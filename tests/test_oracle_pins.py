@@ -87,6 +87,38 @@ def test_decode_attention_ragged_bruteforce():
         assert np.allclose(out[b:b + 1].numpy(), ref, atol=1e-5)
 
 
+def np_chunk_attention(q, kc, vc, lens, scale, groups):
+    """float64 loop: query i of sequence b sees keys 0 .. lens[b] + i."""
+    B, Hq, Sq, D = q.shape
+    out = np.zeros((B, Hq, Sq, D))
+    for b in range(B):
+        for h in range(Hq):
+            kv = h // groups
+            for i in range(Sq):
+                n = lens[b] + i + 1
+                s = np.array([scale * np.dot(q[b, h, i], kc[b, kv, j]) for j in range(n)])
+                p = np.exp(s - s.max())
+                out[b, h, i] = (p / p.sum()) @ vc[b, kv, :n]
+    return out
+
+
+def test_chunk_attention_bruteforce_and_whole_sequence():
+    q, kc, vc = randn(3, 4, 5, 8), randn(3, 2, 16, 8), randn(3, 2, 16, 8)
+    lens = [0, 4, 11]
+    out = O.chunk_attention(q, kc, vc, lens, 0.4, 2)
+    ref = np_chunk_attention(q.double().numpy(), kc.double().numpy(), vc.double().numpy(), lens, 0.4, 2)
+    assert np.allclose(out.numpy(), ref, atol=1e-5)
+    # a chunk is the last Sq rows of causal attention over the whole sequence (queries for the
+    # cached rows are arbitrary: they do not reach the chunk's rows)
+    for b, Lb in enumerate(lens):
+        qfull = torch.cat([randn(1, 4, Lb, 8), q[b:b + 1]], dim=2)
+        whole = O.flash_attention(qfull, kc[b:b + 1, :, :Lb + 5], vc[b:b + 1, :, :Lb + 5], 0.4, True, 2)
+        assert torch.allclose(out[b:b + 1], whole[:, :, Lb:], atol=1e-5)
+    # an empty cache is plain causal attention
+    z = O.chunk_attention(q, kc[:, :, :5], vc[:, :, :5], [0, 0, 0], 0.4, 2)
+    assert torch.allclose(z, O.flash_attention(q, kc[:, :, :5], vc[:, :, :5], 0.4, True, 2), atol=1e-6)
+
+
 # ------------------------------------------------------------------ rotary
 def test_mrope_tables_closed_form_distinct_axes():
     """Element i of the interleaved table uses axis 0/1/2 by the chunked sections, both halves."""
