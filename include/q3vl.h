@@ -12,7 +12,9 @@
  *    launch.
  *  - The library allocates nothing: callers pass outputs and, where a
  *    *_workspace_bytes query says so, a device workspace. It keeps no pointer
- *    after returning and has no global state.
+ *    after returning and has no global state, except the static device
+ *    scratch array of the allocation-free entry point (one per GPU, with its
+ *    device address cached per device on first use).
  *
  * Reference interfaces replaced (paths relative to the reference's
  * CUDA_qwen3_5-main/CUDA_qwen3_5-main/cuda_qwen3_vl/): the torch-op schemas
@@ -38,7 +40,8 @@ typedef enum {
   Q3_ERR_DTYPE = -3,       /* dtype not supported by this op */
   Q3_ERR_ALIGN = -4,       /* pointer / stride alignment violated */
   Q3_ERR_UNSUPPORTED = -5, /* valid request outside what the kernels cover */
-  Q3_ERR_WORKSPACE = -6    /* workspace missing or smaller than *_workspace_bytes */
+  Q3_ERR_WORKSPACE = -6,   /* workspace missing or smaller than *_workspace_bytes */
+  Q3_ERR_SCRATCH = -7      /* request larger than a static scratch buffer (allocation-free entry points) */
 } q3_status;
 
 int q3_abi_version(void);
@@ -202,6 +205,21 @@ int q3_decode_attention(const void* q, const void* k_cache, const void* v_cache,
 int q3_decode_attention_step(const void* q, const void* k_cache, const void* v_cache, int* kv_lens, void* o,
                              int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len, const int64_t* strides,
                              float scale, int dtype, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* q3_decode_attention_step without a workspace argument, for callers that
+ * cannot allocate (code under HIP-graph capture, tight serving loops). No
+ * counterpart in the reference. The workspace lives in a static device array
+ * of q3_decode_attention_step_noalloc_max_bytes() bytes (32 MiB), one per GPU,
+ * held until the process ends; a request whose workspace
+ * (q3_decode_attention_workspace_bytes) exceeds it returns Q3_ERR_SCRATCH
+ * before touching the device. All calls on one GPU share the array: calls
+ * that may run at the same time on one GPU race (stream-ordered calls are
+ * safe; no call relies on its previous contents). The stream must belong to
+ * the current device. Makes no allocation of any kind. */
+int64_t q3_decode_attention_step_noalloc_max_bytes(void);
+int q3_decode_attention_step_noalloc(const void* q, const void* k_cache, const void* v_cache, int* kv_lens, void* o,
+                                     int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len,
+                                     const int64_t* strides, float scale, int dtype, void* stream);
 
 /* ---------------------------------------------------------------- MoE
  * Router of CudaSparseMoE.forward (modules/moe.py:60-65): softmax over the

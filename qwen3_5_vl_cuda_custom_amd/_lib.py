@@ -54,6 +54,9 @@ _SIGS: dict[str, tuple] = {
     "q3_decode_attention": (c_int, [_V, _V, _V, _i32p, _V, _I, _I, _I, _I, _I, _i64p, c_float, c_int, _V, _I, _V]),
     "q3_decode_attention_step": (c_int, [_V, _V, _V, _i32p, _V, _I, _I, _I, _I, _I, _i64p, c_float, c_int, _V, _I,
                                          _V]),
+    "q3_decode_attention_step_noalloc_max_bytes": (c_int64, []),
+    "q3_decode_attention_step_noalloc": (c_int, [_V, _V, _V, _i32p, _V, _I, _I, _I, _I, _I, _i64p, c_float, c_int,
+                                                 _V]),
     "q3_moe_route": (c_int, [_V, _i32p, _V, _f32p, _I, _I, _I, c_int, _V]),
     "q3_moe_experts_workspace_bytes": (c_int64, [_I, _I, _I, _I, _I]),
     "q3_moe_experts": (c_int, [_V, _V, _V, _i32p, _V, _V, _V, _I, _I, _I, _I, _I, _V, _I, _V]),

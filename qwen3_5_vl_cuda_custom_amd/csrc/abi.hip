@@ -21,6 +21,8 @@ const char* q3_error_string(int code) {
       return "request outside what the kernels cover";
     case Q3_ERR_WORKSPACE:
       return "workspace missing or too small";
+    case Q3_ERR_SCRATCH:
+      return "request needs more than the static scratch buffer of the allocation-free entry point";
     default:
       return code > 0 ? hipGetErrorString(static_cast<hipError_t>(code)) : "unknown q3 status";
   }

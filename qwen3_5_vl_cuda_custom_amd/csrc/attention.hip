@@ -19,6 +19,7 @@
 // KV head) pairs, one wave-private DMA ring per wave; the MFMA query columns
 // are the GQA group's heads (see the decode section below).
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "gemm_tile.h"
@@ -1169,6 +1170,17 @@ int64_t q3_decode_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, 
 
 namespace {
 
+// Whether decode_impl takes the MFMA split-K path (the one that uses the
+// workspace) for these arguments.
+bool dec_fast_path(const void* q, const void* k_cache, const void* v_cache, int64_t B, int64_t Hq, int64_t Hkv,
+                   int64_t D, int64_t max_len, const int64_t* strides, int dtype) {
+  const bool aligned = q3_aligned(q, 16) && q3_aligned(k_cache, 16) && q3_aligned(v_cache, 16) &&
+                       strides_aligned8(strides, 8);
+  // The MFMA path addresses the cache with 32-bit buffer offsets.
+  return dtype == Q3_BF16 && D == 128 && Hq / Hkv <= 32 && B <= kDecMaxBatch && aligned &&
+         (max_len + 1) * strides[4] * 2 < 0x7fffffffLL && (max_len + 1) * strides[7] * 2 < 0x7fffffffLL;
+}
+
 int decode_impl(const void* q, const void* k_cache, const void* v_cache, const int* kv_lens, int len_add,
                 int* lens_inc, void* o, int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len,
                 const int64_t* strides, float scale, int dtype, void* workspace, int64_t workspace_bytes,
@@ -1204,11 +1216,7 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
   p.kv_lens = kv_lens;
   p.len_add = len_add;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const bool aligned = q3_aligned(q, 16) && q3_aligned(k_cache, 16) && q3_aligned(v_cache, 16) &&
-                       strides_aligned8(strides, 8);
-  // The MFMA path addresses the cache with 32-bit buffer offsets.
-  if (dtype == Q3_BF16 && D == 128 && p.groups <= 32 && B <= kDecMaxBatch && aligned &&
-      (max_len + 1) * strides[4] * 2 < 0x7fffffffLL && (max_len + 1) * strides[7] * 2 < 0x7fffffffLL) {
+  if (dec_fast_path(q, k_cache, v_cache, B, Hq, Hkv, D, max_len, strides, dtype)) {
     Q3_REQUIRE(workspace != nullptr && workspace_bytes >= decode_ws_bytes(B, Hq, Hkv, max_len, D), Q3_ERR_WORKSPACE);
     Q3_REQUIRE(q3_aligned(workspace, 16), Q3_ERR_ALIGN);
     p.dec_hdr = static_cast<int*>(workspace);
@@ -1262,6 +1270,76 @@ int q3_decode_attention_step(const void* q, const void* k_cache, const void* v_c
                              float scale, int dtype, void* workspace, int64_t workspace_bytes, void* stream) {
   return decode_impl(q, k_cache, v_cache, kv_lens, 1, kv_lens, o, B, Hq, Hkv, D, max_len, strides, scale, dtype,
                      workspace, workspace_bytes, stream);
+}
+
+}  // extern "C"
+
+// ----------------------------------------------------------------- allocation-free decode step
+// The decode step's workspace (unit-prefix header + split-K records) in a
+// static device array instead of a caller allocation. Every GPU the library
+// runs on holds its own copy for the life of the process; calls on one GPU
+// share it, so calls that overlap in time on one GPU race (stream-ordered
+// calls are fine: each call writes every byte it reads before reading it, so
+// nothing needs clearing between calls).
+namespace {
+
+constexpr int64_t kDecScratchBytes = 32ll << 20;
+constexpr int kScratchMaxDevices = 64;
+
+static __device__ __align__(256) unsigned char scratch[kDecScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchMaxDevices] = {};
+
+// The device address of `scratch` on the current device (looked up once per
+// device, with that device current): host code never passes the symbol
+// itself, which names a host-side shadow, to a kernel.
+int scratch_for_current_device(void* stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (stream) {
+    int sdev = -1;
+    e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev);
+    if (e != hipSuccess) return (int)e;
+    if (sdev != dev) return Q3_ERR_UNSUPPORTED;  // the stream must belong to the current device
+  }
+  if (dev < 0 || dev >= kScratchMaxDevices) return Q3_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!ptr) return (int)hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return Q3_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t q3_decode_attention_step_noalloc_max_bytes(void) { return kDecScratchBytes; }
+
+int q3_decode_attention_step_noalloc(const void* q, const void* k_cache, const void* v_cache, int* kv_lens, void* o,
+                                     int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len,
+                                     const int64_t* strides, float scale, int dtype, void* stream) {
+  Q3_REQUIRE(q && k_cache && v_cache && kv_lens && o && strides, Q3_ERR_NULL);
+  Q3_REQUIRE(B >= 0 && Hq >= 1 && Hkv >= 1 && Hq % Hkv == 0 && D >= 1 && max_len >= 1, Q3_ERR_SHAPE);
+  if (B == 0) return Q3_OK;
+  // Sizes whose workspace would not fit the static array are refused before
+  // anything touches the device.
+  const bool fast = dec_fast_path(q, k_cache, v_cache, B, Hq, Hkv, D, max_len, strides, dtype);
+  Q3_REQUIRE(!fast || decode_ws_bytes(B, Hq, Hkv, max_len, D) <= kDecScratchBytes, Q3_ERR_SCRATCH);
+  void* ws = nullptr;
+  if (fast) {
+    const int rc = scratch_for_current_device(stream, &ws);
+    if (rc != Q3_OK) return rc;
+  }
+  return decode_impl(q, k_cache, v_cache, kv_lens, 1, kv_lens, o, B, Hq, Hkv, D, max_len, strides, scale, dtype,
+                     ws, fast ? kDecScratchBytes : 0, stream);
 }
 
 }  // extern "C"

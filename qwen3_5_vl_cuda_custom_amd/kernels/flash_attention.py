@@ -39,7 +39,7 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: fl
 
 def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, kv_lens: torch.Tensor,
                      scale: float, *, out: torch.Tensor | None = None, max_len: int | None = None,
-                     append: bool = False) -> torch.Tensor:
+                     append: bool = False, noalloc: bool = False) -> torch.Tensor:
     """One query token per sequence over a ragged KV cache (split-K flash decoding).
 
     q (B, Hq, D) (or (B, Hq, 1, D)); k_cache/v_cache (B, Hkv, cap, D); kv_lens
@@ -49,6 +49,10 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     append=True is the decode step with the new token's row already at cache
     row kv_lens[b]: sequence b attends to kv_lens[b] + 1 rows and kv_lens is
     then incremented in place (stream-ordered, no host synchronisation).
+    noalloc=True (with append=True, and `out` given) runs the step with the
+    library's static per-GPU scratch instead of a workspace tensor: no
+    allocation at all, for code that cannot allocate; calls overlapping in
+    time on one GPU must not use it.
     """
     check("decode_attention", q, k_cache, v_cache)
     if q.dim() == 4:
@@ -57,8 +61,17 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     Hkv, cap = k_cache.shape[1], k_cache.shape[2]
     if kv_lens.dtype != torch.int32 or not kv_lens.is_cuda or kv_lens.shape != (B,) or kv_lens.stride(0) != 1:
         raise ValueError("decode_attention: kv_lens must be a contiguous int32 (B,) device tensor")
-    o = out if out is not None else torch.empty((B, Hq, D), dtype=q.dtype, device=q.device)
     ml = int(max_len) if max_len is not None else cap
+    strides = (q.stride(0), q.stride(1), *_s4(k_cache), *_s4(v_cache))
+    if noalloc:
+        if not append or out is None:
+            raise ValueError("decode_attention: noalloc=True is the decode step (append=True) into a given `out`")
+        _lib.call("q3_decode_attention_step_noalloc", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                  kv_lens.data_ptr(), out.data_ptr(), B, Hq, Hkv, D, ml,
+                  _lib.i64s(*strides, out.stride(0), out.stride(1)), float(scale), _lib.dtype_code(q.dtype),
+                  _lib.stream())
+        return out
+    o = out if out is not None else torch.empty((B, Hq, D), dtype=q.dtype, device=q.device)
     ws, nws = _lib.workspace(_lib.lib().q3_decode_attention_workspace_bytes(B, Hq, Hkv, ml, D), q.device)
     _lib.call("q3_decode_attention_step" if append else "q3_decode_attention", q.data_ptr(), k_cache.data_ptr(),
               v_cache.data_ptr(), kv_lens.data_ptr(),

@@ -137,6 +137,16 @@ def test_attention_validation():
     assert L.q3_decode_attention_workspace_bytes(32, 32, 8, 8193, 128) == 4352 + (1024 + 32 * 8) * 4 * 130 * 4
     assert L.q3_decode_attention_step(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 8, 2, 128, 100, d, 0.1, 1, None, 0, None) == -6
     assert L.q3_decode_attention_step(FAKE, FAKE, FAKE, None, FAKE, 2, 8, 2, 128, 100, d, 0.1, 1, None, 0, None) == -1
+    # the allocation-free step: requests whose workspace exceeds its static array are refused on the host
+    assert L.q3_decode_attention_step_noalloc_max_bytes() == 32 << 20
+    big = _lib.i64s(*([128] * 10))
+    assert L.q3_decode_attention_step_noalloc(FAKE, FAKE, FAKE, FAKE, FAKE, 1024, 1024, 32, 128, 64, big, 0.1, 1,
+                                              None) == -7
+    assert L.q3_decode_attention_step_noalloc(FAKE, FAKE, FAKE, None, FAKE, 2, 8, 2, 128, 100, d, 0.1, 1,
+                                              None) == -1
+    assert L.q3_decode_attention_step_noalloc(FAKE, FAKE, FAKE, FAKE, FAKE, 0, 8, 2, 128, 100, d, 0.1, 1,
+                                              None) == 0  # empty batch: no-op
+    assert "scratch" in _lib.error_string(-7)
     # prefill chunk over a cache: lengths are required, and the chunk must fit the capacity
     assert L.q3_flash_attention_cache(FAKE, FAKE, FAKE, None, FAKE, 2, 8, 2, 16, 100, 128, st, 0.1, 1, 1, None) == -1
     assert L.q3_flash_attention_cache(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 8, 2, 101, 100, 128, st, 0.1, 1, 1,
