@@ -33,12 +33,8 @@ HIPFLAGS = [
 ]
 
 
-# Per-source extra flags. gemv.hip: thread 0's tile-counter increments must not
-# be rewritten into wave-combined atomics, whose result the compiler then waits
-# for at once (that wait would drain the kernel's in-flight DMA ring).
-EXTRA_FLAGS = {
-    "gemv.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
-}
+# Per-source extra flags (none at present).
+EXTRA_FLAGS: dict[str, list[str]] = {}
 
 
 def _hipcc() -> str:

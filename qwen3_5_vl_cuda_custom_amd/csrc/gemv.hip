@@ -242,10 +242,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
         for (int i = 0; i < kBatch; ++i) {
           const uint32_t o =
               pc0 + i < npieces ? (uint32_t)(((pc0 + i) * kGvPiece + m * kGvBN + nng) * 4) : kOOB - 256;
-          ld[i][0] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o, 0, 16));
-          ld[i][1] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o + 16, 0, 16));
-          ld[i][2] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o + 128, 0, 16));
-          ld[i][3] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o + 144, 0, 16));
+          ld[i][0] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o, 0, 0));
+          ld[i][1] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o + 16, 0, 0));
+          ld[i][2] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o + 128, 0, 0));
+          ld[i][3] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o + 144, 0, 0));
         }
 #pragma unroll
         for (int i = 0; i < kBatch; ++i) {
@@ -282,7 +282,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
               pc0 + i < npieces ? (uint32_t)(((pc0 + i) * kGvPiece + m * kGvBN + nn0) * 4) : kOOB - 256;
 #pragma unroll
           for (int q = 0; q < 4; ++q)
-            ld[i][q] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o + 16 * q, 0, 16));
+            ld[i][q] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, o + 16 * q, 0, 0));
         }
 #pragma unroll
         for (int i = 0; i < kBatch; ++i)
@@ -329,8 +329,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
   };
 
   // Split tiles this block contributes to (at most its first and its last).
-  int np_ = 0, ninc = 0;
-  int pt0 = 0, pt1 = 0, pn0 = 0, pn1 = 0, pu0 = 0;
+  int np_ = 0;
+  int pt0 = 0, pt1 = 0, pn0 = 0, pn1 = 0;
   int old0 = 0, old1 = 0;  // counter values returned to thread 0
   auto bump = [&](int idx) {
     if (tid == 0) {
@@ -348,12 +348,6 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
   for (int u = u0; u < u1; ++u) {
     vm_wait<(NST - 2) * kGvPerWave>();  // this wave's DMAs of stage u have landed
     __syncthreads();                     // ... and every wave's; slot (u - 1) % NST is free
-    // The piece stored at iteration pu0 preceded the DMAs issued from
-    // iteration pu0 + 1 on, so the wait above has retired it once u >= pu0 + NST.
-    if (ninc == 0 && np_ > 0 && u >= pu0 + NST) {
-      bump(0);
-      ninc = 1;
-    }
     issue(u + NST - 1);
     const bf16* st = ring + (u % NST) * kGvStage;
     const int ra = 32 * wave + l32, rb = kGvBN + l32;
@@ -379,12 +373,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
           const int nn = 32 * wave + 8 * g + 4 * h;
           const floatx4 v = {acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]};
           __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rp,
-                                                 (uint32_t)((piece * kGvPiece + l32 * kGvBN + nn) * 4), 0, 16);
+                                                 (uint32_t)((piece * kGvPiece + l32 * kGvBN + nn) * 4), 0, 0);
         }
         if (np_ == 0) {
           pt0 = t;
           pn0 = lb - fb + 1;
-          pu0 = u;
         } else {
           pt1 = t;
           pn1 = lb - fb + 1;
@@ -395,16 +388,23 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
     }
   }
 
-  vm_wait<0>();  // every piece store of this wave has completed
+  // Cross-block hand-off of a split tile: every thread's piece stores are
+  // released at agent scope (the fence writes them back past this XCD's L2)
+  // before the barrier, so they are visible device-wide before thread 0
+  // counts the block's arrival; the block that brings a tile's count to its
+  // piece total reads the pieces only after an agent-scope acquire fence
+  // (which invalidates stale cached lines). The counters themselves are
+  // device-scope atomics.
+  __threadfence();
   __syncthreads();
-  if (ninc == 0 && np_ > 0) bump(0);
+  if (np_ > 0) bump(0);
   if (np_ > 1) bump(1);
   if (tid == 0) {
-    vm_wait<0>();
     s_last[0] = np_ > 0 && old0 == pn0 - 1;
     s_last[1] = np_ > 1 && old1 == pn1 - 1;
   }
   __syncthreads();
+  if (s_last[0] || s_last[1]) __threadfence();
   if (s_last[0]) {
     reduce_tile(pt0, pn0);
     if (tid == 0) __hip_atomic_store(&p.counters[pt0], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
