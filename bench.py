@@ -159,7 +159,7 @@ def parity_leg(cases: dict) -> dict:
                          # the test bar: no worse than the reference bf16 path, up to
                          # equal-rounding ties (2% of mean-rel, one bf16 ulp of the worst element)
                          "within_ref_bf16": (ma <= max(2e-2, ema + ulp_at_worst(gpu_out, ref))
-                                             and mr <= emr * 1.02 and mr <= 5e-3)}
+                                             and mr <= emr * 1.02 and (mr <= 5e-3 or emr > 5e-3))}
             log(f"parity {name}: {res[name]} ({time.perf_counter() - t0:.1f} s)")
     finally:
         torch.set_num_threads(prev)

@@ -82,6 +82,13 @@ int q3_matmul_swiglu(const void* x, const void* w_gate, const void* w_up, void* 
                      int64_t ldx, int64_t ldw, int64_t ldc, int dtype, void* workspace, int64_t workspace_bytes,
                      void* stream);
 
+/* y = gelu_tanh(x . w^T + bias): the fc1 projection and gelu_tanh_forward
+ * (csrc/gelu_tanh_op.cpp:7) of CudaVisionMLP (modules/mlp.py:33-34) and of
+ * CudaVisionPatchMerger (modules/vision_patch.py:68) in one GEMM, the
+ * activation applied in fp32 before the single rounding. bias may be null. */
+int q3_matmul_gelu(const void* x, const void* w, const void* bias, void* y, int64_t M, int64_t N, int64_t K,
+                   int64_t ldx, int64_t ldw, int64_t ldc, int dtype, void* stream);
+
 /* Decode-shaped (1 <= M <= 32 rows, bf16) RMSNorm fused into the projection
  * that consumes it: y = rmsnorm(x; norm_w, eps) . w^T, per segment (+ bias),
  * or silu(. w_gate) * (. w_up). The rows are normalised as X is staged into
@@ -171,6 +178,17 @@ int q3_flash_attention(const void* q, const void* k, const void* v, void* o, flo
                        int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D, const int64_t* strides, float scale,
                        int is_causal, int dtype, void* stream);
 
+/* Attention over packed variable-length sequences (the vision tower's images,
+ * each attending only within itself: HF's cu_seqlens form of the attention
+ * the reference runs over one concatenated sequence, models/common.py:198).
+ * q/k/v/o are (H, total, D) views with strides = [qh, qs, kh, ks, vh, vs, oh,
+ * os]; sequence b is rows [cu_seqlens[b], cu_seqlens[b + 1]) (n_seqs + 1
+ * int32 on the device, cu_seqlens[0] = 0, last = total); max_seqlen >= every
+ * sequence's length. is_causal applies within each sequence. */
+int q3_flash_attention_varlen(const void* q, const void* k, const void* v, void* o, const int* cu_seqlens,
+                              int64_t n_seqs, int64_t total, int64_t max_seqlen, int64_t Hq, int64_t Hkv, int64_t D,
+                              const int64_t* strides, float scale, int is_causal, int dtype, void* stream);
+
 /* A prefill chunk of Sq tokens per sequence over a ragged KV cache: the
  * S > 1 case of CudaFullAttention.forward with a cache
  * (modules/attention.py:89-96) without the torch.cat growth. k/v cache
@@ -220,6 +238,36 @@ int64_t q3_decode_attention_step_noalloc_max_bytes(void);
 int q3_decode_attention_step_noalloc(const void* q, const void* k_cache, const void* v_cache, int* kv_lens, void* o,
                                      int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len,
                                      const int64_t* strides, float scale, int dtype, void* stream);
+
+/* ---------------------------------------------------------------- model edges and vision-tower glue
+ * q3_embedding replaces embedding_forward(Tensor ids, Tensor weight)
+ * (csrc/embedding_op.cpp, csrc/embedding_op.cu:40-70, kernels/embedding.py):
+ * out (n, dim) = weight[ids] for int64 ids; an id outside [0, rows) gives a
+ * zero row and sets bit 0 of *status (a device int32, or null).
+ *
+ * Images are described by an (n_img, 4) int32 table of (t, h, w, first token)
+ * in patch units (first token = running sum of t*h*w), passed both on the
+ * device (`images`, read by the kernel) and on the host (`images_host`,
+ * validated before any launch: h and w multiples of `merge`, consistent
+ * first tokens). Tokens of an image are frame-major, then merge blocks of
+ * merge x merge patches row-major, then the patches of a block row-major (the
+ * Qwen2/3-VL processor's order).
+ * q3_vision_rope_tables replaces CudaVisionTower._rot_pos_emb and the cos/sin
+ * of its forward (models/common.py:85-120, 192-195): cos/sin (total, head_dim)
+ * fp32 with angles row * inv_freq[j] (j < head_dim/4) and col * inv_freq[j -
+ * head_dim/4] (j < head_dim/2), repeated over both halves; inv_freq (head_dim/4)
+ * fp32 on the device.
+ * q3_vision_pos_embed replaces CudaVisionTower._fast_pos_embed_interpolate and
+ * the add that follows it (models/common.py:122-174, 180-181): y = x +
+ * bilinear(table) with table (grid_side^2, hidden), coordinates
+ * linspace(0, grid_side - 1, h or w) per image; x and y (total, hidden) may
+ * alias. */
+int q3_embedding(const int64_t* ids, const void* weight, void* out, int64_t n, int64_t rows, int64_t dim, int dtype,
+                 int* status, void* stream);
+int q3_vision_rope_tables(const int* images, const int* images_host, int64_t n_img, int64_t merge, int64_t head_dim,
+                          const float* inv_freq, float* cos_out, float* sin_out, void* stream);
+int q3_vision_pos_embed(const int* images, const int* images_host, int64_t n_img, int64_t merge, int64_t grid_side,
+                        const void* table, const void* x, void* y, int64_t hidden, int dtype, void* stream);
 
 /* ---------------------------------------------------------------- MoE
  * Router of CudaSparseMoE.forward (modules/moe.py:60-65): softmax over the

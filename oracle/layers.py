@@ -181,3 +181,116 @@ def vision_rope_tables(grid_thw, head_dim: int, theta: float = 10000.0, merge: i
     rot = table[pos].flatten(1)
     emb = torch.cat((rot, rot), dim=-1)
     return emb.cos(), emb.sin()
+
+
+def patch_merger(x, p, *, merge: int, postshuffle: bool, prefix: str = "", eps: float = 1e-6, rd=_ident):
+    """CudaVisionPatchMerger.forward, modules/vision_patch.py:58-68: LayerNorm (over the patch
+    hidden, or over merge^2 patches when postshuffle), rows of merge^2 tokens, fc1, gelu_tanh, fc2."""
+    mh = x.shape[-1] * merge * merge if not postshuffle else p[prefix + "norm.weight"].shape[0]
+    if postshuffle:
+        x = rd(ops.layernorm(x.reshape(-1, mh), p[prefix + "norm.weight"], p[prefix + "norm.bias"], eps))
+    else:
+        x = rd(ops.layernorm(x, p[prefix + "norm.weight"], p[prefix + "norm.bias"], eps)).reshape(-1, mh)
+    h = rd(ops.gelu_tanh(rd(ops.linear(x, p[prefix + "linear_fc1.weight"], p[prefix + "linear_fc1.bias"]))))
+    return rd(ops.linear(h, p[prefix + "linear_fc2.weight"], p[prefix + "linear_fc2.bias"]))
+
+
+def pos_embed_interpolate(table, grid_thw, merge: int):
+    """CudaVisionTower._fast_pos_embed_interpolate, models/common.py:122-174, in fp32.
+
+    Per image: coordinates linspace(0, G-1, h) x linspace(0, G-1, w) on the
+    G x G learned grid, bilinear weights over floor / clipped floor+1, the
+    weighted sum of the four table rows, repeated over the t frames and
+    permuted to the merge-block token order. Returns (total, hidden).
+    """
+    G = int(round(table.shape[0] ** 0.5))
+    out = []
+    for t, h, w in grid_thw:
+        hi = torch.linspace(0, G - 1, h)
+        wi = torch.linspace(0, G - 1, w)
+        hf, wf = hi.int(), wi.int()
+        hc, wc = (hf + 1).clip(max=G - 1), (wf + 1).clip(max=G - 1)
+        dh, dw = hi - hf, wi - wf
+        rows = lambda a, b: table[(a[:, None] * G + b[None, :]).reshape(-1).long()]  # noqa: E731
+        emb = (rows(hf, wf) * ((1 - dh)[:, None] * (1 - dw)[None, :]).reshape(-1, 1)
+               + rows(hf, wc) * ((1 - dh)[:, None] * dw[None, :]).reshape(-1, 1)
+               + rows(hc, wf) * (dh[:, None] * (1 - dw)[None, :]).reshape(-1, 1)
+               + rows(hc, wc) * (dh[:, None] * dw[None, :]).reshape(-1, 1))
+        emb = emb.repeat(t, 1).view(t, h // merge, merge, w // merge, merge, -1).permute(0, 1, 3, 2, 4, 5)
+        out.append(emb.reshape(t * h * w, -1))
+    return torch.cat(out)
+
+
+def vision_tower(patches, p, grid_thw, *, num_heads: int, merge: int, in_channels: int, temporal: int, patch: int,
+                 theta: float = 10000.0, eps: float = 1e-6, deepstack_layers=(), per_frame: bool = True, rd=_ident):
+    """CudaVisionTower.forward, models/common.py:176-212: patch embed + interpolated position
+    embedding, 2D rotary tables, the blocks, deepstack mergers after the listed blocks, the merger.
+
+    per_frame=True: every frame of every image attends only within itself (HF's
+    cu_seqlens attention); per_frame=False: one sequence over all images, as the
+    reference's forward runs it (models/common.py:198). Returns (pooler_output,
+    last_hidden_state, [deepstack features]).
+    """
+    grids = [tuple(int(v) for v in g) for g in grid_thw]
+    x = rd(patch_embed(patches, p["patch_embed.weight"], p["patch_embed.bias"], in_channels, temporal, patch))
+    x = rd(x + pos_embed_interpolate(p["pos_embed.emb.weight"], grids, merge))
+    hd = x.shape[-1] // num_heads
+    cos, sin = vision_rope_tables(grids, hd, theta, merge)
+    lens = [h * w for t, h, w in grids for _ in range(t)] if per_frame else [x.shape[0]]
+    bounds = [0]
+    for n in lens:
+        bounds.append(bounds[-1] + n)
+    deep = []
+    for i in range(len({k.split(".")[1] for k in p if k.startswith("blocks.")})):
+        bp = {k[len(f"blocks.{i}."):]: v for k, v in p.items() if k.startswith(f"blocks.{i}.")}
+        x = torch.cat([vision_block(x[None, a:b], bp, num_heads=num_heads, cos=cos[a:b], sin=sin[a:b], eps=eps,
+                                    rd=rd)[0] for a, b in zip(bounds[:-1], bounds[1:])])
+        if i in deepstack_layers:
+            j = list(deepstack_layers).index(i)
+            deep.append(patch_merger(x, p, merge=merge, postshuffle=True, prefix=f"deepstack_mergers.{j}.", rd=rd))
+    return patch_merger(x, p, merge=merge, postshuffle=False, prefix="merger.", rd=rd), x, deep
+
+
+def text_model(x_embeds, p, *, num_heads, num_kv_heads, head_dim, eps, theta, mrope_section, positions,
+               past_kvs=None, visual_pos_masks=None, deepstack_embeds=None, use_moe=None, top_k=0, rd=_ident):
+    """CudaQwen3VLDenseModel._text_forward + lm_head, models/dense.py:57-75, 115-118: the layers
+    (past_kv each), deepstack adds after the first layers, the final RMSNorm, lm_head.
+    p holds the model's text parameters ("layers.N.*", "norm.weight", "lm_head.weight").
+    Returns (logits, [(k, v)] per layer)."""
+    n_layers = len({k.split(".")[1] for k in p if k.startswith("layers.")})
+    cos3, sin3 = ops.mrope_cos_sin(positions, head_dim, theta)
+    x, kvs = x_embeds, []
+    n_ds = len(deepstack_embeds) if deepstack_embeds is not None else 0
+    for i in range(n_layers):
+        lp = {k[len(f"layers.{i}."):]: v for k, v in p.items() if k.startswith(f"layers.{i}.")}
+        moe = use_moe(i) if use_moe is not None else False
+        x, _, kv = text_decoder_layer(x, lp, num_heads=num_heads, num_kv_heads=num_kv_heads, head_dim=head_dim,
+                                      eps=eps, cos_3d=cos3, sin_3d=sin3, mrope_section=mrope_section, use_moe=moe,
+                                      top_k=top_k, past_kv=past_kvs[i] if past_kvs is not None else None, rd=rd)
+        kvs.append(kv)
+        if visual_pos_masks is not None and i < n_ds:
+            x = x.clone()
+            x[visual_pos_masks] = rd(x[visual_pos_masks] + deepstack_embeds[i])
+    h = rd(ops.rmsnorm(x, p["norm.weight"], eps))
+    return rd(ops.linear(h, p["lm_head.weight"])), kvs
+
+
+def greedy_generate(input_ids, p, *, max_new_tokens, num_heads, num_kv_heads, head_dim, eps, theta, mrope_section,
+                    rd=_ident):
+    """CudaQwen3VLDenseModel.generate, models/dense.py:123-162: prefill, then one token at a time
+    with the grown (k, v) caches at position past_len, argmax of the last logits.
+    Returns (B, S + max_new_tokens) token ids."""
+    B, S = input_ids.shape
+    kw = dict(num_heads=num_heads, num_kv_heads=num_kv_heads, head_dim=head_dim, eps=eps, theta=theta,
+              mrope_section=mrope_section, rd=rd)
+    pos = torch.arange(S).view(1, 1, S).expand(3, B, S)
+    logits, kvs = text_model(p["embed_tokens.weight"][input_ids], p, positions=pos, **kw)
+    tok = logits[:, -1].argmax(-1, keepdim=True)
+    out = torch.cat([input_ids, tok], dim=1)
+    for _ in range(max_new_tokens - 1):
+        past = kvs[0][0].shape[2]
+        pos = torch.full((3, B, 1), past)
+        logits, kvs = text_model(p["embed_tokens.weight"][tok], p, positions=pos, past_kvs=kvs, **kw)
+        tok = logits[:, -1].argmax(-1, keepdim=True)
+        out = torch.cat([out, tok], dim=1)
+    return out

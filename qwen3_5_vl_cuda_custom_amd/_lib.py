@@ -30,6 +30,7 @@ _SIGS: dict[str, tuple] = {
     "q3_matmul_workspace_bytes": (c_int64, [_I, _I, _I, c_int, c_int]),
     "q3_matmul": (c_int, [_V, _V, _V, _V, _V, _I, _I, _I, _I, _I, _I, _I, c_int, _V, _I, _V]),
     "q3_matmul_swiglu": (c_int, [_V, _V, _V, _V, _I, _I, _I, _I, _I, _I, c_int, _V, _I, _V]),
+    "q3_matmul_gelu": (c_int, [_V, _V, _V, _V, _I, _I, _I, _I, _I, _I, c_int, _V]),
     "q3_matmul_segments_workspace_bytes": (c_int64, [_I, _i64p, _I, _I, c_int]),
     "q3_matmul_segments": (c_int, [_V, _V, _V, _i64p, _I, _V, _I, _I, _I, _I, _I, c_int, _V, _I, _V]),
     "q3_rmsnorm_matmul_segments": (c_int, [_V, _V, c_float, _V, _V, _i64p, _I, _V, _I, _I, _I, _I, _I, c_int, _V]),
@@ -48,6 +49,8 @@ _SIGS: dict[str, tuple] = {
                                 _i64p, c_float, _i64p, c_int, _V]),
     "q3_flash_attention": (c_int, [_V, _V, _V, _V, _f32p, _I, _I, _I, _I, _I, _I, _i64p, c_float, c_int, c_int,
                                    _V]),
+    "q3_flash_attention_varlen": (c_int, [_V, _V, _V, _V, _i32p, _I, _I, _I, _I, _I, _I, _i64p, c_float, c_int,
+                                          c_int, _V]),
     "q3_flash_attention_cache": (c_int, [_V, _V, _V, _i32p, _V, _I, _I, _I, _I, _I, _I, _i64p, c_float, c_int,
                                          c_int, _V]),
     "q3_decode_attention_workspace_bytes": (c_int64, [_I, _I, _I, _I, _I]),
@@ -57,6 +60,9 @@ _SIGS: dict[str, tuple] = {
     "q3_decode_attention_step_noalloc_max_bytes": (c_int64, []),
     "q3_decode_attention_step_noalloc": (c_int, [_V, _V, _V, _i32p, _V, _I, _I, _I, _I, _I, _i64p, c_float, c_int,
                                                  _V]),
+    "q3_embedding": (c_int, [_V, _V, _V, _I, _I, _I, c_int, _i32p, _V]),
+    "q3_vision_rope_tables": (c_int, [_i32p, _i32p, _I, _I, _I, _f32p, _f32p, _f32p, _V]),
+    "q3_vision_pos_embed": (c_int, [_i32p, _i32p, _I, _I, _I, _V, _V, _V, _I, c_int, _V]),
     "q3_moe_route": (c_int, [_V, _i32p, _V, _f32p, _I, _I, _I, c_int, _V]),
     "q3_moe_experts_workspace_bytes": (c_int64, [_I, _I, _I, _I, _I]),
     "q3_moe_experts": (c_int, [_V, _V, _V, _i32p, _V, _V, _V, _I, _I, _I, _I, _I, _V, _I, _V]),

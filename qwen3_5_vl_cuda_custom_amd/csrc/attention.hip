@@ -53,6 +53,10 @@ struct AttnParams {
   // sees keys [0, q_off[b] + i] (causal) and the sequence has q_off[b] + Sq
   // keys (clamped to Sk). Null: offset 0, Sk keys.
   const int* q_off;
+  // packed variable-length sequences (vision tower): sequence b is rows
+  // [cu_seqlens[b], cu_seqlens[b + 1]) of one packed (H, total, D) tensor for
+  // q, k, v and o alike (the batch strides are unused); Sq = Sk = max length.
+  const int* cu_seqlens;
   int* lens_inc;    // decode: if set, lens_inc[b] += 1 once the step has read the lengths
   int* dec_hdr;     // decode workspace header: unit prefix over sequences (B + 1 ints)
   int dec_waves;    // decode: waves in the main kernel's grid
@@ -120,25 +124,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int b = yb / p.Hkv;
   const int hq = kvh * p.groups + hg * WH + wh;
 
+  // Packed sequences: this block's sequence starts at row `row0` of every
+  // tensor and has Sq = Sk = its own length; tiles past it have nothing to do.
+  int64_t qb_off = (int64_t)b * p.qb, kb_off = (int64_t)b * p.kb, vb_off = (int64_t)b * p.vb,
+          ob_off = (int64_t)b * p.ob;
+  int Sq = p.Sq, Sk = p.Sk;
+  if (p.cu_seqlens) {
+    const int row0 = __builtin_amdgcn_readfirstlane(p.cu_seqlens[b]);
+    Sq = Sk = __builtin_amdgcn_readfirstlane(p.cu_seqlens[b + 1]) - row0;
+    qb_off = (int64_t)row0 * p.qs;
+    kb_off = (int64_t)row0 * p.ks;
+    vb_off = (int64_t)row0 * p.vs;
+    ob_off = (int64_t)row0 * p.os;
+    if (qt * QB >= Sq) return;  // uniform over the block
+  }
+
   const int q0 = qt * QB + wq * 32;
   const int qidx = q0 + l32;
-  const int qend_block = min(p.Sq, qt * QB + QB);
+  const int qend_block = min(Sq, qt * QB + QB);
   const int off = p.q_off ? __builtin_amdgcn_readfirstlane(max(p.q_off[b], 0)) : 0;
-  const int Skb = p.q_off ? min(p.Sk, off + p.Sq) : p.Sk;  // keys of this sequence
+  const int Skb = p.q_off ? min(Sk, off + Sq) : Sk;  // keys of this sequence
   const int klimit = p.causal ? min(Skb, qend_block + off) : Skb;
   const int nkt = (klimit + kKT - 1) / kKT;
 
-  const bf16* kbase = p.k + (int64_t)b * p.kb + (int64_t)kvh * p.kh;
-  const bf16* vbase = p.v + (int64_t)b * p.vb + (int64_t)kvh * p.vh;
+  const bf16* kbase = p.k + kb_off + (int64_t)kvh * p.kh;
+  const bf16* vbase = p.v + vb_off + (int64_t)kvh * p.vh;
   const int ks2 = (int)p.ks * 2;  // host guarantees Sk * ks * 2 < 2^31
-  const __amdgpu_buffer_rsrc_t krs = q3::make_rsrc(kbase, (int64_t)(p.Sk - 1) * ks2 + D * 2);
+  const __amdgpu_buffer_rsrc_t krs = q3::make_rsrc(kbase, (int64_t)(Sk - 1) * ks2 + D * 2);
   (void)VCH;
 
   // Q fragments (B operand): lane supplies Q[qidx][16 ks + 8 h .. +7].
   bf16x8 qf[KSTEPS];
   {
-    const bf16* qrow = p.q + (int64_t)b * p.qb + (int64_t)hq * p.qh + (int64_t)qidx * p.qs;
-    const bool ok = qidx < p.Sq;
+    const bf16* qrow = p.q + qb_off + (int64_t)hq * p.qh + (int64_t)qidx * p.qs;
+    const bool ok = qidx < Sq;
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks)
       qf[ks] = (ok && ks * 16 + 8 * h < D) ? *reinterpret_cast<const bf16x8*>(qrow + ks * 16 + 8 * h) : bf16x8{};
@@ -194,7 +213,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   q3::vm_wait<0>();
   __syncthreads();
 
-  const int wave_last_q = min(q0 + 31, p.Sq - 1);
+  const int wave_last_q = min(q0 + 31, Sq - 1);
   const float c = p.scale_log2;
   for (int kt = 0; kt < nkt; ++kt) {
     const int cur = kt & 1;
@@ -204,7 +223,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       load_v(kt + 1);
     }
     const int k0 = kt * kKT;
-    if (q0 < p.Sq && (!p.causal || k0 <= wave_last_q + off)) {
+    if (q0 < Sq && (!p.causal || k0 <= wave_last_q + off)) {
       const bf16* sKc = sK[cur];
       const bf16* sVc = sV[cur];
       floatx16 s0 = floatx16{}, s1 = floatx16{};
@@ -263,10 +282,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     __syncthreads();
   }
 
-  if (qidx >= p.Sq) return;
+  if (qidx >= Sq) return;
   const float l = lpart + __shfl_xor(lpart, 32, 64);
   const float inv_l = l > 0.f ? 1.0f / l : 0.f;
-  bf16* orow = p.o + (int64_t)b * p.ob + (int64_t)hq * p.oh + (int64_t)qidx * p.os;
+  bf16* orow = p.o + ob_off + (int64_t)hq * p.oh + (int64_t)qidx * p.os;
 #pragma unroll
   for (int t = 0; t < OT; ++t)
 #pragma unroll
@@ -279,7 +298,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         *reinterpret_cast<bf16x4*>(orow + d) = v4;
       }
     }
-  if (p.lse && h == 0) {
+  if (p.lse && h == 0) {  // (never with packed sequences)
     p.lse[((int64_t)b * p.Hq + hq) * p.Sq + qidx] = (m + log2f(l)) * 0.6931471805599453f;
   }
 }
@@ -971,11 +990,23 @@ __global__ __launch_bounds__(128) void flash_generic_kernel(const AttnParams p, 
   const int hq = (int)((row / p.Sq) % p.Hq);
   const int b = (int)(row / ((int64_t)p.Sq * p.Hq));
   const int kvh = hq / p.groups;
-  const T* q = reinterpret_cast<const T*>(p.q) + (int64_t)b * p.qb + (int64_t)hq * p.qh + (int64_t)i * p.qs;
-  const T* kb = reinterpret_cast<const T*>(p.k) + (int64_t)b * p.kb + (int64_t)kvh * p.kh;
-  const T* vb = reinterpret_cast<const T*>(p.v) + (int64_t)b * p.vb + (int64_t)kvh * p.vh;
+  int64_t qb_off = (int64_t)b * p.qb, kb_off = (int64_t)b * p.kb, vb_off = (int64_t)b * p.vb,
+          ob_off = (int64_t)b * p.ob;
+  int Sk = p.Sk;
+  if (p.cu_seqlens) {  // packed sequences: row i of sequence b is packed row cu_seqlens[b] + i
+    const int row0 = p.cu_seqlens[b];
+    Sk = p.cu_seqlens[b + 1] - row0;
+    if (i >= Sk) return;
+    qb_off = (int64_t)row0 * p.qs;
+    kb_off = (int64_t)row0 * p.ks;
+    vb_off = (int64_t)row0 * p.vs;
+    ob_off = (int64_t)row0 * p.os;
+  }
+  const T* q = reinterpret_cast<const T*>(p.q) + qb_off + (int64_t)hq * p.qh + (int64_t)i * p.qs;
+  const T* kb = reinterpret_cast<const T*>(p.k) + kb_off + (int64_t)kvh * p.kh;
+  const T* vb = reinterpret_cast<const T*>(p.v) + vb_off + (int64_t)kvh * p.vh;
   const int off = p.q_off ? max(p.q_off[b], 0) : 0;
-  int nk = kv_lens ? min(kv_lens[b] + p.len_add, p.Sk) : (p.q_off ? min(p.Sk, off + p.Sq) : p.Sk);
+  int nk = kv_lens ? min(kv_lens[b] + p.len_add, Sk) : (p.q_off ? min(Sk, off + p.Sq) : Sk);
   if (p.causal) nk = min(nk, i + off + 1);
   float acc[256];
   for (int d = 0; d < D; ++d) acc[d] = 0.f;
@@ -994,7 +1025,7 @@ __global__ __launch_bounds__(128) void flash_generic_kernel(const AttnParams p, 
     for (int d = 0; d < D; ++d) acc[d] = acc[d] * a + e * to_f<T>(vr[d]);
     m = mn;
   }
-  T* o = reinterpret_cast<T*>(p.o) + (int64_t)b * p.ob + (int64_t)hq * p.oh + (int64_t)i * p.os;
+  T* o = reinterpret_cast<T*>(p.o) + ob_off + (int64_t)hq * p.oh + (int64_t)i * p.os;
   const float inv = l > 0.f ? 1.0f / l : 0.f;
   for (int d = 0; d < D; ++d) o[d] = from_f<T>(acc[d] * inv);
   if (p.lse) p.lse[((int64_t)b * p.Hq + hq) * p.Sq + i] = m + logf(l);
@@ -1056,7 +1087,7 @@ __global__ void lens_inc_kernel(int* lens, int B, int add) {
 // AttnParams::q_off). lens_add: if set, lens_add[b] += Sq after the attention.
 int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t Hq, int64_t Hkv,
              int64_t Sq, int64_t Sk, int64_t D, const int64_t* strides, float scale, int is_causal, int dtype,
-             const int* q_off, int* lens_add, void* stream) {
+             const int* q_off, int* lens_add, void* stream, const int* cu_seqlens = nullptr) {
   Q3_REQUIRE(q && k && v && o && strides, Q3_ERR_NULL);
   Q3_REQUIRE(B >= 0 && Hq >= 1 && Hkv >= 1 && Sq >= 0 && Sk >= 0 && D >= 1, Q3_ERR_SHAPE);
   Q3_REQUIRE(Hq % Hkv == 0, Q3_ERR_SHAPE);
@@ -1089,6 +1120,7 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
   p.causal = is_causal ? 1 : 0;
   p.groups = (int)(Hq / Hkv);
   p.q_off = q_off;
+  p.cu_seqlens = cu_seqlens;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool aligned = q3_aligned(q, 16) && q3_aligned(k, 16) && q3_aligned(v, 16) && q3_aligned(o, 8) &&
                        strides_aligned8(strides, 12);
@@ -1108,8 +1140,8 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
       case 96:
         rc = launch_fwd<96>(p, st);
         break;
-      default:
-        rc = p.groups % 4 == 0 ? launch_fwd_pipe(p, st) : launch_fwd<128>(p, st);
+      default:  // the pipelined kernel has no packed-sequence form
+        rc = (p.groups % 4 == 0 && !cu_seqlens) ? launch_fwd_pipe(p, st) : launch_fwd<128>(p, st);
     }
   } else {
     const int64_t rows = B * Hq * Sq;
@@ -1140,6 +1172,24 @@ int q3_flash_attention(const void* q, const void* k, const void* v, void* o, flo
                        int is_causal, int dtype, void* stream) {
   return fwd_impl(q, k, v, o, lse, B, Hq, Hkv, Sq, Sk, D, strides, scale, is_causal, dtype, nullptr, nullptr,
                   stream);
+}
+
+// Packed variable-length sequences (the vision tower's images): q/k/v/o are
+// (H, total, D) views with strides [h, s] each (strides = [qh, qs, kh, ks, vh,
+// vs, oh, os]); sequence b is rows [cu_seqlens[b], cu_seqlens[b + 1]) (int32
+// on the device, cu_seqlens[0] = 0), attending only within itself;
+// max_seqlen >= every sequence's length.
+int q3_flash_attention_varlen(const void* q, const void* k, const void* v, void* o, const int* cu_seqlens,
+                              int64_t n_seqs, int64_t total, int64_t max_seqlen, int64_t Hq, int64_t Hkv, int64_t D,
+                              const int64_t* strides, float scale, int is_causal, int dtype, void* stream) {
+  Q3_REQUIRE(q && k && v && o && cu_seqlens && strides, Q3_ERR_NULL);
+  Q3_REQUIRE(n_seqs >= 0 && total >= 0 && max_seqlen >= 0 && max_seqlen <= total, Q3_ERR_SHAPE);
+  if (n_seqs == 0 || total == 0) return Q3_OK;
+  const int64_t st12[12] = {0, strides[0], strides[1], 0, strides[2], strides[3],
+                            0, strides[4], strides[5], 0, strides[6], strides[7]};
+  // Sk = total: keys are addressed within the packed rows (buffer bounds).
+  return fwd_impl(q, k, v, o, nullptr, n_seqs, Hq, Hkv, max_seqlen, total, D, st12, scale, is_causal, dtype,
+                  nullptr, nullptr, stream, cu_seqlens);
 }
 
 // Prefill of Sq new tokens per sequence over a ragged KV cache whose rows

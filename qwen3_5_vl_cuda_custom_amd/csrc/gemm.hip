@@ -24,7 +24,7 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(const T* __restrict__
                                                            T* __restrict__ C, int M, int N, int K, int64_t ldx,
                                                            int64_t ldw, int64_t ldr, int64_t ldc, int64_t bsX,
                                                            int64_t bsW, int64_t bsC, int swiglu,
-                                                           const T* __restrict__ W2) {
+                                                           const T* __restrict__ W2, int act) {
   __shared__ float xs[16][65];
   __shared__ float ws[16][65];
   __shared__ float ws2[16][65];
@@ -74,6 +74,7 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(const T* __restrict__
         v = v / (1.0f + expf(-v)) * acc2[i][j];
       } else {
         if (bias) v += to_f(bias[n]);
+        if (act) v = gelu_tanh_f(v);
         if (R) v += to_f(R[(int64_t)m * ldr + n]);
       }
       C[(int64_t)m * ldc + n] = from_f<T>(v);
@@ -83,12 +84,12 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(const T* __restrict__
 template <typename T>
 int launch_generic(const void* x, const void* w, const void* w2, const void* bias, const void* r, void* y, int64_t M,
                    int64_t N, int64_t K, int64_t batch, int64_t ldx, int64_t ldw, int64_t ldr, int64_t ldc,
-                   int64_t bsX, int64_t bsW, int64_t bsC, bool swiglu, hipStream_t st) {
+                   int64_t bsX, int64_t bsW, int64_t bsC, bool swiglu, hipStream_t st, int act = 0) {
   dim3 grid((unsigned)q3_cdiv(N, 64), (unsigned)q3_cdiv(M, 64), (unsigned)batch);
   hipLaunchKernelGGL(gemm_generic_kernel<T>, grid, dim3(256), 0, st, static_cast<const T*>(x),
                      static_cast<const T*>(w), static_cast<const T*>(bias), static_cast<const T*>(r),
                      static_cast<T*>(y), (int)M, (int)N, (int)K, ldx, ldw, ldr, ldc, bsX, bsW, bsC, swiglu ? 1 : 0,
-                     static_cast<const T*>(w2));
+                     static_cast<const T*>(w2), act);
   Q3_LAUNCH_CHECK();
   return Q3_OK;
 }
@@ -145,7 +146,7 @@ bool bf16_rows_ok(const void* base, int64_t ld, int64_t K) {
 int matmul_impl(const void* x, const void* w, const void* w2, const void* bias, const void* residual, void* y,
                 int64_t M, int64_t N, int64_t K, int64_t batch, int64_t ldx, int64_t ldw, int64_t ldr, int64_t ldc,
                 int64_t bsX, int64_t bsW, int64_t bsC, int dtype, bool swiglu, void* ws, int64_t ws_bytes,
-                hipStream_t st) {
+                hipStream_t st, int act = 0) {
   Q3_REQUIRE(x && w && y, Q3_ERR_NULL);
   Q3_REQUIRE(!swiglu || w2, Q3_ERR_NULL);
   Q3_REQUIRE(M >= 0 && N >= 0 && K >= 0 && batch >= 1, Q3_ERR_SHAPE);
@@ -156,13 +157,13 @@ int matmul_impl(const void* x, const void* w, const void* w2, const void* bias, 
   if (M == 0 || N == 0) return Q3_OK;
   if (dtype == Q3_F32)
     return launch_generic<float>(x, w, w2, bias, residual, y, M, N, K, batch, ldx, ldw, ldr, ldc, bsX, bsW, bsC,
-                                 swiglu, st);
+                                 swiglu, st, act);
   const bool rows_ok = bf16_rows_ok(x, ldx, K) && bf16_rows_ok(w, ldw, K) && (!w2 || bf16_rows_ok(w2, ldw, K)) &&
                        (bsX % 8 == 0) && (bsW % 8 == 0);
   if (!rows_ok || K == 0)
     return launch_generic<bf16>(x, w, w2, bias, residual, y, M, N, K, batch, ldx, ldw, ldr, ldc, bsX, bsW, bsC,
-                                swiglu, st);
-  if (M <= kGemvMaxRows && batch == 1) {
+                                swiglu, st, act);
+  if (M <= kGemvMaxRows && batch == 1 && !act) {
     GemvArgs ga{};
     ga.X = static_cast<const bf16*>(x);
     ga.ldx = ldx;
@@ -197,6 +198,7 @@ int matmul_impl(const void* x, const void* w, const void* w2, const void* bias, 
   p.bsX = bsX;
   p.bsW = bsW;
   p.bsC = bsC;
+  p.act = act;
   return swiglu ? launch_tiled<kEpiSwiGLU>(p, batch, st) : launch_tiled<kEpiStore>(p, batch, st);
 }
 
@@ -333,6 +335,12 @@ int q3_matmul(const void* x, const void* w, const void* bias, const void* residu
               int64_t workspace_bytes, void* stream) {
   return matmul_impl(x, w, nullptr, bias, residual, y, M, N, K, 1, ldx, ldw, ldr, ldc, 0, 0, 0, dtype, false,
                      workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int q3_matmul_gelu(const void* x, const void* w, const void* bias, void* y, int64_t M, int64_t N, int64_t K,
+                   int64_t ldx, int64_t ldw, int64_t ldc, int dtype, void* stream) {
+  return matmul_impl(x, w, nullptr, bias, nullptr, y, M, N, K, 1, ldx, ldw, 0, ldc, 0, 0, 0, dtype, false, nullptr,
+                     0, static_cast<hipStream_t>(stream), 1);
 }
 
 int q3_matmul_swiglu(const void* x, const void* w_gate, const void* w_up, void* y, int64_t M, int64_t N, int64_t K,

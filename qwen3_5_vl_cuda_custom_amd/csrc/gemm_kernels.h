@@ -64,6 +64,7 @@ struct GemmParams {
   const int* n_tiles_total;  // device scalar: number of valid m-tiles
   int64_t expert_stride_w;   // elements between consecutive experts' weights
   WeightSegments seg;        // dense (non-grouped, batch 1) store epilogue only
+  int act;                   // kEpiStore: 1 = gelu_tanh of (acc + bias), before the residual
 };
 
 // Where a block's tile sits: logical rows [m_begin, m_begin + rows_m), output
@@ -230,6 +231,10 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, const TileCtx& t
 #pragma unroll
               for (int q = 0; q < 4; ++q) o[q] += bf2f(b[q]);
             }
+            if (EPI == kEpiStore && p.act) {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) o[q] = gelu_tanh_f(o[q]);
+            }
             if (p.R) {
               const bf16x4 rv = *reinterpret_cast<const bf16x4*>(p.R + (int64_t)m * p.ldr + n);
 #pragma unroll
@@ -247,6 +252,7 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, const TileCtx& t
               if (n + q >= N) continue;
               float v = o[q];
               if (bias) v += bf2f(bias[n + q]);
+              if (EPI == kEpiStore && p.act) v = gelu_tanh_f(v);
               if (p.R) v += bf2f(p.R[(int64_t)m * p.ldr + n + q]);
               if constexpr (EPI == kEpiRowScale) v = bf2f(f2bf(v)) * rs;
               crow[n + q] = f2bf(v);

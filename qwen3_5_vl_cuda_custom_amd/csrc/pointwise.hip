@@ -19,10 +19,7 @@ __device__ __forceinline__ float ew_apply(float a, float b) {
   } else if constexpr (OP == kSwiGLU) {
     return a / (1.0f + expf(-a)) * b;
   } else {
-    // 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))
-    const float k0 = 0.7978845608028654f;
-    const float inner = k0 * (a + 0.044715f * a * a * a);
-    return 0.5f * a * (1.0f + tanhf(inner));
+    return gelu_tanh_f(a);
   }
 }
 

@@ -51,6 +51,13 @@ __device__ __forceinline__ float to_f<float>(float x) { return x; }
 template <>
 __device__ __forceinline__ float to_f<bf16>(bf16 x) { return bf2f(x); }
 
+// gelu with the tanh approximation: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))).
+__device__ __forceinline__ float gelu_tanh_f(float a) {
+  const float k0 = 0.7978845608028654f;
+  const float inner = k0 * (a + 0.044715f * a * a * a);
+  return 0.5f * a * (1.0f + tanhf(inner));
+}
+
 template <typename T>
 __device__ __forceinline__ T from_f(float x);
 template <>

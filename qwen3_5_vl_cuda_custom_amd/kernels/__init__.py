@@ -3,13 +3,15 @@ each backed by a hand-written gfx950 HIP kernel of libq3vl.so. GPU tensors only;
 from ._loader import FALLBACK_LOG, record_fallback, strict_mode, summarize_fallbacks
 from .conv3d_patch import conv3d_patch
 from .elementwise import gelu_tanh, residual_add, swiglu
-from .flash_attention import decode_attention, flash_attention, flash_attention_cache
-from .matmul import (RMSNORM_MATMUL_MAX_ROWS, matmul, matmul_segments, matmul_swiglu, rmsnorm_matmul_segments,
-                     rmsnorm_matmul_swiglu)
+from .embedding import embedding
+from .flash_attention import decode_attention, flash_attention, flash_attention_cache, flash_attention_varlen
+from .matmul import (RMSNORM_MATMUL_MAX_ROWS, matmul, matmul_gelu, matmul_segments, matmul_swiglu,
+                     rmsnorm_matmul_segments, rmsnorm_matmul_swiglu)
 from .moe_routing import (cuda_batched_gemm, cuda_index_add, cuda_topk, moe_experts, moe_permute, moe_route,
                           raise_device_errors)
 from .norms import layernorm, rmsnorm, softmax
 from .rotary import apply_mrope, apply_rope, qk_norm_rope
+from .vision import vision_pos_embed, vision_rope_tables
 
 __all__ = [
     "FALLBACK_LOG",
@@ -22,6 +24,7 @@ __all__ = [
     "cuda_batched_gemm",
     "cuda_index_add",
     "cuda_topk",
+    "embedding",
     "flash_attention",
     "gelu_tanh",
     "layernorm",
@@ -33,6 +36,10 @@ __all__ = [
     # additions beyond the reference API (fused / decode / MoE dispatch paths)
     "decode_attention",
     "flash_attention_cache",
+    "flash_attention_varlen",
+    "matmul_gelu",
+    "vision_rope_tables",
+    "vision_pos_embed",
     "matmul_segments",
     "matmul_swiglu",
     "rmsnorm_matmul_segments",

@@ -114,3 +114,32 @@ def flash_attention_cache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch
               o.data_ptr(), B, Hq, Hkv, Sq, cap, D, _lib.i64s(*_s4(q), *_s4(k_cache), *_s4(v_cache), *_s4(o)),
               float(scale), int(bool(advance)), _lib.dtype_code(q.dtype), _lib.stream())
     return o
+
+
+def flash_attention_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
+                           max_seqlen: int, scale: float, is_causal: bool = False, num_kv_groups: int = 1, *,
+                           out: torch.Tensor | None = None) -> torch.Tensor:
+    """Attention over packed variable-length sequences (HF's cu_seqlens form).
+
+    q (Hq, total, D), k/v (Hkv, total, D), any strides with D contiguous;
+    cu_seqlens (n+1,) int32 on the device with cu_seqlens[0] = 0 and
+    cu_seqlens[-1] = total: sequence b is rows [cu[b], cu[b+1]) and attends only
+    within itself (causally when is_causal). max_seqlen bounds every length.
+    Returns (Hq, total, D) (`out`, when given, is written in place).
+    """
+    check("flash_attention_varlen", q, k, v)
+    q, k, v = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
+    Hq, total, D = q.shape
+    Hkv = k.shape[0]
+    if k.shape != v.shape or k.shape[1] != total or k.shape[2] != D or Hkv * num_kv_groups != Hq:
+        raise ValueError(f"flash_attention_varlen: q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}")
+    if cu_seqlens.dtype != torch.int32 or not cu_seqlens.is_cuda or cu_seqlens.dim() != 1:
+        raise ValueError("flash_attention_varlen: cu_seqlens must be a 1-D int32 device tensor")
+    o = out if out is not None else torch.empty((Hq, total, D), dtype=q.dtype, device=q.device)
+    if o.shape != (Hq, total, D) or o.stride(-1) != 1:
+        raise ValueError("flash_attention_varlen: out must be (Hq, total, D) with a contiguous head dim")
+    st = [q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1), o.stride(0), o.stride(1)]
+    _lib.call("q3_flash_attention_varlen", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+              cu_seqlens.contiguous().data_ptr(), cu_seqlens.numel() - 1, total, int(max_seqlen), Hq, Hkv, D,
+              _lib.i64s(*st), float(scale), int(bool(is_causal)), _lib.dtype_code(q.dtype), _lib.stream())
+    return o

@@ -45,6 +45,27 @@ def matmul(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
     return y
 
 
+def matmul_gelu(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """gelu_tanh(x·Wᵀ + b) in one GEMM (fc1 + gelu_tanh of modules/mlp.py:33-34 and
+    modules/vision_patch.py:68), the activation applied before the single rounding."""
+    check("matmul_gelu", x, weight, bias)
+    K = x.shape[-1]
+    N = weight.shape[0]
+    if weight.dim() != 2 or weight.shape[1] != K:
+        raise ValueError(f"matmul_gelu: weight {tuple(weight.shape)} does not match x (..., {K})")
+    if bias is not None and bias.shape != (N,):
+        raise ValueError(f"matmul_gelu: bias {tuple(bias.shape)} != ({N},)")
+    x2 = x.reshape(-1, K)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    w = weight if weight.stride(-1) == 1 else weight.contiguous()
+    y = torch.empty((*x.shape[:-1], N), dtype=x.dtype, device=x.device)
+    b = bias.contiguous() if bias is not None else None
+    _lib.call("q3_matmul_gelu", x2.data_ptr(), w.data_ptr(), _lib.ptr(b), y.data_ptr(), x2.shape[0], N, K,
+              x2.stride(0), w.stride(0), N, _lib.dtype_code(x.dtype), _lib.stream())
+    return y
+
+
 def matmul_swiglu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
     """silu(x·W_gateᵀ)·(x·W_upᵀ) in one GEMM (the gate/up/swiglu of modules/mlp.py:19-22)."""
     check("matmul_swiglu", x, w_gate, w_up)

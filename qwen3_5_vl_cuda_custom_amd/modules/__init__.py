@@ -1,6 +1,7 @@
 """nn.Module drop-ins with the reference's class names, parameter names and shapes
 (reference modules/__init__.py:1-28), running on libq3vl.so kernels."""
 from .attention import CudaFullAttention, CudaVisionAttention
+from .embedding import CudaEmbedding
 from .graph import StepGraph
 from .kv_cache import StaticKVCache
 from .linear import CudaLinear
@@ -10,11 +11,12 @@ from .norms import CudaLayerNorm, CudaRMSNorm
 from .rotary import MRoPEBinding, TextMRoPE, Vision2DRoPE
 from .text_decoder import CudaTextDecoderLayer
 from .vision_block import CudaVisionBlock
-from .vision_patch import CudaVisionPatchEmbed
+from .vision_patch import CudaVisionPatchEmbed, CudaVisionPatchMerger
 
 __all__ = [
     "CudaFullAttention",
     "CudaVisionAttention",
+    "CudaEmbedding",
     "CudaLinear",
     "CudaSwiGLUMLP",
     "CudaVisionMLP",
@@ -27,6 +29,7 @@ __all__ = [
     "CudaTextDecoderLayer",
     "CudaVisionBlock",
     "CudaVisionPatchEmbed",
+    "CudaVisionPatchMerger",
     "StaticKVCache",
     "StepGraph",
 ]

@@ -4,8 +4,8 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from ..kernels import (apply_rope, decode_attention, flash_attention, flash_attention_cache, matmul_segments,
-                       qk_norm_rope, rmsnorm_matmul_segments)
+from ..kernels import (apply_rope, decode_attention, flash_attention, flash_attention_cache, flash_attention_varlen,
+                       matmul_segments, qk_norm_rope, rmsnorm_matmul_segments)
 from .kv_cache import StaticKVCache
 from .linear import CudaLinear
 from .norms import CudaRMSNorm, fused_norm_ok
@@ -24,8 +24,14 @@ class CudaVisionAttention(nn.Module):
         self.proj = CudaLinear(hidden_size, hidden_size, bias=True)
 
     def forward(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
-                residual: torch.Tensor | None = None) -> torch.Tensor:
-        """x (B, S, h); cos/sin (S, D) (or (B|1, S, D)); images on the batch dim attend separately."""
+                residual: torch.Tensor | None = None, *, cu_seqlens: torch.Tensor | None = None,
+                max_seqlen: int | None = None) -> torch.Tensor:
+        """x (B, S, h); cos/sin (S, D) (or (B|1, S, D)); images on the batch dim attend separately.
+
+        cu_seqlens (int32, on the device) packs images of different sizes into
+        one sequence (B = 1): image i is tokens [cu_seqlens[i], cu_seqlens[i+1])
+        and attends only within itself (max_seqlen: the longest image).
+        """
         B, S, h = x.shape
         H, D = self.num_heads, self.head_dim
         qkv = self.qkv(x).view(B, S, 3, H, D)
@@ -33,7 +39,13 @@ class CudaVisionAttention(nn.Module):
         k = apply_rope(qkv[:, :, 1].transpose(1, 2), cos, sin)
         v = qkv[:, :, 2].transpose(1, 2)
         o = torch.empty((B, S, H, D), dtype=x.dtype, device=x.device)
-        flash_attention(q, k, v, scale=self.scale, is_causal=False, num_kv_groups=1, out=o.transpose(1, 2))
+        if cu_seqlens is not None:
+            if B != 1:
+                raise ValueError("CudaVisionAttention: cu_seqlens packs the images into a batch of one")
+            flash_attention_varlen(q[0], k[0], v[0], cu_seqlens, max_seqlen if max_seqlen is not None else S,
+                                   self.scale, False, 1, out=o[0].transpose(0, 1))
+        else:
+            flash_attention(q, k, v, scale=self.scale, is_causal=False, num_kv_groups=1, out=o.transpose(1, 2))
         return self.proj(o.view(B, S, h), residual=residual)
 
 

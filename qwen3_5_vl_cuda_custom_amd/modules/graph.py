@@ -43,9 +43,14 @@ class StepGraph:
             for _ in range(warmup):
                 fn()
         torch.cuda.current_stream().wait_stream(side)
+        # Capture records the step without running it: the caches' host-side
+        # lengths, which the captured forward advances, are put back after.
+        saved = [(c.min_len, c.max_len) for c in self.caches]
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
             self.out = fn()
+        for c, (lo, hi) in zip(self.caches, saved):
+            c.min_len, c.max_len = lo, hi
 
     def replay(self) -> Any:
         """Launch the captured step on the current stream; returns the static outputs."""

@@ -4,7 +4,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from ..kernels import gelu_tanh, matmul_swiglu, rmsnorm_matmul_swiglu, swiglu
+from ..kernels import matmul_gelu, matmul_swiglu, rmsnorm_matmul_swiglu, swiglu
 from .linear import CudaLinear
 from .norms import CudaRMSNorm, fused_norm_ok
 
@@ -37,7 +37,7 @@ class CudaSwiGLUMLP(nn.Module):
 
 
 class CudaVisionMLP(nn.Module):
-    """linear_fc2(gelu_tanh(linear_fc1(x))), both with bias."""
+    """linear_fc2(gelu_tanh(linear_fc1(x))), both with bias; the gelu runs in fc1's GEMM epilogue."""
 
     def __init__(self, hidden_size: int, intermediate_size: int) -> None:
         super().__init__()
@@ -45,4 +45,4 @@ class CudaVisionMLP(nn.Module):
         self.linear_fc2 = CudaLinear(intermediate_size, hidden_size, bias=True)
 
     def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None) -> torch.Tensor:
-        return self.linear_fc2(gelu_tanh(self.linear_fc1(x)), residual=residual)
+        return self.linear_fc2(matmul_gelu(x, self.linear_fc1.weight, self.linear_fc1.bias), residual=residual)

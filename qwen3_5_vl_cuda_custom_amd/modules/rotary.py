@@ -7,15 +7,34 @@ from torch import nn
 from ..kernels import apply_mrope, apply_rope, qk_norm_rope
 
 
-class Vision2DRoPE(nn.Module):
+def rotary_inv_freq(dim: int, theta: float, device=None) -> torch.Tensor:
+    """inv_freq = 1 / theta^(arange(0, dim, 2) / dim) in fp32 (reference modules/rotary.py:19, 43)."""
+    return 1.0 / (theta ** (torch.arange(0, dim, 2, dtype=torch.float32, device=device) / dim))
+
+
+class _FP32Freqs(nn.Module):
+    """Keeps the `inv_freq` buffer in fp32 through `.to(dtype)` / `.half()` casts of a model:
+    the rotation angles are computed from it in fp32 by the kernels."""
+
+    _freq_dim: int
+    _freq_theta: float
+
+    def _apply(self, fn, recurse=True):
+        super()._apply(fn, recurse)
+        if self.inv_freq.dtype != torch.float32:
+            self.inv_freq = rotary_inv_freq(self._freq_dim, self._freq_theta, self.inv_freq.device)
+        return self
+
+
+class Vision2DRoPE(_FP32Freqs):
     """Vision rotary embedding; forward(seqlen) -> freqs (S, dim//2) (reference modules/rotary.py:9-31)."""
 
     def __init__(self, dim: int, theta: float = 10000.0) -> None:
         super().__init__()
         self.dim = dim
         self.theta = theta
-        inv_freq = 1.0 / (theta ** (torch.arange(0, dim, 2, dtype=torch.float32) / dim))
-        self.register_buffer("inv_freq", inv_freq, persistent=False)
+        self._freq_dim, self._freq_theta = dim, theta
+        self.register_buffer("inv_freq", rotary_inv_freq(dim, theta), persistent=False)
 
     def forward(self, seqlen: int) -> torch.Tensor:
         seq = torch.arange(seqlen, device=self.inv_freq.device, dtype=self.inv_freq.dtype)
@@ -69,7 +88,7 @@ class MRoPEBinding:
         return self.rope.apply(q, k, self.position_ids)
 
 
-class TextMRoPE(nn.Module):
+class TextMRoPE(_FP32Freqs):
     """Text mRoPE: 3D positions (T, H, W) over the head dim by `mrope_section` (reference modules/rotary.py:34-59)."""
 
     def __init__(self, dim: int, theta: float = 500000.0, mrope_section: list[int] | None = None) -> None:
@@ -77,8 +96,8 @@ class TextMRoPE(nn.Module):
         self.dim = dim
         self.theta = theta
         self.mrope_section = list(mrope_section or [24, 20, 20])
-        inv_freq = 1.0 / (theta ** (torch.arange(0, dim, 2, dtype=torch.float32) / dim))
-        self.register_buffer("inv_freq", inv_freq, persistent=False)
+        self._freq_dim, self._freq_theta = dim, theta
+        self.register_buffer("inv_freq", rotary_inv_freq(dim, theta), persistent=False)
 
     def compute_cos_sin(self, position_ids: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         """position_ids (3, B, S) -> cos/sin (3, B, S, dim) fp32 (reference modules/rotary.py:46-55)."""

@@ -19,6 +19,8 @@ class CudaVisionBlock(nn.Module):
         self.norm2 = CudaLayerNorm(hidden_size, eps=eps, bias=True)
         self.mlp = CudaVisionMLP(hidden_size, intermediate_size)
 
-    def forward(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-        x = self.attn(self.norm1(x), cos, sin, residual=x)
+    def forward(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, *,
+                cu_seqlens: torch.Tensor | None = None, max_seqlen: int | None = None) -> torch.Tensor:
+        """cu_seqlens/max_seqlen: images packed into one sequence attend separately (CudaVisionAttention)."""
+        x = self.attn(self.norm1(x), cos, sin, residual=x, cu_seqlens=cu_seqlens, max_seqlen=max_seqlen)
         return self.mlp(self.norm2(x), residual=x)

@@ -4,7 +4,9 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from ..kernels import conv3d_patch
+from ..kernels import conv3d_patch, matmul_gelu
+from .linear import CudaLinear
+from .norms import CudaLayerNorm
 
 
 class CudaVisionPatchEmbed(nn.Module):
@@ -30,3 +32,29 @@ class CudaVisionPatchEmbed(nn.Module):
         if x.dim() == 2:
             x = x.view(-1, self.in_channels, self.temporal_patch_size, self.patch_size, self.patch_size)
         return conv3d_patch(x, self.weight, self.bias)
+
+
+class CudaVisionPatchMerger(nn.Module):
+    """Spatial merge of merge x merge neighbouring patches (reference modules/vision_patch.py:42-68).
+
+    norm (LayerNorm over the patch hidden, or over the merged hidden when
+    `use_postshuffle_norm`), then linear_fc2(gelu_tanh(linear_fc1(.))) on rows
+    of merge^2 consecutive tokens; fc1 and the gelu run as one GEMM.
+    """
+
+    def __init__(self, hidden_size: int, out_hidden_size: int, spatial_merge_size: int = 2,
+                 use_postshuffle_norm: bool = False) -> None:
+        super().__init__()
+        self.hidden_size_in = hidden_size
+        self.merged_hidden = hidden_size * spatial_merge_size ** 2
+        self.use_postshuffle_norm = use_postshuffle_norm
+        self.norm = CudaLayerNorm(self.merged_hidden if use_postshuffle_norm else hidden_size, eps=1e-6, bias=True)
+        self.linear_fc1 = CudaLinear(self.merged_hidden, self.merged_hidden, bias=True)
+        self.linear_fc2 = CudaLinear(self.merged_hidden, out_hidden_size, bias=True)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.use_postshuffle_norm:
+            x = self.norm(x.reshape(-1, self.merged_hidden))
+        else:
+            x = self.norm(x).reshape(-1, self.merged_hidden)
+        return self.linear_fc2(matmul_gelu(x, self.linear_fc1.weight, self.linear_fc1.bias))

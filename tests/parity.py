@@ -74,8 +74,10 @@ def assert_layer_parity(out, ref32, ref_bf16, what=""):
     bf16 rounding after every op (the reference's own bf16 path). A bf16 layer
     carries the quantisation error of its bf16 GEMM operands, so its worst
     element vs fp32 can exceed max-abs 2e-2 whatever the kernels do. Asserted:
-      * mean-rel vs fp32 <= 5e-3, and no larger than the
-        reference bf16 path's mean-rel (up to the equal-rounding tie TIE_REL);
+      * mean-rel vs fp32 no larger than the reference bf16 path's mean-rel (up
+        to the equal-rounding tie TIE_REL), and <= 5e-3
+        unless the reference bf16 path itself is above 5e-3 (deep compositions
+        such as the vision tower's merger output);
       * max-abs vs fp32 <= 2e-2, or, where the reference bf16 path's own
         max-abs is larger, no larger than that (up to one bf16 ulp of the
         reference value at our worst element).
@@ -88,7 +90,7 @@ def assert_layer_parity(out, ref32, ref_bf16, what=""):
     msg = (f"{what}: ours max-abs {ma:.3e} mean-rel {mr:.3e} | reference bf16 path max-abs {ma_r:.3e} "
            f"mean-rel {mr_r:.3e}")
     print(msg)
-    assert mr <= BF16_MEAN_REL, msg
     assert mr <= mr_r * (1 + TIE_REL), msg
+    assert mr <= BF16_MEAN_REL or mr_r > BF16_MEAN_REL, msg
     assert ma <= max(BF16_MAX_ABS, ma_r + _ulp_bf16(worst)), msg
     return ma, mr, ma_r, mr_r

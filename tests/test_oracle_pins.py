@@ -346,3 +346,98 @@ def test_c1_golden_fixture():
     y, _, _ = L.text_decoder_layer(x, p, num_heads=4, num_kv_heads=2, head_dim=64, eps=1e-6, cos_3d=cos3,
                                    sin_3d=sin3, mrope_section=[12, 10, 10])
     assert np.allclose(y.numpy(), fx["y"], atol=2e-5)
+
+
+# ------------------------------------------------------------------ model edges and vision tower
+def _hf_vision_model(seed=5):
+    from transformers.models.qwen3_vl import modeling_qwen3_vl as M
+    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLVisionConfig
+    vc = Qwen3VLVisionConfig(depth=3, hidden_size=64, num_heads=2, intermediate_size=96, patch_size=4,
+                             temporal_patch_size=2, in_channels=3, spatial_merge_size=2, out_hidden_size=48,
+                             num_position_embeddings=25, deepstack_visual_indexes=[0, 2],
+                             hidden_act="gelu_pytorch_tanh")
+    vc._attn_implementation = "eager"
+    hf = M.Qwen3VLVisionModel(vc).eval()
+    gg = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for n, prm in hf.named_parameters():
+            scale = 0.1 if prm.dim() >= 2 else 0.2
+            prm.copy_(torch.randn(prm.shape, generator=gg) * scale
+                      + (1.0 if "norm" in n and n.endswith("weight") else 0.0))
+    from qwen3_5_vl_cuda_custom_amd.loaders import map_hf_name
+    p = {map_hf_name("model.visual." + n)[len("visual."):]: t.detach().clone() for n, t in hf.state_dict().items()}
+    return hf, p
+
+
+def test_vision_tower_matches_hf():
+    """The oracle tower (per-frame attention) against HF Qwen3VLVisionModel: two images of
+    different grids (one with two frames), the deepstack mergers and the final merger; the
+    HF state dict goes through the loader's name map."""
+    hf, p = _hf_vision_model()
+    # The reference's merger applies gelu_tanh (modules/vision_patch.py:68) where HF's applies the
+    # exact gelu: swap HF's activation so the rest of the tower is what is compared.
+    for m in [hf.merger, *hf.deepstack_merger_list]:
+        m.act_fn = torch.nn.GELU(approximate="tanh")
+    grids = [(1, 4, 6), (2, 4, 4)]
+    n = sum(t * h * w for t, h, w in grids)
+    x = torch.randn(n, 3 * 2 * 4 * 4, generator=g)
+    with torch.no_grad():
+        ref = hf(x, torch.tensor(grids))
+    pool, last, deep = L.vision_tower(x, p, grids, num_heads=2, merge=2, in_channels=3, temporal=2, patch=4,
+                                      deepstack_layers=(0, 2))
+    assert torch.allclose(last, ref.last_hidden_state, atol=5e-5), float((last - ref.last_hidden_state).abs().max())
+    assert torch.allclose(pool, ref.pooler_output, atol=5e-5)
+    assert len(deep) == 2 and all(torch.allclose(a, b, atol=5e-5) for a, b in zip(deep, ref.deepstack_features))
+
+
+def test_pos_embed_interpolation_closed_forms():
+    """Bilinear grid lookup: a table linear in (row, col) interpolates to the same linear
+    function of the linspace coordinates; corners of the image hit the table's corners."""
+    G, hid = 5, 3
+    r, c = torch.meshgrid(torch.arange(G).float(), torch.arange(G).float(), indexing="ij")
+    table = torch.stack([r, c, 2 * r - c + 1], dim=-1).reshape(G * G, hid)
+    t, h, w = 1, 4, 6
+    out = L.pos_embed_interpolate(table, [(t, h, w)], 2)
+    hi, wi = torch.linspace(0, G - 1, h), torch.linspace(0, G - 1, w)
+    # token order: merge blocks of 2x2 row-major, the patches of a block row-major
+    order = [(bh * 2 + ih, bw * 2 + iw) for bh in range(h // 2) for bw in range(w // 2) for ih in range(2)
+             for iw in range(2)]
+    exp = torch.stack([torch.tensor([hi[a], wi[b], 2 * hi[a] - wi[b] + 1]) for a, b in order])
+    assert torch.allclose(out, exp, atol=1e-5)
+    assert torch.allclose(out[0], table[0]) and torch.allclose(out[order.index((h - 1, w - 1))], table[-1], atol=1e-5)
+
+
+def test_text_model_matches_hf_and_generate_is_greedy():
+    """The oracle text model (embeddings, two decoder layers, norm, lm_head) against HF
+    Qwen3VLTextModel + an lm_head; the oracle greedy loop (the reference's past_kv
+    generate) against argmax of full re-runs of the growing sequence."""
+    from transformers.models.qwen3_vl import modeling_qwen3_vl as M
+    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLTextConfig
+    cfg = Qwen3VLTextConfig(hidden_size=64, intermediate_size=96, num_attention_heads=4, num_key_value_heads=2,
+                            head_dim=16, num_hidden_layers=2, vocab_size=50, rms_norm_eps=1e-6,
+                            rope_parameters={"rope_type": "default", "rope_theta": 1e4, "mrope_section": [4, 2, 2]})
+    cfg._attn_implementation = "eager"
+    hf = M.Qwen3VLTextModel(cfg).eval()
+    gg = torch.Generator().manual_seed(9)
+    with torch.no_grad():
+        for n, prm in hf.named_parameters():
+            prm.copy_(torch.randn(prm.shape, generator=gg) * (0.2 if prm.dim() >= 2 else 0.1)
+                      + (1.0 if "norm" in n else 0.0))
+    lm = torch.randn(50, 64, generator=gg) * 0.2
+    p = {n: t.detach().clone() for n, t in hf.state_dict().items()}
+    p["lm_head.weight"] = lm
+    ids = torch.randint(0, 50, (2, 7), generator=gg)
+    with torch.no_grad():
+        ref = hf(input_ids=ids).last_hidden_state @ lm.T
+    kw = dict(num_heads=4, num_kv_heads=2, head_dim=16, eps=1e-6, theta=1e4, mrope_section=[4, 2, 2])
+    pos = torch.arange(7).view(1, 1, 7).expand(3, 2, 7)
+    logits, kvs = L.text_model(p["embed_tokens.weight"][ids], p, positions=pos, **kw)
+    assert torch.allclose(logits, ref, atol=1e-4), float((logits - ref).abs().max())
+    gen = L.greedy_generate(ids, p, max_new_tokens=4, **kw)
+    seq = ids
+    for _ in range(4):
+        n = seq.shape[1]
+        lg, _ = L.text_model(p["embed_tokens.weight"][seq], p, positions=torch.arange(n).view(1, 1, n).expand(3, 2, n),
+                             **kw)
+        seq = torch.cat([seq, lg[:, -1].argmax(-1, keepdim=True)], dim=1)
+    assert torch.equal(gen, seq)
