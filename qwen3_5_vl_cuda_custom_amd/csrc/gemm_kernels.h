@@ -265,6 +265,128 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, const TileCtx& t
   }
 }
 
+// Epilogue through LDS. Stored straight from the accumulators, one wave store
+// instruction writes 32 rows x 16 bytes (a lane holds 4 consecutive columns of
+// one row), which the memory system takes at ~1.2 TB/s: at S = 4096 that is
+// ~80 us of the gate/up GEMM. Instead the accumulators (after the register-level
+// part of the epilogue, SwiGLU) go to the LDS ring, free by then, as fp32 in
+// passes of RP rows; every wave then reads whole rows back, 8 consecutive columns
+// per lane, adds bias / applies gelu / adds the residual / the row scale, rounds
+// once and stores 16 bytes per lane: contiguous rows per instruction. The
+// arithmetic and its order are those of the direct store (bit-identical output).
+// LDS rows are BN_OUT fp32; 16-byte chunk c of row r sits at chunk c ^ (r & 15).
+template <int BM, int BN_OUT, int WTM, int WTN, int TN, int TM, int EPI, int NW, int LDS_BYTES>
+__device__ __forceinline__ void store_tile_lds(const GemmParams& p, const TileCtx& t, const floatx16 (&c)[TN][TM],
+                                               int wm, int wn, int lane, float* lds) {
+  constexpr int RP0 = LDS_BYTES / (BN_OUT * 4);
+  constexpr int RP = RP0 >= 256 ? 256 : RP0 >= 128 ? 128 : RP0 >= 64 ? 64 : 32;  // rows per pass
+  constexpr int NPASS = (BM + RP - 1) / RP;
+  constexpr int C8 = BN_OUT / 8;                          // 8-column items per row
+  constexpr int WTN_OUT = EPI == kEpiSwiGLU ? WTN / 2 : WTN;
+  constexpr int TN_OUT = EPI == kEpiSwiGLU ? TN / 2 : TN;
+  static_assert(BN_OUT % 64 == 0 && RP % 32 == 0, "epilogue tiling");
+  const int m_begin = t.m_begin, rows_m = t.rows_m, n0_out = t.n0_out;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int N = p.N;
+  const bool vec_ok = ((p.ldc & 7) == 0) && (reinterpret_cast<uintptr_t>(t.C) & 15) == 0 &&
+                      (p.R == nullptr || ((p.ldr & 7) == 0 && (reinterpret_cast<uintptr_t>(p.R) & 15) == 0));
+  auto slot = [](int r, int col) { return r * BN_OUT + ((((col >> 2) ^ (r & 15))) << 2); };
+  __syncthreads();  // every wave is done with the main loop's LDS
+#pragma unroll
+  for (int pass = 0; pass < NPASS; ++pass) {
+    const int r0 = pass * RP;
+    // 1. this wave's accumulator rows of the pass -> LDS (fp32)
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+      const int mr = wm * WTM + j * 32;  // tile row of this m-tile (wave-uniform)
+      if (mr < r0 || mr >= r0 + RP) continue;
+      const int lr = mr - r0 + l32;
+#pragma unroll
+      for (int i = 0; i < TN_OUT; ++i) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int col = wn * WTN_OUT + i * 32 + 8 * g + 4 * h;
+          floatx4 v;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            if constexpr (EPI == kEpiSwiGLU) {
+              const float gt = c[2 * i][j][4 * g + q];
+              const float up = c[2 * i + 1][j][4 * g + q];
+              v[q] = gt / (1.0f + __expf(-gt)) * up;
+            } else {
+              v[q] = c[i][j][4 * g + q];
+            }
+          }
+          *reinterpret_cast<floatx4*>(lds + slot(lr, col)) = v;
+        }
+      }
+    }
+    __syncthreads();
+    // 2. rows of the pass, 8 columns per lane, finished and stored
+    const int nrows = min(RP, rows_m - r0);
+    for (int it = threadIdx.x; it < nrows * C8; it += NW * 64) {
+      const int lr = it / C8, c8 = it - lr * C8;
+      const int col = c8 * 8;
+      const floatx4 a = *reinterpret_cast<const floatx4*>(lds + slot(lr, col));
+      const floatx4 b = *reinterpret_cast<const floatx4*>(lds + slot(lr, col + 4));
+      float o[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+      const int m = m_begin + r0 + lr;
+      const int n = n0_out + col;
+      bf16* crow = t.C + (int64_t)m * p.ldc;
+      if constexpr (EPI == kEpiStore) {
+        const bf16* bias = t.bias;
+        if (p.seg.n > 1) {  // per lane: the lanes' columns may lie in different segments
+          const int sgi = segment_of(p.seg, n);  // segment starts are multiples of 16
+          const bf16* b = pick4(sgi, p.seg.b[0], p.seg.b[1], p.seg.b[2], p.seg.b[3]);
+          bias = b ? b - pick4(sgi, p.seg.start[0], p.seg.start[1], p.seg.start[2], p.seg.start[3]) : nullptr;
+        }
+        if (bias) {
+          if (vec_ok && n + 7 < N) {
+            const bf16x8 bv = *reinterpret_cast<const bf16x8*>(bias + n);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) o[q] += bf2f(bv[q]);
+          } else {
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+              if (n + q < N) o[q] += bf2f(bias[n + q]);
+          }
+        }
+        if (p.act) {
+#pragma unroll
+          for (int q = 0; q < 8; ++q) o[q] = gelu_tanh_f(o[q]);
+        }
+        if (p.R) {
+          const bf16* rrow = p.R + (int64_t)m * p.ldr;
+          if (vec_ok && n + 7 < N) {
+            const bf16x8 rv = *reinterpret_cast<const bf16x8*>(rrow + n);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) o[q] += bf2f(rv[q]);
+          } else {
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+              if (n + q < N) o[q] += bf2f(rrow[n + q]);
+          }
+        }
+      } else if constexpr (EPI == kEpiRowScale) {
+        const float rs = bf2f(p.rowscale[m]);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) o[q] = bf2f(f2bf(o[q])) * rs;
+      }
+      if (vec_ok && n + 7 < N) {
+        bf16x8 v;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = f2bf(o[q]);
+        *reinterpret_cast<bf16x8*>(crow + n) = v;
+      } else {
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          if (n + q < N) crow[n + q] = f2bf(o[q]);
+      }
+    }
+    if (pass + 1 < NPASS) __syncthreads();  // the next pass overwrites the LDS
+  }
+}
+
 // Swizzle of a BKT-element LDS row (BKT / 8 chunks of 16 bytes): chunk c of
 // row r sits at slot c ^ dma_swz<BKT>(r). For 32 or 16 consecutive rows read
 // one chunk each (a fragment read), the slots land on distinct 16-byte
@@ -494,7 +616,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
   }
   vm_wait<0>();  // the trailing zero-fill DMAs must land before the block's LDS is reused
 
-  store_tile<WTM, WTN, TN, TM, EPI>(p, tc, acc.c, wm, wn, lane);
+  store_tile_lds<BM, BN_OUT, WTM, WTN, TN, TM, EPI, NW, NST * kStage * 2>(p, tc, acc.c, wm, wn, lane,
+                                                                          reinterpret_cast<float*>(smem));
 }
 
 }  // namespace q3
