@@ -445,16 +445,18 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
   const int64_t ldx = p.ldx, ldw = p.ldw;
 
   // Lane geometry of instruction i of this wave: tile row, and the global
-  // chunk that lands in the lane's LDS slot.
+  // chunk that lands in the lane's LDS slot. The swizzle depends on the row
+  // mod 16 only, and instruction i's rows are those of instruction 0 plus a
+  // multiple of 16, so one chunk index serves every instruction.
+  static_assert((NW * RPI) % 16 == 0, "one swizzle chunk per lane");
   const int lrow = lane / CH, lslot = lane % CH;
+  const int dc = lslot ^ dma_swz<BKT>(wave * RPI + lrow);
   uint32_t xoff[PX], woff[PW];
-  int xc[PX], wc[PW];
   const bf16* wsrc[PW];  // weight matrix of each W instruction (its rows share one segment) ...
   int wrows[PW];         // ... and its rows
 #pragma unroll
   for (int i = 0; i < PX; ++i) {
     const int r = (wave + NW * i) * RPI + lrow;
-    xc[i] = lslot ^ dma_swz<BKT>(r);
     if (r < rows_m) {
       const int lr = m_begin + r;
       const int64_t pr = p.gather ? (int64_t)p.gather[lr] : (int64_t)lr;
@@ -466,7 +468,6 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
 #pragma unroll
   for (int i = 0; i < PW; ++i) {
     const int r = (wave + NW * i) * RPI + lrow;
-    wc[i] = lslot ^ dma_swz<BKT>(r);
     int n, rbase = 0, rlim;  // global row n; rows of the source matrix: [rbase, rbase + rlim)
     const bf16* wb;
     if constexpr (EPI == kEpiSwiGLU) {
@@ -505,14 +506,14 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
     const uint32_t sb = lbase + (uint32_t)((kt % NST) * kStage * 2);
 #pragma unroll
     for (int i = 0; i < PX; ++i) {
-      const int k = k0 + xc[i] * 8;
+      const int k = k0 + dc * 8;
       const uint32_t off = (k < K && xoff[i] != kOOB) ? xoff[i] + (uint32_t)k * 2u : kOOB;
       dma16(rx, off, sb + (uint32_t)((wave + NW * i) * 1024));
     }
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
       const int j = wave + NW * i;
-      const int k = k0 + wc[i] * 8;
+      const int k = k0 + dc * 8;
       const uint32_t off = (k < K && woff[i] != kOOB) ? woff[i] + (uint32_t)k * 2u : kOOB;
       dma16(make_rsrc(wsrc[i], (int64_t)wrows[i] * ldw * 2), off, sb + (uint32_t)(BM * BKT * 2 + j * 1024));
     }
@@ -554,13 +555,13 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
     uint32_t doff[ND], dlds[ND];
 #pragma unroll
     for (int i = 0; i < PX; ++i) {
-      const int k = k0 + xc[i] * 8;
+      const int k = k0 + dc * 8;
       doff[i] = (k < K && xoff[i] != kOOB) ? xoff[i] + (uint32_t)k * 2u : kOOB;
       dlds[i] = sb + (uint32_t)((wave + NW * i) * 1024);
     }
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
-      const int k = k0 + wc[i] * 8;
+      const int k = k0 + dc * 8;
       doff[PX + i] = (k < K && woff[i] != kOOB) ? woff[i] + (uint32_t)k * 2u : kOOB;
       dlds[PX + i] = sb + (uint32_t)(BM * BKT * 2 + (wave + NW * i) * 1024);
     }

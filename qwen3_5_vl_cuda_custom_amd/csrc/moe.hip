@@ -31,7 +31,7 @@ using namespace q3;
 
 namespace {
 
-constexpr int kMoeBM = 128;
+constexpr int kMoeBM = 320;
 constexpr int kMoeBN = 256;  // weight rows per tile (SwiGLU: 128 gate/up output columns)
 
 // ------------------------------------------------------------------ routing
