@@ -121,10 +121,12 @@ int launch_tiled(GemmParams p, int64_t batch, hipStream_t st) {
   const double cost_a = waves(q3_cdiv(p.M, 256) * q3_cdiv(p.N, bo) * batch, kCUs) * 256.0 * 256.0;
   const double cost_c =
       waves(q3_cdiv(p.M, 128) * q3_cdiv(p.N, bo / 2) * batch, 2 * kCUs) * 2.0 * 128.0 * 128.0 / 0.75;
-  // 128x256 only when it fills the CUs: below one wave the smaller tiles run
-  // alone on their CUs, faster than the per-slot estimate assumes.
+  // 128x256 only when it fills at least 3/4 of the CUs: with fewer tiles the
+  // 128x128 tiles, one per CU, run faster than the per-slot estimate assumes
+  // (measured: M=1024 N=4096 K=4096, 128 tiles: 56.8 us against 44.8 us for
+  // 256 tiles of 128x128; M=1024 N=6144, 192 tiles: 58.8 us against 70.1).
   const int64_t tiles_d = q3_cdiv(p.M, 128) * q3_cdiv(p.N, bo) * batch;
-  const double cost_d = tiles_d >= kCUs ? waves(tiles_d, kCUs) * 128.0 * 256.0 / 0.9 : 1e300;
+  const double cost_d = 4 * tiles_d >= 3 * kCUs ? waves(tiles_d, kCUs) * 128.0 * 256.0 / 0.9 : 1e300;
   if constexpr (EPI == kEpiSwiGLU) {
     if (cost_c < cost_a && cost_c < cost_d) return launch_tiled_cfg<128, 128, 2, 2, EPI, 4, 32>(p, batch, st);
     if (cost_d < cost_a) return launch_tiled_cfg<128, 256, 2, 4, EPI, 2, 64>(p, batch, st);

@@ -58,11 +58,104 @@ __global__ __launch_bounds__(256) void rope_kernel(const T* __restrict__ x, cons
   }
 }
 
+// The same rotation with V consecutive pairs per thread (vector loads of x,
+// y, cos and sin) and 32-bit index arithmetic: thread t handles slot t % P of
+// row t / P, rows ordered (b, h, s), P = (Dr/2 + D - Dr) / V slots per row.
+// Slots below Dr/2 V rotate pairs [j, j + V) with [j + Dr/2, ...); the others
+// copy V pass-through elements (skipped when y aliases x in place).
+template <typename T, int V>
+using vec_t = T __attribute__((ext_vector_type(V)));
+
+template <typename T, typename TC, int V>
+__global__ __launch_bounds__(256) void rope_vec_kernel(const T* x, const TC* __restrict__ cosp,
+                                                       const TC* __restrict__ sinp, T* y, RopeGeom g,
+                                                       int P, int total, int copy_tail) {
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= total) return;
+  const int half = g.Dr / 2;
+  int row = t / P;
+  const int j = (t - row * P) * V;
+  const int s = row % g.S;
+  row /= g.S;
+  const int h = row % g.H;
+  const int b = row / g.H;
+  const T* xr = x + b * g.xb + h * g.xh + s * g.xs;
+  T* yr = y + b * g.yb + h * g.yh + s * g.ys;
+  if (j < half) {
+    const vec_t<T, V> x1 = *reinterpret_cast<const vec_t<T, V>*>(xr + j);
+    const vec_t<T, V> x2 = *reinterpret_cast<const vec_t<T, V>*>(xr + j + half);
+    float c[V], sn[V];
+    if (g.s0 >= half) {  // one axis: the table row is contiguous
+      const int64_t co = b * g.cb + s * g.cs + j;
+      const vec_t<TC, V> cv = *reinterpret_cast<const vec_t<TC, V>*>(cosp + co);
+      const vec_t<TC, V> sv = *reinterpret_cast<const vec_t<TC, V>*>(sinp + co);
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        c[e] = to_f<TC>(cv[e]);
+        sn[e] = to_f<TC>(sv[e]);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        const int i = j + e;
+        const int axis = (i < g.s0) ? 0 : (i < g.s0 + g.s1 ? 1 : 2);
+        const int64_t co = axis * g.ca + b * g.cb + s * g.cs + i;
+        c[e] = to_f<TC>(cosp[co]);
+        sn[e] = to_f<TC>(sinp[co]);
+      }
+    }
+    vec_t<T, V> y1, y2;
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const float a = to_f<T>(x1[e]), bb = to_f<T>(x2[e]);
+      y1[e] = from_f<T>(a * c[e] - bb * sn[e]);
+      y2[e] = from_f<T>(bb * c[e] + a * sn[e]);
+    }
+    *reinterpret_cast<vec_t<T, V>*>(yr + j) = y1;
+    *reinterpret_cast<vec_t<T, V>*>(yr + j + half) = y2;
+  } else if (copy_tail) {
+    const int d = g.Dr + (j - half);
+    *reinterpret_cast<vec_t<T, V>*>(yr + d) = *reinterpret_cast<const vec_t<T, V>*>(xr + d);
+  }
+}
+
+template <typename T, typename TC, int V>
+bool try_rope_vec(const void* x, const void* cosp, const void* sinp, void* y, const RopeGeom& g, hipStream_t st) {
+  const int half = g.Dr / 2, tail = g.D - g.Dr;
+  if (half % V || tail % V) return false;
+  const int64_t ve = V * (int64_t)sizeof(T), vc = V * (int64_t)sizeof(TC);
+  auto al = [](const void* p, int64_t a) { return (reinterpret_cast<uintptr_t>(p) % (uintptr_t)a) == 0; };
+  const int64_t ts = sizeof(T), cs = sizeof(TC);
+  bool ok = al(x, ve) && al(y, ve) && al(cosp, vc) && al(sinp, vc);
+  for (int64_t st_ : {g.xb, g.xh, g.xs, g.yb, g.yh, g.ys}) ok = ok && (st_ * ts) % ve == 0;
+  for (int64_t st_ : {g.ca, g.cb, g.cs}) ok = ok && (st_ * cs) % vc == 0;
+  const int64_t P = (half + tail) / V;
+  const int64_t rows = (int64_t)g.B * g.H * g.S;
+  if (!ok || rows * P >= (1ll << 31) - 256) return false;
+  const int total = (int)(rows * P);
+  const int copy_tail = tail > 0 && (x != y);
+  hipLaunchKernelGGL((rope_vec_kernel<T, TC, V>), dim3((unsigned)q3_cdiv(total, 256)), dim3(256), 0, st,
+                     static_cast<const T*>(x), static_cast<const TC*>(cosp), static_cast<const TC*>(sinp),
+                     static_cast<T*>(y), g, (int)P, total, copy_tail);
+  return true;
+}
+
+template <typename T, typename TC>
+bool try_rope_fast(const void* x, const void* cosp, const void* sinp, void* y, const RopeGeom& g, hipStream_t st) {
+  return try_rope_vec<T, TC, 4>(x, cosp, sinp, y, g, st) || try_rope_vec<T, TC, 2>(x, cosp, sinp, y, g, st) ||
+         try_rope_vec<T, TC, 1>(x, cosp, sinp, y, g, st);
+}
+
 template <typename T>
 int launch_rope_t(const void* x, const void* cosp, const void* sinp, void* y, const RopeGeom& g, int cos_dtype,
                   hipStream_t st) {
   const int64_t total = (int64_t)g.B * g.H * g.S * (g.Dr / 2 + g.D - g.Dr);
   if (total == 0) return Q3_OK;
+  if (cos_dtype == Q3_F32 ? try_rope_fast<T, float>(x, cosp, sinp, y, g, st)
+                          : cos_dtype == Q3_BF16 && try_rope_fast<T, bf16>(x, cosp, sinp, y, g, st)) {
+    Q3_LAUNCH_CHECK();
+    return Q3_OK;
+  }
   const unsigned blocks = (unsigned)std::min<int64_t>(q3_cdiv(total, 256), 65536);
   if (cos_dtype == Q3_F32)
     hipLaunchKernelGGL((rope_kernel<T, float>), dim3(blocks), dim3(256), 0, st, static_cast<const T*>(x),

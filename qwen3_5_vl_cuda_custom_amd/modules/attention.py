@@ -35,8 +35,9 @@ class CudaVisionAttention(nn.Module):
         B, S, h = x.shape
         H, D = self.num_heads, self.head_dim
         qkv = self.qkv(x).view(B, S, 3, H, D)
-        q = apply_rope(qkv[:, :, 0].transpose(1, 2), cos, sin)
-        k = apply_rope(qkv[:, :, 1].transpose(1, 2), cos, sin)
+        # q and k rotated by one launch: their 2H heads are one strided (B, 2H, S, D) view
+        qk = apply_rope(qkv[:, :, :2].reshape(B, S, 2 * H, D).transpose(1, 2), cos, sin)
+        q, k = qk[:, :H], qk[:, H:]
         v = qkv[:, :, 2].transpose(1, 2)
         o = torch.empty((B, S, H, D), dtype=x.dtype, device=x.device)
         if cu_seqlens is not None:
