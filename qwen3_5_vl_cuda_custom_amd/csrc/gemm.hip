@@ -97,12 +97,12 @@ int launch_generic(const void* x, const void* w, const void* w2, const void* bia
 // =====================================================================
 // Tiled MFMA path.
 // =====================================================================
-template <int BM, int BN, int WM, int WN, int EPI, int NST, int BKT>
+template <int BM, int BN, int WM, int WN, int EPI, int NST, int BKT, int NSTW = NST>
 int launch_tiled_cfg(GemmParams p, int64_t batch, hipStream_t st) {
   constexpr int BN_OUT = (EPI == kEpiSwiGLU) ? BN / 2 : BN;
   const int64_t tiles = q3_cdiv(p.M, BM) * q3_cdiv(p.N, BN_OUT);
   p.group_m = 8;
-  hipLaunchKernelGGL((gemm_bf16_dma_kernel<BM, BN, WM, WN, EPI, false, NST, BKT>),
+  hipLaunchKernelGGL((gemm_bf16_dma_kernel<BM, BN, WM, WN, EPI, false, NST, BKT, NSTW>),
                      dim3((unsigned)tiles, 1, (unsigned)batch), dim3(WM * WN * 64), 0, st, p);
   Q3_LAUNCH_CHECK();
   return Q3_OK;
@@ -110,12 +110,16 @@ int launch_tiled_cfg(GemmParams p, int64_t batch, hipStream_t st) {
 
 // Tile configuration by estimated time: full waves of blocks over 256 CUs,
 // times the block's work over its relative MFMA efficiency (measured on
-// MI355X): 256x256 (8 waves, 64-wide K stages x 2; 1 block per CU) 1.0,
+// MI355X): 256x256 (8 waves, 64-wide K stages: 2 X slots, 3 W slots, the
+// whole 160 KB of LDS; 1 block per CU) 1.0,
 // 128x256 (8 waves, 64-wide K stages x 3: the third stage, which only this
 // tile's 144 KB ring leaves room for, hides the HBM latency of weights read
 // once per layer: with weights rotated past the MALL, M=1024 gate/up 243 ->
 // 189 us, M=4096 o 165 -> 131 us) 0.9, 256x192 (8 waves, 64-wide K
-// stages; plain epilogue only) 0.95, 128x128 (4 waves; 2 blocks per CU) 0.75.
+// stages, 2 X and 3 W slots; plain epilogue only) 0.95, 128x128 (4 waves; 2
+// blocks per CU) 0.75. The third W slot (weights are read from HBM once per
+// layer, activations from L2): M=4096 q/k/v 181 -> 170 us, gate/up 650 ->
+// 633 us with weights rotated past the MALL.
 template <int EPI>
 int launch_tiled(GemmParams p, int64_t batch, hipStream_t st) {
   constexpr int kCUs = 256;
@@ -133,14 +137,14 @@ int launch_tiled(GemmParams p, int64_t batch, hipStream_t st) {
   if constexpr (EPI == kEpiSwiGLU) {
     if (cost_c < cost_a && cost_c < cost_d) return launch_tiled_cfg<128, 128, 2, 2, EPI, 4, 32>(p, batch, st);
     if (cost_d < cost_a) return launch_tiled_cfg<128, 256, 2, 4, EPI, 3, 64>(p, batch, st);
-    return launch_tiled_cfg<256, 256, 2, 4, EPI, 2, 64>(p, batch, st);
+    return launch_tiled_cfg<256, 256, 2, 4, EPI, 2, 64, 3>(p, batch, st);
   } else {
     const double cost_b = waves(q3_cdiv(p.M, 256) * q3_cdiv(p.N, 192) * batch, kCUs) * 256.0 * 192.0 / 0.95;
     const double best = std::min(std::min(cost_a, cost_b), std::min(cost_c, cost_d));
     if (cost_c == best) return launch_tiled_cfg<128, 128, 2, 2, EPI, 4, 32>(p, batch, st);
-    if (cost_b == best) return launch_tiled_cfg<256, 192, 4, 2, EPI, 2, 64>(p, batch, st);
+    if (cost_b == best) return launch_tiled_cfg<256, 192, 4, 2, EPI, 2, 64, 3>(p, batch, st);
     if (cost_d == best) return launch_tiled_cfg<128, 256, 2, 4, EPI, 3, 64>(p, batch, st);
-    return launch_tiled_cfg<256, 256, 2, 4, EPI, 2, 64>(p, batch, st);
+    return launch_tiled_cfg<256, 256, 2, 4, EPI, 2, 64, 3>(p, batch, st);
   }
 }
 

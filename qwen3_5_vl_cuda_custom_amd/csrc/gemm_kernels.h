@@ -409,7 +409,7 @@ __device__ __forceinline__ int dma_swz(int r) {
 // q + 1 are read while the MFMAs of step q run, and each stage's barrier sits
 // before its last step's MFMAs (which overlap the first reads of the next
 // stage), so no wave starts a stage waiting on LDS.
-template <int BM, int BN, int WM, int WN, int EPI, bool GROUPED, int NST, int BKT>
+template <int BM, int BN, int WM, int WN, int EPI, bool GROUPED, int NST, int BKT, int NSTW = NST>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmParams p) {
   constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM;
@@ -422,14 +422,18 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
   constexpr int BN_OUT = (EPI == kEpiSwiGLU) ? BN / 2 : BN;
   constexpr int CH = BKT / 8;              // 16-byte chunks per LDS row
   constexpr int KS = BKT / 16;             // MFMA K steps per stage
-  constexpr int kStage = (BM + BN) * BKT;  // elements per ring slot
+  // X slots (NST) and W slots (NSTW, at most one more: weights come from HBM,
+  // activations from L2, so W is issued one stage further ahead).
+  static_assert(NSTW == NST || NSTW == NST + 1, "W ring depth");
+  constexpr int kStageX = BM * BKT, kStageW = BN * BKT;  // elements per ring slot
+  constexpr int kRing = NST * kStageX + NSTW * kStageW;
   constexpr int RPI = 64 / CH;             // rows per DMA instruction
   constexpr int DX = BM / RPI, DW = BN / RPI;
   static_assert((DX + DW) % NW == 0 && DX % NW == 0, "DMA instructions must split evenly over the waves");
   constexpr int PX = DX / NW, PW = DW / NW;  // per wave and stage
   static_assert(TN * TM >= TN + TM, "the interleave needs more MFMAs than fragment reads");
 
-  __shared__ __attribute__((aligned(1024))) bf16 smem[NST * kStage];
+  __shared__ __attribute__((aligned(1024))) bf16 smem[kRing];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -501,22 +505,37 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
       make_rsrc(tc.X, p.gather ? (int64_t)p.M_src * ldx * 2 : (int64_t)(m_begin + rows_m) * ldx * 2);
   const uint32_t lbase = lds_addr(smem);
 
-  auto issue = [&](int kt) {
-    const int k0 = kt * BKT;
-    const uint32_t sb = lbase + (uint32_t)((kt % NST) * kStage * 2);
+  // LDS byte address of stage kt's X / W slot.
+  auto xslot = [&](int kt) { return lbase + (uint32_t)((kt % NST) * kStageX * 2); };
+  auto wslot = [&](int kt) { return lbase + (uint32_t)((NST * kStageX + (kt % NSTW) * kStageW) * 2); };
+  auto issue_x = [&](int kt) {
+    const int k = kt * BKT + dc * 8;
+    const uint32_t sb = xslot(kt);
 #pragma unroll
     for (int i = 0; i < PX; ++i) {
-      const int k = k0 + dc * 8;
       const uint32_t off = (k < K && xoff[i] != kOOB) ? xoff[i] + (uint32_t)k * 2u : kOOB;
       dma16(rx, off, sb + (uint32_t)((wave + NW * i) * 1024));
     }
+  };
+  auto issue_w = [&](int kt) {
+    const int k = kt * BKT + dc * 8;
+    const uint32_t sb = wslot(kt);
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
-      const int j = wave + NW * i;
-      const int k = k0 + dc * 8;
       const uint32_t off = (k < K && woff[i] != kOOB) ? woff[i] + (uint32_t)k * 2u : kOOB;
-      dma16(make_rsrc(wsrc[i], (int64_t)wrows[i] * ldw * 2), off, sb + (uint32_t)(BM * BKT * 2 + j * 1024));
+      dma16(make_rsrc(wsrc[i], (int64_t)wrows[i] * ldw * 2), off, sb + (uint32_t)((wave + NW * i) * 1024));
     }
+  };
+  // The DMAs are issued in groups, one per stage: the group issued at the end
+  // of stage j is X(j + NST) then W(j + NSTW) (each into the slot stage j has
+  // just released). Stage kt + 1 has landed once every DMA up to X(kt + 1) has
+  // (W(kt + 1) went out no later); the NST - 2 groups after it, and with
+  // NSTW > NST the W of its own group, may still be in flight (vmcnt retires
+  // in issue order).
+  constexpr int kWait = (NST - 2) * (PX + PW) + (NSTW > NST ? PW : 0);
+  auto issue_group = [&](int j) {
+    if (j + NST >= 0) issue_x(j + NST);
+    issue_w(j + NSTW);
   };
 
   WaveAcc<TN, TM> acc;
@@ -525,8 +544,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
   const int rn = wn * WTN, rm = wm * WTM;
   bf16x8 fa[2][TN], fb[2][TM];
   auto read = [&](int buf, int kt, int ks) {
-    const bf16* sx = smem + (kt % NST) * kStage;
-    const bf16* sw = sx + BM * BKT;
+    const bf16* sx = smem + (kt % NST) * kStageX;
+    const bf16* sw = smem + NST * kStageX + (kt % NSTW) * kStageW;
     const int c = ks * 2 + h;
 #pragma unroll
     for (int i = 0; i < TN; ++i) {
@@ -548,22 +567,20 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
   // The stage's last k16 step with the next DMAs spread between its MFMAs
   // (one DMA after each MFMA, order pinned), so the matrix core is not idle
   // while a burst of DMA instructions issues after the barrier.
-  auto last_step = [&](int buf, int kn) {
+  auto last_step = [&](int buf, int kt) {  // issues the group of stage kt: X(kt + NST), W(kt + NSTW)
     constexpr int ND = PX + PW;
-    const int k0 = kn * BKT;
-    const uint32_t sb = lbase + (uint32_t)((kn % NST) * kStage * 2);
+    const int kx = (kt + NST) * BKT + dc * 8, kw = (kt + NSTW) * BKT + dc * 8;
+    const uint32_t sbx = xslot(kt + NST), sbw = wslot(kt + NSTW);
     uint32_t doff[ND], dlds[ND];
 #pragma unroll
     for (int i = 0; i < PX; ++i) {
-      const int k = k0 + dc * 8;
-      doff[i] = (k < K && xoff[i] != kOOB) ? xoff[i] + (uint32_t)k * 2u : kOOB;
-      dlds[i] = sb + (uint32_t)((wave + NW * i) * 1024);
+      doff[i] = (kx < K && xoff[i] != kOOB) ? xoff[i] + (uint32_t)kx * 2u : kOOB;
+      dlds[i] = sbx + (uint32_t)((wave + NW * i) * 1024);
     }
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
-      const int k = k0 + dc * 8;
-      doff[PX + i] = (k < K && woff[i] != kOOB) ? woff[i] + (uint32_t)k * 2u : kOOB;
-      dlds[PX + i] = sb + (uint32_t)(BM * BKT * 2 + (wave + NW * i) * 1024);
+      doff[PX + i] = (kw < K && woff[i] != kOOB) ? woff[i] + (uint32_t)kw * 2u : kOOB;
+      dlds[PX + i] = sbw + (uint32_t)((wave + NW * i) * 1024);
     }
     auto dma = [&](int d) {
       if (d < PX)
@@ -595,10 +612,10 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
   };
 
 #pragma unroll
-  for (int s = 0; s < NST - 1; ++s) issue(s);
-  vm_wait<(NST - 2) * (PX + PW)>();
+  for (int j = -NSTW; j <= -2; ++j) issue_group(j);
+  vm_wait<kWait>();  // stage 0 has landed
   __syncthreads();
-  issue(NST - 1);
+  issue_group(-1);
   read(0, 0, 0);
   for (int kt = 0; kt < nk; ++kt) {
 #pragma unroll
@@ -608,17 +625,17 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
         mma(ks & 1);
         interleave();
       } else {
-        vm_wait<(NST - 2) * (PX + PW)>();  // this wave's part of stage kt + 1 has landed
+        vm_wait<kWait>();                   // this wave's part of stage kt + 1 has landed
         __syncthreads();                    // every wave's; nobody reads stage kt any more
         read((ks + 1) & 1, kt + 1, 0);
-        last_step(ks & 1, kt + NST);        // MFMAs with the DMAs of stage kt + NST (into stage kt's slot) between them
+        last_step(ks & 1, kt);              // MFMAs with stage kt's DMA group (into the slots it released) between them
       }
     }
   }
   vm_wait<0>();  // the trailing zero-fill DMAs must land before the block's LDS is reused
 
-  store_tile_lds<BM, BN_OUT, WTM, WTN, TN, TM, EPI, NW, NST * kStage * 2>(p, tc, acc.c, wm, wn, lane,
-                                                                          reinterpret_cast<float*>(smem));
+  store_tile_lds<BM, BN_OUT, WTM, WTN, TN, TM, EPI, NW, kRing * 2>(p, tc, acc.c, wm, wn, lane,
+                                                                  reinterpret_cast<float*>(smem));
 }
 
 }  // namespace q3
