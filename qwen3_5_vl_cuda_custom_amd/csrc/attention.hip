@@ -727,11 +727,13 @@ __device__ __forceinline__ void scale_acc(floatx16& acc, float alpha) {
 }
 }  // namespace fwdp
 
+template <int D, bool MHA>
 __global__ __launch_bounds__(512) void flash_fwd_pipe_kernel(const AttnParams p) {
   using namespace fwdp;
-  constexpr int D = 128;
-  constexpr int KSTEPS = D / 16;
-  constexpr int OT = D / 32;
+  static_assert(D % 8 == 0 && D <= kRowK, "head_dim");
+  constexpr int KSTEPS = (D + 15) / 16;  // MFMA k-steps over the (zero-padded) head dim
+  constexpr int OT = (D + 31) / 32;      // 32-row tiles of O^T
+  constexpr int QBLK = MHA ? 4 * kQ : kQ;  // queries per block
   constexpr int PERW = 2;  // DMA instructions per wave per tile (1 K + 1 V)
   static_assert(kAhead + 2 == kPipeStages, "step t reuses the slot of tile t - 2");
   __shared__ __attribute__((aligned(1024))) bf16 ring[kPipeStages * 2 * kTile];
@@ -741,38 +743,57 @@ __global__ __launch_bounds__(512) void flash_fwd_pipe_kernel(const AttnParams p)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31;
   const int h = lane >> 5;
-  const int hw = wave & 3, qh = wave >> 2;  // head of the group's 4, query half
+  // GQA: the group's 4 heads x 2 query halves; MHA: one head, 4 query
+  // quarters x 2 halves (every wave of the block shares the K/V tiles).
+  const int hw = wave & 3, qh = wave >> 2;
 
-  const int Sq = p.Sq, Sk = p.Sk;
+  int Sq = p.Sq, Sk = p.Sk;
   const bool causal = p.causal != 0;
-  const int n_qt = (Sq + kQ - 1) / kQ;
+  const int n_qt = (Sq + QBLK - 1) / QBLK;
   const int qt = causal ? (n_qt - 1 - (int)blockIdx.y) : (int)blockIdx.y;  // heaviest first
-  const int hgroups = p.groups / 4;
   int yb = blockIdx.x;
-  const int hg = yb % hgroups;
-  yb /= hgroups;
+  int hg = 0;
+  if constexpr (!MHA) {
+    hg = yb % (p.groups / 4);
+    yb /= p.groups / 4;
+  }
   const int kvh = yb % p.Hkv;
   const int b = yb / p.Hkv;
-  const int hq = kvh * p.groups + hg * 4 + hw;
-  const int q0 = qt * kQ;
-  const int qw0 = q0 + 32 * qh;  // this wave's first query
+  const int hq = MHA ? kvh : kvh * p.groups + hg * 4 + hw;
+  // Packed sequences: this block's sequence starts at row `row0` of every
+  // tensor and has Sq = Sk = its own length; tiles past it have nothing to do.
+  int64_t qb_off = (int64_t)b * p.qb, kb_off = (int64_t)b * p.kb, vb_off = (int64_t)b * p.vb,
+          ob_off = (int64_t)b * p.ob;
+  if (p.cu_seqlens) {
+    const int row0 = __builtin_amdgcn_readfirstlane(p.cu_seqlens[b]);
+    Sq = Sk = __builtin_amdgcn_readfirstlane(p.cu_seqlens[b + 1]) - row0;
+    qb_off = (int64_t)row0 * p.qs;
+    kb_off = (int64_t)row0 * p.ks;
+    vb_off = (int64_t)row0 * p.vs;
+    ob_off = (int64_t)row0 * p.os;
+    if (qt * QBLK >= Sq) return;  // uniform over the block
+  }
+  const int q0 = qt * QBLK;
+  const int qw0 = MHA ? q0 + 64 * hw + 32 * qh : q0 + 32 * qh;  // this wave's first query
   const int off = p.q_off ? __builtin_amdgcn_readfirstlane(max(p.q_off[b], 0)) : 0;
   const int Skb = p.q_off ? min(Sk, off + Sq) : Sk;  // keys of this sequence
-  const int klimit = causal ? min(Skb, q0 + kQ + off) : Skb;
+  const int klimit = causal ? min(Skb, q0 + QBLK + off) : Skb;
   const int nkt = (klimit + kKeys - 1) / kKeys;
 
-  const bf16* kbase = p.k + (int64_t)b * p.kb + (int64_t)kvh * p.kh;
-  const bf16* vbase = p.v + (int64_t)b * p.vb + (int64_t)kvh * p.vh;
+  const bf16* kbase = p.k + kb_off + (int64_t)kvh * p.kh;
+  const bf16* vbase = p.v + vb_off + (int64_t)kvh * p.vh;
   const int ks2 = (int)p.ks * 2, vs2 = (int)p.vs * 2;
   const __amdgpu_buffer_rsrc_t krs = q3::make_rsrc(kbase, (int64_t)(Sk - 1) * ks2 + D * 2);
   const __amdgpu_buffer_rsrc_t vrs = q3::make_rsrc(vbase, (int64_t)(Sk - 1) * vs2 + D * 2);
   const uint32_t lbase = q3::lds_addr(ring);
 
-  // Wave w loads rows 4w .. 4w + 3 of tile t's K and V (one instruction each).
+  // Wave w loads rows 4w .. 4w + 3 of tile t's K and V (one instruction each);
+  // chunks at or past D load as zeros (which pads D to the MFMA k-step).
   const int cs = lane & 15;
   const int r0 = 4 * wave + (lane >> 4);
-  const uint32_t kc0 = (uint32_t)((cs ^ (r0 & 15)) << 4);
-  const uint32_t vc0 = (uint32_t)((cs ^ ((r0 & 3) << 2)) << 4);
+  const int kch = cs ^ (r0 & 15), vch = cs ^ ((r0 & 3) << 2);  // global chunk each lane fetches
+  const uint32_t kc0 = (uint32_t)(kch << 4) | (kch * 8 < D ? 0u : q3::kOOB);
+  const uint32_t vc0 = (uint32_t)(vch << 4) | (vch * 8 < D ? 0u : q3::kOOB);
   auto issue = [&](int t) {
     const uint32_t lk = lbase + (uint32_t)((t % kPipeStages) * 2 * kTile * 2) + (uint32_t)(4 * wave * kRowK * 2);
     const uint32_t lv = lk + kTile * 2;
@@ -786,10 +807,11 @@ __global__ __launch_bounds__(512) void flash_fwd_pipe_kernel(const AttnParams p)
   bf16x8 qf[KSTEPS];
   {
     const int qi = qw0 + l32;
-    const bf16* qrow = p.q + (int64_t)b * p.qb + (int64_t)hq * p.qh + (int64_t)qi * p.qs;
+    const bf16* qrow = p.q + qb_off + (int64_t)hq * p.qh + (int64_t)qi * p.qs;
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks)
-      qf[ks] = qi < Sq ? *reinterpret_cast<const bf16x8*>(qrow + ks * 16 + 8 * h) : bf16x8{};
+      qf[ks] = (qi < Sq && ks * 16 + 8 * h < D) ? *reinterpret_cast<const bf16x8*>(qrow + ks * 16 + 8 * h)
+                                                : bf16x8{};
   }
 
   floatx16 o[OT];
@@ -885,24 +907,25 @@ __global__ __launch_bounds__(512) void flash_fwd_pipe_kernel(const AttnParams p)
     // softmax to hide behind.
     const bf16* sV = ring + ((t - 1) % kPipeStages) * 2 * kTile + kTile;
     const bf16* sK = ring + ((t + 1) % kPipeStages) * 2 * kTile;
-    short4v vlo[8], vhi[8];
+    constexpr int NPV = 2 * OT, NU = NPV + KSTEPS;  // MFMA slots: PV (j, dt), then QK (ks)
+    short4v vlo[NPV], vhi[NPV];
     bf16x8 kf[KSTEPS];
-    auto read_u = [&](int u) {  // u: 16 MFMA slots; PV slots 0-7 (j, dt), QK slots 8-15 (ks)
-      if (u < 8) {
+    auto read_u = [&](int u) {
+      if (u < NPV) {
         const int j = u / OT, dt = u % OT;
         vlo[u] = lds_read_tr16(sV + voff[dt] + 16 * j * kRowK);
         vhi[u] = lds_read_tr16(sV + voff[dt] + (16 * j + 8) * kRowK);
       } else {
-        kf[u - 8] = *reinterpret_cast<const bf16x8*>(sK + koff[u - 8]);
+        kf[u - NPV] = *reinterpret_cast<const bf16x8*>(sK + koff[u - NPV]);
       }
     };
     auto mma_u = [&](int u) {
-      if (u < 8) {
+      if (u < NPV) {
         const int j = u / OT, dt = u % OT;
         const short8v a8 = {vlo[u][0], vlo[u][1], vlo[u][2], vlo[u][3], vhi[u][0], vhi[u][1], vhi[u][2], vhi[u][3]};
         o[dt] = mfma32x32x16(__builtin_bit_cast(bf16x8, a8), pp[j], o[dt]);
       } else {
-        const int ks = u - 8;
+        const int ks = u - NPV;
         nxt = mfma32x32x16(kf[ks], qf[ks], ks == 0 ? floatx16{} : nxt);
       }
     };
@@ -917,10 +940,12 @@ __global__ __launch_bounds__(512) void flash_fwd_pipe_kernel(const AttnParams p)
     read_u(1);
     read_u(2);
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      if (u + 3 < 16) read_u(u + 3);
+    for (int u = 0; u < NU; ++u) {
+      if (u + 3 < NU) read_u(u + 3);
       mma_u(u);
-      exp_i(u);
+      // the tile's 16 exponentials spread over the NU slots
+#pragma unroll
+      for (int r = u * 16 / NU; r < (u + 1) * 16 / NU; ++r) exp_i(r);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -965,18 +990,20 @@ __global__ __launch_bounds__(512) void flash_fwd_pipe_kernel(const AttnParams p)
     const float l = lsum + __shfl_xor(lsum, 32, 64);
     if (qi < Sq) {
       const float inv_l = l > 0.f ? 1.0f / l : 0.f;
-      bf16* orow = p.o + (int64_t)b * p.ob + (int64_t)hq * p.oh + (int64_t)qi * p.os;
+      bf16* orow = p.o + ob_off + (int64_t)hq * p.oh + (int64_t)qi * p.os;
 #pragma unroll
       for (int dt = 0; dt < OT; ++dt)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int d = dt * 32 + 8 * g + 4 * h;
+          if (d >= D) continue;  // rows of O^T past D come from the zero padding
           bf16x4 v4;
 #pragma unroll
           for (int e = 0; e < 4; ++e) v4[e] = f2bf(o[dt][4 * g + e] * inv_l);
           *reinterpret_cast<bf16x4*>(orow + d) = v4;
         }
-      if (p.lse && h == 0) p.lse[((int64_t)b * p.Hq + hq) * Sq + qi] = (m + log2f(l)) * 0.6931471805599453f;
+      if (p.lse && h == 0 && !p.cu_seqlens)
+        p.lse[((int64_t)b * p.Hq + hq) * Sq + qi] = (m + log2f(l)) * 0.6931471805599453f;
     }
   }
 }
@@ -1033,13 +1060,23 @@ __global__ __launch_bounds__(128) void flash_generic_kernel(const AttnParams p, 
 
 bool mfma_head_dim(int64_t D) { return D == 64 || D == 72 || D == 80 || D == 96 || D == 128; }
 
-int launch_fwd_pipe(const AttnParams& p, hipStream_t st) {
-  const int n_qt = (int)q3_cdiv(p.Sq, fwdp::kQ);
+template <int D, bool MHA>
+int launch_fwd_pipe_t(const AttnParams& p, hipStream_t st) {
+  const int n_qt = (int)q3_cdiv(p.Sq, MHA ? 4 * fwdp::kQ : fwdp::kQ);
   Q3_REQUIRE(n_qt <= 65535, Q3_ERR_UNSUPPORTED);
-  dim3 grid((unsigned)(p.B * p.Hkv * (p.groups / 4)), (unsigned)n_qt);
-  hipLaunchKernelGGL(flash_fwd_pipe_kernel, grid, dim3(512), 0, st, p);
+  dim3 grid((unsigned)(p.B * p.Hkv * (MHA ? 1 : p.groups / 4)), (unsigned)n_qt);
+  hipLaunchKernelGGL((flash_fwd_pipe_kernel<D, MHA>), grid, dim3(512), 0, st, p);
   Q3_LAUNCH_CHECK();
   return Q3_OK;
+}
+
+// The pipelined kernel takes GQA groups that are a multiple of 4, and MHA
+// (groups 1) when the (longest) sequence fills most of its 256-query blocks.
+bool pipe_eligible(const AttnParams& p) { return p.groups % 4 == 0 || (p.groups == 1 && p.Sq >= 192); }
+
+template <int D>
+int launch_fwd_pipe(const AttnParams& p, hipStream_t st) {
+  return p.groups == 1 ? launch_fwd_pipe_t<D, true>(p, st) : launch_fwd_pipe_t<D, false>(p, st);
 }
 
 template <int D>
@@ -1127,21 +1164,22 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
   int rc = Q3_OK;
   // The MFMA path addresses K with 32-bit buffer offsets.
   if (dtype == Q3_BF16 && mfma_head_dim(D) && aligned && Sk > 0 && (Sk + 1) * strides[5] * 2 < 0x7fffffffLL) {
+    const bool pipe = pipe_eligible(p);
     switch (D) {
       case 64:
-        rc = launch_fwd<64>(p, st);
+        rc = pipe ? launch_fwd_pipe<64>(p, st) : launch_fwd<64>(p, st);
         break;
       case 72:
-        rc = launch_fwd<72>(p, st);
+        rc = pipe ? launch_fwd_pipe<72>(p, st) : launch_fwd<72>(p, st);
         break;
       case 80:
-        rc = launch_fwd<80>(p, st);
+        rc = pipe ? launch_fwd_pipe<80>(p, st) : launch_fwd<80>(p, st);
         break;
       case 96:
-        rc = launch_fwd<96>(p, st);
+        rc = pipe ? launch_fwd_pipe<96>(p, st) : launch_fwd<96>(p, st);
         break;
-      default:  // the pipelined kernel has no packed-sequence form
-        rc = (p.groups % 4 == 0 && !cu_seqlens) ? launch_fwd_pipe(p, st) : launch_fwd<128>(p, st);
+      default:
+        rc = pipe ? launch_fwd_pipe<128>(p, st) : launch_fwd<128>(p, st);
     }
   } else {
     const int64_t rows = B * Hq * Sq;
