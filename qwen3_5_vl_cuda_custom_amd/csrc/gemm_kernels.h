@@ -438,8 +438,11 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave % WM;
-  const int wn = wave / WM;
+  // Waves w and w + 4 share a SIMD; with wm = wave / WN each SIMD holds waves of
+  // different m-ranges, so a tile whose last rows are empty (MoE remainders, M
+  // edges) leaves no SIMD with all of its waves busy while others idle.
+  const int wn = wave % WN;
+  const int wm = wave / WN;
 
   TileCtx tc;
   if (!tile_ctx<BM, BN_OUT, EPI, GROUPED>(p, tc)) return;
@@ -543,7 +546,11 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
   const int l32 = lane & 31, h = lane >> 5;
   const int rn = wn * WTN, rm = wm * WTM;
   bf16x8 fa[2][TN], fb[2][TM];
-  auto read = [&](int buf, int kt, int ks) {
+  // ACTIVE: the wave's m-range holds rows of the tile. A wave without rows still
+  // issues its share of the DMAs and joins every barrier, but reads no fragments
+  // and issues no MFMAs (its accumulators stay zero and are never stored).
+  auto read = [&](auto active_c, int buf, int kt, int ks) {
+    if constexpr (!decltype(active_c)::value) return;
     const bf16* sx = smem + (kt % NST) * kStageX;
     const bf16* sw = smem + NST * kStageX + (kt % NSTW) * kStageW;
     const int c = ks * 2 + h;
@@ -558,7 +565,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
       fb[buf][j] = *reinterpret_cast<const bf16x8*>(sx + r * BKT + ((c ^ dma_swz<BKT>(r)) << 3));
     }
   };
-  auto mma = [&](int buf) {
+  auto mma = [&](auto active_c, int buf) {
+    if constexpr (!decltype(active_c)::value) return;
 #pragma unroll
     for (int i = 0; i < TN; ++i)
 #pragma unroll
@@ -567,7 +575,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
   // The stage's last k16 step with the next DMAs spread between its MFMAs
   // (one DMA after each MFMA, order pinned), so the matrix core is not idle
   // while a burst of DMA instructions issues after the barrier.
-  auto last_step = [&](int buf, int kt) {  // issues the group of stage kt: X(kt + NST), W(kt + NSTW)
+  auto last_step = [&](auto active_c, int buf, int kt) {  // issues the group of stage kt: X(kt + NST), W(kt + NSTW)
+    constexpr bool kActive = decltype(active_c)::value;
     constexpr int ND = PX + PW;
     const int kx = (kt + NST) * BKT + dc * 8, kw = (kt + NSTW) * BKT + dc * 8;
     const uint32_t sbx = xslot(kt + NST), sbw = wslot(kt + NSTW);
@@ -590,14 +599,16 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
     };
     __builtin_amdgcn_sched_barrier(0);
     int d = 0;
+    if constexpr (kActive) {
 #pragma unroll
-    for (int i = 0; i < TN; ++i)
+      for (int i = 0; i < TN; ++i)
 #pragma unroll
-      for (int j = 0; j < TM; ++j) {
-        acc.c[i][j] = mfma32x32x16(fa[buf][i], fb[buf][j], acc.c[i][j]);
-        if (d < ND) dma(d++);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+        for (int j = 0; j < TM; ++j) {
+          acc.c[i][j] = mfma32x32x16(fa[buf][i], fb[buf][j], acc.c[i][j]);
+          if (d < ND) dma(d++);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+    }
 #pragma unroll
     for (; d < ND; ++d) dma(d);
   };
@@ -616,22 +627,28 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
   vm_wait<kWait>();  // stage 0 has landed
   __syncthreads();
   issue_group(-1);
-  read(0, 0, 0);
-  for (int kt = 0; kt < nk; ++kt) {
+  auto main_loop = [&](auto active_c) {
+    read(active_c, 0, 0, 0);
+    for (int kt = 0; kt < nk; ++kt) {
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      if (ks + 1 < KS) {
-        read((ks + 1) & 1, kt, ks + 1);
-        mma(ks & 1);
-        interleave();
-      } else {
-        vm_wait<kWait>();                   // this wave's part of stage kt + 1 has landed
-        __syncthreads();                    // every wave's; nobody reads stage kt any more
-        read((ks + 1) & 1, kt + 1, 0);
-        last_step(ks & 1, kt);              // MFMAs with stage kt's DMA group (into the slots it released) between them
+      for (int ks = 0; ks < KS; ++ks) {
+        if (ks + 1 < KS) {
+          read(active_c, (ks + 1) & 1, kt, ks + 1);
+          mma(active_c, ks & 1);
+          if constexpr (decltype(active_c)::value) interleave();
+        } else {
+          vm_wait<kWait>();                   // this wave's part of stage kt + 1 has landed
+          __syncthreads();                    // every wave's; nobody reads stage kt any more
+          read(active_c, (ks + 1) & 1, kt + 1, 0);
+          last_step(active_c, ks & 1, kt);    // MFMAs with stage kt's DMA group (into the slots it released) between them
+        }
       }
     }
-  }
+  };
+  if (rm < rows_m)
+    main_loop(std::true_type{});
+  else
+    main_loop(std::false_type{});
   vm_wait<0>();  // the trailing zero-fill DMAs must land before the block's LDS is reused
 
   store_tile_lds<BM, BN_OUT, WTM, WTN, TN, TM, EPI, NW, kRing * 2>(p, tc, acc.c, wm, wn, lane,

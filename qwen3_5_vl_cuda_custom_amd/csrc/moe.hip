@@ -31,8 +31,16 @@ using namespace q3;
 
 namespace {
 
-constexpr int kMoeBM = 320;
-constexpr int kMoeBN = 256;  // weight rows per tile (SwiGLU: 128 gate/up output columns)
+// Expert GEMM tiles: 256 rows x 256 weight rows (SwiGLU: 128 gate/up output
+// columns), 8 waves, 64-wide K stages in 2 X and 3 W slots (the whole 160 KB of
+// LDS). Every expert's weights stream from HBM exactly once per layer, so W is
+// issued two stages ahead. Measured at T=4096, H=2048, I=768, E=128, top-8
+// (random routing, 193 m-tiles): gate/up 274 us, down 184 us, against 312 and
+// 182 us for 320-row tiles with 2 W slots (one m-tile per expert but 1.42x the
+// time per tile wave); with 256 rows per expert, 232 and 156 against 328 and 183.
+constexpr int kMoeBM = 256;
+constexpr int kMoeBN = 256;
+constexpr int kMoeNSTW = 3;
 
 // ------------------------------------------------------------------ routing
 template <int MAXV>
@@ -702,7 +710,7 @@ int q3_moe_experts(const void* x, const void* gate_up, const void* down, const i
     p.expert_stride_w = 2 * I * H;
     const int64_t ntn = q3_cdiv(I, kMoeBN / 2);
     // Grid: a multiple of 8 (the kernel deals the valid tiles out per XCD).
-    hipLaunchKernelGGL((gemm_bf16_dma_kernel<kMoeBM, kMoeBN, 2, 4, kEpiSwiGLU, true, 2, 64>),
+    hipLaunchKernelGGL((gemm_bf16_dma_kernel<kMoeBM, kMoeBN, 2, 4, kEpiSwiGLU, true, 2, 64, kMoeNSTW>),
                        dim3((unsigned)(q3_cdiv(max_tiles * ntn, 8) * 8)),
                        dim3(512), 0, st, p);
     Q3_LAUNCH_CHECK();
@@ -726,7 +734,7 @@ int q3_moe_experts(const void* x, const void* gate_up, const void* down, const i
     p.n_tiles_total = w.n_tiles;
     p.expert_stride_w = H * I;
     const int64_t ntn = q3_cdiv(H, kMoeBN);
-    hipLaunchKernelGGL((gemm_bf16_dma_kernel<kMoeBM, kMoeBN, 2, 4, kEpiRowScale, true, 2, 64>),
+    hipLaunchKernelGGL((gemm_bf16_dma_kernel<kMoeBM, kMoeBN, 2, 4, kEpiRowScale, true, 2, 64, kMoeNSTW>),
                        dim3((unsigned)(q3_cdiv(max_tiles * ntn, 8) * 8)), dim3(512), 0, st, p);
     Q3_LAUNCH_CHECK();
   }
