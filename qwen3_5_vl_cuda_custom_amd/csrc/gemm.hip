@@ -120,28 +120,39 @@ int launch_tiled_cfg(GemmParams p, int64_t batch, hipStream_t st) {
 // blocks per CU) 0.75. The third W slot (weights are read from HBM once per
 // layer, activations from L2): M=4096 q/k/v 181 -> 170 us, gate/up 650 ->
 // 633 us with weights rotated past the MALL.
+//
+// When the 128x128 tiles fit one block per CU (at most 256 of them) they take
+// a deeper ring instead: 64-wide K stages in 4 X and 5 W slots (147 KB).
+// Measured against the 2-blocks-per-CU ring (32-wide stages x 4): M=3136 N=1152
+// K=4304 60.9 -> 49.3 us, M=1024 N=4096 K=12288 147.7 -> 120.1 us, K=4096
+// 48.1 -> 43.7 us, shorter K unchanged; such a wave of tiles takes 0.46-0.56
+// of the time of one wave of 256x256 tiles (estimate: 128 * 128 / 0.47).
+// Rings of 6 or 8 32-wide stages were no faster than 4.
 template <int EPI>
 int launch_tiled(GemmParams p, int64_t batch, hipStream_t st) {
   constexpr int kCUs = 256;
   auto waves = [](int64_t tiles, int64_t slots) { return (double)q3_cdiv(tiles, slots); };
   const int bo = EPI == kEpiSwiGLU ? 128 : 256;
   const double cost_a = waves(q3_cdiv(p.M, 256) * q3_cdiv(p.N, bo) * batch, kCUs) * 256.0 * 256.0;
-  const double cost_c =
-      waves(q3_cdiv(p.M, 128) * q3_cdiv(p.N, bo / 2) * batch, 2 * kCUs) * 2.0 * 128.0 * 128.0 / 0.75;
+  const int64_t tiles_c = q3_cdiv(p.M, 128) * q3_cdiv(p.N, bo / 2) * batch;
+  const bool c_deep = tiles_c <= kCUs;  // one 128x128 block per CU: the deep ring
+  const double cost_c = c_deep ? 128.0 * 128.0 / 0.47 : waves(tiles_c, 2 * kCUs) * 2.0 * 128.0 * 128.0 / 0.75;
   // 128x256 only when it fills at least 3/4 of the CUs: with fewer tiles the
-  // 128x128 tiles, one per CU, run faster than the per-slot estimate assumes
-  // (measured: M=1024 N=4096 K=4096, 128 tiles: 56.8 us against 44.8 us for
-  // 256 tiles of 128x128; M=1024 N=6144, 192 tiles: 58.8 us against 70.1).
+  // 128x128 tiles, one per CU, run faster.
   const int64_t tiles_d = q3_cdiv(p.M, 128) * q3_cdiv(p.N, bo) * batch;
   const double cost_d = 4 * tiles_d >= 3 * kCUs ? waves(tiles_d, kCUs) * 128.0 * 256.0 / 0.9 : 1e300;
+  auto launch_c = [&]() {
+    return c_deep ? launch_tiled_cfg<128, 128, 2, 2, EPI, 4, 64, 5>(p, batch, st)
+                  : launch_tiled_cfg<128, 128, 2, 2, EPI, 4, 32>(p, batch, st);
+  };
   if constexpr (EPI == kEpiSwiGLU) {
-    if (cost_c < cost_a && cost_c < cost_d) return launch_tiled_cfg<128, 128, 2, 2, EPI, 4, 32>(p, batch, st);
+    if (cost_c < cost_a && cost_c < cost_d) return launch_c();
     if (cost_d < cost_a) return launch_tiled_cfg<128, 256, 2, 4, EPI, 3, 64>(p, batch, st);
     return launch_tiled_cfg<256, 256, 2, 4, EPI, 2, 64, 3>(p, batch, st);
   } else {
     const double cost_b = waves(q3_cdiv(p.M, 256) * q3_cdiv(p.N, 192) * batch, kCUs) * 256.0 * 192.0 / 0.95;
     const double best = std::min(std::min(cost_a, cost_b), std::min(cost_c, cost_d));
-    if (cost_c == best) return launch_tiled_cfg<128, 128, 2, 2, EPI, 4, 32>(p, batch, st);
+    if (cost_c == best) return launch_c();
     if (cost_b == best) return launch_tiled_cfg<256, 192, 4, 2, EPI, 2, 64, 3>(p, batch, st);
     if (cost_d == best) return launch_tiled_cfg<128, 256, 2, 4, EPI, 3, 64>(p, batch, st);
     return launch_tiled_cfg<256, 256, 2, 4, EPI, 2, 64, 3>(p, batch, st);

@@ -31,15 +31,20 @@ __device__ __forceinline__ bf16x8 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32
 
 // 16 bytes per lane from the buffer at `voff` into LDS at byte address
 // `lds_byte` + 16 * lane. Issued as inline asm (m0 holds the LDS address) so the
-// compiler inserts no wait of its own; callers fence with vm_wait<N>().
+// compiler inserts no wait of its own; callers fence with vm_wait<N>(). The LDS
+// address is wave-uniform by contract; it is pinned to a scalar register here,
+// since the compiler can leave a uniform value in a vector register (the "s"
+// constraint then fails to assemble).
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t lds_byte) {
-  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds" ::"v"(voff), "s"(lds_byte), "s"(r)
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_byte);
+  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds" ::"v"(voff), "s"(m0v), "s"(r)
                : "memory");
 }
 // dma16 with the non-temporal hint, for data read exactly once (the KV cache
 // in decode): streaming it past the caches keeps HBM reads near their peak.
 __device__ __forceinline__ void dma16_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t lds_byte) {
-  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen nt lds" ::"v"(voff), "s"(lds_byte), "s"(r)
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_byte);
+  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen nt lds" ::"v"(voff), "s"(m0v), "s"(r)
                : "memory");
 }
 template <int N>

@@ -42,6 +42,7 @@ def f32(t):
     (1024, 1536, 2048, False),
     (4096, 4096, 512, True),     # >= 256 tiles of 256x256: the direct-to-LDS kernel
     (4000, 4200, 520, True),     # same kernel with ragged M, N and a K tail
+    (4100, 3840, 512, True),     # 256x256 tiles whose last m-tile has 4 rows: its upper waves skip their MFMAs
 ])
 def test_matmul_bf16(M, N, Kd, bias):
     x = rnd(M, Kd, seed=1)
@@ -65,7 +66,7 @@ def test_matmul_residual_fused():
     assert_bf16_close(y2, O.linear(f32(x[:16]), f32(w)) + f32(r[:16]), what="skinny matmul+residual")
 
 
-@pytest.mark.parametrize("M", [7, 32, 300, 1024, 8192])
+@pytest.mark.parametrize("M", [7, 32, 300, 1024, 4100, 8192])
 def test_matmul_swiglu(M):
     x, wg, wu = rnd(M, 1024, seed=7), rnd(1536, 1024, seed=8, std=0.02), rnd(1536, 1024, seed=9, std=0.02)
     y = K.matmul_swiglu(gpu(x), gpu(wg), gpu(wu))
@@ -549,6 +550,28 @@ def test_moe_experts_against_oracle_loop():
     pf = {n: f32(t) for n, t in p.items()}
     ref, _ = sparse_moe(f32(x), pf, top_k=k, router_logits=logits.float().cpu())
     assert_bf16_close(out, ref[0], what="moe_experts")
+
+
+def test_moe_experts_skewed_routing():
+    """One expert takes every token (600 rows: m-tiles of 256, 256 and 88 rows, the last with
+    an empty upper half), the second choice spreads over the others (~86 rows each)."""
+    from oracle.layers import sparse_moe
+    T, H, I, E, k = 600, 256, 128, 8, 2
+    g = torch.Generator().manual_seed(71)
+    x = torch.randn(1, T, H, generator=g).to(torch.bfloat16)
+    p = {"gate_weight": (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16),
+         "gate_up_proj": (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(torch.bfloat16),
+         "down_proj": (torch.randn(E, H, I, generator=g) * 0.02).to(torch.bfloat16)}
+    logits = torch.randn(T, E, generator=g)
+    logits[:, 0] += 10.0
+    logits = logits.to(torch.bfloat16)
+    idx, w = K.moe_route(gpu(logits), k, True)
+    counts = torch.bincount(idx.long().flatten().cpu(), minlength=E)
+    assert counts[0].item() == T and counts[1:].sum().item() == T
+    out = K.moe_experts(gpu(x[0]), gpu(p["gate_up_proj"]), gpu(p["down_proj"]), idx, w)
+    pf = {n: f32(t) for n, t in p.items()}
+    ref, _ = sparse_moe(f32(x), pf, top_k=k, router_logits=logits.float())
+    assert_bf16_close(out, ref[0], what="moe_experts skewed")
 
 
 # ------------------------------------------------------------------ prefill chunk over a KV cache
