@@ -128,6 +128,10 @@ int launch_tiled_cfg(GemmParams p, int64_t batch, hipStream_t st) {
 // 48.1 -> 43.7 us, shorter K unchanged; such a wave of tiles takes 0.46-0.56
 // of the time of one wave of 256x256 tiles (estimate: 128 * 128 / 0.47).
 // Rings of 6 or 8 32-wide stages were no faster than 4.
+//
+// 256x192 tiles over K >= 4096 take a fourth W slot (W issued three stages
+// ahead; 2 X + 4 W slots fill the 160 KB): M=4096 N=6144 K=4096 (q/k/v over
+// three segments) 190.7 -> 179.6 us; at K=2048 no change, at K=1152 15% slower.
 template <int EPI>
 int launch_tiled(GemmParams p, int64_t batch, hipStream_t st) {
   constexpr int kCUs = 256;
@@ -153,7 +157,9 @@ int launch_tiled(GemmParams p, int64_t batch, hipStream_t st) {
     const double cost_b = waves(q3_cdiv(p.M, 256) * q3_cdiv(p.N, 192) * batch, kCUs) * 256.0 * 192.0 / 0.95;
     const double best = std::min(std::min(cost_a, cost_b), std::min(cost_c, cost_d));
     if (cost_c == best) return launch_c();
-    if (cost_b == best) return launch_tiled_cfg<256, 192, 4, 2, EPI, 2, 64, 3>(p, batch, st);
+    if (cost_b == best)  // a fourth W slot (the whole 160 KB) pays off over long K loops only
+      return p.K >= 4096 ? launch_tiled_cfg<256, 192, 4, 2, EPI, 2, 64, 4>(p, batch, st)
+                         : launch_tiled_cfg<256, 192, 4, 2, EPI, 2, 64, 3>(p, batch, st);
     if (cost_d == best) return launch_tiled_cfg<128, 256, 2, 4, EPI, 3, 64>(p, batch, st);
     return launch_tiled_cfg<256, 256, 2, 4, EPI, 2, 64, 3>(p, batch, st);
   }

@@ -422,9 +422,9 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
   constexpr int BN_OUT = (EPI == kEpiSwiGLU) ? BN / 2 : BN;
   constexpr int CH = BKT / 8;              // 16-byte chunks per LDS row
   constexpr int KS = BKT / 16;             // MFMA K steps per stage
-  // X slots (NST) and W slots (NSTW, at most one more: weights come from HBM,
-  // activations from L2, so W is issued one stage further ahead).
-  static_assert(NSTW == NST || NSTW == NST + 1, "W ring depth");
+  // X slots (NST) and W slots (NSTW, up to two more: weights come from HBM,
+  // activations from L2, so W may be issued further ahead).
+  static_assert(NSTW >= NST && NSTW <= NST + 2, "W ring depth");
   constexpr int kStageX = BM * BKT, kStageW = BN * BKT;  // elements per ring slot
   constexpr int kRing = NST * kStageX + NSTW * kStageW;
   constexpr int RPI = 64 / CH;             // rows per DMA instruction
