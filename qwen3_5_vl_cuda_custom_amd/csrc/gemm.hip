@@ -129,9 +129,11 @@ int launch_tiled_cfg(GemmParams p, int64_t batch, hipStream_t st) {
 // of the time of one wave of 256x256 tiles (estimate: 128 * 128 / 0.47).
 // Rings of 6 or 8 32-wide stages were no faster than 4.
 //
-// 256x192 tiles over K >= 4096 take a fourth W slot (W issued three stages
-// ahead; 2 X + 4 W slots fill the 160 KB): M=4096 N=6144 K=4096 (q/k/v over
-// three segments) 190.7 -> 179.6 us; at K=2048 no change, at K=1152 15% slower.
+// 256x192 tiles over K >= 2048 take a fourth W slot (W issued three stages
+// ahead; 2 X + 4 W slots fill the 160 KB). With the weights rotated over 384 MB
+// (past the MALL, as in a layer): M=4096 N=6144 K=4096 (q/k/v over three
+// segments) 186.1 -> 180.1 us, M=4096 N=5120 K=2048 98.4 -> 92.6 us; at
+// K=1152 10% slower.
 template <int EPI>
 int launch_tiled(GemmParams p, int64_t batch, hipStream_t st) {
   constexpr int kCUs = 256;
@@ -158,7 +160,7 @@ int launch_tiled(GemmParams p, int64_t batch, hipStream_t st) {
     const double best = std::min(std::min(cost_a, cost_b), std::min(cost_c, cost_d));
     if (cost_c == best) return launch_c();
     if (cost_b == best)  // a fourth W slot (the whole 160 KB) pays off over long K loops only
-      return p.K >= 4096 ? launch_tiled_cfg<256, 192, 4, 2, EPI, 2, 64, 4>(p, batch, st)
+      return p.K >= 2048 ? launch_tiled_cfg<256, 192, 4, 2, EPI, 2, 64, 4>(p, batch, st)
                          : launch_tiled_cfg<256, 192, 4, 2, EPI, 2, 64, 3>(p, batch, st);
     if (cost_d == best) return launch_tiled_cfg<128, 256, 2, 4, EPI, 3, 64>(p, batch, st);
     return launch_tiled_cfg<256, 256, 2, 4, EPI, 2, 64, 3>(p, batch, st);
