@@ -386,6 +386,30 @@ def main() -> int:
         cases = {}
         if not args.no_cpu_baseline:
             cases[f"c2_prefill_s{S}"] = text_layer_case(cfg, layer, x, pos, step()[0])
+        # Order of the GPU measurements: the layer's other GEMMs and attention
+        # (for the record, ~40 ms of load), then the headline steps, so that the
+        # headline's W warm-up and K timed steps run on a GPU already at its
+        # steady clocks, then the dominant GEMM. From idle, the first ~40 ms of
+        # load run slower (same box: the first 20 steps after a 2 s idle with 5
+        # warm-up steps averaged 1.500 ms per layer, every later round
+        # 1.437-1.445 ms).
+        # Other GEMMs of the layer and attention, for the record.
+        a = torch.empty(S, cfg.hidden, dtype=torch.bfloat16, device=dev).normal_()
+        detail = {}
+        for name, w in [("q_proj", layer.self_attn.q_proj.weight), ("k_proj", layer.self_attn.k_proj.weight),
+                        ("o_proj", layer.self_attn.o_proj.weight)]:
+            t = time_gpu(lambda w=w: K.matmul(a, w), 40, 2)
+            detail[name] = round(2 * S * w.shape[0] * w.shape[1] / (t / 1e3) / 1e12, 1)
+        act = torch.empty(S, cfg.intermediate, dtype=torch.bfloat16, device=dev).normal_()
+        t = time_gpu(lambda: K.matmul(act, layer.mlp.down_proj.weight), 40, 2)
+        detail["down_proj"] = round(2 * S * cfg.hidden * cfg.intermediate / (t / 1e3) / 1e12, 1)
+        q = torch.empty(1, cfg.heads, S, cfg.head_dim, dtype=torch.bfloat16, device=dev).normal_()
+        kk = torch.empty(1, cfg.kv_heads, S, cfg.head_dim, dtype=torch.bfloat16, device=dev).normal_()
+        t = time_gpu(lambda: K.flash_attention(q, kk, kk, cfg.head_dim ** -0.5, True, 4), 40, 2)
+        detail["flash_attention"] = round(cfg.causal_attn_flops(S) / (t / 1e3) / 1e12, 1)
+        log(f"per-kernel TFLOP/s: {detail}")
+        del a, act, q, kk
+
         for _ in range(args.warmup):
             step()
         torch.cuda.synchronize()
@@ -408,23 +432,6 @@ def main() -> int:
         gemm_tflops = gemm_flop / (gemm_ms / 1e3) / 1e12
         log(f"dominant kernel gate/up+SwiGLU GEMM (M={S}, N=2x{cfg.intermediate}, K={cfg.hidden}): "
             f"{gemm_ms:.3f} ms, {gemm_tflops:.1f} TFLOP/s ({gemm_tflops / PEAK_BF16_TFLOPS:.1%})")
-
-        # Other GEMMs of the layer, for the record.
-        a = torch.empty(S, cfg.hidden, dtype=torch.bfloat16, device=dev).normal_()
-        detail = {}
-        for name, w in [("q_proj", layer.self_attn.q_proj.weight), ("k_proj", layer.self_attn.k_proj.weight),
-                        ("o_proj", layer.self_attn.o_proj.weight)]:
-            t = time_gpu(lambda w=w: K.matmul(a, w), 10, 2)
-            detail[name] = round(2 * S * w.shape[0] * w.shape[1] / (t / 1e3) / 1e12, 1)
-        act = torch.empty(S, cfg.intermediate, dtype=torch.bfloat16, device=dev).normal_()
-        t = time_gpu(lambda: K.matmul(act, layer.mlp.down_proj.weight), 10, 2)
-        detail["down_proj"] = round(2 * S * cfg.hidden * cfg.intermediate / (t / 1e3) / 1e12, 1)
-        q = torch.empty(1, cfg.heads, S, cfg.head_dim, dtype=torch.bfloat16, device=dev).normal_()
-        kk = torch.empty(1, cfg.kv_heads, S, cfg.head_dim, dtype=torch.bfloat16, device=dev).normal_()
-        t = time_gpu(lambda: K.flash_attention(q, kk, kk, cfg.head_dim ** -0.5, True, 4), 10, 2)
-        detail["flash_attention"] = round(cfg.causal_attn_flops(S) / (t / 1e3) / 1e12, 1)
-        log(f"per-kernel TFLOP/s: {detail}")
-        del a, act, q, kk
 
         decode = None
         if not args.no_decode:
