@@ -224,6 +224,38 @@ int q3_decode_attention_step(const void* q, const void* k_cache, const void* v_c
                              int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len, const int64_t* strides,
                              float scale, int dtype, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Paged KV cache (no counterpart in the reference, whose cache grows by
+ * torch.cat, modules/attention.py:89-92; serves the preallocated, optionally
+ * paged cache of the decode loop): each KV head's rows live in pages of page_rows rows (a multiple of
+ * 32) in pools k_pages / v_pages (num_pages, Hkv, page_rows, D); cache row r
+ * of sequence b is row r % page_rows of page block_table[b * max_pages +
+ * r / page_rows] (int32 on the device). A page id outside [0, num_pages)
+ * reads as zero rows / drops the write and sets bit 1 of *status (a device
+ * int32, or null; never cleared here).
+ *
+ * q3_qk_norm_rope_paged: q3_qk_norm_rope whose k/v outputs are the page pools,
+ * rows appended at cache rows kv_lens[b] + s (< max_pages * page_rows).
+ * strides = q3_qk_norm_rope's, with the k/v output (b, s, h) strides replaced
+ * by (page, row, head) strides of the pools. */
+int q3_qk_norm_rope_paged(const void* q_in, const void* k_in, const void* v_in, void* q_out, void* k_pages,
+                          void* v_pages, const void* q_weight, const void* k_weight, const int* positions,
+                          const float* inv_freq, const int* block_table, int64_t max_pages, int64_t page_rows,
+                          int64_t num_pages, const int* kv_lens, int64_t B, int64_t S, int64_t Hq, int64_t Hkv,
+                          int64_t D, const int64_t* section, float eps, const int64_t* strides, int dtype,
+                          int* status, void* stream);
+
+/* Decode attention over a paged cache: sequence b attends to its cache rows
+ * [0, kv_lens[b] + advance) (advance = 1: the step, whose new K/V row is
+ * already appended; kv_lens[b] is then incremented in place). strides = [qb,
+ * qh, k page, kh, ks, v page, vh, vs, ob, oh]; workspace as
+ * q3_decode_attention with max_len = max_pages * page_rows. bf16, D = 128,
+ * Hq / Hkv <= 32, B <= 1024 only (else Q3_ERR_UNSUPPORTED). */
+int q3_decode_attention_paged(const void* q, const void* k_pages, const void* v_pages, const int* block_table,
+                              int64_t max_pages, int64_t page_rows, int64_t num_pages, int* kv_lens, int advance,
+                              void* o, int64_t B, int64_t Hq, int64_t Hkv, int64_t D, const int64_t* strides,
+                              float scale, int dtype, void* workspace, int64_t workspace_bytes, int* status,
+                              void* stream);
+
 /* q3_decode_attention_step without a workspace argument, for callers that
  * cannot allocate (code under HIP-graph capture, tight serving loops). No
  * counterpart in the reference. The workspace lives in a static device array

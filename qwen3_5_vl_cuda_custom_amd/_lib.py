@@ -57,6 +57,10 @@ _SIGS: dict[str, tuple] = {
     "q3_decode_attention": (c_int, [_V, _V, _V, _i32p, _V, _I, _I, _I, _I, _I, _i64p, c_float, c_int, _V, _I, _V]),
     "q3_decode_attention_step": (c_int, [_V, _V, _V, _i32p, _V, _I, _I, _I, _I, _I, _i64p, c_float, c_int, _V, _I,
                                          _V]),
+    "q3_qk_norm_rope_paged": (c_int, [_V, _V, _V, _V, _V, _V, _V, _V, _i32p, _f32p, _i32p, _I, _I, _I, _i32p, _I,
+                                      _I, _I, _I, _I, _i64p, c_float, _i64p, c_int, _i32p, _V]),
+    "q3_decode_attention_paged": (c_int, [_V, _V, _V, _i32p, _I, _I, _I, _i32p, c_int, _V, _I, _I, _I, _I, _i64p,
+                                          c_float, c_int, _V, _I, _i32p, _V]),
     "q3_decode_attention_step_noalloc_max_bytes": (c_int64, []),
     "q3_decode_attention_step_noalloc": (c_int, [_V, _V, _V, _i32p, _V, _I, _I, _I, _I, _I, _i64p, c_float, c_int,
                                                  _V]),
@@ -176,6 +180,7 @@ def gemm_workspace(nbytes: int, device: torch.device) -> tuple[torch.Tensor | No
 _status: dict[int, torch.Tensor] = {}
 
 STATUS_INDEX_OUT_OF_RANGE = 1
+STATUS_BAD_PAGE = 2  # a paged-cache block table named a page outside the pool
 
 
 def status_word(device: torch.device) -> torch.Tensor:

@@ -61,6 +61,14 @@ struct AttnParams {
   int* dec_hdr;     // decode workspace header: unit prefix over sequences (B + 1 ints)
   int dec_waves;    // decode: waves in the main kernel's grid
   float* partial;  // decode workspace
+  // Paged KV cache (decode): cache row r of sequence b is row r % page_rows of
+  // page block_table[b * max_pages + r / page_rows] (page_rows a multiple of the
+  // 32-key unit); kb / vb are then the page strides. Null: one contiguous cache
+  // per sequence. A page id outside [0, num_pages) reads as zero rows and sets
+  // bit 1 of *status (when given).
+  const int* block_table;
+  int max_pages, page_rows, num_pages;
+  int* status;
 };
 
 // ----------------------------------------------------------------- prefill
@@ -461,23 +469,61 @@ __global__ __launch_bounds__(64 * BW) void flash_decode_kernel(const AttnParams 
   // DMA of one unit into ring slot `slot` (zeros when `live` is false).
   auto issue = [&](const DecCursor& c, bool live, bool need_q, int slot) {
     const int L = live ? s_len[c.b] : 1;
-    const bf16* kbase = p.k + (int64_t)c.b * p.kb + (int64_t)c.kvh * p.kh;
-    const bf16* vbase = p.v + (int64_t)c.b * p.vb + (int64_t)c.kvh * p.vh;
+    const int k0 = c.tile * kDecUnit;
+    // Unit rows: cache rows [k0, k0 + 32) at rows [kr0, kr0 + 32) of kbase /
+    // vbase; rows at or past L load zeros (past the buffer resource's end).
+    const bf16* kbase;
+    const bf16* vbase;
+    int kr0, nrow;
+    bool lv = live;
+    if (p.block_table) {
+      // The page id is wave-uniform (one unit per wave); pinned to a scalar so
+      // the buffer resources built from it stay scalar.
+      int pg = lv ? __builtin_amdgcn_readfirstlane(p.block_table[(int64_t)c.b * p.max_pages + k0 / p.page_rows]) : 0;
+      if ((unsigned)pg >= (unsigned)p.num_pages) {
+        if (lv && p.status && lane == 0) atomicOr(p.status, 2);
+        lv = false;
+        pg = 0;
+      }
+      kr0 = k0 % p.page_rows;
+      // A unit that loads nothing (a prefetch past the wave's range, whose tile
+      // may lie beyond L = 1, or a rejected page) keeps a one-row resource, so
+      // its kOOB offsets stay out of range.
+      nrow = lv ? kr0 + min(kDecUnit, L - k0) : 1;
+      kbase = p.k + (int64_t)pg * p.kb + (int64_t)c.kvh * p.kh;
+      vbase = p.v + (int64_t)pg * p.vb + (int64_t)c.kvh * p.vh;
+    } else {
+      kr0 = k0;
+      nrow = L;
+      kbase = p.k + (int64_t)c.b * p.kb + (int64_t)c.kvh * p.kh;
+      vbase = p.v + (int64_t)c.b * p.vb + (int64_t)c.kvh * p.vh;
+    }
+    // Wave-uniform by construction; pinned to scalars so the buffer resources
+    // built from them stay scalar after the two branches merge.
+    auto pin = [](const bf16* x) {
+      const uint64_t v = reinterpret_cast<uint64_t>(x);
+      const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+      const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+      return reinterpret_cast<const bf16*>(((uint64_t)hi << 32) | lo);
+    };
+    kbase = pin(kbase);
+    vbase = pin(vbase);
+    kr0 = __builtin_amdgcn_readfirstlane(kr0);
+    nrow = __builtin_amdgcn_readfirstlane(nrow);
     const bf16* qbase = p.q + (int64_t)c.b * p.qb + (int64_t)c.kvh * G * p.qh;
-    const __amdgpu_buffer_rsrc_t krs = q3::make_rsrc(kbase, (int64_t)(L - 1) * ks2 + D * 2);
-    const __amdgpu_buffer_rsrc_t vrs = q3::make_rsrc(vbase, (int64_t)(L - 1) * vs2 + D * 2);
+    const __amdgpu_buffer_rsrc_t krs = q3::make_rsrc(kbase, (int64_t)(nrow - 1) * ks2 + D * 2);
+    const __amdgpu_buffer_rsrc_t vrs = q3::make_rsrc(vbase, (int64_t)(nrow - 1) * vs2 + D * 2);
     const __amdgpu_buffer_rsrc_t qrs = q3::make_rsrc(qbase, (int64_t)(G - 1) * p.qh * 2 + D * 2);
     const uint32_t lk = lring + (uint32_t)(slot * SLOT * 2);
-    const uint32_t lv = lk + kDecTile * 2, lq = lv + kDecTile * 2;
-    const int k0 = c.tile * kDecUnit;
+    const uint32_t lv_ = lk + kDecTile * 2, lq = lv_ + kDecTile * 2;
     const int cs = lane & 15;
 #pragma unroll
     for (int i = 0; i < kDecUnit / 4; ++i) {
       const int r = 4 * i + (lane >> 4);
-      const uint32_t ko = live ? (uint32_t)((k0 + r) * ks2 + ((cs ^ (r & 15)) << 4)) : q3::kOOB;
-      const uint32_t vo = live ? (uint32_t)((k0 + r) * vs2 + ((cs ^ ((r & 3) << 2)) << 4)) : q3::kOOB;
+      const uint32_t ko = lv ? (uint32_t)((kr0 + r) * ks2 + ((cs ^ (r & 15)) << 4)) : q3::kOOB;
+      const uint32_t vo = lv ? (uint32_t)((kr0 + r) * vs2 + ((cs ^ ((r & 3) << 2)) << 4)) : q3::kOOB;
       q3::dma16_nt(krs, ko, lk + i * 1024);
-      q3::dma16_nt(vrs, vo, lv + i * 1024);
+      q3::dma16_nt(vrs, vo, lv_ + i * 1024);
     }
 #pragma unroll
     for (int i = 0; i < QI; ++i) {
@@ -1269,12 +1315,21 @@ bool dec_fast_path(const void* q, const void* k_cache, const void* v_cache, int6
          (max_len + 1) * strides[4] * 2 < 0x7fffffffLL && (max_len + 1) * strides[7] * 2 < 0x7fffffffLL;
 }
 
+// Paged cache (block_table set): kb / vb in `strides` are the page strides and
+// max_len = max_pages * page_rows; only the MFMA path reads pages.
 int decode_impl(const void* q, const void* k_cache, const void* v_cache, const int* kv_lens, int len_add,
                 int* lens_inc, void* o, int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len,
                 const int64_t* strides, float scale, int dtype, void* workspace, int64_t workspace_bytes,
-                void* stream) {
+                void* stream, const int* block_table = nullptr, int64_t max_pages = 0, int64_t page_rows = 0,
+                int64_t num_pages = 0, int* status = nullptr) {
   Q3_REQUIRE(q && k_cache && v_cache && kv_lens && o && strides, Q3_ERR_NULL);
   Q3_REQUIRE(B >= 0 && Hq >= 1 && Hkv >= 1 && Hq % Hkv == 0 && D >= 1 && max_len >= 1, Q3_ERR_SHAPE);
+  if (block_table) {
+    const bool fast = dtype == Q3_BF16 && D == 128 && Hq / Hkv <= 32 && B <= kDecMaxBatch && q3_aligned(q, 16) &&
+                      q3_aligned(k_cache, 16) && q3_aligned(v_cache, 16) && strides_aligned8(strides, 8) &&
+                      page_rows * strides[4] * 2 < 0x7fffffffLL && page_rows * strides[7] * 2 < 0x7fffffffLL;
+    Q3_REQUIRE(fast, Q3_ERR_UNSUPPORTED);
+  }
   if (B == 0) return Q3_OK;
   AttnParams p{};
   p.q = static_cast<const bf16*>(q);
@@ -1303,8 +1358,13 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
   p.groups = (int)(Hq / Hkv);
   p.kv_lens = kv_lens;
   p.len_add = len_add;
+  p.block_table = block_table;
+  p.max_pages = (int)max_pages;
+  p.page_rows = (int)page_rows;
+  p.num_pages = (int)num_pages;
+  p.status = status;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dec_fast_path(q, k_cache, v_cache, B, Hq, Hkv, D, max_len, strides, dtype)) {
+  if (block_table || dec_fast_path(q, k_cache, v_cache, B, Hq, Hkv, D, max_len, strides, dtype)) {
     Q3_REQUIRE(workspace != nullptr && workspace_bytes >= decode_ws_bytes(B, Hq, Hkv, max_len, D), Q3_ERR_WORKSPACE);
     Q3_REQUIRE(q3_aligned(workspace, 16), Q3_ERR_ALIGN);
     p.dec_hdr = static_cast<int*>(workspace);
@@ -1358,6 +1418,19 @@ int q3_decode_attention_step(const void* q, const void* k_cache, const void* v_c
                              float scale, int dtype, void* workspace, int64_t workspace_bytes, void* stream) {
   return decode_impl(q, k_cache, v_cache, kv_lens, 1, kv_lens, o, B, Hq, Hkv, D, max_len, strides, scale, dtype,
                      workspace, workspace_bytes, stream);
+}
+
+int q3_decode_attention_paged(const void* q, const void* k_pages, const void* v_pages, const int* block_table,
+                              int64_t max_pages, int64_t page_rows, int64_t num_pages, int* kv_lens, int advance,
+                              void* o, int64_t B, int64_t Hq, int64_t Hkv, int64_t D, const int64_t* strides,
+                              float scale, int dtype, void* workspace, int64_t workspace_bytes, int* status,
+                              void* stream) {
+  Q3_REQUIRE(block_table, Q3_ERR_NULL);
+  Q3_REQUIRE(max_pages >= 1 && num_pages >= 1 && page_rows >= kDecUnit && page_rows % kDecUnit == 0, Q3_ERR_SHAPE);
+  Q3_REQUIRE(max_pages * page_rows < (1ll << 31) && num_pages < (1ll << 31), Q3_ERR_SHAPE);
+  return decode_impl(q, k_pages, v_pages, kv_lens, advance ? 1 : 0, advance ? kv_lens : nullptr, o, B, Hq, Hkv, D,
+                     max_pages * page_rows, strides, scale, dtype, workspace, workspace_bytes, stream, block_table,
+                     max_pages, page_rows, num_pages, status);
 }
 
 }  // extern "C"

@@ -18,9 +18,10 @@ constexpr int kStages = 4;   // LDS ring depth (default GEMM configuration)
 
 // Buffer resource over `bytes` bytes at `base`: loads at byte offsets >= bytes
 // return zeros (branch-free edges: rows past the matrix, the K tail, stages
-// past the end of the loop).
+// past the end of the loop). `bytes` is clamped to [0, 2^31 - 1]: a
+// non-positive size gives an empty range, never a wrapped huge one.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
-  const int32_t n = bytes >= 0x7fffffffLL ? 0x7fffffff : (int32_t)bytes;
+  const int32_t n = bytes <= 0 ? 0 : (bytes >= 0x7fffffffLL ? 0x7fffffff : (int32_t)bytes);
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
 }
 constexpr uint32_t kOOB = 0x80000000u;  // a byte offset that is always out of range

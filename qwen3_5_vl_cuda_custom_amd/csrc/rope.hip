@@ -198,6 +198,13 @@ struct QKNormRopeArgs {
   int s0, s1;
   float eps;
   int64_t st[18];  // (b, s, h) strides of q_in, k_in, v_in, q_out, k_out, v_out
+  // Paged k_out / v_out (null: strided as above): cache row r (= s + offset) of
+  // sequence b is row r % page_rows of page block_table[b * max_pages +
+  // r / page_rows], and the b strides of k_out / v_out are the page strides. A
+  // page id outside [0, num_pages) drops the row and sets bit 1 of *status.
+  const int* block_table;
+  int max_pages, page_rows, num_pages;
+  int* status;
 };
 
 // One block per (b, s) token. The D/2 rotary angles of the token (pos[axis]
@@ -319,9 +326,19 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const QKNormRopeArgs 
       int kind, h;
       row_kind(row, kind, h);
       const int so = kind > 0 ? so_b : 0;
-      const bool skip_store = kind > 0 && (s + (int64_t)so >= a.dst_seq_cap || s + so < 0);
+      bool skip_store = kind > 0 && (s + (int64_t)so >= a.dst_seq_cap || s + so < 0);
+      int64_t ob = b, orow = s + so;  // k / v: page and row within it when paged
+      if (kind > 0 && a.block_table && !skip_store) {
+        const int pg = a.block_table[(int64_t)b * a.max_pages + orow / a.page_rows];
+        if ((unsigned)pg >= (unsigned)a.num_pages) {
+          if (a.status && j == 0) atomicOr(a.status, 2);
+          skip_store = true;
+        }
+        ob = pg;
+        orow %= a.page_rows;
+      }
       T* out = static_cast<T*>(kind == 0 ? a.q_out : (kind == 1 ? a.k_out : a.v_out)) +
-               b * pick3(kind, a.st[9], a.st[12], a.st[15]) + (int64_t)(s + so) * pick3(kind, a.st[10], a.st[13], a.st[16]) +
+               ob * pick3(kind, a.st[9], a.st[12], a.st[15]) + orow * pick3(kind, a.st[10], a.st[13], a.st[16]) +
                h * pick3(kind, a.st[11], a.st[14], a.st[17]);
       float x[8];
 #pragma unroll
@@ -388,32 +405,13 @@ int launch_qk(const QKNormRopeArgs& a, hipStream_t st) {
 
 }  // namespace
 
-extern "C" {
+namespace {
 
-int q3_rope(const void* x, const void* cos, const void* sin, void* y, int64_t B, int64_t H, int64_t S, int64_t D,
-            int64_t D_rope, const int64_t* x_strides, const int64_t* y_strides, int64_t cos_batch_stride,
-            int64_t cos_seq_stride, int dtype, int cos_dtype, void* stream) {
-  Q3_REQUIRE(x_strides && y_strides, Q3_ERR_NULL);
-  RopeGeom g{(int)B, (int)H, (int)S, (int)D, (int)D_rope, x_strides[0], x_strides[1], x_strides[2],
-             y_strides[0], y_strides[1], y_strides[2], 0, cos_batch_stride, cos_seq_stride, (int)(D_rope / 2), 0};
-  return launch_rope(x, cos, sin, y, g, dtype, cos_dtype, static_cast<hipStream_t>(stream));
-}
-
-int q3_mrope(const void* x, const void* cos3d, const void* sin3d, void* y, int64_t B, int64_t H, int64_t S, int64_t D,
-             int64_t D_rope, const int64_t* section, const int64_t* x_strides, const int64_t* y_strides,
-             const int64_t* cos_strides, int dtype, int cos_dtype, void* stream) {
-  Q3_REQUIRE(section && x_strides && y_strides && cos_strides, Q3_ERR_NULL);
-  RopeGeom g{(int)B, (int)H, (int)S, (int)D, (int)D_rope, x_strides[0], x_strides[1], x_strides[2],
-             y_strides[0], y_strides[1], y_strides[2], cos_strides[0], cos_strides[1], cos_strides[2],
-             (int)section[0], (int)section[1]};
-  Q3_REQUIRE(section[0] + section[1] + section[2] == D_rope / 2, Q3_ERR_SHAPE);
-  return launch_rope(x, cos3d, sin3d, y, g, dtype, cos_dtype, static_cast<hipStream_t>(stream));
-}
-
-int q3_qk_norm_rope(const void* q_in, const void* k_in, const void* v_in, void* q_out, void* k_out, void* v_out,
-                    const void* q_weight, const void* k_weight, const int* positions, const float* inv_freq,
-                    const int* dst_seq_offset, int64_t dst_seq_cap, int64_t B, int64_t S, int64_t Hq, int64_t Hkv,
-                    int64_t D, const int64_t* section, float eps, const int64_t* strides, int dtype, void* stream) {
+int qk_impl(const void* q_in, const void* k_in, const void* v_in, void* q_out, void* k_out, void* v_out,
+            const void* q_weight, const void* k_weight, const int* positions, const float* inv_freq,
+            const int* dst_seq_offset, int64_t dst_seq_cap, int64_t B, int64_t S, int64_t Hq, int64_t Hkv,
+            int64_t D, const int64_t* section, float eps, const int64_t* strides, int dtype, const int* block_table,
+            int64_t max_pages, int64_t page_rows, int64_t num_pages, int* status, void* stream) {
   Q3_REQUIRE(q_in && k_in && q_out && k_out && positions && inv_freq && section && strides, Q3_ERR_NULL);
   Q3_REQUIRE((q_weight == nullptr) == (k_weight == nullptr), Q3_ERR_NULL);
   Q3_REQUIRE((v_in == nullptr) == (v_out == nullptr), Q3_ERR_NULL);
@@ -443,10 +441,61 @@ int q3_qk_norm_rope(const void* q_in, const void* k_in, const void* v_in, void* 
   a.s1 = (int)section[1];
   a.eps = eps;
   for (int i = 0; i < 18; ++i) a.st[i] = strides[i];
+  a.block_table = block_table;
+  a.max_pages = (int)max_pages;
+  a.page_rows = (int)page_rows;
+  a.num_pages = (int)num_pages;
+  a.status = status;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == Q3_BF16) return launch_qk<bf16>(a, st);
   if (dtype == Q3_F32) return launch_qk<float>(a, st);
   return Q3_ERR_DTYPE;
+}
+
+}  // namespace
+
+extern "C" {
+
+int q3_rope(const void* x, const void* cos, const void* sin, void* y, int64_t B, int64_t H, int64_t S, int64_t D,
+            int64_t D_rope, const int64_t* x_strides, const int64_t* y_strides, int64_t cos_batch_stride,
+            int64_t cos_seq_stride, int dtype, int cos_dtype, void* stream) {
+  Q3_REQUIRE(x_strides && y_strides, Q3_ERR_NULL);
+  RopeGeom g{(int)B, (int)H, (int)S, (int)D, (int)D_rope, x_strides[0], x_strides[1], x_strides[2],
+             y_strides[0], y_strides[1], y_strides[2], 0, cos_batch_stride, cos_seq_stride, (int)(D_rope / 2), 0};
+  return launch_rope(x, cos, sin, y, g, dtype, cos_dtype, static_cast<hipStream_t>(stream));
+}
+
+int q3_mrope(const void* x, const void* cos3d, const void* sin3d, void* y, int64_t B, int64_t H, int64_t S, int64_t D,
+             int64_t D_rope, const int64_t* section, const int64_t* x_strides, const int64_t* y_strides,
+             const int64_t* cos_strides, int dtype, int cos_dtype, void* stream) {
+  Q3_REQUIRE(section && x_strides && y_strides && cos_strides, Q3_ERR_NULL);
+  RopeGeom g{(int)B, (int)H, (int)S, (int)D, (int)D_rope, x_strides[0], x_strides[1], x_strides[2],
+             y_strides[0], y_strides[1], y_strides[2], cos_strides[0], cos_strides[1], cos_strides[2],
+             (int)section[0], (int)section[1]};
+  Q3_REQUIRE(section[0] + section[1] + section[2] == D_rope / 2, Q3_ERR_SHAPE);
+  return launch_rope(x, cos3d, sin3d, y, g, dtype, cos_dtype, static_cast<hipStream_t>(stream));
+}
+
+int q3_qk_norm_rope(const void* q_in, const void* k_in, const void* v_in, void* q_out, void* k_out, void* v_out,
+                    const void* q_weight, const void* k_weight, const int* positions, const float* inv_freq,
+                    const int* dst_seq_offset, int64_t dst_seq_cap, int64_t B, int64_t S, int64_t Hq, int64_t Hkv,
+                    int64_t D, const int64_t* section, float eps, const int64_t* strides, int dtype, void* stream) {
+  return qk_impl(q_in, k_in, v_in, q_out, k_out, v_out, q_weight, k_weight, positions, inv_freq, dst_seq_offset,
+                 dst_seq_cap, B, S, Hq, Hkv, D, section, eps, strides, dtype, nullptr, 0, 0, 0, nullptr, stream);
+}
+
+int q3_qk_norm_rope_paged(const void* q_in, const void* k_in, const void* v_in, void* q_out, void* k_pages,
+                          void* v_pages, const void* q_weight, const void* k_weight, const int* positions,
+                          const float* inv_freq, const int* block_table, int64_t max_pages, int64_t page_rows,
+                          int64_t num_pages, const int* kv_lens, int64_t B, int64_t S, int64_t Hq, int64_t Hkv,
+                          int64_t D, const int64_t* section, float eps, const int64_t* strides, int dtype,
+                          int* status, void* stream) {
+  Q3_REQUIRE(block_table && kv_lens, Q3_ERR_NULL);
+  Q3_REQUIRE(max_pages >= 1 && num_pages >= 1 && page_rows >= 32 && page_rows % 32 == 0, Q3_ERR_SHAPE);
+  Q3_REQUIRE(max_pages * page_rows < (1ll << 31) && num_pages < (1ll << 31), Q3_ERR_SHAPE);
+  return qk_impl(q_in, k_in, v_in, q_out, k_pages, v_pages, q_weight, k_weight, positions, inv_freq, kv_lens,
+                 max_pages * page_rows, B, S, Hq, Hkv, D, section, eps, strides, dtype, block_table, max_pages,
+                 page_rows, num_pages, status, stream);
 }
 
 }  // extern "C"

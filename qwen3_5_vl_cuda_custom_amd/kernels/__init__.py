@@ -4,13 +4,14 @@ from ._loader import FALLBACK_LOG, record_fallback, strict_mode, summarize_fallb
 from .conv3d_patch import conv3d_patch
 from .elementwise import gelu_tanh, residual_add, swiglu
 from .embedding import embedding
-from .flash_attention import decode_attention, flash_attention, flash_attention_cache, flash_attention_varlen
+from .flash_attention import (decode_attention, decode_attention_paged, flash_attention, flash_attention_cache,
+                              flash_attention_varlen)
 from .matmul import (RMSNORM_MATMUL_MAX_ROWS, matmul, matmul_gelu, matmul_segments, matmul_swiglu,
                      rmsnorm_matmul_segments, rmsnorm_matmul_swiglu)
 from .moe_routing import (cuda_batched_gemm, cuda_index_add, cuda_topk, moe_experts, moe_permute, moe_route,
                           raise_device_errors)
 from .norms import layernorm, rmsnorm, softmax
-from .rotary import apply_mrope, apply_rope, qk_norm_rope
+from .rotary import apply_mrope, apply_rope, qk_norm_rope, qk_norm_rope_paged
 from .vision import vision_pos_embed, vision_rope_tables
 
 __all__ = [
@@ -35,6 +36,7 @@ __all__ = [
     "swiglu",
     # additions beyond the reference API (fused / decode / MoE dispatch paths)
     "decode_attention",
+    "decode_attention_paged",
     "flash_attention_cache",
     "flash_attention_varlen",
     "matmul_gelu",
@@ -50,4 +52,5 @@ __all__ = [
     "moe_permute",
     "raise_device_errors",
     "qk_norm_rope",
+    "qk_norm_rope_paged",
 ]

@@ -81,6 +81,45 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     return o
 
 
+def decode_attention_paged(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor, block_table: torch.Tensor,
+                           kv_lens: torch.Tensor, scale: float, *, out: torch.Tensor | None = None,
+                           append: bool = False, status: torch.Tensor | None = None) -> torch.Tensor:
+    """decode_attention over a paged cache (no reference counterpart: the paged form of the decode loop's cache).
+
+    q (B, Hq, D); k_pages/v_pages (num_pages, Hkv, page_rows, D) pools; block_table
+    (B, max_pages) int32 on the device: cache row r of sequence b is row
+    r % page_rows of page block_table[b, r // page_rows]. kv_lens (B,) int32.
+    append=True: the step (the new token's row is already appended; attends to
+    kv_lens[b] + 1 rows, then kv_lens += 1 in place). A page id outside the
+    pool reads as zero rows and sets bit 1 of `status` (default: the device's
+    status word, see _lib.device_status).
+    """
+    check("decode_attention_paged", q, k_pages, v_pages)
+    if q.dim() == 4:
+        q = q[:, :, 0]
+    B, Hq, D = q.shape
+    num_pages, Hkv, page_rows = k_pages.shape[0], k_pages.shape[1], k_pages.shape[2]
+    if k_pages.shape != v_pages.shape or k_pages.shape[3] != D or k_pages.stride(-1) != 1 or v_pages.stride(-1) != 1:
+        raise ValueError(f"decode_attention_paged: q {tuple(q.shape)}, pages {tuple(k_pages.shape)}")
+    if (block_table.dtype != torch.int32 or not block_table.is_cuda or block_table.dim() != 2
+            or block_table.shape[0] != B or not block_table.is_contiguous()):
+        raise ValueError("decode_attention_paged: block_table must be a contiguous int32 (B, max_pages) device tensor")
+    if kv_lens.dtype != torch.int32 or not kv_lens.is_cuda or kv_lens.shape != (B,) or kv_lens.stride(0) != 1:
+        raise ValueError("decode_attention_paged: kv_lens must be a contiguous int32 (B,) device tensor")
+    max_pages = block_table.shape[1]
+    st = status if status is not None else _lib.status_word(q.device)
+    o = out if out is not None else torch.empty((B, Hq, D), dtype=q.dtype, device=q.device)
+    ws, nws = _lib.workspace(_lib.lib().q3_decode_attention_workspace_bytes(B, Hq, Hkv, max_pages * page_rows, D),
+                             q.device)
+    _lib.call("q3_decode_attention_paged", q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(),
+              block_table.data_ptr(), max_pages, page_rows, num_pages, kv_lens.data_ptr(), int(bool(append)),
+              o.data_ptr(), B, Hq, Hkv, D,
+              _lib.i64s(q.stride(0), q.stride(1), k_pages.stride(0), k_pages.stride(1), k_pages.stride(2),
+                        v_pages.stride(0), v_pages.stride(1), v_pages.stride(2), o.stride(0), o.stride(1)),
+              float(scale), _lib.dtype_code(q.dtype), _lib.ptr(ws), nws, st.data_ptr(), _lib.stream())
+    return o
+
+
 def flash_attention_cache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, kv_lens: torch.Tensor,
                           scale: float, num_kv_groups: int = 1, *, out: torch.Tensor | None = None,
                           advance: bool = False) -> torch.Tensor:

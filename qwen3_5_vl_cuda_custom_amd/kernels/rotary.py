@@ -112,3 +112,49 @@ def qk_norm_rope(q_in, k_in, v_in, q_out, k_out, v_out, q_weight, k_weight, posi
               inv_freq.data_ptr(), _lib.ptr(dst_seq_offset), int(dst_seq_cap), B, S, Hq, Hkv, D,
               _lib.i64s(*mrope_section),
               float(eps), _lib.i64s(*strides), _lib.dtype_code(q_in.dtype), _lib.stream())
+
+
+def qk_norm_rope_paged(q_in, k_in, v_in, q_out, k_pages, v_pages, q_weight, k_weight, positions, inv_freq,
+                       mrope_section, eps: float, block_table: torch.Tensor, kv_lens: torch.Tensor,
+                       status: torch.Tensor | None = None) -> None:
+    """qk_norm_rope with the k/v rows appended to a paged cache (no reference counterpart).
+
+    q_in/k_in/v_in/q_out (B, S, H, D) views as for qk_norm_rope; k_pages/v_pages
+    (num_pages, Hkv, page_rows, D) pools; block_table (B, max_pages) int32 and
+    kv_lens (B,) int32 on the device: the rows go to cache rows kv_lens[b] + s.
+    A page id outside the pool drops the row and sets bit 1 of `status`
+    (default: the device's status word).
+    """
+    B, S, Hq, D = q_in.shape
+    Hkv = k_in.shape[2]
+    if (positions.dtype != torch.int32 or not positions.is_cuda or tuple(positions.shape) != (3, B, S)
+            or not positions.is_contiguous()):
+        raise ValueError(f"qk_norm_rope_paged: positions must be a contiguous int32 (3, {B}, {S}) device tensor")
+    if inv_freq.dtype != torch.float32 or not inv_freq.is_cuda or inv_freq.numel() != D // 2:
+        raise ValueError(f"qk_norm_rope_paged: inv_freq must be a float32 ({D // 2},) device tensor")
+    if (block_table.dtype != torch.int32 or not block_table.is_cuda or block_table.dim() != 2
+            or block_table.shape[0] != B or not block_table.is_contiguous()):
+        raise ValueError("qk_norm_rope_paged: block_table must be a contiguous int32 (B, max_pages) device tensor")
+    if kv_lens.dtype != torch.int32 or not kv_lens.is_cuda or kv_lens.shape != (B,) or kv_lens.stride(0) != 1:
+        raise ValueError("qk_norm_rope_paged: kv_lens must be a contiguous int32 (B,) device tensor")
+    if tuple(k_in.shape) != (B, S, Hkv, D) or tuple(q_out.shape) != (B, S, Hq, D):
+        raise ValueError("qk_norm_rope_paged: q/k views must be (B, S, H, D) with matching B, S and D")
+    if k_pages.shape != v_pages.shape or k_pages.shape[1] != Hkv or k_pages.shape[3] != D:
+        raise ValueError(f"qk_norm_rope_paged: pages {tuple(k_pages.shape)} for Hkv={Hkv}, D={D}")
+    if sum(mrope_section) * 2 != D:
+        raise ValueError(f"qk_norm_rope_paged: mrope_section {list(mrope_section)} must sum to D/2 = {D // 2}")
+    strides = []
+    for t in [q_in, k_in, v_in, q_out]:
+        if t.stride(-1) != 1:
+            raise ValueError("qk_norm_rope_paged: the head dim must be contiguous")
+        strides += [t.stride(0), t.stride(1), t.stride(2)]
+    for t in [k_pages, v_pages]:
+        if t.stride(-1) != 1:
+            raise ValueError("qk_norm_rope_paged: the pages' head dim must be contiguous")
+        strides += [t.stride(0), t.stride(2), t.stride(1)]  # (page, row, head)
+    st = status if status is not None else _lib.status_word(q_in.device)
+    _lib.call("q3_qk_norm_rope_paged", q_in.data_ptr(), k_in.data_ptr(), v_in.data_ptr(), q_out.data_ptr(),
+              k_pages.data_ptr(), v_pages.data_ptr(), _lib.ptr(q_weight), _lib.ptr(k_weight), positions.data_ptr(),
+              inv_freq.data_ptr(), block_table.data_ptr(), block_table.shape[1], k_pages.shape[2], k_pages.shape[0],
+              kv_lens.data_ptr(), B, S, Hq, Hkv, D, _lib.i64s(*mrope_section), float(eps), _lib.i64s(*strides),
+              _lib.dtype_code(q_in.dtype), st.data_ptr(), _lib.stream())

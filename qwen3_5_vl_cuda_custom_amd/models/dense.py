@@ -16,7 +16,8 @@ from torch import nn
 
 from ..configs import Qwen3VLConfig
 from ..kernels import cuda_index_add
-from ..modules import (CudaEmbedding, CudaLinear, CudaRMSNorm, CudaTextDecoderLayer, StaticKVCache, StepGraph,
+from ..modules import (CudaEmbedding, CudaLinear, CudaRMSNorm, CudaTextDecoderLayer, PagedKVCache, StaticKVCache,
+                       StepGraph,
                        TextMRoPE)
 from .common import CudaVisionTower
 
@@ -86,11 +87,19 @@ class _TextLM(nn.Module):
         return self.norm(x), new_kvs
 
     # ------------------------------------------------------------ KV-cache serving path
-    def new_caches(self, batch: int, capacity: int, device=None, dtype=None) -> list[StaticKVCache]:
-        """One StaticKVCache per layer, empty, for `batch` sequences of up to `capacity` tokens."""
+    def new_caches(self, batch: int, capacity: int, device=None, dtype=None, *, page_rows: int = 0,
+                   num_pages: int | None = None) -> list[StaticKVCache] | list[PagedKVCache]:
+        """One cache per layer, empty, for `batch` sequences of up to `capacity` tokens: a StaticKVCache,
+        or with page_rows > 0 a PagedKVCache of `num_pages` pages (default: enough for every sequence
+        to reach `capacity`)."""
         t = self.cfg.text
         dev = device if device is not None else self.lm_head.weight.device
         dt = dtype if dtype is not None else self.lm_head.weight.dtype
+        if page_rows > 0:
+            per_seq = -(-capacity // page_rows)
+            n = num_pages if num_pages is not None else batch * per_seq
+            return [PagedKVCache(batch, t.num_kv_heads, t.head_dim, num_pages=n, max_pages=per_seq,
+                                 page_rows=page_rows, dtype=dt, device=dev) for _ in range(t.num_layers)]
         return [StaticKVCache(batch, t.num_kv_heads, capacity, t.head_dim, dtype=dt, device=dev)
                 for _ in range(t.num_layers)]
 
@@ -99,7 +108,8 @@ class _TextLM(nn.Module):
                  position_ids: torch.Tensor | None = None, visual_pos_masks: torch.Tensor | None = None,
                  deepstack_visual_embeds: list[torch.Tensor] | None = None,
                  inputs_embeds: torch.Tensor | None = None, *, prompt_lens=None,
-                 rope_deltas: torch.Tensor | None = None, use_graph: bool = True) -> torch.Tensor:
+                 rope_deltas: torch.Tensor | None = None, use_graph: bool = True,
+                 page_rows: int = 0) -> torch.Tensor:
         """Greedy decoding (reference models/dense.py:123-162). Returns (B, S + new tokens):
         each row's prompt (as given, padding included) followed by its generated tokens.
 
@@ -107,14 +117,16 @@ class _TextLM(nn.Module):
         (default: all S). rope_deltas (B,): added to a sequence's cache length
         to give its decode position (the mRoPE offset after images; default 0).
         Generation stops early only when every sequence has just produced
-        `eos_token_id`, as in the reference.
+        `eos_token_id`, as in the reference. page_rows > 0 keeps the KV cache
+        in pages of that many rows (a multiple of 32) instead of one
+        preallocated block per sequence.
         """
         B, S = input_ids.shape
         dev = self.lm_head.weight.device
         lens = [int(v) for v in prompt_lens] if prompt_lens is not None else [S] * B
         if len(lens) != B or min(lens) < 1 or max(lens) > S:
             raise ValueError("generate: prompt_lens must give 1..S tokens for every sequence")
-        caches = self.new_caches(B, S + max_new_tokens, dev)
+        caches = self.new_caches(B, S + max_new_tokens, dev, page_rows=page_rows)
         emb = inputs_embeds if inputs_embeds is not None else self.embed_tokens(input_ids.to(dev))
         pos3 = text_positions(position_ids, B, S, 0, dev)
         h, _ = self._run_layers(emb, self.rotary.bind(pos3), visual_pos_masks, deepstack_visual_embeds,

@@ -3,7 +3,7 @@
 from .attention import CudaFullAttention, CudaVisionAttention
 from .embedding import CudaEmbedding
 from .graph import StepGraph
-from .kv_cache import StaticKVCache
+from .kv_cache import PagedKVCache, StaticKVCache
 from .linear import CudaLinear
 from .mlp import CudaSwiGLUMLP, CudaVisionMLP
 from .moe import CudaSparseMoE
@@ -30,6 +30,7 @@ __all__ = [
     "CudaVisionBlock",
     "CudaVisionPatchEmbed",
     "CudaVisionPatchMerger",
+    "PagedKVCache",
     "StaticKVCache",
     "StepGraph",
 ]

@@ -4,9 +4,10 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from ..kernels import (apply_rope, decode_attention, flash_attention, flash_attention_cache, flash_attention_varlen,
-                       matmul_segments, qk_norm_rope, rmsnorm_matmul_segments)
-from .kv_cache import StaticKVCache
+from ..kernels import (apply_rope, decode_attention, decode_attention_paged, flash_attention, flash_attention_cache,
+                       flash_attention_varlen, matmul_segments, qk_norm_rope, qk_norm_rope_paged,
+                       rmsnorm_matmul_segments)
+from .kv_cache import PagedKVCache, StaticKVCache
 from .linear import CudaLinear
 from .norms import CudaRMSNorm, fused_norm_ok
 from .rotary import MRoPEBinding
@@ -64,6 +65,10 @@ class CudaFullAttention(nn.Module):
                               ragged cache: decode when S == 1, else a
                               prefill chunk whose token i attends causally to
                               the cache rows up to its own (lens[b] + i)
+      kv_cache=PagedKVCache   the same over a paged cache: decode reads the
+                              pages through the block table; a prefill chunk
+                              attends over a contiguous copy of the pages its
+                              sequences hold; returns (k_pages, v_pages)
       residual=tensor         added to o_proj's output in the GEMM epilogue
       input_norm=CudaRMSNorm  x is the layer input before this RMSNorm; for
                               decode shapes (at most 32 tokens, bf16) the norm
@@ -92,7 +97,7 @@ class CudaFullAttention(nn.Module):
                 and self.head_dim % 16 == 0 and self.head_dim <= 256 and x.is_cuda)
 
     def forward(self, x: torch.Tensor, mrope_apply, past_kv: tuple[torch.Tensor, torch.Tensor] | None = None, *,
-                kv_cache: StaticKVCache | None = None, residual: torch.Tensor | None = None,
+                kv_cache: StaticKVCache | PagedKVCache | None = None, residual: torch.Tensor | None = None,
                 input_norm: CudaRMSNorm | None = None):
         B, S, _ = x.shape
         Hq, Hkv, D = self.num_heads, self.num_kv_heads, self.head_dim
@@ -121,6 +126,8 @@ class CudaFullAttention(nn.Module):
             rope = mrope_apply.rope
             pos = mrope_apply.positions_int32(x.device, B, S)
             kv_cache.reserve(S)  # raises, before any launch, if a sequence would overflow the cache
+            if isinstance(kv_cache, PagedKVCache):
+                return self._forward_paged(q, k, v, o, pos, rope, kv_cache, residual)
             kc, vc = kv_cache.k.transpose(1, 2), kv_cache.v.transpose(1, 2)  # (B, cap, Hkv, D) views
             # The new tokens' K/V rows go to cache rows [lens[b], lens[b] + S).
             qk_norm_rope(q, k, v, q, kc, vc, self.q_norm.weight, self.k_norm.weight, pos, rope.inv_freq,
@@ -155,3 +162,20 @@ class CudaFullAttention(nn.Module):
         flash_attention(qh, kh, vh, scale=self.scale, is_causal=is_causal, num_kv_groups=self.num_kv_groups,
                         out=o.transpose(1, 2))
         return self.o_proj(o.view(B, S, Hq * D), residual=residual), (kh, vh)
+
+    def _forward_paged(self, q, k, v, o, pos, rope, kv_cache: PagedKVCache, residual):
+        B, S, Hq, D = q.shape
+        pt = kv_cache.block_table
+        # The new tokens' K/V rows go to cache rows [lens[b], lens[b] + S) through the block table.
+        qk_norm_rope_paged(q, k, v, q, kv_cache.k_pages, kv_cache.v_pages, self.q_norm.weight, self.k_norm.weight,
+                           pos, rope.inv_freq, rope.mrope_section, self.q_norm.eps, pt, kv_cache.lens)
+        if S == 1:
+            decode_attention_paged(q[:, 0], kv_cache.k_pages, kv_cache.v_pages, pt, kv_cache.lens, self.scale,
+                                   out=o[:, 0], append=True)
+        else:
+            # Prefill chunk: the pages the sequences hold, copied in row order, are
+            # a (B, Hkv, n * page_rows, D) cache for the ragged chunk kernel.
+            kc, vc = kv_cache.gather(kv_cache.max_len)
+            flash_attention_cache(q.transpose(1, 2), kc, vc, kv_cache.lens, self.scale, self.num_kv_groups,
+                                  out=o.transpose(1, 2), advance=True)
+        return self.o_proj(o.view(B, S, Hq * D), residual=residual), (kv_cache.k_pages, kv_cache.v_pages)

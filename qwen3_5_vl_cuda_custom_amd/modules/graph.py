@@ -24,10 +24,11 @@ import torch
 class StepGraph:
     """Capture `fn()` (after `warmup` eager runs on a side stream) and replay it.
 
-    `caches`: the StaticKVCaches the step appends to, `tokens` rows per
-    sequence each replay; replay() accounts for the rows on the host first
-    (StaticKVCache.reserve), so a replay that would overflow a cache raises
-    instead of launching.
+    `caches`: the StaticKVCaches or PagedKVCaches the step appends to,
+    `tokens` rows per sequence each replay; replay() accounts for the rows on
+    the host first (`reserve`, which for a paged cache assigns the pages and
+    updates the block table before the launch), so a replay that would
+    overflow a cache raises instead of launching.
     """
 
     def __init__(self, fn: Callable[[], Any], warmup: int = 2, *, caches: Sequence[Any] = (),
@@ -45,18 +46,21 @@ class StepGraph:
         torch.cuda.current_stream().wait_stream(side)
         # Capture records the step without running it: the caches' host-side
         # lengths, which the captured forward advances, are put back after.
-        saved = [(c.min_len, c.max_len) for c in self.caches]
+        # Pages the captured append writes are assigned first (a block-table
+        # update is a host copy, which capture cannot record).
+        for c in self.caches:
+            c.prepare_append(tokens)
+        saved = [c.host_state() for c in self.caches]
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
             self.out = fn()
-        for c, (lo, hi) in zip(self.caches, saved):
-            c.min_len, c.max_len = lo, hi
+        for c, state in zip(self.caches, saved):
+            c.set_host_state(state)
 
     def replay(self) -> Any:
         """Launch the captured step on the current stream; returns the static outputs."""
         for c in self.caches:
-            if c.max_len + self.tokens > c.capacity:
-                c.reserve(self.tokens)  # raises, before any cache has been advanced
+            c.check_reserve(self.tokens)  # raises before any cache has been advanced
         for c in self.caches:
             c.reserve(self.tokens)
         self.graph.replay()

@@ -155,6 +155,21 @@ def test_attention_validation():
                                       None) == -2  # Hq % Hkv
     assert L.q3_flash_attention_cache(FAKE, FAKE, FAKE, FAKE, FAKE, 0, 8, 2, 16, 100, 128, st, 0.1, 1, 1,
                                       None) == 0  # empty batch: no-op
+    # paged decode: (num_pages, Hkv=2, page_rows=32, D) pools, 4 pages per sequence
+    pg = _lib.i64s(8 * 128, 128, 2 * 32 * 128, 32 * 128, 128, 2 * 32 * 128, 32 * 128, 128, 8 * 128, 128)
+    ws = L.q3_decode_attention_workspace_bytes(2, 8, 2, 128, 128)
+    assert L.q3_decode_attention_paged(FAKE, FAKE, FAKE, None, 4, 32, 10, FAKE, 0, FAKE, 2, 8, 2, 128, pg, 0.1, 1,
+                                       FAKE, ws, None, None) == -1  # no block table
+    assert L.q3_decode_attention_paged(FAKE, FAKE, FAKE, FAKE, 4, 48, 10, FAKE, 0, FAKE, 2, 8, 2, 128, pg, 0.1, 1,
+                                       FAKE, ws, None, None) == -2  # page rows not a multiple of 32
+    assert L.q3_decode_attention_paged(FAKE, FAKE, FAKE, FAKE, 4, 32, 10, FAKE, 0, FAKE, 2, 8, 2, 64, pg, 0.1, 1,
+                                       FAKE, ws, None, None) == -5  # only the D = 128 bf16 kernel reads pages
+    assert L.q3_decode_attention_paged(FAKE, FAKE, FAKE, FAKE, 4, 32, 10, FAKE, 0, FAKE, 2, 8, 2, 128, pg, 0.1, 0,
+                                       FAKE, ws, None, None) == -5  # fp32
+    assert L.q3_decode_attention_paged(FAKE, FAKE, FAKE, FAKE, 4, 32, 10, FAKE, 0, FAKE, 2, 8, 2, 128, pg, 0.1, 1,
+                                       FAKE, ws - 16, None, None) == -6
+    assert L.q3_decode_attention_paged(FAKE, FAKE, FAKE, FAKE, 4, 32, 10, FAKE, 0, FAKE, 0, 8, 2, 128, pg, 0.1, 1,
+                                       FAKE, ws, None, None) == 0  # empty batch: no-op
 
 
 def test_rope_validation():
@@ -168,6 +183,12 @@ def test_rope_validation():
                              sec, 1e-6, st, 1, None) == -5  # head dim not a multiple of 16
     assert L.q3_qk_norm_rope(FAKE, FAKE, FAKE, FAKE, FAKE, None, None, None, FAKE, FAKE, None, 0, 1, 1, 1, 1, 128,
                              sec, 1e-6, st, 1, None) == -1  # v_in without v_out
+    assert L.q3_qk_norm_rope_paged(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, None, FAKE, FAKE, None, 4, 32, 10, FAKE,
+                                   1, 1, 1, 1, 128, sec, 1e-6, st, 1, None, None) == -1  # no block table
+    assert L.q3_qk_norm_rope_paged(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, None, FAKE, FAKE, FAKE, 4, 32, 10, None,
+                                   1, 1, 1, 1, 128, sec, 1e-6, st, 1, None, None) == -1  # no lengths
+    assert L.q3_qk_norm_rope_paged(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, None, FAKE, FAKE, FAKE, 4, 40, 10, FAKE,
+                                   1, 1, 1, 1, 128, sec, 1e-6, st, 1, None, None) == -2  # page rows
 
 
 def test_moe_validation():

@@ -1,8 +1,9 @@
-"""Host-side logic that needs no GPU: KV-cache length accounting and mRoPE position checks."""
+"""Host-side logic that needs no GPU: KV-cache length accounting, the paged cache's page
+allocator and block table, and mRoPE position checks."""
 import pytest
 import torch
 
-from qwen3_5_vl_cuda_custom_amd.modules import StaticKVCache, TextMRoPE
+from qwen3_5_vl_cuda_custom_amd.modules import PagedKVCache, StaticKVCache, TextMRoPE
 
 
 def test_kv_cache_accounts_appends_and_refuses_overflow():
@@ -29,6 +30,56 @@ def test_kv_cache_initial_lengths():
     assert (c.min_len, c.max_len) == (0, 16) and c.lens.dtype == torch.int32
     with pytest.raises(ValueError):
         c.reserve(1)
+
+
+def test_paged_cache_assigns_pages_as_sequences_grow():
+    c = PagedKVCache(3, 2, 8, num_pages=10, max_pages=4, page_rows=32, dtype=torch.float32, device="cpu")
+    assert c.capacity == 128 and c.empty and c.num_free_pages == 10
+    assert bool((c.block_table == -1).all())
+    c.set_lens([5, 40, 0])  # 1, 2 and 0 pages, handed out from page 0 up
+    assert c.block_table.tolist() == [[0, -1, -1, -1], [1, 2, -1, -1], [-1] * 4]
+    assert c.lens.tolist() == [5, 40, 0] and (c.min_len, c.max_len) == (0, 40) and c.num_free_pages == 7
+    c.reserve(30)  # 35, 70, 30 rows: one more page each
+    assert c.block_table[:, :3].tolist() == [[0, 3, -1], [1, 2, 4], [5, -1, -1]] and c.num_free_pages == 4
+    assert c.lens.tolist() == [5, 40, 0], "device lengths advance in the kernels, not here"
+    c.release(1)
+    assert c.block_table[1].tolist() == [-1] * 4 and c.lens[1] == 0 and c.num_free_pages == 7
+    assert (c.min_len, c.max_len) == (0, 35)
+    c.reserve(1)  # sequence 1 restarts with a recycled page (the most recently freed first)
+    assert c.block_table[1, 0].item() == 1
+
+
+def test_paged_cache_refuses_overflow_without_changing_state():
+    c = PagedKVCache(2, 1, 4, num_pages=5, max_pages=3, page_rows=32, dtype=torch.float32, device="cpu")
+    c.reserve(64)  # 2 pages each: 1 free
+    table = c.block_table.clone()
+    with pytest.raises(ValueError, match="pages needed"):
+        c.reserve(1)  # 2 more pages, 1 free
+    with pytest.raises(ValueError, match="pages needed"):
+        c.check_reserve(1)
+    with pytest.raises(ValueError, match="overflow"):
+        c.check_reserve(33)  # 97 rows > 3 pages of 32
+    assert c.host_state() == [64, 64] and torch.equal(c.block_table, table) and c.num_free_pages == 1
+    c.set_lens([64, 0])
+    c.prepare_append(1)  # the next append's rows get their pages now
+    assert c.host_state() == [64, 0] and c.block_table[:, 2].tolist() == [4, -1] and c.num_free_pages == 0
+    with pytest.raises(ValueError):
+        c.set_lens([97, 0])
+    with pytest.raises(ValueError):
+        PagedKVCache(1, 1, 4, num_pages=2, max_pages=2, page_rows=48, device="cpu")  # not a multiple of 32
+
+
+def test_paged_cache_gather_puts_pages_in_row_order():
+    c = PagedKVCache(2, 2, 4, num_pages=6, max_pages=3, page_rows=32, dtype=torch.float32, device="cpu")
+    c.set_lens([70, 33])  # sequence 0: pages 0, 1, 2; sequence 1: pages 3, 4
+    for pg in range(6):
+        c.k_pages[pg] = pg
+        c.v_pages[pg] = -pg
+    k, v = c.gather(70)
+    assert k.shape == (2, 2, 96, 4)
+    assert k[0, :, ::32, 0].tolist() == [[0, 1, 2], [0, 1, 2]]
+    assert k[1, 1, ::32, 0].tolist() == [3, 4, 0]  # past its pages: page 0's rows (never attended)
+    assert torch.equal(v[0], -k[0])
 
 
 def test_mrope_positions_checked_and_broadcast():
