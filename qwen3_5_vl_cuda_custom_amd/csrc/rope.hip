@@ -211,11 +211,15 @@ struct QKNormRopeArgs {
 // * inv_freq[i], fp32, sincosf) are computed once into LDS and shared by all
 // of its q, k (and v) head rows. A group of G = D/8 lanes handles one head
 // row, lane j holding elements [8j, 8j+8); the rotate-half partner of lane j
-// is lane j ^ (G/2). Every load of a batch of up to kQKBatch rows per lane
-// group (the rows, both norm weights, the positions and frequencies) is issued
-// before the first use, so a decode call (one batch) costs one memory round
-// trip before its stores.
-constexpr int kQKBatch = 4;
+// is lane j ^ (G/2). A lane group loads BATCH of its rows at a time (rows
+// past the end repeat the last one). BATCH = 1 with at most 80 VGPRs (six
+// waves per SIMD) measured fastest at D = 128, 48 rows per token: S=4096
+// 27.8 -> 23.5 us, a 32-token decode step 5.4 -> 5.1 us; a batch that does
+// not divide the 16-row passes into the token's rows (2, 4) loads rows it
+// never uses, and 8 waves per SIMD spill. The fp32 and unaligned forms keep
+// the default bound (at 80 VGPRs they spill).
+constexpr int kQKBatch = 1;
+constexpr int kQKMinBlocks = 6;
 
 // One of three kernel arguments by a per-lane index, as selects (indexing the
 // argument array with a lane-varying index would load it from memory).
@@ -258,8 +262,75 @@ __device__ __forceinline__ void store8(T* p, const float (&v)[8]) {
   }
 }
 
+// Row `row` of a token's q | k | v rows: kind 0 = q, 1 = k, 2 = v, and its head.
+__device__ __forceinline__ void qk_row_kind(const QKNormRopeArgs& a, int row, int& kind, int& h) {
+  kind = row < a.Hq ? 0 : (row < a.Hq + a.Hkv ? 1 : 2);
+  h = kind == 0 ? row : (kind == 1 ? row - a.Hq : row - a.Hq - a.Hkv);
+}
+
+// Input row `row` of token (b, s).
+template <typename T>
+__device__ __forceinline__ const T* qk_in_row(const QKNormRopeArgs& a, int64_t b, int64_t s, int row) {
+  int kind, h;
+  qk_row_kind(a, row, kind, h);
+  return static_cast<const T*>(kind == 0 ? a.q_in : (kind == 1 ? a.k_in : a.v_in)) +
+         b * pick3(kind, a.st[0], a.st[3], a.st[6]) + s * pick3(kind, a.st[1], a.st[4], a.st[7]) +
+         h * pick3(kind, a.st[2], a.st[5], a.st[8]);
+}
+
+// One head row of token (b, s), held by a group of G lanes (lane j: elements
+// [8j, 8j+8) in x): RMSNorm (with weights) and mRoPE for q and k rows, then the
+// store (k / v rows at sequence offset so_b, through the block table when
+// paged; rows past dst_seq_cap or on a rejected page are not written).
 template <typename T, int G, bool VEC>
-__global__ __launch_bounds__(256) void qk_norm_rope_kernel(const QKNormRopeArgs a) {
+__device__ __forceinline__ void qk_row(const QKNormRopeArgs& a, int64_t b, int64_t s, int row, int j, int so_b,
+                                       float (&x)[8], const float (&cs)[8], const float (&sn)[8],
+                                       const float (&wq)[8], const float (&wk)[8]) {
+  constexpr int D = G * 8;
+  const bool lo = j < G / 2;
+  int kind, h;
+  qk_row_kind(a, row, kind, h);
+  const int so = kind > 0 ? so_b : 0;
+  bool skip_store = kind > 0 && (s + (int64_t)so >= a.dst_seq_cap || s + so < 0);
+  int64_t ob = b, orow = s + so;  // k / v: page and row within it when paged
+  if (kind > 0 && a.block_table && !skip_store) {
+    const int pg = a.block_table[b * a.max_pages + orow / a.page_rows];
+    if ((unsigned)pg >= (unsigned)a.num_pages) {
+      if (a.status && j == 0) atomicOr(a.status, 2);
+      skip_store = true;
+    }
+    ob = pg;
+    orow %= a.page_rows;
+  }
+  T* out = static_cast<T*>(kind == 0 ? a.q_out : (kind == 1 ? a.k_out : a.v_out)) +
+           ob * pick3(kind, a.st[9], a.st[12], a.st[15]) + orow * pick3(kind, a.st[10], a.st[13], a.st[16]) +
+           h * pick3(kind, a.st[11], a.st[14], a.st[17]);
+  if (kind < 2) {
+    // RMSNorm over the head (skipped when no weights are given).
+    if (a.q_w != nullptr) {
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+      ss = group_sum<G>(ss);
+      const float rstd = rsqrtf(ss / (float)D + a.eps);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = x[e] * rstd * (kind == 0 ? wq[e] : wk[e]);
+    }
+    // mRoPE.
+    float p[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) p[e] = __shfl_xor(x[e], G / 2, 64);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      // lo half: x1*c - x2*s  (partner holds x2); hi half: x2*c + x1*s (partner holds x1).
+      x[e] = lo ? (x[e] * cs[e] - p[e] * sn[e]) : (x[e] * cs[e] + p[e] * sn[e]);
+  }
+  if (skip_store) return;
+  store8<T, VEC>(out + 8 * j, x);
+}
+
+template <typename T, int G, bool VEC, int BATCH = kQKBatch, int MINB = 1>
+__global__ __launch_bounds__(256, MINB) void qk_norm_rope_kernel(const QKNormRopeArgs a) {
   constexpr int D = G * 8;
   constexpr int HALF = D / 2;
   constexpr int RPP = 256 / G;  // rows per pass of the block
@@ -268,7 +339,6 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const QKNormRopeArgs 
   const int b = blockIdx.x / a.S, s = blockIdx.x % a.S;
   const int j = tid % G;
   const int nrows = a.Hq + a.Hkv + (a.v_out ? a.Hkv : 0);
-  const bool lo = j < G / 2;
 
   // The token's angles: thread i < HALF loads its position and frequency.
   int posv = 0;
@@ -283,22 +353,11 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const QKNormRopeArgs 
   float wq[8], wk[8];
   load8<T, VEC>(static_cast<const T*>(has_w ? a.q_w : a.q_in) + 8 * j, wq);
   load8<T, VEC>(static_cast<const T*>(has_w ? a.k_w : a.q_in) + 8 * j, wk);
-  auto row_kind = [&](int row, int& kind, int& h) {
-    kind = row < a.Hq ? 0 : (row < a.Hq + a.Hkv ? 1 : 2);  // 0 = q, 1 = k, 2 = v
-    h = kind == 0 ? row : (kind == 1 ? row - a.Hq : row - a.Hq - a.Hkv);
-  };
   // Rows past the end load row nrows - 1 again (no branch around the loads).
-  float v[kQKBatch][8];
+  float v[BATCH][8];
   auto load_batch = [&](int r0) {
 #pragma unroll
-    for (int u = 0; u < kQKBatch; ++u) {
-      int kind, h;
-      row_kind(min(r0 + u * RPP, nrows - 1), kind, h);
-      const T* in = static_cast<const T*>(kind == 0 ? a.q_in : (kind == 1 ? a.k_in : a.v_in)) +
-                    b * pick3(kind, a.st[0], a.st[3], a.st[6]) + s * pick3(kind, a.st[1], a.st[4], a.st[7]) +
-                    h * pick3(kind, a.st[2], a.st[5], a.st[8]);
-      load8<T, VEC>(in + 8 * j, v[u]);
-    }
+    for (int u = 0; u < BATCH; ++u) load8<T, VEC>(qk_in_row<T>(a, b, s, min(r0 + u * RPP, nrows - 1)) + 8 * j, v[u]);
   };
   const int first = tid / G;
   load_batch(first);
@@ -317,54 +376,13 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const QKNormRopeArgs 
     cs[e] = s_cos[i];
     sn[e] = s_sin[i];
   }
-  for (int r0 = first; r0 < nrows; r0 += kQKBatch * RPP) {  // uniform per lane group
+  for (int r0 = first; r0 < nrows; r0 += BATCH * RPP) {  // uniform per lane group
     if (r0 != first) load_batch(r0);
 #pragma unroll
-    for (int u = 0; u < kQKBatch; ++u) {
+    for (int u = 0; u < BATCH; ++u) {
       const int row = r0 + u * RPP;
       if (row >= nrows) break;
-      int kind, h;
-      row_kind(row, kind, h);
-      const int so = kind > 0 ? so_b : 0;
-      bool skip_store = kind > 0 && (s + (int64_t)so >= a.dst_seq_cap || s + so < 0);
-      int64_t ob = b, orow = s + so;  // k / v: page and row within it when paged
-      if (kind > 0 && a.block_table && !skip_store) {
-        const int pg = a.block_table[(int64_t)b * a.max_pages + orow / a.page_rows];
-        if ((unsigned)pg >= (unsigned)a.num_pages) {
-          if (a.status && j == 0) atomicOr(a.status, 2);
-          skip_store = true;
-        }
-        ob = pg;
-        orow %= a.page_rows;
-      }
-      T* out = static_cast<T*>(kind == 0 ? a.q_out : (kind == 1 ? a.k_out : a.v_out)) +
-               ob * pick3(kind, a.st[9], a.st[12], a.st[15]) + orow * pick3(kind, a.st[10], a.st[13], a.st[16]) +
-               h * pick3(kind, a.st[11], a.st[14], a.st[17]);
-      float x[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = v[u][e];
-      if (kind < 2) {
-        // RMSNorm over the head (skipped when no weights are given).
-        if (has_w) {
-          float ss = 0.f;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
-          ss = group_sum<G>(ss);
-          const float rstd = rsqrtf(ss / (float)D + a.eps);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) x[e] = x[e] * rstd * (kind == 0 ? wq[e] : wk[e]);
-        }
-        // mRoPE.
-        float p[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) p[e] = __shfl_xor(x[e], G / 2, 64);
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          // lo half: x1*c - x2*s  (partner holds x2); hi half: x2*c + x1*s (partner holds x1).
-          x[e] = lo ? (x[e] * cs[e] - p[e] * sn[e]) : (x[e] * cs[e] + p[e] * sn[e]);
-      }
-      if (skip_store) continue;
-      store8<T, VEC>(out + 8 * j, x);
+      qk_row<T, G, VEC>(a, b, s, row, j, so_b, v[u], cs, sn, wq, wk);
     }
   }
 }
@@ -381,8 +399,9 @@ int launch_qk(const QKNormRopeArgs& a, hipStream_t st) {
              (!a.q_w || (q3_aligned(a.q_w, 16) && q3_aligned(a.k_w, 16)));
   for (int i = 0; i < 18; ++i) vec = vec && (a.st[i] * (int64_t)sizeof(T)) % 16 == 0;
   auto go = [&](auto g, auto v) {
-    hipLaunchKernelGGL((qk_norm_rope_kernel<T, decltype(g)::value, decltype(v)::value>), dim3((unsigned)tokens),
-                       dim3(256), 0, st, a);
+    constexpr int minb = std::is_same<T, bf16>::value && decltype(v)::value ? kQKMinBlocks : 1;
+    hipLaunchKernelGGL((qk_norm_rope_kernel<T, decltype(g)::value, decltype(v)::value, kQKBatch, minb>),
+                       dim3((unsigned)tokens), dim3(256), 0, st, a);
   };
   using VT = std::true_type;
   using VF = std::false_type;
