@@ -387,6 +387,124 @@ __device__ __forceinline__ void store_tile_lds(const GemmParams& p, const TileCt
   }
 }
 
+// True when the stored value takes no fp32 arithmetic after its one rounding:
+// SwiGLU, the row scale (whose first step rounds the accumulator), a plain
+// store without bias, activation or residual.
+template <int EPI>
+__device__ __forceinline__ bool epi_rounds_first(const GemmParams& p, const TileCtx& t) {
+  if constexpr (EPI == kEpiSwiGLU || EPI == kEpiRowScale) {
+    return true;
+  } else {
+    bool bias = p.seg.n > 1 ? false : t.bias != nullptr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bias = bias || (p.seg.n > 1 && i < p.seg.n && p.seg.b[i] != nullptr);
+    return !bias && !p.act && p.R == nullptr;
+  }
+}
+
+// The LDS epilogue for outputs that round first (epi_rounds_first): the
+// accumulators go to LDS already rounded to bf16, half the bytes of the fp32
+// staging (a 256x256 tile fits one pass), and every lane then moves whole
+// 16-byte chunks from LDS to memory, with all of a full pass's LDS reads in
+// flight before its stores. Values are those of store_tile_lds (one rounding,
+// same arithmetic). LDS rows are BN_OUT bf16; 16-byte chunk c of row r sits
+// at chunk c ^ (r & SWZ).
+template <int BM, int BN_OUT, int WTM, int WTN, int TN, int TM, int EPI, int NW, int LDS_BYTES>
+__device__ __forceinline__ void store_tile_lds_bf16(const GemmParams& p, const TileCtx& t,
+                                                    const floatx16 (&c)[TN][TM], int wm, int wn, int lane,
+                                                    bf16* lds) {
+  constexpr int RP0 = LDS_BYTES / (BN_OUT * 2);
+  constexpr int RP1 = RP0 >= 256 ? 256 : RP0 >= 128 ? 128 : RP0 >= 64 ? 64 : 32;
+  constexpr int RP = RP1 < BM ? RP1 : BM;  // rows per pass
+  constexpr int NPASS = (BM + RP - 1) / RP;
+  constexpr int C8 = BN_OUT / 8;  // 16-byte chunks per row
+  // XOR swizzle over aligned blocks of chunks that divide the row (24 chunks:
+  // blocks of 8), so a swizzled chunk stays in its row.
+  constexpr int SWZ = C8 % 16 == 0 ? 15 : 7;
+  static_assert(C8 % (SWZ + 1) == 0, "swizzle blocks must divide the row");
+  constexpr int WTN_OUT = EPI == kEpiSwiGLU ? WTN / 2 : WTN;
+  constexpr int TN_OUT = EPI == kEpiSwiGLU ? TN / 2 : TN;
+  constexpr int NT = NW * 64;
+  static_assert(BN_OUT % 64 == 0 && RP % 32 == 0, "epilogue tiling");
+  constexpr int ITEMS = (RP * C8) / NT;  // chunks per thread in a full pass
+  static_assert(ITEMS >= 1 && (RP * C8) % NT == 0, "whole chunks per thread");
+  const int m_begin = t.m_begin, rows_m = t.rows_m, n0_out = t.n0_out;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int N = p.N;
+  const bool vec_ok = ((p.ldc & 7) == 0) && (reinterpret_cast<uintptr_t>(t.C) & 15) == 0;
+  const bool full_n = vec_ok && n0_out + BN_OUT <= N;
+  auto slot = [](int r, int c8) { return r * BN_OUT + ((c8 ^ (r & SWZ)) << 3); };
+  // One finished chunk (8 columns) of tile row lr of the pass at r0.
+  auto finish = [&](bf16x8 v, int r0, int lr, int c8, bool whole) {
+    const int m = m_begin + r0 + lr;
+    const int n = n0_out + c8 * 8;
+    if constexpr (EPI == kEpiRowScale) {
+      const float rs = bf2f(p.rowscale[m]);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = f2bf(bf2f(v[q]) * rs);
+    }
+    bf16* crow = t.C + (int64_t)m * p.ldc;
+    if (whole || (vec_ok && n + 7 < N)) {
+      *reinterpret_cast<bf16x8*>(crow + n) = v;
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (n + q < N) crow[n + q] = v[q];
+    }
+  };
+  __syncthreads();  // every wave is done with the main loop's LDS
+#pragma unroll
+  for (int pass = 0; pass < NPASS; ++pass) {
+    const int r0 = pass * RP;
+    // 1. this wave's accumulator rows of the pass -> LDS, rounded once
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+      const int mr = wm * WTM + j * 32;  // tile row of this m-tile (wave-uniform)
+      if (mr < r0 || mr >= r0 + RP) continue;
+      const int lr = mr - r0 + l32;
+#pragma unroll
+      for (int i = 0; i < TN_OUT; ++i) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int col = wn * WTN_OUT + i * 32 + 8 * g + 4 * h;
+          bf16x4 v;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            if constexpr (EPI == kEpiSwiGLU) {
+              const float gt = c[2 * i][j][4 * g + q];
+              const float up = c[2 * i + 1][j][4 * g + q];
+              v[q] = f2bf(gt / (1.0f + __expf(-gt)) * up);
+            } else {
+              v[q] = f2bf(c[i][j][4 * g + q]);
+            }
+          }
+          *reinterpret_cast<bf16x4*>(lds + slot(lr, col >> 3) + (col & 7)) = v;
+        }
+      }
+    }
+    __syncthreads();
+    // 2. rows of the pass -> memory, one 16-byte chunk per lane and item
+    const int nrows = min(RP, rows_m - r0);
+    if (nrows == RP && full_n) {
+      bf16x8 v[ITEMS];
+#pragma unroll
+      for (int u = 0; u < ITEMS; ++u) {
+        const int it = threadIdx.x + u * NT;
+        v[u] = *reinterpret_cast<const bf16x8*>(lds + slot(it / C8, it % C8));
+      }
+#pragma unroll
+      for (int u = 0; u < ITEMS; ++u) {
+        const int it = threadIdx.x + u * NT;
+        finish(v[u], r0, it / C8, it % C8, true);
+      }
+    } else {
+      for (int it = threadIdx.x; it < nrows * C8; it += NT)
+        finish(*reinterpret_cast<const bf16x8*>(lds + slot(it / C8, it % C8)), r0, it / C8, it % C8, false);
+    }
+    if (pass + 1 < NPASS) __syncthreads();  // the next pass overwrites the LDS
+  }
+}
+
 // Swizzle of a BKT-element LDS row (BKT / 8 chunks of 16 bytes): chunk c of
 // row r sits at slot c ^ dma_swz<BKT>(r). For 32 or 16 consecutive rows read
 // one chunk each (a fragment read), the slots land on distinct 16-byte
@@ -651,8 +769,11 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
     main_loop(std::false_type{});
   vm_wait<0>();  // the trailing zero-fill DMAs must land before the block's LDS is reused
 
-  store_tile_lds<BM, BN_OUT, WTM, WTN, TN, TM, EPI, NW, kRing * 2>(p, tc, acc.c, wm, wn, lane,
-                                                                  reinterpret_cast<float*>(smem));
+  if (epi_rounds_first<EPI>(p, tc))
+    store_tile_lds_bf16<BM, BN_OUT, WTM, WTN, TN, TM, EPI, NW, kRing * 2>(p, tc, acc.c, wm, wn, lane, smem);
+  else if constexpr (EPI == kEpiStore)
+    store_tile_lds<BM, BN_OUT, WTM, WTN, TN, TM, EPI, NW, kRing * 2>(p, tc, acc.c, wm, wn, lane,
+                                                                    reinterpret_cast<float*>(smem));
 }
 
 }  // namespace q3
