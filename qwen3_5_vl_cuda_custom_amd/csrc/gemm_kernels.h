@@ -190,7 +190,7 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, const TileCtx& t
           for (int q = 0; q < 4; ++q) {
             const float gt = c[2 * i][j][4 * g + q];
             const float up = c[2 * i + 1][j][4 * g + q];
-            o[q] = gt / (1.0f + __expf(-gt)) * up;
+            o[q] = silu_mul(gt, up);
           }
           if (vec_ok && n + 3 < N) {
             bf16x4 v = {f2bf(o[0]), f2bf(o[1]), f2bf(o[2]), f2bf(o[3])};
@@ -312,7 +312,7 @@ __device__ __forceinline__ void store_tile_lds(const GemmParams& p, const TileCt
             if constexpr (EPI == kEpiSwiGLU) {
               const float gt = c[2 * i][j][4 * g + q];
               const float up = c[2 * i + 1][j][4 * g + q];
-              v[q] = gt / (1.0f + __expf(-gt)) * up;
+              v[q] = silu_mul(gt, up);
             } else {
               v[q] = c[i][j][4 * g + q];
             }
@@ -473,7 +473,7 @@ __device__ __forceinline__ void store_tile_lds_bf16(const GemmParams& p, const T
             if constexpr (EPI == kEpiSwiGLU) {
               const float gt = c[2 * i][j][4 * g + q];
               const float up = c[2 * i + 1][j][4 * g + q];
-              v[q] = f2bf(gt / (1.0f + __expf(-gt)) * up);
+              v[q] = f2bf(silu_mul(gt, up));
             } else {
               v[q] = f2bf(c[i][j][4 * g + q]);
             }

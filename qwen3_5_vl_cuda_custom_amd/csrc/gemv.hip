@@ -98,8 +98,6 @@ __device__ __forceinline__ SegPick seg_pick(const WeightSegments& sg, int N, int
   return r;
 }
 
-__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + __expf(-g)) * u; }
-
 template <bool SWIGLU>
 __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
   constexpr int NST = kGvStages;

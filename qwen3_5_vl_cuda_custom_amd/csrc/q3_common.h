@@ -90,6 +90,15 @@ __device__ __forceinline__ float wave_max(float v) {
   for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;
 }
+// silu(g) * u of the fused SwiGLU epilogues (GEMM tiles, decode GEMVs), in
+// fp32 before the one rounding: the hardware reciprocal (v_rcp_f32, ~1 ulp)
+// instead of an IEEE division, which cost ~1.8 us per wave of 256x256 tiles.
+// Ordered g * rcp * u so that a reciprocal of 0 (exp overflow) gives a signed
+// zero rather than inf * 0.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+}
+
 // Reduction over aligned groups of G lanes (G a power of two <= 64).
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
