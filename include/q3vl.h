@@ -310,6 +310,19 @@ int q3_vision_pos_embed(const int* images, const int* images_host, int64_t n_img
 int q3_moe_route(const void* logits, int* top_idx, void* top_w, float* top_p, int64_t T, int64_t E, int64_t k,
                  int norm, void* stream);
 
+/* The router whole (modules/moe.py:60-65 with the gate projection of
+ * modules/moe.py:59, matmul_forward, csrc/matmul_op.cpp:10): logits (T, E)
+ * bf16 = x (T, H) . gate_w (E, H)^T, computed as fp32 partial products over
+ * K splits (q3_moe_router_workspace_bytes: splits x T x E fp32) summed in
+ * split order and rounded once, then q3_moe_route on those logits. For
+ * prefill-sized T, where a (T, 128) output has too few tiles to occupy the
+ * GPU (4096 x 128: 32 tiles). bf16 only; H a multiple of 8, x and gate_w
+ * 16-byte aligned. */
+int64_t q3_moe_router_workspace_bytes(int64_t T, int64_t H, int64_t E);
+int q3_moe_router(const void* x, const void* gate_w, void* logits, int* top_idx, void* top_w, float* top_p,
+                  int64_t T, int64_t H, int64_t E, int64_t k, int norm, void* workspace, int64_t workspace_bytes,
+                  void* stream);
+
 /* Expert dispatch, SwiGLU experts and combine of CudaSparseMoE.forward
  * (modules/moe.py:70-83): replaces the per-expert loop of matmul_forward,
  * swiglu_forward and index_add_forward (csrc/moe_routing_op.cpp:11) with a

@@ -68,6 +68,8 @@ _SIGS: dict[str, tuple] = {
     "q3_vision_rope_tables": (c_int, [_i32p, _i32p, _I, _I, _I, _f32p, _f32p, _f32p, _V]),
     "q3_vision_pos_embed": (c_int, [_i32p, _i32p, _I, _I, _I, _V, _V, _V, _I, c_int, _V]),
     "q3_moe_route": (c_int, [_V, _i32p, _V, _f32p, _I, _I, _I, c_int, _V]),
+    "q3_moe_router_workspace_bytes": (c_int64, [_I, _I, _I]),
+    "q3_moe_router": (c_int, [_V, _V, _V, _i32p, _V, _f32p, _I, _I, _I, _I, c_int, _V, _I, _V]),
     "q3_moe_experts_workspace_bytes": (c_int64, [_I, _I, _I, _I, _I]),
     "q3_moe_experts": (c_int, [_V, _V, _V, _i32p, _V, _V, _V, _I, _I, _I, _I, _I, _V, _I, _V]),
     "q3_moe_permute_workspace_bytes": (c_int64, [_I, _I, _I]),

@@ -10,6 +10,7 @@ enum Epilogue : int {
   kEpiStore = 0,     // C = acc (+ bias[n]) (+ R[m, n]), rounded once
   kEpiSwiGLU = 1,    // C = silu(acc_gate) * acc_up, rounded once
   kEpiRowScale = 2,  // C = bf16(bf16(acc) * s[m])  (MoE expert output x routing weight)
+  kEpiStoreF32 = 3,  // C (fp32, ld = ldc floats, batch stride bsC floats) = acc, not rounded (split-K partials)
 };
 
 // Up to 4 weight matrices stacked along N and computed in one launch (the
@@ -127,7 +128,10 @@ __device__ __forceinline__ bool tile_ctx(const GemmParams& p, TileCtx& t) {
     const int z = blockIdx.z;
     X += z * p.bsX;
     W += z * p.bsW;
-    C += z * p.bsC;
+    if constexpr (EPI == kEpiStoreF32)
+      C = reinterpret_cast<bf16*>(reinterpret_cast<float*>(C) + z * p.bsC);
+    else
+      C += z * p.bsC;
   }
   const int rows_m = m_end - m_begin;
   const int n0_out = tile_n * BN_OUT;
@@ -161,120 +165,16 @@ __device__ __forceinline__ const bf16* seg_bias(const WeightSegments& sg, int n)
   return b ? b - st : nullptr;
 }
 
-// Epilogue of one wave's (TN x TM) 32x32 accumulator tiles at wave offset
-// (wm * WTM, wn * WTN) of the block tile.
-template <int WTM, int WTN, int TN, int TM, int EPI>
-__device__ __forceinline__ void store_tile(const GemmParams& p, const TileCtx& t, const floatx16 (&c)[TN][TM],
-                                           int wm, int wn, int lane) {
-  const int m_begin = t.m_begin, rows_m = t.rows_m, n0_out = t.n0_out;
-  const bf16* bias = t.bias;
-  bf16* C = t.C;
-  const int l32 = lane & 31;
-  const int h = lane >> 5;
-  const int N = p.N;
-  const bool vec_ok = ((p.ldc & 3) == 0) && (p.R == nullptr || (p.ldr & 3) == 0);
-
-  if constexpr (EPI == kEpiSwiGLU) {
-#pragma unroll
-    for (int i = 0; i < TN / 2; ++i) {
-#pragma unroll
-      for (int j = 0; j < TM; ++j) {
-        const int mr = wm * WTM + j * 32 + l32;
-        if (mr >= rows_m) continue;
-        bf16* crow = C + (int64_t)(m_begin + mr) * p.ldc;
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int n = n0_out + (wn * WTN) / 2 + i * 32 + 8 * g + 4 * h;
-          float o[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float gt = c[2 * i][j][4 * g + q];
-            const float up = c[2 * i + 1][j][4 * g + q];
-            o[q] = silu_mul(gt, up);
-          }
-          if (vec_ok && n + 3 < N) {
-            bf16x4 v = {f2bf(o[0]), f2bf(o[1]), f2bf(o[2]), f2bf(o[3])};
-            *reinterpret_cast<bf16x4*>(crow + n) = v;
-          } else {
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-              if (n + q < N) crow[n + q] = f2bf(o[q]);
-          }
-        }
-        __builtin_amdgcn_sched_barrier(0);  // one accumulator tile live at a time
-      }
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < TN; ++i) {
-#pragma unroll
-      for (int j = 0; j < TM; ++j) {
-        const int mr = wm * WTM + j * 32 + l32;
-        if (mr >= rows_m) continue;
-        const int m = m_begin + mr;
-        bf16* crow = C + (int64_t)m * p.ldc;
-        float rs = 1.0f;
-        if constexpr (EPI == kEpiRowScale) rs = bf2f(p.rowscale[m]);
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int n = n0_out + wn * WTN + i * 32 + 8 * g + 4 * h;
-          float o[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) o[q] = c[i][j][4 * g + q];
-          if constexpr (EPI == kEpiStore) {
-            // segment starts are multiples of 16: both lane halves' columns share a segment
-            if (p.seg.n > 1) bias = seg_bias(p.seg, n - 4 * h);
-          }
-          if (vec_ok && n + 3 < N) {
-            if (bias) {
-              const bf16x4 b = *reinterpret_cast<const bf16x4*>(bias + n);
-#pragma unroll
-              for (int q = 0; q < 4; ++q) o[q] += bf2f(b[q]);
-            }
-            if (EPI == kEpiStore && p.act) {
-#pragma unroll
-              for (int q = 0; q < 4; ++q) o[q] = gelu_tanh_f(o[q]);
-            }
-            if (p.R) {
-              const bf16x4 rv = *reinterpret_cast<const bf16x4*>(p.R + (int64_t)m * p.ldr + n);
-#pragma unroll
-              for (int q = 0; q < 4; ++q) o[q] += bf2f(rv[q]);
-            }
-            if constexpr (EPI == kEpiRowScale) {
-#pragma unroll
-              for (int q = 0; q < 4; ++q) o[q] = bf2f(f2bf(o[q])) * rs;
-            }
-            bf16x4 v = {f2bf(o[0]), f2bf(o[1]), f2bf(o[2]), f2bf(o[3])};
-            *reinterpret_cast<bf16x4*>(crow + n) = v;
-          } else {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              if (n + q >= N) continue;
-              float v = o[q];
-              if (bias) v += bf2f(bias[n + q]);
-              if (EPI == kEpiStore && p.act) v = gelu_tanh_f(v);
-              if (p.R) v += bf2f(p.R[(int64_t)m * p.ldr + n + q]);
-              if constexpr (EPI == kEpiRowScale) v = bf2f(f2bf(v)) * rs;
-              crow[n + q] = f2bf(v);
-            }
-          }
-        }
-        __builtin_amdgcn_sched_barrier(0);  // one accumulator tile live at a time
-      }
-    }
-  }
-}
-
 // Epilogue through LDS. Stored straight from the accumulators, one wave store
 // instruction writes 32 rows x 16 bytes (a lane holds 4 consecutive columns of
 // one row), which the memory system takes at ~1.2 TB/s: at S = 4096 that is
 // ~80 us of the gate/up GEMM. Instead the accumulators (after the register-level
 // part of the epilogue, SwiGLU) go to the LDS ring, free by then, as fp32 in
 // passes of RP rows; every wave then reads whole rows back, 8 consecutive columns
-// per lane, adds bias / applies gelu / adds the residual / the row scale, rounds
-// once and stores 16 bytes per lane: contiguous rows per instruction. The
-// arithmetic and its order are those of the direct store (bit-identical output).
-// LDS rows are BN_OUT fp32; 16-byte chunk c of row r sits at chunk c ^ (r & 15).
+// per lane, adds bias / applies gelu / adds the residual, rounds once and
+// stores 16 bytes per lane (kEpiStoreF32: 32 bytes of fp32, not rounded):
+// contiguous rows per instruction. LDS rows are BN_OUT fp32; 16-byte chunk c
+// of row r sits at chunk c ^ (r & 15).
 template <int BM, int BN_OUT, int WTM, int WTN, int TN, int TM, int EPI, int NW, int LDS_BYTES>
 __device__ __forceinline__ void store_tile_lds(const GemmParams& p, const TileCtx& t, const floatx16 (&c)[TN][TM],
                                                int wm, int wn, int lane, float* lds) {
@@ -367,12 +267,18 @@ __device__ __forceinline__ void store_tile_lds(const GemmParams& p, const TileCt
               if (n + q < N) o[q] += bf2f(rrow[n + q]);
           }
         }
-      } else if constexpr (EPI == kEpiRowScale) {
-        const float rs = bf2f(p.rowscale[m]);
-#pragma unroll
-        for (int q = 0; q < 8; ++q) o[q] = bf2f(f2bf(o[q])) * rs;
       }
-      if (vec_ok && n + 7 < N) {
+      if constexpr (EPI == kEpiStoreF32) {
+        float* frow = reinterpret_cast<float*>(t.C) + (int64_t)m * p.ldc;
+        if (vec_ok && n + 7 < N) {
+          *reinterpret_cast<floatx4*>(frow + n) = floatx4{o[0], o[1], o[2], o[3]};
+          *reinterpret_cast<floatx4*>(frow + n + 4) = floatx4{o[4], o[5], o[6], o[7]};
+        } else {
+#pragma unroll
+          for (int q = 0; q < 8; ++q)
+            if (n + q < N) frow[n + q] = o[q];
+        }
+      } else if (vec_ok && n + 7 < N) {
         bf16x8 v;
 #pragma unroll
         for (int q = 0; q < 8; ++q) v[q] = f2bf(o[q]);
@@ -394,6 +300,8 @@ template <int EPI>
 __device__ __forceinline__ bool epi_rounds_first(const GemmParams& p, const TileCtx& t) {
   if constexpr (EPI == kEpiSwiGLU || EPI == kEpiRowScale) {
     return true;
+  } else if constexpr (EPI == kEpiStoreF32) {
+    return false;
   } else {
     bool bias = p.seg.n > 1 ? false : t.bias != nullptr;
 #pragma unroll
@@ -771,7 +679,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
 
   if (epi_rounds_first<EPI>(p, tc))
     store_tile_lds_bf16<BM, BN_OUT, WTM, WTN, TN, TM, EPI, NW, kRing * 2>(p, tc, acc.c, wm, wn, lane, smem);
-  else if constexpr (EPI == kEpiStore)
+  else if constexpr (EPI == kEpiStore || EPI == kEpiStoreF32)
     store_tile_lds<BM, BN_OUT, WTM, WTN, TN, TM, EPI, NW, kRing * 2>(p, tc, acc.c, wm, wn, lane,
                                                                     reinterpret_cast<float*>(smem));
 }

@@ -43,10 +43,15 @@ constexpr int kMoeBN = 256;
 constexpr int kMoeNSTW = 3;
 
 // ------------------------------------------------------------------ routing
+// partials (split-K router, q3_moe_router): the logits are first summed from
+// nsplit fp32 planes of (T, E), in plane order, rounded once to bf16 and
+// written to `logits_out`; the routing then uses those bf16 values.
 template <int MAXV>
 __global__ __launch_bounds__(256) void moe_route_kernel(const bf16* __restrict__ logits, int* __restrict__ top_idx,
                                                         bf16* __restrict__ top_w, float* __restrict__ top_p,
-                                                        int T, int E, int k, int norm) {
+                                                        int T, int E, int k, int norm,
+                                                        const float* __restrict__ partials, int nsplit,
+                                                        bf16* __restrict__ logits_out) {
   const int lane = threadIdx.x & 63;
   const int t = (int)(((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6);
   if (t >= T) return;
@@ -54,13 +59,28 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const bf16* __restrict__
   float v[MAXV];
   bool live[MAXV];
   float mx = -INFINITY;
+  if (partials) {
+    const int64_t plane = (int64_t)T * E;
 #pragma unroll
-  for (int i = 0; i < MAXV; ++i) {
-    const int e = lane + 64 * i;
-    live[i] = e < E;
-    v[i] = live[i] ? bf2f(lr[e]) : -INFINITY;
-    mx = fmaxf(mx, v[i]);
+    for (int i = 0; i < MAXV; ++i) {
+      const int e = lane + 64 * i;
+      live[i] = e < E;
+      float acc = 0.f;
+      for (int z = 0; z < nsplit; ++z) acc += live[i] ? partials[z * plane + (int64_t)t * E + e] : 0.f;
+      const bf16 b = f2bf(acc);
+      if (live[i]) logits_out[(int64_t)t * E + e] = b;
+      v[i] = live[i] ? bf2f(b) : -INFINITY;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < MAXV; ++i) {
+      const int e = lane + 64 * i;
+      live[i] = e < E;
+      v[i] = live[i] ? bf2f(lr[e]) : -INFINITY;
+    }
   }
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) mx = fmaxf(mx, v[i]);
   mx = wave_max(mx);
   float s = 0.f;
 #pragma unroll
@@ -630,6 +650,41 @@ int index_add_t(void* target, const void* src, const int64_t* idx, int64_t ns, i
 
 }  // namespace
 
+namespace {
+
+// Splits over K of the router GEMM (q3_moe_router): enough (T/128 x E/128)
+// tiles x splits to give every CU one (at most 256), each split a multiple of
+// 64 columns dividing H (a 2048-wide router at 4096 tokens: 32 tiles x 8
+// splits of 256).
+int router_splits(int64_t T, int64_t H, int64_t E) {
+  const int64_t tiles = q3_cdiv(T, 128) * q3_cdiv(E, 128);
+  int best = 1;
+  for (int s = 2; s <= 64; ++s)
+    if (tiles * s <= 256 && H % s == 0 && (H / s) % 64 == 0) best = s;
+  return best;
+}
+
+int launch_route(const bf16* lg, int* top_idx, bf16* tw, float* top_p, int64_t T, int64_t E, int64_t k, int norm,
+                 const float* partials, int ns, bf16* lg_out, hipStream_t st) {
+  const unsigned blocks = (unsigned)q3_cdiv(T, 4);
+  if (E <= 64)
+    hipLaunchKernelGGL(moe_route_kernel<1>, dim3(blocks), dim3(256), 0, st, lg, top_idx, tw, top_p, (int)T, (int)E,
+                       (int)k, norm, partials, ns, lg_out);
+  else if (E <= 128)
+    hipLaunchKernelGGL(moe_route_kernel<2>, dim3(blocks), dim3(256), 0, st, lg, top_idx, tw, top_p, (int)T, (int)E,
+                       (int)k, norm, partials, ns, lg_out);
+  else if (E <= 256)
+    hipLaunchKernelGGL(moe_route_kernel<4>, dim3(blocks), dim3(256), 0, st, lg, top_idx, tw, top_p, (int)T, (int)E,
+                       (int)k, norm, partials, ns, lg_out);
+  else
+    hipLaunchKernelGGL(moe_route_kernel<8>, dim3(blocks), dim3(256), 0, st, lg, top_idx, tw, top_p, (int)T, (int)E,
+                       (int)k, norm, partials, ns, lg_out);
+  Q3_LAUNCH_CHECK();
+  return Q3_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 // logits (T, E) bf16 -> top_idx (T, k) int32, top_w (T, k) bf16 (renormalised
@@ -640,24 +695,52 @@ int q3_moe_route(const void* logits, int* top_idx, void* top_w, float* top_p, in
   Q3_REQUIRE(T >= 0 && E >= 1 && k >= 1 && k <= E, Q3_ERR_SHAPE);
   Q3_REQUIRE(E <= 512 && k <= 32, Q3_ERR_UNSUPPORTED);
   if (T == 0) return Q3_OK;
+  return launch_route(static_cast<const bf16*>(logits), top_idx, static_cast<bf16*>(top_w), top_p, T, E, k, norm,
+                      nullptr, 0, nullptr, static_cast<hipStream_t>(stream));
+}
+
+int64_t q3_moe_router_workspace_bytes(int64_t T, int64_t H, int64_t E) {
+  if (T <= 0 || H <= 0 || E <= 0) return 0;
+  return (int64_t)router_splits(T, H, E) * T * E * 4;
+}
+
+int q3_moe_router(const void* x, const void* gate_w, void* logits, int* top_idx, void* top_w, float* top_p,
+                  int64_t T, int64_t H, int64_t E, int64_t k, int norm, void* workspace, int64_t workspace_bytes,
+                  void* stream) {
+  Q3_REQUIRE(x && gate_w && logits && top_idx && top_w, Q3_ERR_NULL);
+  Q3_REQUIRE(T >= 0 && H >= 1 && E >= 1 && k >= 1 && k <= E, Q3_ERR_SHAPE);
+  Q3_REQUIRE(E <= 512 && k <= 32, Q3_ERR_UNSUPPORTED);
+  Q3_REQUIRE(H % 8 == 0 && q3_aligned(x, 16) && q3_aligned(gate_w, 16), Q3_ERR_ALIGN);
+  Q3_REQUIRE(T * H * 2 < 0x7fffffffLL && E * H * 2 < 0x7fffffffLL, Q3_ERR_UNSUPPORTED);
+  if (T == 0) return Q3_OK;
+  const int ns = router_splits(T, H, E);
+  const int64_t ks = H / ns;
+  Q3_REQUIRE(workspace != nullptr && workspace_bytes >= (int64_t)ns * T * E * 4, Q3_ERR_WORKSPACE);
+  Q3_REQUIRE(q3_aligned(workspace, 16), Q3_ERR_ALIGN);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const unsigned blocks = (unsigned)q3_cdiv(T, 4);
-  const bf16* lg = static_cast<const bf16*>(logits);
-  bf16* tw = static_cast<bf16*>(top_w);
-  if (E <= 64)
-    hipLaunchKernelGGL(moe_route_kernel<1>, dim3(blocks), dim3(256), 0, st, lg, top_idx, tw, top_p, (int)T, (int)E,
-                       (int)k, norm);
-  else if (E <= 128)
-    hipLaunchKernelGGL(moe_route_kernel<2>, dim3(blocks), dim3(256), 0, st, lg, top_idx, tw, top_p, (int)T, (int)E,
-                       (int)k, norm);
-  else if (E <= 256)
-    hipLaunchKernelGGL(moe_route_kernel<4>, dim3(blocks), dim3(256), 0, st, lg, top_idx, tw, top_p, (int)T, (int)E,
-                       (int)k, norm);
-  else
-    hipLaunchKernelGGL(moe_route_kernel<8>, dim3(blocks), dim3(256), 0, st, lg, top_idx, tw, top_p, (int)T, (int)E,
-                       (int)k, norm);
+  // Split z: X and W columns [z ks, (z + 1) ks) -> fp32 plane z of (T, E).
+  GemmParams p{};
+  p.X = static_cast<const bf16*>(x);
+  p.W = static_cast<const bf16*>(gate_w);
+  p.C = static_cast<bf16*>(workspace);
+  p.M = (int)T;
+  p.N = (int)E;
+  p.K = (int)ks;
+  p.ldx = H;
+  p.ldw = H;
+  p.ldc = E;
+  p.bsX = ks;
+  p.bsW = ks;
+  p.bsC = T * E;
+  p.group_m = 8;
+  p.seg.n = 1;
+  p.seg.w[0] = p.W;
+  const int64_t tiles = q3_cdiv(T, 128) * q3_cdiv(E, 128);
+  hipLaunchKernelGGL((gemm_bf16_dma_kernel<128, 128, 2, 2, kEpiStoreF32, false, 4, 64, 5>),
+                     dim3((unsigned)tiles, 1, (unsigned)ns), dim3(256), 0, st, p);
   Q3_LAUNCH_CHECK();
-  return Q3_OK;
+  return launch_route(static_cast<const bf16*>(logits), top_idx, static_cast<bf16*>(top_w), top_p, T, E, k, norm,
+                      static_cast<const float*>(workspace), ns, static_cast<bf16*>(logits), st);
 }
 
 int64_t q3_moe_experts_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k) {

@@ -9,7 +9,7 @@ from .flash_attention import (decode_attention, decode_attention_paged, flash_at
 from .matmul import (RMSNORM_MATMUL_MAX_ROWS, matmul, matmul_gelu, matmul_segments, matmul_swiglu,
                      rmsnorm_matmul_segments, rmsnorm_matmul_swiglu)
 from .moe_routing import (cuda_batched_gemm, cuda_index_add, cuda_topk, moe_experts, moe_permute, moe_route,
-                          raise_device_errors)
+                          moe_router, raise_device_errors)
 from .norms import layernorm, rmsnorm, softmax
 from .rotary import apply_mrope, apply_rope, qk_norm_rope, qk_norm_rope_paged
 from .vision import vision_pos_embed, vision_rope_tables
@@ -49,6 +49,7 @@ __all__ = [
     "RMSNORM_MATMUL_MAX_ROWS",
     "moe_experts",
     "moe_route",
+    "moe_router",
     "moe_permute",
     "raise_device_errors",
     "qk_norm_rope",

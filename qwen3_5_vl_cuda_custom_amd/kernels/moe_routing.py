@@ -95,6 +95,30 @@ def moe_route(router_logits: torch.Tensor, top_k: int, norm_topk_prob: bool = Tr
     return idx, w
 
 
+def moe_router(x: torch.Tensor, gate_weight: torch.Tensor, top_k: int, norm_topk_prob: bool = True):
+    """Router logits and routing in one call (modules/moe.py:59-65), for prefill-sized T.
+
+    x (T, H) bf16; gate_weight (E, H) bf16. The logits GEMM runs split over K into
+    fp32 partials (enough tiles for every CU at T = 4096, E = 128), summed in split
+    order and rounded once. Returns (logits (T, E) bf16, top_idx int32 (T, k), top_w bf16 (T, k)).
+    """
+    check("moe_router", x, gate_weight)
+    if x.dtype != torch.bfloat16 or gate_weight.dtype != torch.bfloat16:
+        raise TypeError("moe_router: bf16 inputs expected")
+    xc, wc = x.contiguous(), gate_weight.contiguous()
+    T, H = xc.shape
+    E = wc.shape[0]
+    if wc.shape[1] != H:
+        raise ValueError(f"moe_router: x {tuple(xc.shape)} and gate_weight {tuple(wc.shape)} do not match")
+    logits = torch.empty((T, E), dtype=torch.bfloat16, device=xc.device)
+    idx = torch.empty((T, top_k), dtype=torch.int32, device=xc.device)
+    w = torch.empty((T, top_k), dtype=torch.bfloat16, device=xc.device)
+    ws, nws = _lib.workspace(_lib.lib().q3_moe_router_workspace_bytes(T, H, E), xc.device)
+    _lib.call("q3_moe_router", xc.data_ptr(), wc.data_ptr(), logits.data_ptr(), idx.data_ptr(), w.data_ptr(), None,
+              T, H, E, top_k, int(bool(norm_topk_prob)), _lib.ptr(ws), nws, _lib.stream())
+    return logits, idx, w
+
+
 def moe_experts(x: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor, top_idx: torch.Tensor,
                 top_w: torch.Tensor, residual: torch.Tensor | None = None) -> torch.Tensor:
     """Dispatch, per-expert SwiGLU MLPs and combine (modules/moe.py:70-83) for routed tokens.

@@ -4,7 +4,8 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from ..kernels import (cuda_index_add, cuda_topk, matmul, moe_experts, moe_route, residual_add, softmax, swiglu)
+from ..kernels import (cuda_index_add, cuda_topk, matmul, moe_experts, moe_route, moe_router, residual_add, softmax,
+                       swiglu)
 
 
 class CudaSparseMoE(nn.Module):
@@ -36,7 +37,10 @@ class CudaSparseMoE(nn.Module):
 
     def route(self, x_flat: torch.Tensor):
         """router_logits (T, E) in x dtype, top_idx (T, k), top_w (T, k)."""
-        logits = matmul(x_flat, self.gate_weight)
+        if x_flat.dtype == torch.bfloat16 and x_flat.shape[0] > 32:
+            # prefill sizes: the logits GEMM split over K, reduced inside the routing kernel
+            return moe_router(x_flat, self.gate_weight, self.top_k, self.norm_topk_prob)
+        logits = matmul(x_flat, self.gate_weight)  # decode sizes: the weight-streaming GEMV
         if x_flat.dtype == torch.bfloat16:
             idx, w = moe_route(logits, self.top_k, self.norm_topk_prob)
             return logits, idx, w

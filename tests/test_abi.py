@@ -194,6 +194,14 @@ def test_rope_validation():
 def test_moe_validation():
     assert L.q3_moe_route(FAKE, FAKE, FAKE, None, 16, 8, 9, 1, None) == -2           # k > E
     assert L.q3_moe_route(FAKE, FAKE, FAKE, None, 16, 1024, 8, 1, None) == -5        # E beyond register-resident
+    # router with the split-K logits GEMM: 4096 x 2048 x 128 takes 8 splits of 256 columns
+    assert L.q3_moe_router_workspace_bytes(4096, 2048, 128) == 8 * 4096 * 128 * 4
+    assert L.q3_moe_router_workspace_bytes(77, 520, 96) == 77 * 96 * 4  # 520 has no 64-column split
+    assert L.q3_moe_router(FAKE, FAKE, FAKE, FAKE, FAKE, None, 16, 64, 8, 2, 1, None, 0, None) == -6
+    assert L.q3_moe_router(FAKE, FAKE, FAKE, FAKE, FAKE, None, 16, 60, 8, 2, 1, FAKE, 1 << 20, None) == -4  # H % 8
+    assert L.q3_moe_router(FAKE, None, FAKE, FAKE, FAKE, None, 16, 64, 8, 2, 1, FAKE, 1 << 20, None) == -1
+    assert L.q3_moe_router(FAKE, FAKE, FAKE, FAKE, FAKE, None, 16, 64, 8, 9, 1, FAKE, 1 << 20, None) == -2  # k > E
+    assert L.q3_moe_router(FAKE, FAKE, FAKE, FAKE, FAKE, None, 0, 64, 8, 2, 1, None, 0, None) == 0  # no tokens
     assert L.q3_moe_experts(FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE, 16, 20, 8, 4, 2, None, 0, None) == -5  # H % 8
     ws = L.q3_moe_experts_workspace_bytes(4096, 2048, 768, 128, 8)
     assert ws > 4096 * 8 * (2048 + 768) * 2

@@ -536,6 +536,29 @@ def test_moe_route_exact_indices():
     assert_bf16_close(w, rv / rv.sum(-1, keepdim=True), max_abs=4e-3, what="routing weights")
 
 
+@pytest.mark.parametrize("T,H,E,k", [(4096, 2048, 128, 8), (1000, 2048, 128, 8), (333, 1024, 64, 4), (77, 520, 96, 2)])
+def test_moe_router_split_k(T, H, E, k):
+    """The router with its logits GEMM split over K: logits against the fp32 oracle's linear,
+    within a bf16 ulp of the unsplit GEMM; top-k indices bit-exact against the oracle's softmax +
+    top-k on the returned logits; weights as moe_route gives them on the same logits. The last
+    shape has H with no 64-column split (one split)."""
+    x = rnd(T, H, seed=63, std=1.0)
+    wg = rnd(E, H, seed=64, std=H ** -0.5)
+    logits, idx, w = K.moe_router(gpu(x), gpu(wg), k, True)
+    ref = O.linear(f32(x), f32(wg))
+    assert_bf16_close(logits, ref, what=f"router logits T={T} H={H} E={E}")
+    # one bf16 ulp of the unsplit result, with an absolute floor for logits near zero, where the
+    # two fp32 summation orders differ by more than an ulp of the tiny result (cancellation)
+    plain = K.matmul(gpu(x), gpu(wg)).float().cpu()
+    ulp = torch.exp2(torch.floor(torch.log2(plain.abs().clamp_min(1e-30))) - 7).clamp_min(2.0 ** -14)
+    assert bool(((logits.float().cpu() - plain).abs() <= ulp).all()), "split-K logits within 1 bf16 ulp"
+    probs = O.softmax(logits.float().cpu())
+    rv, ri = O.topk(probs, k)
+    assert torch.equal(idx.cpu().long(), ri), "router top-k indices must be bit-exact"
+    idx2, w2 = K.moe_route(logits, k, True)
+    assert torch.equal(idx2, idx) and torch.equal(w2, w)
+
+
 def test_moe_experts_against_oracle_loop():
     from oracle.layers import sparse_moe
     T, H, I, E, k = 256, 256, 128, 16, 4
