@@ -31,11 +31,11 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # and memory per launch, from two rocprofv3 --pmc passes over `bench.py
 # --traffic-probe` (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled
 # by what the same counter reads for a plain 512 MiB device copy in the same
-# run (FETCH_SIZE 262157.5 KiB -> x1.9999; WRITE_SIZE 524288 KiB -> x1.000).
-# GEMM (2 X + 3 W ring slots, LDS-staged epilogue): FETCH_SIZE 590076.6,
+# run (FETCH_SIZE 262157.6 KiB -> x1.9999; WRITE_SIZE 524288 KiB -> x1.000).
+# GEMM (2 X + 3 W ring slots, bf16 LDS-staged epilogue): FETCH_SIZE 589976.5,
 # WRITE_SIZE 98304.0 KiB. Re-measure when the kernel changes; the command and
 # per-dispatch counts are in profiles/.
-GATE_UP_TRAFFIC_BYTES = int((590076.6 * (524_288 / 262157.5) + 98304.0 * 1.0) * 1024)
+GATE_UP_TRAFFIC_BYTES = int((589976.5 * (524_288 / 262157.6) + 98304.0 * 1.0) * 1024)
 
 
 def log(*a):
