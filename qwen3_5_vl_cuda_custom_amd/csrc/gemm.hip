@@ -167,6 +167,120 @@ int launch_tiled(GemmParams p, int64_t batch, hipStream_t st) {
   }
 }
 
+// ---------------------------------------------------------------- split over K
+// A plain store (bias and residual allowed, no activation, batch 1) whose
+// 256x256 tiles would leave most CUs idle and whose fallback, the one-wave
+// 128x128 ring, is bound by each CU's operand stream over a long K (M=1024,
+// N=4096, K=12288: 6.3 MB per tile, 135 us) runs as S splits of 256x256 tiles
+// (the tile GEMM's batch dimension: split z reads X and W columns
+// [z K/S, (z + 1) K/S) and writes fp32 partial plane z), then one kernel sums
+// the planes in split order, adds bias and residual and rounds once, the
+// order of the unsplit epilogue. Chosen by estimates from measured rates: a
+// wave of 256x256 tiles takes ~9.8 + 0.0243 K us, +4 us for an fp32 epilogue;
+// the 128x128 ring ~0.45 of that at full K; the reduction moves its bytes
+// (planes, residual, output) at ~5 TB/s after a ~4 us launch (the estimate
+// counts a residual, so the plan and workspace size depend on M, N, K only). The partial planes follow the GEMM
+// workspace's 16 KiB counter region, which they never touch.
+constexpr int64_t kSplitWsOffset = 16 << 10;
+
+int split_k_plan(int64_t M, int64_t N, int64_t K) {
+  if (M <= kGemvMaxRows || K < 2048 || M >= (1 << 20) || N >= (1 << 20)) return 1;
+  const int64_t tiles_a = q3_cdiv(M, 256) * q3_cdiv(N, 256);
+  if (q3_cdiv(M, 128) * q3_cdiv(N, 128) > 256) return 1;  // not the one-wave 128x128 case
+  const double t_c = 0.45 * (9.8 + 0.0243 * (double)K);
+  int best = 1;
+  double t_best = t_c;
+  for (int s = 2; s <= 8; s *= 2) {
+    if (tiles_a * s > 256 || K % (64 * s) != 0) continue;
+    const double bytes = (double)s * M * N * 4 + (double)M * N * 4;  // planes, residual in, C out
+    const double t = 9.8 + 0.0243 * (double)(K / s) + 4.0 + bytes / 5e6 + 4.0;
+    if (t < t_best) {
+      t_best = t;
+      best = s;
+    }
+  }
+  return best;
+}
+
+int64_t split_k_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  const int s = split_k_plan(M, N, K);
+  return s > 1 ? kSplitWsOffset + (int64_t)s * M * N * 4 : 0;
+}
+
+// One thread per 8 output columns: C = bf16(sum_z P[z] + bias + R).
+__global__ __launch_bounds__(256) void split_k_reduce_kernel(const float* __restrict__ parts, int S, int64_t M,
+                                                             int64_t N, const bf16* __restrict__ bias,
+                                                             const bf16* __restrict__ R, int64_t ldr,
+                                                             bf16* __restrict__ C, int64_t ldc, int vec) {
+  const int64_t n8 = (N + 7) / 8;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= M * n8) return;
+  const int64_t m = i / n8, n = (i % n8) * 8;
+  const int64_t plane = M * N;
+  float o[8];
+  if (vec && n + 7 < N) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) o[q] = 0.f;
+    for (int z = 0; z < S; ++z) {
+      const floatx4 a = *reinterpret_cast<const floatx4*>(parts + z * plane + m * N + n);
+      const floatx4 b = *reinterpret_cast<const floatx4*>(parts + z * plane + m * N + n + 4);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        o[q] += a[q];
+        o[4 + q] += b[q];
+      }
+    }
+    if (bias) {
+      const bf16x8 bv = *reinterpret_cast<const bf16x8*>(bias + n);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) o[q] += bf2f(bv[q]);
+    }
+    if (R) {
+      const bf16x8 rv = *reinterpret_cast<const bf16x8*>(R + m * ldr + n);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) o[q] += bf2f(rv[q]);
+    }
+    bf16x8 v;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) v[q] = f2bf(o[q]);
+    *reinterpret_cast<bf16x8*>(C + m * ldc + n) = v;
+  } else {
+    for (int q = 0; q < 8 && n + q < N; ++q) {
+      float acc = 0.f;
+      for (int z = 0; z < S; ++z) acc += parts[z * plane + m * N + n + q];
+      if (bias) acc += bf2f(bias[n + q]);
+      if (R) acc += bf2f(R[m * ldr + n + q]);
+      C[m * ldc + n + q] = f2bf(acc);
+    }
+  }
+}
+
+int launch_split_k(const GemmParams& p0, int S, void* ws, hipStream_t st) {
+  GemmParams p = p0;
+  float* parts = reinterpret_cast<float*>(static_cast<char*>(ws) + kSplitWsOffset);
+  const int64_t ks = p0.K / S;
+  p.C = reinterpret_cast<bf16*>(parts);
+  p.K = (int)ks;
+  p.ldc = p0.N;
+  p.bsX = ks;
+  p.bsW = ks;
+  p.bsC = (int64_t)p0.M * p0.N;
+  p.bias = nullptr;
+  p.R = nullptr;
+  p.act = 0;
+  p.seg.n = 1;
+  p.seg.w[0] = p.W;
+  const int rc = launch_tiled_cfg<256, 256, 2, 4, kEpiStoreF32, 2, 64, 3>(p, S, st);
+  if (rc != Q3_OK) return rc;
+  const bool vec = p0.N % 8 == 0 && p0.ldc % 8 == 0 && q3_aligned(p0.C, 16) &&
+                   (!p0.bias || q3_aligned(p0.bias, 16)) && (!p0.R || (q3_aligned(p0.R, 16) && p0.ldr % 8 == 0));
+  const int64_t items = (int64_t)p0.M * q3_cdiv(p0.N, 8);
+  hipLaunchKernelGGL(split_k_reduce_kernel, dim3((unsigned)q3_cdiv(items, 256)), dim3(256), 0, st, parts, S,
+                     (int64_t)p0.M, (int64_t)p0.N, p0.bias, p0.R, p0.ldr, p0.C, p0.ldc, vec ? 1 : 0);
+  Q3_LAUNCH_CHECK();
+  return Q3_OK;
+}
+
 bool bf16_rows_ok(const void* base, int64_t ld, int64_t K) {
   return q3_aligned(base, 16) && (ld % 8 == 0) && (K % 8 == 0);
 }
@@ -227,6 +341,11 @@ int matmul_impl(const void* x, const void* w, const void* w2, const void* bias, 
   p.bsW = bsW;
   p.bsC = bsC;
   p.act = act;
+  if (!swiglu && !act && batch == 1) {
+    const int S = split_k_plan(M, N, K);
+    if (S > 1 && ws != nullptr && q3_aligned(ws, 16) && ws_bytes >= split_k_workspace_bytes(M, N, K))
+      return launch_split_k(p, S, ws, st);
+  }
   return swiglu ? launch_tiled<kEpiSwiGLU>(p, batch, st) : launch_tiled<kEpiStore>(p, batch, st);
 }
 
@@ -354,7 +473,8 @@ int q3_matmul_segments(const void* x, const void* const* w, const void* const* b
 }
 
 int64_t q3_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int dtype, int swiglu) {
-  if (dtype != Q3_BF16 || M > kGemvMaxRows || M <= 0 || N <= 0 || K <= 0) return 0;
+  if (dtype != Q3_BF16 || M <= 0 || N <= 0 || K <= 0) return 0;
+  if (M > kGemvMaxRows) return swiglu ? 0 : split_k_workspace_bytes(M, N, K);
   return gemv_workspace_bytes(M, N, K, swiglu != 0);
 }
 

@@ -58,6 +58,12 @@ def test_matmul_validation():
     # decode-shaped bf16 GEMM: the row-owned kernel (M <= 8 or K <= 16384) needs no
     # workspace; the stream-K kernel (M > 8, K > 16384) needs its split-K workspace
     assert L.q3_matmul_workspace_bytes(32, 4096, 12288, 1, 0) == 0
+    # prefill-sized plain GEMMs: a split over K only where 256x256 tiles leave the GPU idle and K
+    # is long (the planes follow the 16 KiB counter region)
+    assert L.q3_matmul_workspace_bytes(1024, 4096, 12288, 1, 0) == (16 << 10) + 4 * 1024 * 4096 * 4
+    assert L.q3_matmul_workspace_bytes(1024, 4096, 4096, 1, 0) == 0
+    assert L.q3_matmul_workspace_bytes(4096, 4096, 12288, 1, 0) == 0
+    assert L.q3_matmul_workspace_bytes(1024, 4096, 12288, 1, 1) == 0  # SwiGLU: never split
     assert L.q3_matmul_workspace_bytes(8, 4096, 20480, 1, 0) == 0
     ws = L.q3_matmul_workspace_bytes(32, 4096, 20480, 1, 0)
     assert ws > 0

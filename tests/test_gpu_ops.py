@@ -10,6 +10,7 @@ import pytest
 import torch
 
 from oracle import ops as O
+from qwen3_5_vl_cuda_custom_amd import _lib
 from qwen3_5_vl_cuda_custom_amd import kernels as K
 from tests.parity import assert_bf16_close, assert_close, assert_layer_parity, assert_within_ulp, bf16_round
 
@@ -64,6 +65,28 @@ def test_matmul_residual_fused():
     assert_bf16_close(yl, O.linear(f32(xl), f32(wl), f32(bl)) + f32(rl), what="large matmul+bias+residual")
     y2 = K.matmul(gpu(x[:16]), gpu(w), residual=gpu(r[:16]))  # skinny path epilogue
     assert_bf16_close(y2, O.linear(f32(x[:16]), f32(w)) + f32(r[:16]), what="skinny matmul+residual")
+
+
+@pytest.mark.parametrize("M,N,Kd,bias,res", [
+    (1024, 4096, 12288, False, True),   # the S=1024 down projection: 4 splits of 3072
+    (1000, 4000, 12288, True, True),    # ragged M and N, bias and residual: 4 splits
+    (1024, 2048, 12288, False, False),  # 8 splits, plain store
+])
+def test_matmul_split_k(M, N, Kd, bias, res):
+    """Few-tile, long-K GEMMs take the split over K (fp32 partial planes summed in split order,
+    then bias, residual, one rounding): the plan and its workspace, and parity with the oracle."""
+    ws = _lib.lib().q3_matmul_workspace_bytes(M, N, Kd, 1, 0)
+    assert ws > M * N * 4, "the split plan must ask for its partial planes"
+    x, w = rnd(M, Kd, seed=70), rnd(N, Kd, seed=71, std=Kd ** -0.5)
+    b = rnd(N, seed=72, std=0.02) if bias else None
+    r = rnd(M, N, seed=73) if res else None
+    y = K.matmul(gpu(x), gpu(w), gpu(b) if bias else None, residual=gpu(r) if res else None)
+    ref = O.linear(f32(x), f32(w), f32(b) if bias else None)
+    if res:
+        ref = ref + f32(r)
+    assert_bf16_close(y, ref, what=f"split-K matmul {M}x{N}x{Kd}")
+    again = K.matmul(gpu(x), gpu(w), gpu(b) if bias else None, residual=gpu(r) if res else None)
+    assert torch.equal(y, again), "the split-K path must be deterministic"
 
 
 @pytest.mark.parametrize("M", [7, 32, 300, 1024, 4100, 8192])
