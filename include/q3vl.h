@@ -55,9 +55,12 @@ const char* q3_error_string(int code);
  * bias/residual may be null. M <= 32 (bf16) runs the weight-streaming path,
  * which needs a workspace (q3_matmul_workspace_bytes): its first 16 KiB hold
  * tile counters that must be zero before the workspace's first use (allocate
- * it zero-filled) and that every call leaves zero. Calls that may run at the
- * same time must not share a workspace; any number of stream-ordered calls,
- * of any shape, may. */
+ * it zero-filled) and that every call leaves zero. A few-tile, long-K plain
+ * GEMM (q3_matmul, M > 32) may also ask for one: the query then returns 16 KiB
+ * plus fp32 partial planes of a split over K (behind the counters, never
+ * touching them); given a smaller workspace, or none, the call runs unsplit.
+ * Calls that may run at the same time must not share a workspace; any number
+ * of stream-ordered calls, of any shape, may. */
 int64_t q3_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int dtype, int swiglu);
 int q3_matmul(const void* x, const void* w, const void* bias, const void* residual, void* y, int64_t M, int64_t N,
               int64_t K, int64_t ldx, int64_t ldw, int64_t ldr, int64_t ldc, int dtype, void* workspace,
