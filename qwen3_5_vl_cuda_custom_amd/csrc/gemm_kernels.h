@@ -253,7 +253,7 @@ __device__ __forceinline__ void store_tile_lds(const GemmParams& p, const TileCt
         }
         if (p.act) {
 #pragma unroll
-          for (int q = 0; q < 8; ++q) o[q] = gelu_tanh_f(o[q]);
+          for (int q = 0; q < 8; ++q) o[q] = gelu_tanh_fast(o[q]);
         }
         if (p.R) {
           const bf16* rrow = p.R + (int64_t)m * p.ldr;

@@ -90,6 +90,18 @@ __device__ __forceinline__ float wave_max(float v) {
   for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;
 }
+// gelu_tanh of the fused GEMM epilogue (vision fc1, patch mergers): tanh(u) =
+// 1 - 2 / (exp(2u) + 1) with the fast exponential and the hardware reciprocal
+// (absolute error ~1e-7 against tanhf, far below the bf16 rounding that
+// follows), instead of the libm tanhf the op-level kernel keeps. exp(2u)
+// overflowing to inf gives 1, underflowing to 0 gives -1.
+__device__ __forceinline__ float gelu_tanh_fast(float a) {
+  const float k0 = 0.7978845608028654f;
+  const float inner = k0 * (a + 0.044715f * a * a * a);
+  const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(__expf(2.0f * inner) + 1.0f);
+  return 0.5f * a * (1.0f + t);
+}
+
 // silu(g) * u of the fused SwiGLU epilogues (GEMM tiles, decode GEMVs), in
 // fp32 before the one rounding: the hardware reciprocal (v_rcp_f32, ~1 ulp)
 // instead of an IEEE division, which cost ~1.8 us per wave of 256x256 tiles.
