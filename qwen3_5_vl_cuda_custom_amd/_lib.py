@@ -151,11 +151,13 @@ def workspace(nbytes: int, device: torch.device) -> tuple[torch.Tensor | None, i
     return torch.empty(int(nbytes), dtype=torch.uint8, device=device), int(nbytes)
 
 
-# Per-device GEMM workspaces (M <= 32 path). They start zero-filled: their
-# first 16 KiB are tile counters that every call leaves at zero again. A larger
-# request allocates a new buffer; the old ones are kept, because captured HIP
-# graphs may still point at them. Calls on different streams that run at the
-# same time must not share one: these are for the stream-ordered decode step.
+# Per-device GEMM workspaces: the decode GEMVs' (M <= 32) and the fp32 partial
+# planes of a prefill-sized GEMM split over K. They start zero-filled: their
+# first 16 KiB are tile counters that every call leaves at zero again (the
+# planes lie behind them). A larger request allocates a new buffer; the old
+# ones are kept, because captured HIP graphs may still point at them. Calls on
+# different streams that run at the same time must not share one: these serve
+# stream-ordered work (a layer's GEMMs, the decode step).
 _gemm_ws: dict[tuple[str, int | None], list[torch.Tensor]] = {}
 
 
