@@ -181,6 +181,25 @@ int q3_flash_attention(const void* q, const void* k, const void* v, void* o, flo
                        int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D, const int64_t* strides, float scale,
                        int is_causal, int dtype, void* stream);
 
+/* The attention half of CudaFullAttention.forward without a cache (reference
+ * modules/attention.py:83-96: q_norm / k_norm, mRoPE, attention) in two
+ * launches: k is RMS-normalised and rotated in place (the layer returns it),
+ * and q, read raw from the projection output, is normalised and rotated
+ * inside the attention kernel as it is loaded; q_in is not modified. q_in,
+ * k, v, o are (B, H, S, D) views with strides = [qb, qh, qs, kb, kh, ks, vb,
+ * vh, vs, ob, oh, os] (Sq = Sk = S); positions (3, B, S) int32; inv_freq
+ * (D/2) fp32; section as q3_qk_norm_rope; weights (D). The workspace holds
+ * the per-token rotary table: q3_qk_norm_rope_attention_workspace_bytes.
+ * Results equal q3_qk_norm_rope followed by q3_flash_attention up to the
+ * order of the q row's sum of squares. bf16, D in {64, 128}, Hq / Hkv a
+ * multiple of 4 only (else Q3_ERR_UNSUPPORTED, checked before any launch). */
+int64_t q3_qk_norm_rope_attention_workspace_bytes(int64_t B, int64_t S, int64_t D);
+int q3_qk_norm_rope_attention(const void* q_in, void* k, const void* v, void* o, const void* q_weight,
+                              const void* k_weight, const int* positions, const float* inv_freq, int64_t B,
+                              int64_t S, int64_t Hq, int64_t Hkv, int64_t D, const int64_t* section, float eps,
+                              const int64_t* strides, float scale, int is_causal, int dtype, void* workspace,
+                              int64_t workspace_bytes, void* stream);
+
 /* Attention over packed variable-length sequences (the vision tower's images,
  * each attending only within itself: HF's cu_seqlens form of the attention
  * the reference runs over one concatenated sequence, models/common.py:198).

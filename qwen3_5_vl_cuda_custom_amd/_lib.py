@@ -49,6 +49,9 @@ _SIGS: dict[str, tuple] = {
                                 _i64p, c_float, _i64p, c_int, _V]),
     "q3_flash_attention": (c_int, [_V, _V, _V, _V, _f32p, _I, _I, _I, _I, _I, _I, _i64p, c_float, c_int, c_int,
                                    _V]),
+    "q3_qk_norm_rope_attention_workspace_bytes": (c_int64, [_I, _I, _I]),
+    "q3_qk_norm_rope_attention": (c_int, [_V, _V, _V, _V, _V, _V, _i32p, _f32p, _I, _I, _I, _I, _I, _i64p, c_float,
+                                          _i64p, c_float, c_int, c_int, _V, _I, _V]),
     "q3_flash_attention_varlen": (c_int, [_V, _V, _V, _V, _i32p, _I, _I, _I, _I, _I, _I, _i64p, c_float, c_int,
                                           c_int, _V]),
     "q3_flash_attention_cache": (c_int, [_V, _V, _V, _i32p, _V, _I, _I, _I, _I, _I, _I, _i64p, c_float, c_int,

@@ -69,6 +69,14 @@ struct AttnParams {
   const int* block_table;
   int max_pages, page_rows, num_pages;
   int* status;
+  // Prefill with the q prologue fused (pipelined kernel, D a multiple of 32):
+  // q holds the projection output; each query row is RMS-normalised (weight
+  // qn_w, eps qn_eps) and rotated by the row of rope_tab for token b * Sq + i
+  // (D fp32: cos of the D/2 angles, then their sin) before use. Null: q is used
+  // as given.
+  const bf16* qn_w;
+  const float* rope_tab;
+  float qn_eps;
 };
 
 // ----------------------------------------------------------------- prefill
@@ -771,6 +779,56 @@ __device__ __forceinline__ void scale_acc(floatx16& acc, float alpha) {
   }
   asm volatile("s_nop 4" ::: "memory");
 }
+
+// The q prologue of the fused prefill on one query's fragments: the lane holds
+// elements 16 ks + 8 h + e (ks < D / 16, e < 8), the other lane half (lane ^
+// 32) the rest of the row. RMSNorm over the row (fp32 sum of squares, the
+// halves exchanged once), times the weight, then rotate-half with the table's
+// cos / sin: element i < D/2 pairs with i + D/2, which is k-step ks + D/32 of
+// the same lane. One rounding to bf16 at the end, as the separate fused
+// norm + rotation kernel.
+template <int D>
+__device__ __forceinline__ void q_norm_rope_frag(bf16x8 (&qf)[D / 16], const bf16* __restrict__ w,
+                                                 const float* __restrict__ tab, float eps, int h) {
+  constexpr int KS = D / 16, HK = KS / 2;
+  // Weights and table first: their loads overlap the q fragments' (one round
+  // trip for all of them).
+  bf16x8 wv[KS];
+  float4 cs4[HK][2], sn4[HK][2];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) wv[ks] = *reinterpret_cast<const bf16x8*>(w + ks * 16 + 8 * h);
+#pragma unroll
+  for (int ks = 0; ks < HK; ++ks)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      cs4[ks][j] = reinterpret_cast<const float4*>(tab + ks * 16 + 8 * h)[j];
+      sn4[ks][j] = reinterpret_cast<const float4*>(tab + D / 2 + ks * 16 + 8 * h)[j];
+    }
+  float ss = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = (float)qf[ks][e];
+      ss += v * v;
+    }
+  ss += __shfl_xor(ss, 32, 64);
+  const float rstd = rsqrtf(ss / (float)D + eps);
+#pragma unroll
+  for (int ks = 0; ks < HK; ++ks) {
+    const float c[8] = {cs4[ks][0].x, cs4[ks][0].y, cs4[ks][0].z, cs4[ks][0].w,
+                        cs4[ks][1].x, cs4[ks][1].y, cs4[ks][1].z, cs4[ks][1].w};
+    const float sn[8] = {sn4[ks][0].x, sn4[ks][0].y, sn4[ks][0].z, sn4[ks][0].w,
+                         sn4[ks][1].x, sn4[ks][1].y, sn4[ks][1].z, sn4[ks][1].w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float lo = (float)qf[ks][e] * rstd * (float)wv[ks][e];
+      const float hi = (float)qf[ks + HK][e] * rstd * (float)wv[ks + HK][e];
+      qf[ks][e] = (bf16)(lo * c[e] - hi * sn[e]);
+      qf[ks + HK][e] = (bf16)(hi * c[e] + lo * sn[e]);
+    }
+  }
+}
 }  // namespace fwdp
 
 template <int D, bool MHA>
@@ -849,6 +907,14 @@ __global__ __launch_bounds__(512) void flash_fwd_pipe_kernel(const AttnParams p)
     q3::dma16(vrs, live ? (uint32_t)((row + r0) * vs2) + vc0 : q3::kOOB, lv);
   };
 
+  // With the fused q prologue, the first K/V tiles are requested before q so
+  // that their loads overlap the prologue's.
+  const bool qpro = D % 32 == 0 && p.rope_tab != nullptr;
+  if (qpro && nkt > 0) {
+#pragma unroll
+    for (int s = 0; s <= kAhead; ++s) issue(s);
+  }
+
   // Q fragments (B operand): lane supplies Q[qw0 + l32][16 ks + 8 h .. + 7].
   bf16x8 qf[KSTEPS];
   {
@@ -858,6 +924,10 @@ __global__ __launch_bounds__(512) void flash_fwd_pipe_kernel(const AttnParams p)
     for (int ks = 0; ks < KSTEPS; ++ks)
       qf[ks] = (qi < Sq && ks * 16 + 8 * h < D) ? *reinterpret_cast<const bf16x8*>(qrow + ks * 16 + 8 * h)
                                                 : bf16x8{};
+    if constexpr (D % 32 == 0) {
+      if (p.rope_tab != nullptr && qi < Sq)
+        q_norm_rope_frag<D>(qf, p.qn_w, p.rope_tab + ((int64_t)b * Sq + qi) * D, p.qn_eps, h);
+    }
   }
 
   floatx16 o[OT];
@@ -999,8 +1069,10 @@ __global__ __launch_bounds__(512) void flash_fwd_pipe_kernel(const AttnParams p)
   constexpr std::false_type kUnmasked{};
 
   if (nkt > 0) {
+    if (!qpro) {
 #pragma unroll
-    for (int s = 0; s <= kAhead; ++s) issue(s);
+      for (int s = 0; s <= kAhead; ++s) issue(s);
+    }
     q3::vm_wait<(kAhead - 1) * PERW>();
     __syncthreads();
     floatx16 sa, sb;
@@ -1170,7 +1242,8 @@ __global__ void lens_inc_kernel(int* lens, int B, int add) {
 // AttnParams::q_off). lens_add: if set, lens_add[b] += Sq after the attention.
 int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t Hq, int64_t Hkv,
              int64_t Sq, int64_t Sk, int64_t D, const int64_t* strides, float scale, int is_causal, int dtype,
-             const int* q_off, int* lens_add, void* stream, const int* cu_seqlens = nullptr) {
+             const int* q_off, int* lens_add, void* stream, const int* cu_seqlens = nullptr,
+             const bf16* qn_w = nullptr, const float* rope_tab = nullptr, float qn_eps = 0.f) {
   Q3_REQUIRE(q && k && v && o && strides, Q3_ERR_NULL);
   Q3_REQUIRE(B >= 0 && Hq >= 1 && Hkv >= 1 && Sq >= 0 && Sk >= 0 && D >= 1, Q3_ERR_SHAPE);
   Q3_REQUIRE(Hq % Hkv == 0, Q3_ERR_SHAPE);
@@ -1204,10 +1277,20 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
   p.groups = (int)(Hq / Hkv);
   p.q_off = q_off;
   p.cu_seqlens = cu_seqlens;
+  p.qn_w = qn_w;
+  p.rope_tab = rope_tab;
+  p.qn_eps = qn_eps;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool aligned = q3_aligned(q, 16) && q3_aligned(k, 16) && q3_aligned(v, 16) && q3_aligned(o, 8) &&
                        strides_aligned8(strides, 12);
   int rc = Q3_OK;
+  if (rope_tab) {  // the fused q prologue exists in the pipelined kernel only (D a multiple of 32)
+    Q3_REQUIRE(dtype == Q3_BF16, Q3_ERR_DTYPE);
+    Q3_REQUIRE(aligned && q3_aligned(qn_w, 16), Q3_ERR_ALIGN);
+    Q3_REQUIRE((D == 64 || D == 96 || D == 128) && pipe_eligible(p) && q_off == nullptr && cu_seqlens == nullptr &&
+                   (Sk + 1) * strides[5] * 2 < 0x7fffffffLL,
+               Q3_ERR_UNSUPPORTED);
+  }
   // The MFMA path addresses K with 32-bit buffer offsets.
   if (dtype == Q3_BF16 && mfma_head_dim(D) && aligned && Sk > 0 && (Sk + 1) * strides[5] * 2 < 0x7fffffffLL) {
     const bool pipe = pipe_eligible(p);
@@ -1249,7 +1332,55 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
 
 }  // namespace
 
+namespace q3 {
+int k_norm_rope_table(void* k, const void* q_weight, const void* k_weight, const int* positions,
+                      const float* inv_freq, float* tab, int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D,
+                      const int64_t* section, float eps, const int64_t* kst, hipStream_t st);
+}
+
 extern "C" {
+
+int64_t q3_qk_norm_rope_attention_workspace_bytes(int64_t B, int64_t S, int64_t D) {
+  if (B < 0 || S < 0 || D < 0) return 0;
+  return B * S * D * (int64_t)sizeof(float);
+}
+
+int q3_qk_norm_rope_attention(const void* q_in, void* k, const void* v, void* o, const void* q_weight,
+                              const void* k_weight, const int* positions, const float* inv_freq, int64_t B,
+                              int64_t S, int64_t Hq, int64_t Hkv, int64_t D, const int64_t* section, float eps,
+                              const int64_t* strides, float scale, int is_causal, int dtype, void* workspace,
+                              int64_t workspace_bytes, void* stream) {
+  Q3_REQUIRE(q_in && k && v && o && q_weight && k_weight && positions && inv_freq && section && strides, Q3_ERR_NULL);
+  Q3_REQUIRE(B >= 0 && S >= 0 && Hq >= 1 && Hkv >= 1 && Hq % Hkv == 0 && D >= 1, Q3_ERR_SHAPE);
+  Q3_REQUIRE(section[0] >= 0 && section[1] >= 0 && section[2] >= 0 && section[0] + section[1] + section[2] == D / 2,
+             Q3_ERR_SHAPE);
+  Q3_REQUIRE(dtype == Q3_BF16, Q3_ERR_DTYPE);
+  Q3_REQUIRE(D == 64 || D == 128, Q3_ERR_UNSUPPORTED);  // the k kernel's lane groups: D / 8 in {8, 16}
+  Q3_REQUIRE((Hq / Hkv) % 4 == 0, Q3_ERR_UNSUPPORTED);
+  Q3_REQUIRE(B * S < (1ll << 31), Q3_ERR_SHAPE);
+  const int64_t need = q3_qk_norm_rope_attention_workspace_bytes(B, S, D);
+  Q3_REQUIRE(workspace != nullptr && workspace_bytes >= need, Q3_ERR_WORKSPACE);
+  Q3_REQUIRE(q3_aligned(workspace, 16) && q3_aligned(k_weight, 16), Q3_ERR_ALIGN);
+  if (B == 0 || S == 0) return Q3_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  float* tab = static_cast<float*>(workspace);
+  // Validate the attention call before the k rows are rewritten in place.
+  {
+    AttnParams probe{};
+    probe.groups = (int)(Hq / Hkv);
+    probe.Sq = (int)S;
+    const bool aligned = q3_aligned(q_in, 16) && q3_aligned(k, 16) && q3_aligned(v, 16) && q3_aligned(o, 8) &&
+                         q3_aligned(q_weight, 16) && strides_aligned8(strides, 12);
+    Q3_REQUIRE(aligned, Q3_ERR_ALIGN);
+    Q3_REQUIRE(pipe_eligible(probe) && (S + 1) * strides[5] * 2 < 0x7fffffffLL, Q3_ERR_UNSUPPORTED);
+  }
+  const int64_t kst[3] = {strides[3], strides[5], strides[4]};  // (b, s, h)
+  const int rc = q3::k_norm_rope_table(k, q_weight, k_weight, positions, inv_freq, tab, B, S, Hq, Hkv, D, section,
+                                       eps, kst, st);
+  if (rc != Q3_OK) return rc;
+  return fwd_impl(q_in, k, v, o, nullptr, B, Hq, Hkv, S, S, D, strides, scale, is_causal, dtype, nullptr, nullptr,
+                  stream, nullptr, static_cast<const bf16*>(q_weight), tab, eps);
+}
 
 int q3_flash_attention(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t Hq,
                        int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D, const int64_t* strides, float scale,

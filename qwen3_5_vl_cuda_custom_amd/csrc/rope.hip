@@ -205,6 +205,10 @@ struct QKNormRopeArgs {
   const int* block_table;
   int max_pages, page_rows, num_pages;
   int* status;
+  // If set, token t = b * S + s writes its rotary table row: D fp32 values,
+  // cos of the D/2 angles then their sin (for a consumer that rotates q
+  // itself). q_in == null: the q rows are not processed (k and v only).
+  float* rope_tab;
 };
 
 // One block per (b, s) token. The D/2 rotary angles of the token (pos[axis]
@@ -359,7 +363,7 @@ __global__ __launch_bounds__(256, MINB) void qk_norm_rope_kernel(const QKNormRop
 #pragma unroll
     for (int u = 0; u < BATCH; ++u) load8<T, VEC>(qk_in_row<T>(a, b, s, min(r0 + u * RPP, nrows - 1)) + 8 * j, v[u]);
   };
-  const int first = tid / G;
+  const int first = (a.q_in ? 0 : a.Hq) + tid / G;
   load_batch(first);
   const int so_b = a.dst_seq_off ? a.dst_seq_off[b] : 0;
   if (tid < HALF) {
@@ -367,6 +371,11 @@ __global__ __launch_bounds__(256, MINB) void qk_norm_rope_kernel(const QKNormRop
     sincosf((float)posv * fr, &sn, &c);
     s_cos[tid] = c;
     s_sin[tid] = sn;
+    if (a.rope_tab) {
+      float* tr = a.rope_tab + (int64_t)blockIdx.x * D;
+      tr[tid] = c;
+      tr[HALF + tid] = sn;
+    }
   }
   __syncthreads();
   float cs[8], sn[8];
@@ -384,6 +393,75 @@ __global__ __launch_bounds__(256, MINB) void qk_norm_rope_kernel(const QKNormRop
       if (row >= nrows) break;
       qk_row<T, G, VEC>(a, b, s, row, j, so_b, v[u], cs, sn, wq, wk);
     }
+  }
+}
+
+// k rows only, with the rotary table written (the fused prefill prologue: q
+// is rotated by the attention kernel). TPB tokens per block, so that the
+// per-token latency chain (position load, sincosf, LDS exchange) of several
+// tokens overlaps: thread i < TPB * D/2 computes angle i % (D/2) of token
+// i / (D/2); lane groups of G take the block's TPB * Hkv k rows, RPP at a
+// time. bf16 with 16-byte aligned rows; same per-row arithmetic as
+// qk_norm_rope_kernel (qk_row).
+template <int G, int TPB>
+__global__ __launch_bounds__(256) void k_norm_rope_table_kernel(const QKNormRopeArgs a) {
+  constexpr int D = G * 8;
+  constexpr int HALF = D / 2;
+  constexpr int RPP = 256 / G;
+  static_assert(TPB * HALF <= 256, "one angle per thread");
+  __shared__ float s_cos[TPB][HALF], s_sin[TPB][HALF];
+  const int tid = threadIdx.x;
+  const int j = tid % G;
+  const int64_t ntok = (int64_t)a.B * a.S;
+  const int64_t tok0 = (int64_t)blockIdx.x * TPB;
+  const int nrows = TPB * a.Hkv;
+  auto token_of = [&](int r, int64_t& b, int64_t& s) {
+    const int64_t tok = min(tok0 + r / a.Hkv, ntok - 1);
+    b = tok / a.S;
+    s = tok % a.S;
+  };
+  float wq[8], wk[8];
+  load8<bf16, true>(static_cast<const bf16*>(a.q_w) + 8 * j, wq);
+  load8<bf16, true>(static_cast<const bf16*>(a.k_w) + 8 * j, wk);
+  const int first = tid / G;
+  float x[8];
+  {
+    int64_t b, s;
+    token_of(min(first, nrows - 1), b, s);
+    load8<bf16, true>(qk_in_row<bf16>(a, b, s, a.Hq + min(first, nrows - 1) % a.Hkv) + 8 * j, x);
+  }
+  if (tid < TPB * HALF) {
+    const int tt = tid / HALF, i = tid % HALF;
+    const int64_t tok = min(tok0 + tt, ntok - 1);
+    const int64_t b = tok / a.S, s = tok % a.S;
+    const int axis = (i < a.s0) ? 0 : (i < a.s0 + a.s1 ? 1 : 2);
+    const int posv = a.pos[((int64_t)axis * a.B + b) * a.S + s];
+    float sn, c;
+    sincosf((float)posv * a.inv_freq[i], &sn, &c);
+    s_cos[tt][i] = c;
+    s_sin[tt][i] = sn;
+    if (tok0 + tt < ntok) {
+      float* tr = a.rope_tab + tok * D;
+      tr[i] = c;
+      tr[HALF + i] = sn;
+    }
+  }
+  __syncthreads();
+  for (int r = first; r < nrows; r += RPP) {  // uniform per lane group
+    if (tok0 + r / a.Hkv >= ntok) break;
+    int64_t b, s;
+    token_of(r, b, s);
+    const int row = a.Hq + r % a.Hkv;
+    if (r != first) load8<bf16, true>(qk_in_row<bf16>(a, b, s, row) + 8 * j, x);
+    const int tt = r / a.Hkv;
+    float cs[8], sn[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int i = (8 * j + e) % HALF;
+      cs[e] = s_cos[tt][i];
+      sn[e] = s_sin[tt][i];
+    }
+    qk_row<bf16, G, true>(a, b, s, row, j, 0, x, cs, sn, wq, wk);
   }
 }
 
@@ -472,6 +550,49 @@ int qk_impl(const void* q_in, const void* k_in, const void* v_in, void* q_out, v
 }
 
 }  // namespace
+
+namespace q3 {
+
+// k rows only: per-head RMSNorm + mRoPE of k in place ((b, s, h) element
+// strides kst), and each token's rotary table row into tab (B * S rows of D
+// fp32). bf16; the caller has validated shapes and pointers.
+int k_norm_rope_table(void* k, const void* q_weight, const void* k_weight, const int* positions,
+                      const float* inv_freq, float* tab, int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D,
+                      const int64_t* section, float eps, const int64_t* kst, hipStream_t st) {
+  QKNormRopeArgs a{};
+  a.k_in = k;
+  a.k_out = k;
+  a.q_w = q_weight;
+  a.k_w = k_weight;
+  a.pos = positions;
+  a.inv_freq = inv_freq;
+  a.dst_seq_cap = INT64_MAX;
+  a.B = (int)B;
+  a.S = (int)S;
+  a.Hq = (int)Hq;
+  a.Hkv = (int)Hkv;
+  a.D = (int)D;
+  a.s0 = (int)section[0];
+  a.s1 = (int)section[1];
+  a.eps = eps;
+  for (int i = 0; i < 3; ++i) a.st[3 + i] = a.st[12 + i] = kst[i];
+  a.rope_tab = tab;
+  bool vec = q3_aligned(k, 16) && q3_aligned(q_weight, 16) && q3_aligned(k_weight, 16);
+  for (int i = 0; i < 3; ++i) vec = vec && (kst[i] * 2) % 16 == 0;
+  if (!vec || (D != 64 && D != 128)) return launch_qk<bf16>(a, st);  // one token per block
+  const int64_t tokens = B * S;
+  if (tokens == 0) return Q3_OK;
+  constexpr int kTPB = 4;
+  const dim3 grid((unsigned)q3_cdiv(tokens, kTPB));
+  if (D == 128)
+    hipLaunchKernelGGL((k_norm_rope_table_kernel<16, kTPB>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((k_norm_rope_table_kernel<8, kTPB>), grid, dim3(256), 0, st, a);
+  Q3_LAUNCH_CHECK();
+  return Q3_OK;
+}
+
+}  // namespace q3
 
 extern "C" {
 

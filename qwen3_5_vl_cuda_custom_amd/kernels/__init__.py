@@ -5,7 +5,7 @@ from .conv3d_patch import conv3d_patch
 from .elementwise import gelu_tanh, residual_add, swiglu
 from .embedding import embedding
 from .flash_attention import (decode_attention, decode_attention_paged, flash_attention, flash_attention_cache,
-                              flash_attention_varlen)
+                              flash_attention_varlen, qk_norm_rope_attention, qk_norm_rope_attention_ok)
 from .matmul import (RMSNORM_MATMUL_MAX_ROWS, matmul, matmul_gelu, matmul_segments, matmul_swiglu,
                      rmsnorm_matmul_segments, rmsnorm_matmul_swiglu)
 from .moe_routing import (cuda_batched_gemm, cuda_index_add, cuda_topk, moe_experts, moe_permute, moe_route,
@@ -54,4 +54,6 @@ __all__ = [
     "raise_device_errors",
     "qk_norm_rope",
     "qk_norm_rope_paged",
+    "qk_norm_rope_attention",
+    "qk_norm_rope_attention_ok",
 ]

@@ -37,6 +37,59 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: fl
     return o
 
 
+def qk_norm_rope_attention_ok(q: torch.Tensor, k: torch.Tensor, num_kv_groups: int) -> bool:
+    """Whether qk_norm_rope_attention covers these (B, S, H, D) views (else use
+    qk_norm_rope followed by flash_attention)."""
+    D = q.shape[-1]
+    return (q.is_cuda and q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16 and D in (64, 128)
+            and num_kv_groups % 4 == 0 and q.shape[1] > 0)
+
+
+def qk_norm_rope_attention(q_in: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_weight: torch.Tensor,
+                           k_weight: torch.Tensor, positions: torch.Tensor, inv_freq: torch.Tensor, mrope_section,
+                           eps: float, scale: float, is_causal: bool = True, *,
+                           out: torch.Tensor | None = None) -> torch.Tensor:
+    """q/k RMSNorm + mRoPE + attention of one prefill (reference modules/attention.py:83-96) in two launches.
+
+    q_in (B, S, Hq, D), k/v (B, S, Hkv, D) views of the projection output (any
+    strides, D contiguous); positions (3, B, S) int32, inv_freq (D/2) fp32 on
+    the device. k is normalised and rotated in place; q is normalised and
+    rotated inside the attention kernel as it is read (q_in is unchanged).
+    Returns o (B, S, Hq, D) (or writes `out`, such a view). Equal to
+    qk_norm_rope followed by flash_attention up to the summation order of each
+    q row's sum of squares. bf16, D in (64, 128), GQA groups a multiple of 4.
+    """
+    check("qk_norm_rope_attention", q_in, k, v)
+    B, S, Hq, D = q_in.shape
+    Hkv = k.shape[2]
+    if k.shape != v.shape or tuple(k.shape[:2]) != (B, S) or k.shape[3] != D or Hq % Hkv:
+        raise ValueError(f"qk_norm_rope_attention: q {tuple(q_in.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}")
+    if not qk_norm_rope_attention_ok(q_in, k, Hq // Hkv):
+        raise ValueError("qk_norm_rope_attention: bf16, D in (64, 128) and GQA groups a multiple of 4 only")
+    if (positions.dtype != torch.int32 or not positions.is_cuda or tuple(positions.shape) != (3, B, S)
+            or not positions.is_contiguous()):
+        raise ValueError(f"qk_norm_rope_attention: positions must be a contiguous int32 (3, {B}, {S}) device tensor")
+    if inv_freq.dtype != torch.float32 or not inv_freq.is_cuda or inv_freq.numel() != D // 2:
+        raise ValueError(f"qk_norm_rope_attention: inv_freq must be a float32 ({D // 2},) device tensor")
+    for w in (q_weight, k_weight):
+        if w.dtype != q_in.dtype or not w.is_cuda or w.shape != (D,) or not w.is_contiguous():
+            raise ValueError(f"qk_norm_rope_attention: norm weights must be contiguous ({D},) device tensors")
+    if sum(mrope_section) * 2 != D:
+        raise ValueError(f"qk_norm_rope_attention: mrope_section {list(mrope_section)} must sum to D/2 = {D // 2}")
+    if any(t.stride(-1) != 1 for t in (q_in, k, v)):
+        raise ValueError("qk_norm_rope_attention: the head dim must be contiguous")
+    o = out if out is not None else torch.empty((B, S, Hq, D), dtype=q_in.dtype, device=q_in.device)
+    if o.shape != (B, S, Hq, D) or o.stride(-1) != 1:
+        raise ValueError("qk_norm_rope_attention: out must be (B, S, Hq, D) with a contiguous head dim")
+    ws, nws = _lib.workspace(_lib.lib().q3_qk_norm_rope_attention_workspace_bytes(B, S, D), q_in.device)
+    qh, kh, vh, oh = (t.transpose(1, 2) for t in (q_in, k, v, o))  # (B, H, S, D) views
+    _lib.call("q3_qk_norm_rope_attention", q_in.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+              q_weight.data_ptr(), k_weight.data_ptr(), positions.data_ptr(), inv_freq.data_ptr(), B, S, Hq, Hkv, D,
+              _lib.i64s(*mrope_section), float(eps), _lib.i64s(*_s4(qh), *_s4(kh), *_s4(vh), *_s4(oh)),
+              float(scale), int(bool(is_causal)), _lib.dtype_code(q_in.dtype), _lib.ptr(ws), nws, _lib.stream())
+    return o
+
+
 def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, kv_lens: torch.Tensor,
                      scale: float, *, out: torch.Tensor | None = None, max_len: int | None = None,
                      append: bool = False, noalloc: bool = False) -> torch.Tensor:

@@ -5,8 +5,8 @@ import torch
 from torch import nn
 
 from ..kernels import (apply_rope, decode_attention, decode_attention_paged, flash_attention, flash_attention_cache,
-                       flash_attention_varlen, matmul_segments, qk_norm_rope, qk_norm_rope_paged,
-                       rmsnorm_matmul_segments)
+                       flash_attention_varlen, matmul_segments, qk_norm_rope, qk_norm_rope_attention,
+                       qk_norm_rope_attention_ok, qk_norm_rope_paged, rmsnorm_matmul_segments)
 from .kv_cache import PagedKVCache, StaticKVCache
 from .linear import CudaLinear
 from .norms import CudaRMSNorm, fused_norm_ok
@@ -74,7 +74,9 @@ class CudaFullAttention(nn.Module):
                               decode shapes (at most 32 tokens, bf16) the norm
                               runs inside the q/k/v projection, else first
     When `mrope_apply` is a TextMRoPE.bind(...) binding, q/k normalisation and
-    rotation run as one fused kernel on the projection outputs.
+    rotation run as one fused kernel on the projection outputs; for a long
+    prefill without past_kv (bf16, GQA groups a multiple of 4), k's runs alone
+    and q's inside the attention kernel (qk_norm_rope_attention).
     """
 
     def __init__(self, hidden_size: int, num_heads: int, num_kv_heads: int, head_dim: int | None = None,
@@ -147,6 +149,17 @@ class CudaFullAttention(nn.Module):
         if self._fusable(mrope_apply, x):
             rope = mrope_apply.rope
             pos = mrope_apply.positions_int32(x.device, B, S)
+            # The q prologue inside the attention kernel pays where its latency
+            # hides behind other blocks: at least two attention blocks (64
+            # queries of 4 heads each) per CU of the 256, e.g. S >= 4096 at 8 KV
+            # heads (S=4096: -12 us per layer; S=1024, one block per CU: +2 us).
+            attn_blocks = B * Hkv * (self.num_kv_groups // 4) * -(-S // 64)
+            if (past_kv is None and self.q_norm.weight.dtype == q.dtype and attn_blocks >= 512
+                    and qk_norm_rope_attention_ok(q, k, self.num_kv_groups)):
+                # k normalised and rotated in place; q inside the attention kernel
+                qk_norm_rope_attention(q, k, v, self.q_norm.weight, self.k_norm.weight, pos, rope.inv_freq,
+                                       rope.mrope_section, self.q_norm.eps, self.scale, True, out=o)
+                return self.o_proj(o.view(B, S, Hq * D), residual=residual), (k.transpose(1, 2), v.transpose(1, 2))
             qk_norm_rope(q, k, None, q, k, None, self.q_norm.weight, self.k_norm.weight, pos, rope.inv_freq,
                          rope.mrope_section, self.q_norm.eps)
             qh, kh, vh = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)

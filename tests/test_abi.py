@@ -176,6 +176,23 @@ def test_attention_validation():
                                        FAKE, ws - 16, None, None) == -6
     assert L.q3_decode_attention_paged(FAKE, FAKE, FAKE, FAKE, 4, 32, 10, FAKE, 0, FAKE, 0, 8, 2, 128, pg, 0.1, 1,
                                        FAKE, ws, None, None) == 0  # empty batch: no-op
+    # fused q/k norm + mRoPE + attention: one fp32 rotary table row (D floats) per token
+    assert L.q3_qk_norm_rope_attention_workspace_bytes(1, 4096, 128) == 4096 * 128 * 4
+    sec = _lib.i64s(24, 20, 20)
+    ws = 2 * 40 * 128 * 4
+
+    def fused(Hq=8, Hkv=2, D=128, dtype=1, qw=FAKE, nws=ws, B=2, section=sec):
+        return L.q3_qk_norm_rope_attention(FAKE, FAKE, FAKE, FAKE, qw, FAKE, FAKE, FAKE, B, 40, Hq, Hkv, D, section,
+                                           1e-6, st, 0.1, 1, dtype, FAKE, nws, None)
+    assert fused(qw=None) == -1  # the norm weights are required
+    assert fused(Hq=6, Hkv=4) == -2
+    assert fused(section=_lib.i64s(24, 20, 19)) == -2
+    assert fused(dtype=0) == -3  # bf16 only
+    assert fused(D=72, section=_lib.i64s(12, 12, 12)) == -5  # rotate-half pairs must share a lane
+    assert fused(D=96, section=_lib.i64s(16, 16, 16)) == -5  # no 12-lane groups in the k kernel
+    assert fused(Hq=4, Hkv=2) == -5  # GQA groups of 2: not the pipelined kernel
+    assert fused(nws=ws - 4) == -6
+    assert fused(B=0) == 0  # empty batch: no-op
 
 
 def test_rope_validation():

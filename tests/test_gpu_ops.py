@@ -463,6 +463,50 @@ def test_qk_norm_rope_fused(D, section):
     assert torch.equal(vo.cpu(), v)
 
 
+@pytest.mark.parametrize("B,S,Hq,Hkv,D,section,causal", [
+    (2, 300, 16, 4, 128, (24, 20, 20), True),   # ragged last query tile
+    (1, 256, 32, 4, 128, (24, 20, 20), True),   # groups 8 (C4's)
+    (2, 130, 8, 1, 64, (12, 10, 10), False),
+    (1, 64, 8, 2, 128, (24, 20, 20), False),  # one query tile, non-causal
+])
+def test_qk_norm_rope_attention(B, S, Hq, Hkv, D, section, causal):
+    """q/k norm + mRoPE + attention in two launches (q rotated inside the attention kernel) against
+    the fp32 oracle chain, and against qk_norm_rope followed by flash_attention on the same views."""
+    N = (Hq + 2 * Hkv) * D
+    qkv = rnd(B, S, N, seed=60)
+    qw, kw = rnd(D, seed=61, std=0.1) + 1, rnd(D, seed=62, std=0.1) + 1
+    pos = torch.stack([torch.arange(S) + 5, torch.arange(S) // 3, torch.arange(S) % 17]).view(3, 1, S).expand(3, B, S)
+    pos_d = gpu(pos.to(torch.int32).contiguous())
+    inv = gpu(O.mrope_inv_freq(D, 5e6))
+    scale = D ** -0.5
+
+    def views(t):
+        return (t[..., :Hq * D].view(B, S, Hq, D), t[..., Hq * D:(Hq + Hkv) * D].view(B, S, Hkv, D),
+                t[..., (Hq + Hkv) * D:].view(B, S, Hkv, D))
+    fused_buf = gpu(qkv)
+    q, k, v = views(fused_buf)
+    o = K.qk_norm_rope_attention(q, k, v, gpu(qw), gpu(kw), pos_d, inv, section, 1e-6, scale, causal)
+    assert torch.equal(fused_buf[..., :Hq * D].cpu(), qkv[..., :Hq * D]), "q_in must not be modified"
+
+    two_buf = gpu(qkv)
+    q2, k2, v2 = views(two_buf)
+    qk_out = torch.empty_like(q2)
+    K.qk_norm_rope(q2, k2, None, qk_out, k2, None, gpu(qw), gpu(kw), pos_d, inv, section, 1e-6)
+    o2 = K.flash_attention(qk_out.transpose(1, 2), k2.transpose(1, 2), v2.transpose(1, 2), scale, causal,
+                           Hq // Hkv).transpose(1, 2)
+    assert torch.equal(k.cpu(), k2.cpu()), "k rows: the same kernel code as qk_norm_rope"
+    # q may differ from the separate kernel's by one bf16 ulp in rare elements (sum-of-squares order)
+    assert (o.float() - o2.float()).abs().max().item() <= 4e-3
+
+    cos3, sin3 = O.mrope_cos_sin(pos, D, 5e6)
+    qs, ks, vs = views(f32(qkv))
+    qr = O.apply_mrope(O.rmsnorm(qs, f32(qw)).transpose(1, 2), cos3, sin3, section)
+    kr = O.apply_mrope(O.rmsnorm(ks, f32(kw)).transpose(1, 2), cos3, sin3, section)
+    ref = O.flash_attention(qr, kr, vs.transpose(1, 2), scale, causal, Hq // Hkv).transpose(1, 2)
+    assert_bf16_close(k, kr.transpose(1, 2), what="fused k rows")
+    assert_bf16_close(o, ref, what=f"qk_norm_rope_attention {B},{S},{Hq},{Hkv},{D}")
+
+
 # ------------------------------------------------------------------ norms / elementwise
 @pytest.mark.parametrize("rows,cols", [(4096, 4096), (2048, 128), (100, 1152), (33, 2048), (17, 37), (8, 256)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
