@@ -363,7 +363,8 @@ __global__ __launch_bounds__(256, MINB) void qk_norm_rope_kernel(const QKNormRop
 #pragma unroll
     for (int u = 0; u < BATCH; ++u) load8<T, VEC>(qk_in_row<T>(a, b, s, min(r0 + u * RPP, nrows - 1)) + 8 * j, v[u]);
   };
-  const int first = (a.q_in ? 0 : a.Hq) + tid / G;
+  // gridDim.y blocks share a token's rows: block y takes passes y, y + gridDim.y, ...
+  const int first = (a.q_in ? 0 : a.Hq) + (int)blockIdx.y * BATCH * RPP + tid / G;
   load_batch(first);
   const int so_b = a.dst_seq_off ? a.dst_seq_off[b] : 0;
   if (tid < HALF) {
@@ -385,7 +386,7 @@ __global__ __launch_bounds__(256, MINB) void qk_norm_rope_kernel(const QKNormRop
     cs[e] = s_cos[i];
     sn[e] = s_sin[i];
   }
-  for (int r0 = first; r0 < nrows; r0 += BATCH * RPP) {  // uniform per lane group
+  for (int r0 = first; r0 < nrows; r0 += BATCH * RPP * (int)gridDim.y) {  // uniform per lane group
     if (r0 != first) load_batch(r0);
 #pragma unroll
     for (int u = 0; u < BATCH; ++u) {
@@ -476,10 +477,15 @@ int launch_qk(const QKNormRopeArgs& a, hipStream_t st) {
              q3_aligned(a.k_out, 16) && (!a.v_in || (q3_aligned(a.v_in, 16) && q3_aligned(a.v_out, 16))) &&
              (!a.q_w || (q3_aligned(a.q_w, 16) && q3_aligned(a.k_w, 16)));
   for (int i = 0; i < 18; ++i) vec = vec && (a.st[i] * (int64_t)sizeof(T)) % 16 == 0;
+  // Few tokens (decode): the passes over a token's rows run in parallel blocks
+  // instead of one after another (each block recomputes the token's angles).
+  const int rows = (a.q_in ? a.Hq : 0) + a.Hkv + (a.v_out ? a.Hkv : 0);
+  const int passes = (int)q3_cdiv(rows, kQKBatch * (256 / G));
+  const unsigned ysplit = tokens <= 256 ? (unsigned)std::max(passes, 1) : 1u;
   auto go = [&](auto g, auto v) {
     constexpr int minb = std::is_same<T, bf16>::value && decltype(v)::value ? kQKMinBlocks : 1;
     hipLaunchKernelGGL((qk_norm_rope_kernel<T, decltype(g)::value, decltype(v)::value, kQKBatch, minb>),
-                       dim3((unsigned)tokens), dim3(256), 0, st, a);
+                       dim3((unsigned)tokens, ysplit), dim3(256), 0, st, a);
   };
   using VT = std::true_type;
   using VF = std::false_type;
