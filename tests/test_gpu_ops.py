@@ -468,6 +468,7 @@ def test_qk_norm_rope_fused(D, section):
     (1, 256, 32, 4, 128, (24, 20, 20), True),   # groups 8 (C4's)
     (2, 130, 8, 1, 64, (12, 10, 10), False),
     (1, 64, 8, 2, 128, (24, 20, 20), False),  # one query tile, non-causal
+    (1, 253, 8, 2, 128, (24, 20, 20), True),  # token count not a multiple of the k kernel's 4 per block
 ])
 def test_qk_norm_rope_attention(B, S, Hq, Hkv, D, section, causal):
     """q/k norm + mRoPE + attention in two launches (q rotated inside the attention kernel) against
