@@ -783,27 +783,22 @@ __device__ __forceinline__ void scale_acc(floatx16& acc, float alpha) {
 // The q prologue of the fused prefill on one query's fragments: the lane holds
 // elements 16 ks + 8 h + e (ks < D / 16, e < 8), the other lane half (lane ^
 // 32) the rest of the row. RMSNorm over the row (fp32 sum of squares, the
-// halves exchanged once), times the weight, then rotate-half with the table's
-// cos / sin: element i < D/2 pairs with i + D/2, which is k-step ks + D/32 of
-// the same lane. One rounding to bf16 at the end, as the separate fused
-// norm + rotation kernel.
+// halves exchanged once), times the weight, then rotate-half with the rotary
+// table row (cos of the D/2 angles, then their sin): element i < D/2 pairs
+// with i + D/2, which is k-step ks + D/32 of the same lane. One rounding to
+// bf16 at the end, as the separate fused norm + rotation kernel. The table
+// row sits in LDS as D/4 16-byte chunks, chunk c of row r at slot
+// (c + r) mod D/4 (conflict-free reads across the 32 rows of a wave).
 template <int D>
 __device__ __forceinline__ void q_norm_rope_frag(bf16x8 (&qf)[D / 16], const bf16* __restrict__ w,
-                                                 const float* __restrict__ tab, float eps, int h) {
-  constexpr int KS = D / 16, HK = KS / 2;
-  // Weights and table first: their loads overlap the q fragments' (one round
-  // trip for all of them).
+                                                 const char* tab_lds, int row, float eps, int h) {
+  constexpr int KS = D / 16, HK = KS / 2, CPR = D / 4;
+  auto chunk = [&](int c) {
+    return *reinterpret_cast<const float4*>(tab_lds + (row * CPR + ((c + row) & (CPR - 1))) * 16);
+  };
   bf16x8 wv[KS];
-  float4 cs4[HK][2], sn4[HK][2];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) wv[ks] = *reinterpret_cast<const bf16x8*>(w + ks * 16 + 8 * h);
-#pragma unroll
-  for (int ks = 0; ks < HK; ++ks)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      cs4[ks][j] = reinterpret_cast<const float4*>(tab + ks * 16 + 8 * h)[j];
-      sn4[ks][j] = reinterpret_cast<const float4*>(tab + D / 2 + ks * 16 + 8 * h)[j];
-    }
   float ss = 0.f;
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks)
@@ -816,10 +811,10 @@ __device__ __forceinline__ void q_norm_rope_frag(bf16x8 (&qf)[D / 16], const bf1
   const float rstd = rsqrtf(ss / (float)D + eps);
 #pragma unroll
   for (int ks = 0; ks < HK; ++ks) {
-    const float c[8] = {cs4[ks][0].x, cs4[ks][0].y, cs4[ks][0].z, cs4[ks][0].w,
-                        cs4[ks][1].x, cs4[ks][1].y, cs4[ks][1].z, cs4[ks][1].w};
-    const float sn[8] = {sn4[ks][0].x, sn4[ks][0].y, sn4[ks][0].z, sn4[ks][0].w,
-                         sn4[ks][1].x, sn4[ks][1].y, sn4[ks][1].z, sn4[ks][1].w};
+    const int c0 = ks * 4 + 2 * h;  // cos chunks c0, c0 + 1; sin chunks D/8 further
+    const float4 ca = chunk(c0), cb = chunk(c0 + 1), sa = chunk(D / 8 + c0), sb = chunk(D / 8 + c0 + 1);
+    const float c[8] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w};
+    const float sn[8] = {sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, sb.z, sb.w};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float lo = (float)qf[ks][e] * rstd * (float)wv[ks][e];
@@ -907,12 +902,33 @@ __global__ __launch_bounds__(512) void flash_fwd_pipe_kernel(const AttnParams p)
     q3::dma16(vrs, live ? (uint32_t)((row + r0) * vs2) + vc0 : q3::kOOB, lv);
   };
 
-  // With the fused q prologue, the first K/V tiles are requested before q so
-  // that their loads overlap the prologue's.
-  const bool qpro = D % 32 == 0 && p.rope_tab != nullptr;
-  if (qpro && nkt > 0) {
+  // Fused q prologue (GQA, D = 64 or 128): the first kAhead K/V tiles are
+  // requested first; ring slots kAhead and kAhead + 1 (free until tile kAhead
+  // is issued, after the prologue) take the rotary-table rows of the block's
+  // kQ queries by direct-to-LDS loads, read once per block instead of once
+  // per head wave.
+  constexpr bool kQpro = !MHA && (D == 64 || D == 128);
+  static_assert(!kQpro || kQ * D * 4 <= 2 * 2 * kTile * 2, "table rows fit two ring slots");
+  const bool qpro = kQpro && p.rope_tab != nullptr;
+  if constexpr (kQpro) {
+    if (qpro) {
+      if (nkt > 0) {
 #pragma unroll
-    for (int s = 0; s <= kAhead; ++s) issue(s);
+        for (int s = 0; s < kAhead; ++s) issue(s);
+      }
+      constexpr int CPR = D / 4;          // 16-byte chunks per table row
+      constexpr int NI = kQ * CPR / 512;  // direct-to-LDS loads per thread
+      const int ntab = min(kQ, Sq - q0);  // rows past the sequence load as zeros
+      const __amdgpu_buffer_rsrc_t trs =
+          q3::make_rsrc(p.rope_tab + ((int64_t)b * Sq + q0) * D, (int64_t)ntab * D * 4);
+      const uint32_t ltab = lbase + (uint32_t)(kAhead * 2 * kTile * 2);
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int pos = (i * 8 + wave) * 64 + lane;  // LDS slot of 16 bytes
+        const int row = pos / CPR, chunk = ((pos % CPR) - row) & (CPR - 1);
+        q3::dma16(trs, (uint32_t)((row * D + chunk * 4) * 4), ltab + (uint32_t)((i * 8 + wave) * 64 * 16));
+      }
+    }
   }
 
   // Q fragments (B operand): lane supplies Q[qw0 + l32][16 ks + 8 h .. + 7].
@@ -924,9 +940,16 @@ __global__ __launch_bounds__(512) void flash_fwd_pipe_kernel(const AttnParams p)
     for (int ks = 0; ks < KSTEPS; ++ks)
       qf[ks] = (qi < Sq && ks * 16 + 8 * h < D) ? *reinterpret_cast<const bf16x8*>(qrow + ks * 16 + 8 * h)
                                                 : bf16x8{};
-    if constexpr (D % 32 == 0) {
-      if (p.rope_tab != nullptr && qi < Sq)
-        q_norm_rope_frag<D>(qf, p.qn_w, p.rope_tab + ((int64_t)b * Sq + qi) * D, p.qn_eps, h);
+    if constexpr (kQpro) {
+      if (qpro) {
+        q3::vm_wait<0>();
+        __syncthreads();
+        if (qi < Sq)
+          q_norm_rope_frag<D>(qf, p.qn_w, reinterpret_cast<const char*>(ring) + kAhead * 2 * kTile * 2,
+                              qw0 - q0 + l32, p.qn_eps, h);
+        __syncthreads();  // the table's slots are free again
+        if (nkt > 0) issue(kAhead);
+      }
     }
   }
 
@@ -1073,6 +1096,8 @@ __global__ __launch_bounds__(512) void flash_fwd_pipe_kernel(const AttnParams p)
 #pragma unroll
       for (int s = 0; s <= kAhead; ++s) issue(s);
     }
+    // (with the q prologue, tiles 0 .. kAhead - 1 have landed and only tile
+    // kAhead is in flight)
     q3::vm_wait<(kAhead - 1) * PERW>();
     __syncthreads();
     floatx16 sa, sb;
@@ -1284,10 +1309,10 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
   const bool aligned = q3_aligned(q, 16) && q3_aligned(k, 16) && q3_aligned(v, 16) && q3_aligned(o, 8) &&
                        strides_aligned8(strides, 12);
   int rc = Q3_OK;
-  if (rope_tab) {  // the fused q prologue exists in the pipelined kernel only (D a multiple of 32)
+  if (rope_tab) {  // the fused q prologue exists in the pipelined GQA kernel only (D = 64 or 128)
     Q3_REQUIRE(dtype == Q3_BF16, Q3_ERR_DTYPE);
     Q3_REQUIRE(aligned && q3_aligned(qn_w, 16), Q3_ERR_ALIGN);
-    Q3_REQUIRE((D == 64 || D == 96 || D == 128) && pipe_eligible(p) && q_off == nullptr && cu_seqlens == nullptr &&
+    Q3_REQUIRE((D == 64 || D == 128) && p.groups % 4 == 0 && q_off == nullptr && cu_seqlens == nullptr &&
                    (Sk + 1) * strides[5] * 2 < 0x7fffffffLL,
                Q3_ERR_UNSUPPORTED);
   }
