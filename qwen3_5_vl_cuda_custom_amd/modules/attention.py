@@ -74,9 +74,9 @@ class CudaFullAttention(nn.Module):
                               decode shapes (at most 32 tokens, bf16) the norm
                               runs inside the q/k/v projection, else first
     When `mrope_apply` is a TextMRoPE.bind(...) binding, q/k normalisation and
-    rotation run as one fused kernel on the projection outputs; for a long
-    prefill without past_kv (bf16, GQA groups a multiple of 4), k's runs alone
-    and q's inside the attention kernel (qk_norm_rope_attention).
+    rotation run as one fused kernel on the projection outputs; for a prefill
+    without past_kv (bf16, GQA groups a multiple of 4), k's runs alone and q's
+    inside the attention kernel (qk_norm_rope_attention).
     """
 
     def __init__(self, hidden_size: int, num_heads: int, num_kv_heads: int, head_dim: int | None = None,
@@ -149,12 +149,7 @@ class CudaFullAttention(nn.Module):
         if self._fusable(mrope_apply, x):
             rope = mrope_apply.rope
             pos = mrope_apply.positions_int32(x.device, B, S)
-            # The q prologue inside the attention kernel pays where its latency
-            # hides behind other blocks: at least two attention blocks (64
-            # queries of 4 heads each) per CU of the 256, e.g. S >= 4096 at 8 KV
-            # heads (S=4096: -12 us per layer; S=1024, one block per CU: +2 us).
-            attn_blocks = B * Hkv * (self.num_kv_groups // 4) * -(-S // 64)
-            if (past_kv is None and self.q_norm.weight.dtype == q.dtype and attn_blocks >= 512
+            if (past_kv is None and self.q_norm.weight.dtype == q.dtype
                     and qk_norm_rope_attention_ok(q, k, self.num_kv_groups)):
                 # k normalised and rotated in place; q inside the attention kernel
                 qk_norm_rope_attention(q, k, v, self.q_norm.weight, self.k_norm.weight, pos, rope.inv_freq,
