@@ -463,6 +463,34 @@ def test_qk_norm_rope_fused(D, section):
     assert torch.equal(vo.cpu(), v)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_qk_norm_rope_decode_rows_split(dtype):
+    """A decode step's q/k/v rows (32 + 8 + 8 heads of 128: three 16-row passes per token) run
+    as parallel blocks per token; each block's rows must match the oracle, cache offsets too."""
+    B, Hq, Hkv, D, cap = 5, 32, 8, 128, 24
+    q, k, v = rnd(B, 1, Hq, D, seed=80, dtype=dtype), rnd(B, 1, Hkv, D, seed=81, dtype=dtype), \
+        rnd(B, 1, Hkv, D, seed=82, dtype=dtype)
+    qw, kw = (rnd(D, seed=83, std=0.1) + 1).to(dtype), (rnd(D, seed=84, std=0.1) + 1).to(dtype)
+    lens = torch.tensor([0, 3, 17, 9, 23], dtype=torch.int32)
+    pos = lens.view(1, B, 1).expand(3, B, 1).contiguous()
+    qo = torch.empty(B, 1, Hq, D, dtype=dtype, device=DEV)
+    kc = torch.zeros(B, cap, Hkv, D, dtype=dtype, device=DEV)
+    vc = torch.zeros_like(kc)
+    K.qk_norm_rope(gpu(q), gpu(k), gpu(v), qo, kc, vc, gpu(qw), gpu(kw), gpu(pos.to(torch.int32)),
+                   gpu(O.mrope_inv_freq(D, 5e6)), (24, 20, 20), 1e-6, dst_seq_offset=gpu(lens), dst_seq_cap=cap)
+    cos3, sin3 = O.mrope_cos_sin(pos, D, 5e6)
+    qr = O.apply_mrope(O.rmsnorm(f32(q), f32(qw)).transpose(1, 2), cos3, sin3, (24, 20, 20)).transpose(1, 2)
+    kr = O.apply_mrope(O.rmsnorm(f32(k), f32(kw)).transpose(1, 2), cos3, sin3, (24, 20, 20)).transpose(1, 2)
+    check = assert_bf16_close if dtype == torch.bfloat16 else (lambda o, r, what: assert_close(o, r, 1e-4, what=what))
+    check(qo, qr, what="decode q rows")
+    kcc, vcc = kc.cpu(), vc.cpu()
+    for b in range(B):
+        check(kcc[b, int(lens[b])], kr[b, 0], what=f"decode k row of sequence {b}")
+        assert torch.equal(vcc[b, int(lens[b])], v[b, 0]), f"v row of sequence {b}"
+        others = [r for r in range(cap) if r != int(lens[b])]
+        assert not kcc[b, others].any() and not vcc[b, others].any(), "only the appended row is written"
+
+
 @pytest.mark.parametrize("B,S,Hq,Hkv,D,section,causal", [
     (2, 300, 16, 4, 128, (24, 20, 20), True),   # ragged last query tile
     (1, 256, 32, 4, 128, (24, 20, 20), True),   # groups 8 (C4's)
