@@ -42,8 +42,12 @@ def full_attention(x, p, *, num_heads, num_kv_heads, head_dim, eps, cos_3d, sin_
     q = rd(ops.rmsnorm(q, p[prefix + "q_norm.weight"], eps)).transpose(1, 2)
     k = rd(ops.rmsnorm(k, p[prefix + "k_norm.weight"], eps)).transpose(1, 2)
     v = v.transpose(1, 2)
-    q = rd(ops.apply_mrope(q, cos_3d, sin_3d, mrope_section))
-    k = rd(ops.apply_mrope(k, cos_3d, sin_3d, mrope_section))
+    # The reference casts the fp32 cos/sin tables to the activation dtype before
+    # its rotation kernel (kernels/mrope.py:92-93), so its bf16 path rotates with
+    # bf16-rounded tables.
+    cos_r, sin_r = rd(cos_3d), rd(sin_3d)
+    q = rd(ops.apply_mrope(q, cos_r, sin_r, mrope_section))
+    k = rd(ops.apply_mrope(k, cos_r, sin_r, mrope_section))
     if past_kv is not None:
         k = torch.cat([past_kv[0], k], dim=2)
         v = torch.cat([past_kv[1], v], dim=2)
@@ -126,8 +130,9 @@ def vision_attention(x, p, *, num_heads, cos, sin, prefix="", rd=_ident):
     hd = h // num_heads
     qkv = rd(ops.linear(x, p[prefix + "qkv.weight"], p[prefix + "qkv.bias"])).reshape(B, S, 3, num_heads, hd)
     q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
-    q = rd(ops.apply_rope(q, cos, sin))
-    k = rd(ops.apply_rope(k, cos, sin))
+    # cos/sin cast to the activation dtype first, as kernels/rope.py:60-61 does.
+    q = rd(ops.apply_rope(q, rd(cos), rd(sin)))
+    k = rd(ops.apply_rope(k, rd(cos), rd(sin)))
     out = rd(ops.flash_attention(q, k, v, hd ** -0.5, False, 1)).transpose(1, 2).reshape(B, S, -1)
     return rd(ops.linear(out, p[prefix + "proj.weight"], p[prefix + "proj.bias"]))
 

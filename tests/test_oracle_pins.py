@@ -12,6 +12,7 @@ import math
 import numpy as np
 import pytest
 import torch
+import torch.nn.functional as F
 
 from oracle import layers as L
 from oracle import ops as O
@@ -334,6 +335,197 @@ def test_vision_block_matches_hf_per_image():
     p = {n: t.detach() for n, t in hf.named_parameters()}
     y = L.vision_block(x.view(nimg, S, 288), p, num_heads=4, cos=cos, sin=sin, eps=1e-6)
     assert torch.allclose(y.reshape(-1, 288), ref, atol=5e-5), float((y.reshape(-1, 288) - ref).abs().max())
+
+
+# ------------------------------------------------------------------ the bf16 emulation (rd=round_bf16)
+# The layer bar at C2-C5 uses the oracle run with a bf16 rounding after every
+# op, standing for the reference's own bf16 path. Here that emulation is checked
+# against the reference's op sequence run natively on bf16 tensors with torch
+# CPU ops, each op computed as the reference's kernel computes it (fp32 inside,
+# one rounding to bf16 at its output; bf16 elementwise ops such as the routing
+# multiply, index_add_ and the residual adds run as torch bf16 ops). The only
+# freedom between the two is the summation order inside the GEMMs and the
+# attention (fp32 accumulation in both), which can move an output by one bf16
+# ulp and propagate (99.9% of elements bit-identical for the text layer and the
+# MoE block, 98.7% for the vision block, whose attention passes such flips to
+# whole rows). A planted one-rounding difference in the oracle leaves ~95%.
+BF = torch.bfloat16
+
+
+def _native_rms(t, w, eps):
+    """csrc/rmsnorm_op.cu:8-60 / kernels/rmsnorm.py:12-17: fp32 inside, one rounding."""
+    tf = t.float()
+    return (tf * torch.rsqrt(tf.pow(2).mean(-1, keepdim=True) + eps) * w.float()).to(BF)
+
+
+def _native_swiglu(gate, up):
+    """csrc/swiglu_op.cu:6-18: silu(g)*u in fp32, one rounding."""
+    return (F.silu(gate.float()) * up.float()).to(BF)
+
+
+def _native_rotate(x, c, s):
+    """csrc/mrope_op.cu:30-47 and csrc/rope_op.cu: bf16 cos/sin (cast by the caller,
+    kernels/mrope.py:92-93, kernels/rope.py:60-61), fp32 products, one rounding."""
+    h = x.shape[-1] // 2
+    xf, cf, sf = x.float(), c.float()[..., :h], s.float()[..., :h]
+    x1, x2 = xf[..., :h], xf[..., h:]
+    return torch.cat([x1 * cf - x2 * sf, x2 * cf + x1 * sf], -1).to(BF)
+
+
+def _native_text_layer(x, p, pos, heads, kv, hd, eps, theta, section):
+    """CudaTextDecoderLayer.forward (modules/text_decoder.py:51-65, modules/attention.py:75-98,
+    modules/mlp.py:19-22) on bf16 tensors. The mRoPE table picks, for output column c (and c + D/2),
+    the axis whose section holds c: sections [T, H, W] = mrope_section over each half
+    (kernels/mrope.py:19-35), angles pos_axis * theta^(-2j/D) (modules/rotary.py:43-55)."""
+    B, S, _ = x.shape
+    hn = _native_rms(x, p["input_layernorm.weight"], eps)
+    q = F.linear(hn, p["self_attn.q_proj.weight"]).view(B, S, heads, hd)
+    k = F.linear(hn, p["self_attn.k_proj.weight"]).view(B, S, kv, hd)
+    v = F.linear(hn, p["self_attn.v_proj.weight"]).view(B, S, kv, hd)
+    q = _native_rms(q, p["self_attn.q_norm.weight"], eps).transpose(1, 2)
+    k = _native_rms(k, p["self_attn.k_norm.weight"], eps).transpose(1, 2)
+    v = v.transpose(1, 2)
+    half = hd // 2
+    axis = torch.tensor([0 if c < section[0] else 1 if c < section[0] + section[1] else 2 for c in range(half)])
+    inv = 1.0 / (theta ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))
+    ang = pos.float()[..., None] * torch.cat([inv, inv])                        # (3, B, S, D)
+    ang = torch.gather(ang, 0, torch.cat([axis, axis]).view(1, 1, 1, hd).expand(1, B, S, hd))[0]
+    c, s_ = ang.cos().to(BF)[:, None], ang.sin().to(BF)[:, None]
+    q, k = _native_rotate(q, c, s_), _native_rotate(k, c, s_)
+    g_ = heads // kv
+    ke = k[:, :, None].expand(B, kv, g_, S, hd).reshape(B, heads, S, hd)
+    ve = v[:, :, None].expand(B, kv, g_, S, hd).reshape(B, heads, S, hd)
+    a = F.scaled_dot_product_attention(q.float(), ke.float(), ve.float(), is_causal=True, scale=hd ** -0.5).to(BF)
+    h = F.linear(a.transpose(1, 2).reshape(B, S, -1), p["self_attn.o_proj.weight"]) + x
+    m = _native_rms(h, p["post_attention_layernorm.weight"], eps)
+    act = _native_swiglu(F.linear(m, p["mlp.gate_proj.weight"]), F.linear(m, p["mlp.up_proj.weight"]))
+    return F.linear(act, p["mlp.down_proj.weight"]) + h
+
+
+def _native_moe(x, p, top_k):
+    """CudaSparseMoE.forward, modules/moe.py:54-85, on bf16 tensors: bf16 router GEMM, softmax of the
+    fp32 upcast, top-k with the lowest index winning ties (a stable descending sort), renormalise in
+    fp32 and cast, per expert in ascending order its tokens in ascending order (nonzero), bf16 GEMMs,
+    the bf16 multiply by the routing weight and a bf16 index_add_."""
+    xf = x.reshape(-1, x.shape[-1])
+    logits = F.linear(xf, p["gate_weight"])
+    vals, idx = torch.sort(torch.softmax(logits.float(), -1), dim=-1, descending=True, stable=True)
+    vals, idx = vals[:, :top_k], idx[:, :top_k]
+    vals = (vals / vals.sum(-1, keepdim=True)).to(BF)
+    inter = p["down_proj"].shape[2]
+    out = torch.zeros_like(xf)
+    for e in range(p["gate_weight"].shape[0]):
+        tok, slot = (idx == e).nonzero(as_tuple=True)
+        if tok.numel() == 0:
+            continue
+        gu = F.linear(xf[tok], p["gate_up_proj"][e])
+        eo = F.linear(_native_swiglu(gu[:, :inter], gu[:, inter:]), p["down_proj"][e])
+        out.index_add_(0, tok, eo * vals[tok, slot, None])
+    return out.reshape(x.shape), logits
+
+
+def _native_vision_block(x, p, heads, cos, sin, eps):
+    """CudaVisionBlock.forward (modules/vision_block.py:21-24, modules/attention.py:25-42,
+    modules/mlp.py:33-34) on bf16 tensors; layernorm and gelu_tanh in fp32 with one rounding
+    (csrc/layernorm_op.cu, csrc/gelu_tanh_op.cu)."""
+    B, S, H = x.shape
+    hd = H // heads
+
+    def ln(t, w, b):
+        return F.layer_norm(t.float(), (H,), w.float(), b.float(), eps).to(BF)
+
+    qkv = F.linear(ln(x, p["norm1.weight"], p["norm1.bias"]), p["attn.qkv.weight"], p["attn.qkv.bias"])
+    qkv = qkv.reshape(B, S, 3, heads, hd)
+    q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
+    c, s_ = cos.to(BF), sin.to(BF)
+    q, k = _native_rotate(q, c, s_), _native_rotate(k, c, s_)
+    a = F.scaled_dot_product_attention(q.float(), k.float(), v.float(), scale=hd ** -0.5).to(BF)
+    x = F.linear(a.transpose(1, 2).reshape(B, S, H), p["attn.proj.weight"], p["attn.proj.bias"]) + x
+    f1 = F.linear(ln(x, p["norm2.weight"], p["norm2.bias"]), p["mlp.linear_fc1.weight"], p["mlp.linear_fc1.bias"])
+    f1 = F.gelu(f1.float(), approximate="tanh").to(BF)
+    return F.linear(f1, p["mlp.linear_fc2.weight"], p["mlp.linear_fc2.bias"]) + x
+
+
+def _assert_equal_up_to_order(native, emu, what):
+    """At least 98% of elements bit-identical; none more than 2 bf16 ulps apart, ulps taken at the
+    element's magnitude or the output's mean magnitude, whichever is larger (a flipped rounding
+    upstream reaches small outputs as an absolute perturbation)."""
+    a, b = native.float(), emu.float()
+    d = (a - b).abs()
+    mag = torch.maximum(b.abs(), b.abs().mean()).clamp_min(2.0 ** -126)
+    ulp = 2.0 ** (torch.floor(torch.log2(mag)) - 7)
+    same = float((d == 0).float().mean())
+    worst = float((d / ulp).max())
+    assert same >= 0.98 and worst <= 2.0, f"{what}: {same:.4f} bit-identical, worst {worst:.1f} ulps"
+
+
+def _double_rounding_swiglu(gate, up):
+    # planted mistake: the fallback's two bf16 roundings (silu, then the product) in place of the kernel's one
+    return O.round_bf16(F.silu(gate)) * up
+
+
+def test_bf16_emulation_text_layer_matches_native_bf16(monkeypatch):
+    H, heads, kv, hd, inter, S = 256, 4, 2, 64, 688, 128
+    shapes = {"input_layernorm.weight": (H,), "post_attention_layernorm.weight": (H,),
+              "self_attn.q_proj.weight": (heads * hd, H), "self_attn.k_proj.weight": (kv * hd, H),
+              "self_attn.v_proj.weight": (kv * hd, H), "self_attn.o_proj.weight": (H, heads * hd),
+              "self_attn.q_norm.weight": (hd,), "self_attn.k_norm.weight": (hd,),
+              "mlp.gate_proj.weight": (inter, H), "mlp.up_proj.weight": (inter, H),
+              "mlp.down_proj.weight": (H, inter)}
+    p = {n: (randn(*s, std=0.02) if len(s) == 2 else 1 + 0.1 * randn(*s)).to(BF) for n, s in shapes.items()}
+    x = randn(1, S, H).to(BF)
+    t = torch.arange(S)
+    pos = torch.stack([t, t // 4, t % 7]).view(3, 1, S)  # distinct T/H/W positions: the section layout matters
+    native = _native_text_layer(x, p, pos, heads, kv, hd, 1e-6, 5e6, [12, 10, 10])
+    cos3, sin3 = O.mrope_cos_sin(pos, hd, 5e6)
+    kw = dict(num_heads=heads, num_kv_heads=kv, head_dim=hd, eps=1e-6, cos_3d=cos3, sin_3d=sin3,
+              mrope_section=[12, 10, 10], rd=O.round_bf16)
+    pf = {n: v.float() for n, v in p.items()}
+    emu, _, _ = L.text_decoder_layer(x.float(), pf, **kw)
+    _assert_equal_up_to_order(native, emu, "text layer")
+    monkeypatch.setattr(O, "swiglu", _double_rounding_swiglu)
+    planted, _, _ = L.text_decoder_layer(x.float(), pf, **kw)
+    with pytest.raises(AssertionError):
+        _assert_equal_up_to_order(native, planted, "planted")
+
+
+def test_bf16_emulation_moe_matches_native_bf16(monkeypatch):
+    T, H, inter, E, k = 96, 128, 48, 16, 4
+    p = {"gate_weight": randn(E, H, std=0.05).to(BF), "gate_up_proj": randn(E, 2 * inter, H, std=0.05).to(BF),
+         "down_proj": randn(E, H, inter, std=0.05).to(BF)}
+    x = randn(1, T, H).to(BF)
+    native, nlogits = _native_moe(x, p, k)
+    pf = {n: v.float() for n, v in p.items()}
+    emu, elogits = L.sparse_moe(x.float(), pf, top_k=k, rd=O.round_bf16)
+    assert torch.equal(nlogits.float(), elogits)
+    _assert_equal_up_to_order(native, emu, "moe block")
+    monkeypatch.setattr(O, "swiglu", _double_rounding_swiglu)
+    planted, _ = L.sparse_moe(x.float(), pf, top_k=k, rd=O.round_bf16)
+    with pytest.raises(AssertionError):
+        _assert_equal_up_to_order(native, planted, "planted")
+
+
+def test_bf16_emulation_vision_block_matches_native_bf16(monkeypatch):
+    nimg, S, H, heads, inter = 2, 64, 288, 4, 400
+    shapes = {"norm1.weight": (H,), "norm1.bias": (H,), "norm2.weight": (H,), "norm2.bias": (H,),
+              "attn.qkv.weight": (3 * H, H), "attn.qkv.bias": (3 * H,), "attn.proj.weight": (H, H),
+              "attn.proj.bias": (H,), "mlp.linear_fc1.weight": (inter, H), "mlp.linear_fc1.bias": (inter,),
+              "mlp.linear_fc2.weight": (H, inter), "mlp.linear_fc2.bias": (H,)}
+    p = {n: (randn(*s, std=0.05) + (1.0 if n.startswith("norm") and n.endswith("weight") else 0.0)).to(BF)
+         for n, s in shapes.items()}
+    x = randn(nimg, S, H).to(BF)
+    cos, sin = L.vision_rope_tables([(1, 8, 8)], H // heads, 1e4, 2)
+    native = _native_vision_block(x, p, heads, cos, sin, 1e-6)
+    emu = L.vision_block(x.float(), {n: v.float() for n, v in p.items()}, num_heads=heads, cos=cos, sin=sin,
+                         eps=1e-6, rd=O.round_bf16)
+    _assert_equal_up_to_order(native, emu, "vision block")
+    # planted mistake: the rotation with the fp32 tables (no cast to the activation dtype)
+    rope = O.apply_rope
+    monkeypatch.setattr(O, "apply_rope", lambda t, c, s_: rope(t, cos, sin))
+    planted = L.vision_block(x.float(), {n: v.float() for n, v in p.items()}, num_heads=heads, cos=cos, sin=sin,
+                             eps=1e-6, rd=O.round_bf16)
+    with pytest.raises(AssertionError):
+        _assert_equal_up_to_order(native, planted, "planted")
 
 
 def test_c1_golden_fixture():
