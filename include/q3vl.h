@@ -382,6 +382,110 @@ int64_t q3_index_add_workspace_bytes(int64_t n_src, int64_t n_target);
 int q3_index_add(void* target, const void* src, const int64_t* idx, int64_t n_src, int64_t n_target, int64_t D,
                  int dtype, void* workspace, int64_t workspace_bytes, int* status, void* stream);
 
+/* ---------------------------------------------------------------- the rest of the op namespace
+ * q3_sigmoid_mul replaces sigmoid_mul_forward(Tensor x, Tensor gate)
+ * (csrc/sigmoid_mul_op.cpp:9, csrc/sigmoid_mul_op.cu:5-16): y = x * sigmoid(gate)
+ * in fp32, one rounding; n contiguous elements.
+ * q3_cross_entropy replaces cross_entropy_forward(Tensor logits, Tensor targets,
+ * int ignore_index) -> [loss_per_token, lse] (csrc/cross_entropy_op.cpp:11,
+ * csrc/cross_entropy_op.cu:10-62) and the mean that kernels/cross_entropy.py:60-64
+ * takes after it: logits (N, V) contiguous, targets (N) int64; loss_per_token
+ * and lse (N) fp32 (both 0 for a target equal to ignore_index), *loss (fp32) =
+ * sum(loss_per_token) / max(#valid targets, 1), *n_valid (int32, or null) = the
+ * count. A target outside [0, V) other than ignore_index counts as ignored and
+ * sets bit 0 of *status (a device int32, or null). Nothing synchronises. */
+int q3_sigmoid_mul(const void* x, const void* gate, void* y, int64_t n, int dtype, void* stream);
+int q3_cross_entropy(const void* logits, const int64_t* targets, float* loss_per_token, float* lse, float* loss,
+                     int* n_valid, int64_t N, int64_t V, int64_t ignore_index, int dtype, int* status, void* stream);
+
+/* ---------------------------------------------------------------- backward
+ * Gradients of the ops the reference wraps in torch.autograd.Function. Every
+ * reduction runs in a fixed order (no atomics): results are bitwise
+ * reproducible. fp32 and bf16; fp32 math, one rounding per output.
+ *
+ * Elementwise (n contiguous elements), replacing
+ *   sigmoid_mul_backward(x, gate, grad_out) -> [gx, gg] (csrc/sigmoid_mul_op.cpp:10, .cu:18-34),
+ *   swiglu_backward(gate, up, grad_out) -> [gg, gu] (csrc/swiglu_op.cpp:10, .cu:20-39),
+ *   gelu_tanh_backward(x, grad_out) (csrc/gelu_tanh_op.cpp:8, .cu:20-36).
+ * Softmax rows (rows, cols): gx = out * (dy - sum(out * dy)), replacing
+ *   softmax_backward(out, grad_out) (csrc/softmax_op.cpp:8, .cu:55-88). */
+int q3_sigmoid_mul_backward(const void* x, const void* gate, const void* grad_out, void* grad_x, void* grad_gate,
+                            int64_t n, int dtype, void* stream);
+int q3_swiglu_backward(const void* gate, const void* up, const void* grad_out, void* grad_gate, void* grad_up,
+                       int64_t n, int dtype, void* stream);
+int q3_gelu_tanh_backward(const void* x, const void* grad_out, void* grad_x, int64_t n, int dtype, void* stream);
+int q3_softmax_backward(const void* out, const void* grad_out, void* grad_x, int64_t rows, int64_t cols, int dtype,
+                        void* stream);
+
+/* RMSNorm / LayerNorm rows (rows, cols), contiguous. q3_rmsnorm_backward
+ * replaces rmsnorm_backward(x, weight, grad_out, eps) -> [gx, gw]
+ * (csrc/rmsnorm_op.cpp:11, csrc/rmsnorm_op.cu:63-130,158-186);
+ * q3_layernorm_backward has no CUDA counterpart (the reference differentiates
+ * F.layer_norm with torch autograd, kernels/layernorm.py:35-52). grad_weight /
+ * grad_bias may be null; when set, the call needs a workspace of
+ * q3_norm_backward_workspace_bytes(rows, cols) (per-block partial column sums,
+ * summed in block order). */
+int64_t q3_norm_backward_workspace_bytes(int64_t rows, int64_t cols);
+int q3_rmsnorm_backward(const void* x, const void* weight, const void* grad_out, void* grad_x, void* grad_weight,
+                        int64_t rows, int64_t cols, float eps, int dtype, void* workspace, int64_t workspace_bytes,
+                        void* stream);
+int q3_layernorm_backward(const void* x, const void* weight, const void* grad_out, void* grad_x, void* grad_weight,
+                          void* grad_bias, int64_t rows, int64_t cols, float eps, int dtype, void* workspace,
+                          int64_t workspace_bytes, void* stream);
+
+/* Cross entropy, replacing cross_entropy_backward(logits, targets, lse,
+ * grad_scale, ignore_index) (csrc/cross_entropy_op.cpp:12, .cu:66-116):
+ * grad = (exp(logits - lse) - onehot(target)) * (*grad_loss) / max(*n_valid, 1),
+ * zero rows for ignored targets; grad_loss (fp32) and n_valid (int32, from
+ * q3_cross_entropy) are read on the device. */
+int q3_cross_entropy_backward(const void* logits, const int64_t* targets, const float* lse, const float* grad_loss,
+                              const int* n_valid, void* grad_logits, int64_t N, int64_t V, int64_t ignore_index,
+                              int dtype, void* stream);
+
+/* Top-k: grad_x (rows, cols) = grad_vals (rows, k) scattered to idx (int64),
+ * zeros elsewhere (the reference's scatter_add_, kernels/moe_routing.py:44-52). */
+int q3_topk_backward(const void* grad_vals, const int64_t* idx, void* grad_x, int64_t rows, int64_t cols, int64_t k,
+                     int dtype, void* stream);
+
+/* (E, R, C) -> (E, C, R), contiguous (operand layouts of the GEMM backward). */
+int q3_transpose(const void* a, void* b, int64_t E, int64_t R, int64_t C, int dtype, void* stream);
+
+/* GEMM backward, replacing matmul_backward(x, weight, grad_out,
+ * needs_bias_grad) -> [gx, gw, gb] (csrc/matmul_op.cpp:13, .cu:151-233): for
+ * y = x . w^T (+ b) with x (M, K), w (N, K), dy (M, N), all contiguous:
+ * gx = dy . w (M, K), gw = dy^T . x (N, K), gb = sum over rows of dy (N); any of
+ * the three may be null. The operands are transposed into `workspace`
+ * (q3_matmul_backward_workspace_bytes) and multiplied by q3_matmul, which may
+ * use `gemm_ws` as q3_matmul's workspace (zero-filled before first use, as
+ * there; size at least q3_matmul_workspace_bytes of both products). */
+int64_t q3_matmul_backward_workspace_bytes(int64_t M, int64_t N, int64_t K, int dtype);
+int q3_matmul_backward(const void* x, const void* w, const void* dy, void* gx, void* gw, void* gb, int64_t M,
+                       int64_t N, int64_t K, int dtype, void* workspace, int64_t workspace_bytes, void* gemm_ws,
+                       int64_t gemm_ws_bytes, void* stream);
+
+/* Batched GEMM backward (the reference's _BatchedGemmFunction,
+ * kernels/moe_routing.py:146-181): for y[e] = x[e] . w[e]^T with x (E, M, K),
+ * w (E, N, K), dy (E, M, N): gx[e] = dy[e] . w[e], gw[e] = dy[e]^T . x[e];
+ * either may be null. */
+int64_t q3_batched_gemm_backward_workspace_bytes(int64_t E, int64_t M, int64_t N, int64_t K, int dtype);
+int q3_batched_gemm_backward(const void* x, const void* w, const void* dy, void* gx, void* gw, int64_t E, int64_t M,
+                             int64_t N, int64_t K, int dtype, void* workspace, int64_t workspace_bytes,
+                             void* stream);
+
+/* Flash-attention backward, replacing flash_attention_backward(q, k, v, o, lse,
+ * grad_o, scale, is_causal, num_kv_groups) -> [dq, dk, dv]
+ * (csrc/flash_attention_op.cpp:15, .cu:235-390): q, o, grad_out, grad_q
+ * (B, Hq, Sq, D), k, v, grad_k, grad_v (B, Hkv, Sk, D), all contiguous; lse
+ * (B, Hq, Sq) fp32 natural-log row log-sum-exp of the scaled scores (as
+ * q3_flash_attention writes it); D <= 128; causal masks key j > query i.
+ * Workspace: q3_flash_attention_backward_workspace_bytes (one fp32 per query
+ * row). */
+int64_t q3_flash_attention_backward_workspace_bytes(int64_t B, int64_t Hq, int64_t Sq);
+int q3_flash_attention_backward(const void* q, const void* k, const void* v, const void* o, const float* lse,
+                                const void* grad_out, void* grad_q, void* grad_k, void* grad_v, int64_t B, int64_t Hq,
+                                int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D, float scale, int is_causal,
+                                int dtype, void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

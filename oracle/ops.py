@@ -15,7 +15,7 @@ __all__ = [
     "linear", "batched_gemm", "conv3d_patch", "flash_attention", "decode_attention", "chunk_attention",
     "interleave_cos_sin", "rotate_half_apply", "mrope_inv_freq", "mrope_cos_sin",
     "apply_mrope", "apply_rope", "rmsnorm", "layernorm", "swiglu", "residual_add",
-    "gelu_tanh", "softmax", "topk", "index_add", "round_bf16",
+    "gelu_tanh", "softmax", "topk", "index_add", "round_bf16", "sigmoid_mul", "cross_entropy",
 ]
 
 
@@ -226,3 +226,26 @@ def index_add(target, source, index):
     """target[index[i]] += source[i] (in place, returns target). kernels/moe_routing.py:111-115."""
     target.index_add_(0, index, source)
     return target
+
+
+# ---------------------------------------------------------------- the rest of the op namespace
+
+def sigmoid_mul(x, gate):
+    """x·sigmoid(gate). kernels/sigmoid_mul.py:12-13."""
+    return x * torch.sigmoid(gate)
+
+
+def cross_entropy(logits, targets, ignore_index: int = -100):
+    """Mean over targets != ignore_index of logsumexp(row) − row[target].
+
+    kernels/cross_entropy.py:56-64 (the op's path): per-token losses
+    (csrc/cross_entropy_op.cu:10-62, 0 for an ignored target) summed and divided
+    by the valid count clamped to at least 1, so a batch with every target
+    ignored gives 0 where the fallback `F.cross_entropy` (:13-14) gives nan; the
+    two agree otherwise. Differentiable in logits.
+    """
+    valid = targets != ignore_index
+    safe = torch.where(valid, targets, torch.zeros_like(targets))
+    lse = torch.logsumexp(logits, dim=-1)
+    per_token = torch.where(valid, lse - logits.gather(-1, safe[:, None])[:, 0], torch.zeros_like(lse))
+    return per_token.sum() / valid.sum().clamp(min=1)

@@ -79,6 +79,26 @@ _SIGS: dict[str, tuple] = {
     "q3_moe_permute": (c_int, [_i32p, _V, _i32p, _i32p, _V, _i32p, _I, _I, _I, _V, _I, _V]),
     "q3_index_add_workspace_bytes": (c_int64, [_I, _I]),
     "q3_index_add": (c_int, [_V, _V, _V, _I, _I, _I, c_int, _V, _I, _i32p, _V]),
+    # the rest of the op namespace and the backward entry points (train.hip, attention_bwd.hip)
+    "q3_sigmoid_mul": (c_int, [_V, _V, _V, _I, c_int, _V]),
+    "q3_sigmoid_mul_backward": (c_int, [_V, _V, _V, _V, _V, _I, c_int, _V]),
+    "q3_swiglu_backward": (c_int, [_V, _V, _V, _V, _V, _I, c_int, _V]),
+    "q3_gelu_tanh_backward": (c_int, [_V, _V, _V, _I, c_int, _V]),
+    "q3_softmax_backward": (c_int, [_V, _V, _V, _I, _I, c_int, _V]),
+    "q3_norm_backward_workspace_bytes": (c_int64, [_I, _I]),
+    "q3_rmsnorm_backward": (c_int, [_V, _V, _V, _V, _V, _I, _I, c_float, c_int, _V, _I, _V]),
+    "q3_layernorm_backward": (c_int, [_V, _V, _V, _V, _V, _V, _I, _I, c_float, c_int, _V, _I, _V]),
+    "q3_cross_entropy": (c_int, [_V, _V, _f32p, _f32p, _f32p, _i32p, _I, _I, _I, c_int, _i32p, _V]),
+    "q3_cross_entropy_backward": (c_int, [_V, _V, _f32p, _f32p, _i32p, _V, _I, _I, _I, c_int, _V]),
+    "q3_topk_backward": (c_int, [_V, _V, _V, _I, _I, _I, c_int, _V]),
+    "q3_transpose": (c_int, [_V, _V, _I, _I, _I, c_int, _V]),
+    "q3_matmul_backward_workspace_bytes": (c_int64, [_I, _I, _I, c_int]),
+    "q3_matmul_backward": (c_int, [_V, _V, _V, _V, _V, _V, _I, _I, _I, c_int, _V, _I, _V, _I, _V]),
+    "q3_batched_gemm_backward_workspace_bytes": (c_int64, [_I, _I, _I, _I, c_int]),
+    "q3_batched_gemm_backward": (c_int, [_V, _V, _V, _V, _V, _I, _I, _I, _I, c_int, _V, _I, _V]),
+    "q3_flash_attention_backward_workspace_bytes": (c_int64, [_I, _I, _I]),
+    "q3_flash_attention_backward": (c_int, [_V, _V, _V, _V, _f32p, _V, _V, _V, _V, _I, _I, _I, _I, _I, _I, c_float,
+                                            c_int, c_int, _V, _I, _V]),
 }
 
 EXPORTED = tuple(_SIGS)

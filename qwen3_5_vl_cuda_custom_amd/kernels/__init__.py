@@ -1,8 +1,10 @@
 """Functional ops with the reference's names and signatures (reference kernels/__init__.py:1-45),
-each backed by a hand-written gfx950 HIP kernel of libq3vl.so. GPU tensors only; no fallback."""
+each backed by a hand-written gfx950 HIP kernel of libq3vl.so. GPU tensors only; no fallback.
+The ops the reference wraps in torch.autograd.Function are differentiable here too (kernels/backward.py)."""
 from ._loader import FALLBACK_LOG, record_fallback, strict_mode, summarize_fallbacks
 from .conv3d_patch import conv3d_patch
-from .elementwise import gelu_tanh, residual_add, swiglu
+from .cross_entropy import cross_entropy
+from .elementwise import gelu_tanh, residual_add, sigmoid_mul, swiglu
 from .embedding import embedding
 from .flash_attention import (decode_attention, decode_attention_paged, flash_attention, flash_attention_cache,
                               flash_attention_varlen, qk_norm_rope_attention, qk_norm_rope_attention_ok)
@@ -22,6 +24,7 @@ __all__ = [
     "apply_mrope",
     "apply_rope",
     "conv3d_patch",
+    "cross_entropy",
     "cuda_batched_gemm",
     "cuda_index_add",
     "cuda_topk",
@@ -32,6 +35,7 @@ __all__ = [
     "matmul",
     "residual_add",
     "rmsnorm",
+    "sigmoid_mul",
     "softmax",
     "swiglu",
     # additions beyond the reference API (fused / decode / MoE dispatch paths)

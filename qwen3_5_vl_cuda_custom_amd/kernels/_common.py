@@ -12,8 +12,9 @@ def require_device(op: str, *tensors: torch.Tensor | None) -> None:
 
 def require_no_grad(op: str, *tensors: torch.Tensor | None) -> None:
     if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
-        raise NotImplementedError(f"{op}: backward is not implemented (forward/inference only); "
-                                  "run under torch.no_grad() or torch.inference_mode()")
+        raise NotImplementedError(f"{op}: this fused / decode op has no backward; the reference's differentiable "
+                                  "ops (matmul, flash_attention, rmsnorm, ... see kernels.backward) have one, or "
+                                  "run under torch.no_grad() / torch.inference_mode()")
 
 
 def require_same_dtype(op: str, ref: torch.Tensor, *tensors: torch.Tensor | None) -> None:
@@ -31,3 +32,41 @@ def check(op: str, *tensors: torch.Tensor | None) -> None:
 
 def last_dim_contiguous(t: torch.Tensor) -> torch.Tensor:
     return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def _strict() -> bool:
+    from ._loader import strict_mode
+    return strict_mode()
+
+
+def note_slow_path(op: str, reason: str) -> None:
+    """A bf16 call that runs a SIMT kernel instead of the MFMA one (the layout or
+    shape rules it out and no copy helps): recorded in FALLBACK_LOG, or raised
+    under CUDA_QWEN3_VL_STRICT=1, like the reference's fallbacks."""
+    from ._loader import record_fallback
+    if _strict():
+        raise RuntimeError(f"{op}: {reason} (strict mode: the MFMA kernel cannot take this call)")
+    record_fallback(op, f"simt_kernel: {reason}")
+
+
+def mfma_operand(op: str, t: torch.Tensor, rows_from: int = 1) -> torch.Tensor:
+    """`t` as the MFMA kernels read it: a 16-byte aligned base and strides in
+    multiples of 8 elements on every dim but the last (contiguous) one, from
+    dim `rows_from` - 1 on. bf16 views that miss it are copied into a fresh
+    contiguous buffer (the allocator aligns it) and the copy is recorded in
+    FALLBACK_LOG as `aligned_copy` (raised under strict mode); the kernel then
+    runs on the copy instead of dropping to its SIMT form. Other dtypes pass
+    through."""
+    if t.dtype != torch.bfloat16:
+        return t
+    if (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
+            and all(t.stride(i) % 8 == 0 for i in range(max(0, rows_from - 1), t.dim() - 1))):
+        return t
+    if t.shape[-1] % 8:
+        return t  # a copy keeps the rows misaligned: the caller reports the SIMT path
+    from ._loader import record_fallback
+    if _strict():
+        raise RuntimeError(f"{op}: a bf16 operand is not 16-byte aligned with strides in multiples of 8 "
+                           "(strict mode: no aligned copy)")
+    record_fallback(op, "aligned_copy")
+    return t.contiguous() if not t.is_contiguous() else t.clone()

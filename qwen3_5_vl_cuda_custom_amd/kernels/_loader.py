@@ -1,10 +1,12 @@
-"""API-compatible fallback registry (reference: kernels/_loader.py:29-33, 161-269).
+"""Fallback registry with the reference's names (reference: kernels/_loader.py:29-33, 161-269).
 
 The reference records every CUDA->torch fallback in `FALLBACK_LOG` and can be
-made strict with CUDA_QWEN3_VL_STRICT=1. This implementation has no fallback
-path at all: an op whose kernel cannot run raises. The names stay importable
-so code written against the reference keeps working; `FALLBACK_LOG` only ever
-holds entries added through `record_fallback` by callers.
+made strict with CUDA_QWEN3_VL_STRICT=1. This implementation has no torch or
+CPU fallback: an op whose kernel cannot run raises. What it records instead are
+the slower device paths a call can take: `aligned_copy` (a bf16 operand that
+misses the MFMA kernels' 16-byte alignment, copied into an aligned buffer
+first) and `simt_kernel: ...` (a bf16 call whose shape or layout only the SIMT
+kernel takes). Under CUDA_QWEN3_VL_STRICT=1 those raise.
 """
 from __future__ import annotations
 
@@ -16,11 +18,11 @@ _TAG = "[QWEN3-VL-HIP]"
 
 
 def summarize_fallbacks() -> None:
-    """Print the (caller-recorded) fallback events; the kernels themselves never fall back."""
+    """Print the recorded slow-path events (aligned copies, SIMT kernels)."""
     if not FALLBACK_LOG:
-        print(f"{_TAG} no fallbacks recorded — every op ran its HIP kernel.", file=sys.stderr)
+        print(f"{_TAG} no fallbacks recorded — every op ran its MFMA / vector HIP kernel.", file=sys.stderr)
         return
-    print(f"{_TAG} {len(FALLBACK_LOG)} caller-recorded fallback event(s):", file=sys.stderr)
+    print(f"{_TAG} {len(FALLBACK_LOG)} fallback event(s):", file=sys.stderr)
     for op, reason, exc in FALLBACK_LOG:
         print(f"  {op}: {reason} {exc}", file=sys.stderr)
 
@@ -30,7 +32,7 @@ def record_fallback(op_name: str, reason: str = "not_implemented") -> None:
 
 
 def strict_mode() -> bool:
-    """Reference env switch; the HIP ops always behave strictly (they raise)."""
+    """Reference env switch: slow device paths raise instead of being recorded."""
     return os.environ.get("CUDA_QWEN3_VL_STRICT") == "1"
 
 

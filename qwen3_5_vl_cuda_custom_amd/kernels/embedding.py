@@ -5,6 +5,7 @@ import torch
 
 from .. import _lib
 from ._common import check
+from .backward import EmbeddingFunction, needs_grad
 
 
 def embedding(ids: torch.Tensor, weight: torch.Tensor, padding_idx: int | None = None) -> torch.Tensor:
@@ -15,6 +16,8 @@ def embedding(ids: torch.Tensor, weight: torch.Tensor, padding_idx: int | None =
     zero rows and are recorded on the device (kernels.raise_device_errors),
     without synchronising with the host.
     """
+    if needs_grad(weight):
+        return EmbeddingFunction.apply(ids, weight, padding_idx)
     check("embedding", weight)
     if not ids.is_cuda:
         raise RuntimeError("embedding: ids must be on the GPU")

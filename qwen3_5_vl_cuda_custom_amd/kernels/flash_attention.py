@@ -4,7 +4,23 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
-from ._common import check
+from ._common import check, mfma_operand, note_slow_path
+from .backward import FlashAttentionFunction, needs_grad
+
+
+MFMA_HEAD_DIMS = (64, 72, 80, 96, 128)
+
+
+def _attn_operands(op: str, D: int, o: torch.Tensor | None, *ts):
+    """q/k/v as the MFMA attention kernels read them (aligned copies where needed);
+    calls that only the SIMT kernel takes are reported."""
+    out = [mfma_operand(op, t) for t in ts]
+    if ts[0].dtype == torch.bfloat16:
+        if D not in MFMA_HEAD_DIMS:
+            note_slow_path(op, f"head_dim {D} (the MFMA kernels take {MFMA_HEAD_DIMS})")
+        elif o is not None and (o.data_ptr() % 8 or any(o.stride(i) % 8 for i in range(o.dim() - 1))):
+            note_slow_path(op, "the output view is not 8-byte aligned with strides in multiples of 8")
+    return out
 
 
 def _s4(t: torch.Tensor):
@@ -20,8 +36,26 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: fl
     the head dim is contiguous (no copies). Causal masks key j > query i.
     `out`, when given, is a (B, Hq, Sq, D) view written in place.
     """
+    if needs_grad(q, k, v):
+        if out is not None:
+            raise ValueError("flash_attention: out= is not supported when autograd records the op")
+        return FlashAttentionFunction.apply(q, k, v, scale, is_causal, num_kv_groups)
+    return _flash_fwd(q, k, v, scale, is_causal, num_kv_groups, out, None)
+
+
+def flash_attention_lse(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, is_causal: bool = True,
+                        num_kv_groups: int = 1) -> tuple[torch.Tensor, torch.Tensor]:
+    """flash_attention that also returns the row log-sum-exp of the scaled scores, lse (B, Hq, Sq) fp32
+    (the forward schema's second output, csrc/flash_attention_op.cpp:14), which the backward reads."""
+    B, Hq, Sq = q.shape[:3]
+    lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=q.device)
+    return _flash_fwd(q, k, v, scale, is_causal, num_kv_groups, None, lse), lse
+
+
+def _flash_fwd(q, k, v, scale, is_causal, num_kv_groups, out, lse):
     check("flash_attention", q, k, v)
     q, k, v = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
+    q, k, v = _attn_operands("flash_attention", q.shape[-1], out, q, k, v)
     B, Hq, Sq, D = q.shape
     Hkv, Sk = k.shape[1], k.shape[2]
     if k.shape != v.shape or k.shape[0] != B or k.shape[3] != D:
@@ -31,18 +65,29 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: fl
     o = out if out is not None else torch.empty((B, Hq, Sq, D), dtype=q.dtype, device=q.device)
     if o.shape != (B, Hq, Sq, D) or o.stride(-1) != 1:
         raise ValueError("flash_attention: out must be (B, Hq, Sq, D) with a contiguous head dim")
-    _lib.call("q3_flash_attention", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), None, B, Hq, Hkv, Sq,
+    _lib.call("q3_flash_attention", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), _lib.ptr(lse), B, Hq, Hkv, Sq,
               Sk, D, _lib.i64s(*_s4(q), *_s4(k), *_s4(v), *_s4(o)), float(scale), int(bool(is_causal)),
               _lib.dtype_code(q.dtype), _lib.stream())
     return o
 
 
-def qk_norm_rope_attention_ok(q: torch.Tensor, k: torch.Tensor, num_kv_groups: int) -> bool:
+def qk_norm_rope_attention_ok(q: torch.Tensor, k: torch.Tensor, num_kv_groups: int,
+                              v: torch.Tensor | None = None) -> bool:
     """Whether qk_norm_rope_attention covers these (B, S, H, D) views (else use
-    qk_norm_rope followed by flash_attention)."""
-    D = q.shape[-1]
-    return (q.is_cuda and q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16 and D in (64, 128)
-            and num_kv_groups % 4 == 0 and q.shape[1] > 0)
+    qk_norm_rope followed by flash_attention). Mirrors every check of the C
+    entry point (q3_qk_norm_rope_attention): bf16, D in (64, 128), GQA groups
+    a multiple of 4, 16-byte aligned base pointers, batch / head / sequence
+    strides that are multiples of 8 elements, a contiguous head dim, and 32-bit
+    offsets within a KV head's rows ((S + 1) * seq stride * 2 < 2^31)."""
+    B, S, _, D = q.shape
+    ts = (q, k) if v is None else (q, k, v)
+    if not (q.is_cuda and all(t.dtype == torch.bfloat16 for t in ts) and D in (64, 128)
+            and num_kv_groups % 4 == 0 and S > 0 and B * S < 2 ** 31):
+        return False
+    for t in ts:
+        if t.data_ptr() % 16 or t.stride(-1) != 1 or any(t.stride(i) % 8 for i in range(3)):
+            return False
+    return (S + 1) * k.stride(1) * 2 < 2 ** 31
 
 
 def qk_norm_rope_attention(q_in: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_weight: torch.Tensor,
@@ -64,8 +109,9 @@ def qk_norm_rope_attention(q_in: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     Hkv = k.shape[2]
     if k.shape != v.shape or tuple(k.shape[:2]) != (B, S) or k.shape[3] != D or Hq % Hkv:
         raise ValueError(f"qk_norm_rope_attention: q {tuple(q_in.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}")
-    if not qk_norm_rope_attention_ok(q_in, k, Hq // Hkv):
-        raise ValueError("qk_norm_rope_attention: bf16, D in (64, 128) and GQA groups a multiple of 4 only")
+    if not qk_norm_rope_attention_ok(q_in, k, Hq // Hkv, v):
+        raise ValueError("qk_norm_rope_attention: bf16, D in (64, 128), GQA groups a multiple of 4, 16-byte "
+                         "aligned views with strides in multiples of 8 only")
     if (positions.dtype != torch.int32 or not positions.is_cuda or tuple(positions.shape) != (3, B, S)
             or not positions.is_contiguous()):
         raise ValueError(f"qk_norm_rope_attention: positions must be a contiguous int32 (3, {B}, {S}) device tensor")
@@ -189,6 +235,10 @@ def flash_attention_cache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch
     check("flash_attention_cache", q, k_cache, v_cache)
     if q.stride(-1) != 1:
         q = q.contiguous()
+    (q,) = _attn_operands("flash_attention_cache", q.shape[-1], out, q)
+    if q.dtype == torch.bfloat16 and any(t.data_ptr() % 16 or any(t.stride(i) % 8 for i in range(3))
+                                         for t in (k_cache, v_cache)):
+        note_slow_path("flash_attention_cache", "the caches are not 16-byte aligned with strides in multiples of 8")
     B, Hq, Sq, D = q.shape
     Hkv, cap = k_cache.shape[1], k_cache.shape[2]
     if k_cache.shape != v_cache.shape or k_cache.shape[0] != B or k_cache.shape[3] != D:
@@ -221,6 +271,7 @@ def flash_attention_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu
     """
     check("flash_attention_varlen", q, k, v)
     q, k, v = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
+    q, k, v = _attn_operands("flash_attention_varlen", q.shape[-1], out, q, k, v)
     Hq, total, D = q.shape
     Hkv = k.shape[0]
     if k.shape != v.shape or k.shape[1] != total or k.shape[2] != D or Hkv * num_kv_groups != Hq:

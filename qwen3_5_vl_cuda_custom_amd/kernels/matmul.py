@@ -4,7 +4,17 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
-from ._common import check
+from ._common import check, mfma_operand, note_slow_path
+from .backward import MatmulFunction, needs_grad
+
+
+def _gemm_rows(op: str, K: int, *ts):
+    """The row operands as the MFMA GEMM reads them (aligned copies where needed); a bf16 K that is not a
+    multiple of 8 leaves only the SIMT kernel, which is reported."""
+    out = [mfma_operand(op, t) for t in ts]
+    if ts[0].dtype == torch.bfloat16 and K % 8:
+        note_slow_path(op, f"K={K} is not a multiple of 8")
+    return out
 
 
 def matmul(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None, *,
@@ -12,8 +22,13 @@ def matmul(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
     """nn.Linear semantics: x (..., K), weight (N, K), bias (N) -> (..., N).
 
     `residual` (same shape as the output) is added in the GEMM epilogue before
-    the single rounding (fuses the following residual_add).
+    the single rounding (fuses the following residual_add). Differentiable
+    (x, weight, bias, residual) when grad mode records it.
     """
+    if needs_grad(x, weight, bias, residual):
+        if out is not None:
+            raise ValueError("matmul: out= is not supported when autograd records the op")
+        return MatmulFunction.apply(x, weight, bias, residual)
     check("matmul", x, weight, bias, residual)
     K = x.shape[-1]
     N = weight.shape[0]
@@ -25,6 +40,7 @@ def matmul(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
     if x2.stride(-1) != 1:
         x2 = x2.contiguous()
     w = weight if weight.stride(-1) == 1 else weight.contiguous()
+    x2, w = _gemm_rows("matmul", K, x2, w)
     M = x2.shape[0]
     out_shape = (*x.shape[:-1], N)
     y = out if out is not None else torch.empty(out_shape, dtype=x.dtype, device=x.device)
@@ -59,6 +75,7 @@ def matmul_gelu(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None
     if x2.stride(-1) != 1:
         x2 = x2.contiguous()
     w = weight if weight.stride(-1) == 1 else weight.contiguous()
+    x2, w = _gemm_rows("matmul_gelu", K, x2, w)
     y = torch.empty((*x.shape[:-1], N), dtype=x.dtype, device=x.device)
     b = bias.contiguous() if bias is not None else None
     _lib.call("q3_matmul_gelu", x2.data_ptr(), w.data_ptr(), _lib.ptr(b), y.data_ptr(), x2.shape[0], N, K,
@@ -76,7 +93,7 @@ def matmul_swiglu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor) -> 
     x2 = x.reshape(-1, K)
     if x2.stride(-1) != 1:
         x2 = x2.contiguous()
-    wg, wu = w_gate.contiguous(), w_up.contiguous()
+    x2, wg, wu = _gemm_rows("matmul_swiglu", K, x2, w_gate.contiguous(), w_up.contiguous())
     M = x2.shape[0]
     y = torch.empty((*x.shape[:-1], N), dtype=x.dtype, device=x.device)
     dt = _lib.dtype_code(x.dtype)
@@ -111,6 +128,7 @@ def matmul_segments(x: torch.Tensor, weights, biases=None, *, out: torch.Tensor 
     x2 = x.reshape(-1, K)
     if x2.stride(-1) != 1:
         x2 = x2.contiguous()
+    x2, *ws_ = _gemm_rows("matmul_segments", K, x2, *ws_)
     M = x2.shape[0]
     y = out if out is not None else torch.empty((*x.shape[:-1], N), dtype=x.dtype, device=x.device)
     y2 = y.view(-1, N)
@@ -138,7 +156,7 @@ def _norm_args(name: str, x: torch.Tensor, norm_weight: torch.Tensor, K: int):
         x2 = x2.contiguous()
     if x2.shape[0] > RMSNORM_MATMUL_MAX_ROWS:
         raise ValueError(f"{name}: at most {RMSNORM_MATMUL_MAX_ROWS} rows (decode shapes)")
-    return x2, norm_weight.contiguous()
+    return mfma_operand(name, x2), mfma_operand(name, norm_weight.contiguous())
 
 
 def rmsnorm_matmul_segments(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, weights,
@@ -155,7 +173,8 @@ def rmsnorm_matmul_segments(x: torch.Tensor, norm_weight: torch.Tensor, eps: flo
     check("rmsnorm_matmul_segments", x, norm_weight, *weights, *biases)
     K = x.shape[-1]
     x2, nw = _norm_args("rmsnorm_matmul_segments", x, norm_weight, K)
-    ws_ = [w if w.stride(-1) == 1 and w.stride(0) == K else w.contiguous() for w in weights]
+    ws_ = [mfma_operand("rmsnorm_matmul_segments", w if w.stride(-1) == 1 and w.stride(0) == K else w.contiguous())
+           for w in weights]
     for w, b in zip(ws_, biases):
         if w.dim() != 2 or w.shape[1] != K:
             raise ValueError(f"rmsnorm_matmul_segments: weight {tuple(w.shape)} does not match x (..., {K})")
@@ -182,7 +201,7 @@ def rmsnorm_matmul_swiglu(x: torch.Tensor, norm_weight: torch.Tensor, eps: float
     if w_gate.shape != w_up.shape or w_gate.shape[1] != K:
         raise ValueError("rmsnorm_matmul_swiglu: gate/up weights must both be (N, K)")
     x2, nw = _norm_args("rmsnorm_matmul_swiglu", x, norm_weight, K)
-    wg, wu = w_gate.contiguous(), w_up.contiguous()
+    wg, wu = (mfma_operand("rmsnorm_matmul_swiglu", w.contiguous()) for w in (w_gate, w_up))
     M = x2.shape[0]
     y = torch.empty((*x.shape[:-1], N), dtype=x.dtype, device=x.device)
     _lib.call("q3_rmsnorm_matmul_swiglu", x2.data_ptr(), nw.data_ptr(), float(eps), wg.data_ptr(), wu.data_ptr(),

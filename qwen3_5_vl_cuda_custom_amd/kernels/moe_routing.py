@@ -5,11 +5,14 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
-from ._common import check
+from ._common import check, mfma_operand, note_slow_path
+from .backward import BatchedGemmFunction, IndexAddFunction, TopKFunction, needs_grad
 
 
 def cuda_topk(x: torch.Tensor, k: int) -> tuple[torch.Tensor, torch.Tensor]:
     """Top-k over the last dim: (values in x dtype, int64 indices); equal values go to the lower index."""
+    if needs_grad(x):
+        return TopKFunction.apply(x, k)
     check("cuda_topk", x)
     cols = x.shape[-1]
     if not 1 <= k <= cols:
@@ -30,8 +33,12 @@ def cuda_index_add(target: torch.Tensor, source: torch.Tensor, index: torch.Tens
     starting from its own value, and rounds once (torch's index_add_
     semantics). Indices must lie in [0, target.shape[0]): the kernel skips any
     other and records it on the device (see raise_device_errors); the call
-    itself never synchronises with the host.
+    itself never synchronises with the host. When autograd records the op it
+    returns a new tensor (target + the scattered sources), as the reference's
+    autograd form does.
     """
+    if needs_grad(target, source):
+        return IndexAddFunction.apply(target, source, index)
     check("cuda_index_add", target, source)
     if index.dim() != 1 or index.shape[0] != source.shape[0] or not index.is_cuda:
         raise ValueError("cuda_index_add: index must be a 1-D device tensor with one entry per source row")
@@ -66,12 +73,16 @@ def raise_device_errors(device=None) -> None:
 
 def cuda_batched_gemm(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     """Y[e] = X[e]·W[e]ᵀ: x (E, M, K), w (E, N, K) -> (E, M, N)."""
+    if needs_grad(x, w):
+        return BatchedGemmFunction.apply(x, w)
     check("cuda_batched_gemm", x, w)
     if x.dim() != 3 or w.dim() != 3 or x.shape[0] != w.shape[0] or x.shape[2] != w.shape[2]:
         raise ValueError(f"cuda_batched_gemm: x {tuple(x.shape)} and w {tuple(w.shape)} mismatch")
     E, M, K = x.shape
     N = w.shape[1]
-    x, w = x.contiguous(), w.contiguous()
+    x, w = (mfma_operand("cuda_batched_gemm", t.contiguous()) for t in (x, w))
+    if x.dtype == torch.bfloat16 and K % 8:
+        note_slow_path("cuda_batched_gemm", f"K={K} is not a multiple of 8")
     y = torch.empty((E, M, N), dtype=x.dtype, device=x.device)
     _lib.call("q3_batched_gemm", x.data_ptr(), w.data_ptr(), y.data_ptr(), E, M, N, K, _lib.dtype_code(x.dtype),
               _lib.stream())

@@ -6,10 +6,13 @@ import torch
 
 from .. import _lib
 from ._common import check
+from .backward import LayerNormFunction, RMSNormFunction, SoftmaxFunction, needs_grad
 
 
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     """x·rsqrt(mean(x²)+eps)·w over the last dim, fp32 inside, rounded once."""
+    if needs_grad(x, weight):
+        return RMSNormFunction.apply(x, weight, eps)
     check("rmsnorm", x, weight)
     cols = x.shape[-1]
     if weight.shape != (cols,):
@@ -24,6 +27,8 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.T
 def layernorm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
               eps: float = 1e-6) -> torch.Tensor:
     """(x−μ)·rsqrt(var+eps)·w + b over the last dim (two-pass statistics in registers)."""
+    if needs_grad(x, weight, bias):
+        return LayerNormFunction.apply(x, weight, bias, eps)
     check("layernorm", x, weight, bias)
     cols = x.shape[-1]
     if weight.shape != (cols,) or (bias is not None and bias.shape != (cols,)):
@@ -38,6 +43,8 @@ def layernorm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None =
 
 def softmax(x: torch.Tensor) -> torch.Tensor:
     """Row softmax over the last dim."""
+    if needs_grad(x):
+        return SoftmaxFunction.apply(x)
     check("softmax", x)
     cols = x.shape[-1]
     x = x.contiguous()

@@ -6,6 +6,7 @@ import torch
 
 from .. import _lib
 from ._common import check
+from .backward import MRopeFunction, RopeFunction, needs_grad
 
 
 def _bhsd_strides(t: torch.Tensor):
@@ -22,6 +23,8 @@ def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.T
     cos/sin are read in their own dtype (fp32 or x dtype); a batch of 1 is
     broadcast over B. Dims beyond D_rope pass through.
     """
+    if needs_grad(x):
+        return RopeFunction.apply(x, cos, sin)
     check("apply_rope", x)
     if not cos.is_cuda or not sin.is_cuda:
         raise RuntimeError("apply_rope: cos/sin must be on the GPU")
@@ -52,6 +55,8 @@ def apply_mrope(x: torch.Tensor, cos_3d: torch.Tensor, sin_3d: torch.Tensor, mro
     Element i < D_rope/2 takes axis 0 for i < s0, axis 1 for i < s0+s1, else
     axis 2 (kernels/mrope.py:19-35), read straight from the 3-axis tables.
     """
+    if needs_grad(x):
+        return MRopeFunction.apply(x, cos_3d, sin_3d, mrope_section)
     check("apply_mrope", x)
     if x.stride(-1) != 1:
         x = x.contiguous()

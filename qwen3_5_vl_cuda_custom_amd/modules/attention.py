@@ -4,6 +4,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
+from ..kernels.backward import needs_grad
 from ..kernels import (apply_rope, decode_attention, decode_attention_paged, flash_attention, flash_attention_cache,
                        flash_attention_varlen, matmul_segments, qk_norm_rope, qk_norm_rope_attention,
                        qk_norm_rope_attention_ok, qk_norm_rope_paged, rmsnorm_matmul_segments)
@@ -35,6 +36,16 @@ class CudaVisionAttention(nn.Module):
         """
         B, S, h = x.shape
         H, D = self.num_heads, self.head_dim
+        if needs_grad(x, residual, *self.parameters()):
+            # training: the reference composition (modules/attention.py:34-42) on the differentiable ops
+            if cu_seqlens is not None:
+                raise NotImplementedError("CudaVisionAttention: packed images (cu_seqlens) have no backward; "
+                                          "put the images on the batch dim to train")
+            qkv = self.qkv(x).reshape(B, S, 3, H, D)
+            q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
+            q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
+            o = flash_attention(q, k, v, scale=self.scale, is_causal=False, num_kv_groups=1)
+            return self.proj(o.transpose(1, 2).reshape(B, S, h), residual=residual)
         qkv = self.qkv(x).view(B, S, 3, H, D)
         # q and k rotated by one launch: their 2H heads are one strided (B, 2H, S, D) view
         qk = apply_rope(qkv[:, :, :2].reshape(B, S, 2 * H, D).transpose(1, 2), cos, sin)
@@ -103,6 +114,8 @@ class CudaFullAttention(nn.Module):
                 input_norm: CudaRMSNorm | None = None):
         B, S, _ = x.shape
         Hq, Hkv, D = self.num_heads, self.num_kv_heads, self.head_dim
+        if needs_grad(x, residual, *self.parameters()):
+            return self._forward_autograd(x, mrope_apply, past_kv, kv_cache, residual, input_norm)
         # q/k/v projections in one GEMM over the three weights (no concatenated
         # copy); q, k, v are column views of its output.
         weights = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight)
@@ -127,6 +140,8 @@ class CudaFullAttention(nn.Module):
                 raise ValueError(f"kv_cache holds {kv_cache.batch} sequences, the input has {B}")
             rope = mrope_apply.rope
             pos = mrope_apply.positions_int32(x.device, B, S)
+            if isinstance(kv_cache, PagedKVCache):
+                kv_cache.check_kernels(self.num_kv_groups)
             kv_cache.reserve(S)  # raises, before any launch, if a sequence would overflow the cache
             if isinstance(kv_cache, PagedKVCache):
                 return self._forward_paged(q, k, v, o, pos, rope, kv_cache, residual)
@@ -150,7 +165,7 @@ class CudaFullAttention(nn.Module):
             rope = mrope_apply.rope
             pos = mrope_apply.positions_int32(x.device, B, S)
             if (past_kv is None and self.q_norm.weight.dtype == q.dtype
-                    and qk_norm_rope_attention_ok(q, k, self.num_kv_groups)):
+                    and qk_norm_rope_attention_ok(q, k, self.num_kv_groups, v)):
                 # k normalised and rotated in place; q inside the attention kernel
                 qk_norm_rope_attention(q, k, v, self.q_norm.weight, self.k_norm.weight, pos, rope.inv_freq,
                                        rope.mrope_section, self.q_norm.eps, self.scale, True, out=o)
@@ -170,6 +185,27 @@ class CudaFullAttention(nn.Module):
         flash_attention(qh, kh, vh, scale=self.scale, is_causal=is_causal, num_kv_groups=self.num_kv_groups,
                         out=o.transpose(1, 2))
         return self.o_proj(o.view(B, S, Hq * D), residual=residual), (kh, vh)
+
+    def _forward_autograd(self, x, mrope_apply, past_kv, kv_cache, residual, input_norm):
+        """Training: the reference composition (modules/attention.py:75-98) on the differentiable ops
+        (projections, q/k RMSNorm, mRoPE, attention and o_proj each with its own backward)."""
+        if kv_cache is not None:
+            raise NotImplementedError("CudaFullAttention: kv_cache decoding has no backward; run it under "
+                                      "torch.no_grad() or torch.inference_mode()")
+        B, S, _ = x.shape
+        Hq, Hkv, D = self.num_heads, self.num_kv_heads, self.head_dim
+        if input_norm is not None:
+            x = input_norm(x)
+        q = self.q_norm(self.q_proj(x).view(B, S, Hq, D)).transpose(1, 2)
+        k = self.k_norm(self.k_proj(x).view(B, S, Hkv, D)).transpose(1, 2)
+        v = self.v_proj(x).view(B, S, Hkv, D).transpose(1, 2)
+        q, k = mrope_apply(q, k)
+        if past_kv is not None:
+            k = torch.cat([past_kv[0], k], dim=2)
+            v = torch.cat([past_kv[1], v], dim=2)
+        o = flash_attention(q, k, v, scale=self.scale, is_causal=q.shape[2] == k.shape[2],
+                            num_kv_groups=self.num_kv_groups)
+        return self.o_proj(o.transpose(1, 2).reshape(B, S, Hq * D), residual=residual), (k, v)
 
     def _forward_paged(self, q, k, v, o, pos, rope, kv_cache: PagedKVCache, residual):
         B, S, Hq, D = q.shape

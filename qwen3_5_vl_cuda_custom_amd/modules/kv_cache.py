@@ -73,6 +73,10 @@ class StaticKVCache:
         self.min_len, self.max_len = state
 
 
+PAGED_MAX_BATCH = 1024  # the paged decode kernel's batch bound
+PAGED_MAX_GROUPS = 32  # query heads per KV head in the paged decode kernel
+
+
 class PagedKVCache:
     """KV cache in fixed-size pages with a per-sequence block table (no reference
     counterpart: the paged form of the decode loop's preallocated cache).
@@ -113,6 +117,17 @@ class PagedKVCache:
     @property
     def batch(self) -> int:
         return self.block_table.shape[0]
+
+    def check_kernels(self, num_kv_groups: int) -> None:
+        """Raise unless the paged kernels (q3_qk_norm_rope_paged, q3_decode_attention_paged) take this
+        cache: bf16 rows of head_dim 128, at most PAGED_MAX_BATCH sequences and PAGED_MAX_GROUPS query
+        heads per KV head. Checked before a step changes any state (lengths, pages, cache rows)."""
+        D = self.k_pages.shape[-1]
+        if (self.k_pages.dtype != torch.bfloat16 or D != 128 or self.batch > PAGED_MAX_BATCH
+                or not 1 <= num_kv_groups <= PAGED_MAX_GROUPS):
+            raise ValueError(f"PagedKVCache: the paged kernels take bf16, head_dim 128, at most {PAGED_MAX_BATCH} "
+                             f"sequences and {PAGED_MAX_GROUPS} query heads per KV head (got "
+                             f"{self.k_pages.dtype}, head_dim {D}, batch {self.batch}, groups {num_kv_groups})")
 
     @property
     def capacity(self) -> int:

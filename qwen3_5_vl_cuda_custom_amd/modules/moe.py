@@ -6,6 +6,7 @@ from torch import nn
 
 from ..kernels import (cuda_index_add, cuda_topk, matmul, moe_experts, moe_route, moe_router, residual_add, softmax,
                        swiglu)
+from ..kernels.backward import needs_grad
 
 
 class CudaSparseMoE(nn.Module):
@@ -50,6 +51,8 @@ class CudaSparseMoE(nn.Module):
         return logits, idx, vals.to(x_flat.dtype)
 
     def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None):
+        if needs_grad(x, residual, *self.parameters()):
+            return self._forward_autograd(x, residual)
         B, S, H = x.shape
         x_flat = x.reshape(-1, H)
         logits, idx, w = self.route(x_flat)
@@ -71,4 +74,29 @@ class CudaSparseMoE(nn.Module):
             cuda_index_add(final, (eo * w[token_idx, slot_idx, None]).to(x.dtype), token_idx)
         if r_flat is not None:
             final = residual_add(final, r_flat)
+        return final.view(B, S, H), logits
+
+    def _forward_autograd(self, x: torch.Tensor, residual: torch.Tensor | None):
+        """Training: the reference's forward (modules/moe.py:54-85) on the differentiable ops: router
+        GEMM, softmax of the fp32 logits, top-k, renormalise and cast, then per expert its tokens'
+        gate_up GEMM, swiglu, down GEMM, the routing-weight product and the autograd form of
+        index_add (a new tensor per expert)."""
+        B, S, H = x.shape
+        x_flat = x.reshape(-1, H)
+        logits = matmul(x_flat, self.gate_weight)
+        vals, idx = cuda_topk(softmax(logits.float()), self.top_k)
+        if self.norm_topk_prob:
+            vals = vals / vals.sum(dim=-1, keepdim=True)
+        vals = vals.to(x.dtype)
+        final = torch.zeros_like(x_flat)
+        I = self.moe_intermediate_size
+        for e in range(self.num_experts):
+            token_idx, slot_idx = (idx == e).nonzero(as_tuple=True)
+            if token_idx.numel() == 0:
+                continue
+            gu = matmul(x_flat[token_idx], self.gate_up_proj[e])
+            eo = matmul(swiglu(gu[:, :I], gu[:, I:]), self.down_proj[e])
+            final = cuda_index_add(final, (eo * vals[token_idx, slot_idx, None]).to(x.dtype), token_idx)
+        if residual is not None:
+            final = residual_add(final, residual.reshape(-1, H))
         return final.view(B, S, H), logits

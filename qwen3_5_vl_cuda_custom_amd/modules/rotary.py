@@ -5,6 +5,7 @@ import torch
 from torch import nn
 
 from ..kernels import apply_mrope, apply_rope, qk_norm_rope
+from ..kernels.backward import needs_grad
 
 
 def rotary_inv_freq(dim: int, theta: float, device=None) -> torch.Tensor:
@@ -107,7 +108,8 @@ class TextMRoPE(_FP32Freqs):
 
     def apply(self, q: torch.Tensor, k: torch.Tensor, position_ids: torch.Tensor):
         """Rotate q (B, Hq, S, D) and k (B, Hkv, S, D); angles position·inv_freq computed in-kernel in fp32."""
-        if q.shape[-1] % 16 == 0 and q.shape[-1] == self.dim and q.dtype == k.dtype:
+        if (q.shape[-1] % 16 == 0 and q.shape[-1] == self.dim and q.dtype == k.dtype
+                and not needs_grad(q, k)):  # the fused kernel has no backward; apply_mrope has one
             qo = torch.empty_like(q, memory_format=torch.contiguous_format)
             ko = torch.empty_like(k, memory_format=torch.contiguous_format)
             pos = position_ids.to(device=q.device, dtype=torch.int32).contiguous()

@@ -4,7 +4,8 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from ..kernels import conv3d_patch, matmul_gelu
+from ..kernels import conv3d_patch, gelu_tanh, matmul_gelu
+from ..kernels.backward import needs_grad
 from .linear import CudaLinear
 from .norms import CudaLayerNorm
 
@@ -57,4 +58,6 @@ class CudaVisionPatchMerger(nn.Module):
             x = self.norm(x.reshape(-1, self.merged_hidden))
         else:
             x = self.norm(x).reshape(-1, self.merged_hidden)
+        if needs_grad(x, *self.parameters()):  # training: fc1, gelu_tanh, fc2 on differentiable ops
+            return self.linear_fc2(gelu_tanh(self.linear_fc1(x)))
         return self.linear_fc2(matmul_gelu(x, self.linear_fc1.weight, self.linear_fc1.bias))

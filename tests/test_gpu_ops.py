@@ -315,6 +315,18 @@ def test_conv3d_patch():
     (4, 4, 4, 784, 72, False),   # vision: head_dim 72, per-image
     (1, 2, 2, 77, 80, True),
     (1, 6, 2, 64, 96, False),
+    # the eight-wave pipelined kernel's other forms: causal MHA (groups 1, Sq >= 192), whose
+    # 256-query blocks have waves with up to 7 fully masked key tiles, and GQA groups 4 at
+    # the padded head dims (72, 80, 96)
+    (1, 4, 4, 300, 128, True),
+    (1, 4, 4, 300, 64, True),
+    (2, 3, 3, 520, 128, True),
+    (1, 8, 2, 300, 72, True),
+    (1, 8, 2, 300, 72, False),
+    (1, 8, 2, 260, 80, True),
+    (1, 8, 2, 260, 80, False),
+    (1, 8, 2, 333, 96, True),
+    (1, 8, 2, 333, 96, False),
 ])
 def test_flash_attention_bf16(B, Hq, Hkv, S, D, causal):
     q, k, v = rnd(B, Hq, S, D, seed=20), rnd(B, Hkv, S, D, seed=21), rnd(B, Hkv, S, D, seed=22)
@@ -694,17 +706,19 @@ def test_moe_experts_skewed_routing():
 
 
 # ------------------------------------------------------------------ prefill chunk over a KV cache
-@pytest.mark.parametrize("Hq,Hkv,D,dtype", [
-    (8, 2, 128, torch.bfloat16),   # groups 4: the eight-wave pipelined kernel
-    (8, 4, 64, torch.bfloat16),    # groups 2: the four-wave kernel family
-    (4, 2, 72, torch.bfloat16),    # vision head dim through the same kernel family
-    (4, 2, 32, torch.float32),     # fp32: the SIMT kernel
+@pytest.mark.parametrize("Hq,Hkv,D,dtype,Sq,cap", [
+    (8, 2, 128, torch.bfloat16, 77, 300),   # groups 4: the eight-wave pipelined kernel
+    (8, 4, 64, torch.bfloat16, 77, 300),    # groups 2: the four-wave kernel family
+    (4, 2, 72, torch.bfloat16, 77, 300),    # vision head dim through the same kernel family
+    (4, 2, 32, torch.float32, 77, 300),     # fp32: the SIMT kernel
+    (4, 4, 128, torch.bfloat16, 200, 520),  # groups 1 with Sq >= 192: the pipelined kernel's MHA form
+    (4, 4, 64, torch.bfloat16, 250, 520),
 ])
-def test_flash_attention_cache_ragged(Hq, Hkv, D, dtype):
+def test_flash_attention_cache_ragged(Hq, Hkv, D, dtype, Sq, cap):
     """Chunk of Sq tokens per sequence over cache rows [0, lens[b] + i] (causal over the
     whole sequence), ragged lens incl. 0 and lens + Sq == cap; advance adds Sq in place."""
-    B, Sq, cap = 4, 77, 300
-    lens = torch.tensor([0, 5, 150, cap - Sq], dtype=torch.int32)
+    B = 4
+    lens = torch.tensor([0, 5, min(150, cap - Sq - 1), cap - Sq], dtype=torch.int32)
     q = rnd(B, Hq, Sq, D, seed=200, dtype=dtype)
     kc = rnd(B, Hkv, cap, D, seed=201, dtype=dtype)
     vc = rnd(B, Hkv, cap, D, seed=202, dtype=dtype)
@@ -768,3 +782,37 @@ def test_index_add_out_of_range_is_skipped_and_flagged():
     with pytest.raises(IndexError):
         K.raise_device_errors(DEV)
     K.raise_device_errors(DEV)  # the check clears the word
+
+
+# ------------------------------------------------------------------ slow paths are reported, not silent
+def test_unaligned_bf16_operands_run_on_aligned_copies(monkeypatch):
+    from qwen3_5_vl_cuda_custom_amd.kernels import _loader
+    monkeypatch.delenv("CUDA_QWEN3_VL_STRICT", raising=False)
+    _loader.FALLBACK_LOG.clear()
+    x, w = rnd(300, 520, seed=300), rnd(264, 520, seed=301)
+    xb = torch.empty(300 * 520 + 1, dtype=torch.bfloat16, device=DEV)
+    xu = xb[1:].view(300, 520)  # base 2 bytes past the allocation: not 16-byte aligned
+    xu.copy_(gpu(x))
+    y_al = K.matmul(gpu(x), gpu(w))
+    y_un = K.matmul(xu, gpu(w))
+    assert torch.equal(y_al, y_un), "the aligned copy must give the aligned call's result"
+    assert ("matmul", "aligned_copy", "") in _loader.FALLBACK_LOG
+    # attention: a q view at an odd offset
+    q, k, v = rnd(1, 8, 96, 128, seed=302), rnd(1, 2, 96, 128, seed=303), rnd(1, 2, 96, 128, seed=304)
+    qb = torch.empty(q.numel() + 1, dtype=torch.bfloat16, device=DEV)
+    qu = qb[1:].view(q.shape)
+    qu.copy_(gpu(q))
+    assert torch.equal(K.flash_attention(qu, gpu(k), gpu(v), 0.1, True, 4),
+                       K.flash_attention(gpu(q), gpu(k), gpu(v), 0.1, True, 4))
+    assert ("flash_attention", "aligned_copy", "") in _loader.FALLBACK_LOG
+    # K = 12 (not a multiple of 8): only the SIMT kernel takes it, and that is recorded
+    _loader.FALLBACK_LOG.clear()
+    a, b = rnd(40, 12, seed=305), rnd(24, 12, seed=306)
+    assert_bf16_close(K.matmul(gpu(a), gpu(b)), O.linear(f32(a), f32(b)), what="K=12 SIMT GEMM")
+    assert any(op == "matmul" and r.startswith("simt_kernel") for op, r, _ in _loader.FALLBACK_LOG)
+    monkeypatch.setenv("CUDA_QWEN3_VL_STRICT", "1")
+    with pytest.raises(RuntimeError, match="strict"):
+        K.matmul(xu, gpu(w))
+    with pytest.raises(RuntimeError, match="strict"):
+        K.matmul(gpu(a), gpu(b))
+    _loader.FALLBACK_LOG.clear()

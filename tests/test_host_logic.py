@@ -99,3 +99,18 @@ def test_mrope_positions_checked_and_broadcast():
     # an int32 (3, B, S) tensor is used as is (in-place updates reach the kernels)
     own = torch.zeros(3, 2, 1, dtype=torch.int32)
     assert rope.bind(own).positions_int32(torch.device("cpu"), batch=2, seq=1).data_ptr() == own.data_ptr()
+
+
+def test_paged_cache_refuses_shapes_the_paged_kernels_do_not_take():
+    ok = PagedKVCache(2, 2, 128, num_pages=4, max_pages=2, page_rows=32, device="cpu")
+    ok.check_kernels(4)
+    ok.check_kernels(32)
+    for cache, groups in ((ok, 33),
+                          (PagedKVCache(2, 2, 64, num_pages=4, max_pages=2, page_rows=32, device="cpu"), 4),
+                          (PagedKVCache(2, 2, 128, num_pages=4, max_pages=2, page_rows=32, dtype=torch.float32,
+                                        device="cpu"), 4)):
+        before = (cache.host_state(), cache.block_table.clone(), cache.num_free_pages)
+        with pytest.raises(ValueError, match="paged kernels"):
+            cache.check_kernels(groups)
+        assert (cache.host_state(), cache.num_free_pages) == (before[0], before[2])
+        assert torch.equal(cache.block_table, before[1])
