@@ -422,7 +422,8 @@ def main() -> int:
         layer_flop = cfg.gemm_flops_per_token() * S + cfg.causal_attn_flops(S)
         layer_tflops = layer_flop / (ms / 1e3) / 1e12
         log(f"prefill S={S}: {ms:.3f} ms/layer, {tok_s:,.0f} tok/s, {layer_tflops:.1f} TFLOP/s "
-            f"({layer_tflops / PEAK_BF16_TFLOPS:.1%} of bf16 peak)")
+            f"({layer_tflops / PEAK_BF16_TFLOPS:.1%} of bf16 peak); HIP events {ms_events:.3f} ms, "
+            f"host wall {wall * 1e3 / args.steps:.3f} ms per step")
 
         # Dominant kernel: the fused gate/up/SwiGLU GEMM on the post-attention activations.
         h = layer.post_attention_layernorm(x)

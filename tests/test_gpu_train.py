@@ -27,7 +27,8 @@ def rnd(*shape, seed=0, std=1.0, dtype=torch.float32):
 def run_grads(fn, inputs, dy, device=DEV, dtype=None):
     """Gradients of sum(fn(*inputs) * dy) w.r.t. the float inputs (computed on `device`)."""
     with torch.enable_grad():
-        xs = [t.to(device).to(dtype if (dtype and t.is_floating_point()) else t.dtype).requires_grad_(True)
+        # fresh leaves every call: .to() alone returns the caller's tensor when nothing changes
+        xs = [t.detach().to(device=device, dtype=dtype or t.dtype).clone().requires_grad_(True)
               if t.is_floating_point() else t.to(device) for t in inputs]
         out = fn(*xs)
         out.backward(dy.to(device).to(out.dtype))
@@ -38,12 +39,12 @@ def ref_grads(fn, inputs, dy):
     return run_grads(fn, [t.float() if t.is_floating_point() else t for t in inputs], dy.float(), device="cpu")
 
 
-def assert_grad_close(got, ref, what):
+def assert_grad_close(got, ref, what, max_rel=1.5e-2, mean_rel=5e-3):
     g, r = got.float().cpu(), ref.float().cpu()
     err = (g - r).abs()
     scale = float(r.abs().max())
-    assert float(err.max()) <= 1.5e-2 * scale + 1e-12, f"{what}: max err {float(err.max()):.3e} vs scale {scale:.3e}"
-    assert float(err.mean()) <= 5e-3 * float(r.abs().mean()) + 1e-12, f"{what}: mean err {float(err.mean()):.3e}"
+    assert float(err.max()) <= max_rel * scale + 1e-12, f"{what}: max err {float(err.max()):.3e} vs scale {scale:.3e}"
+    assert float(err.mean()) <= mean_rel * float(r.abs().mean()) + 1e-12, f"{what}: mean err {float(err.mean()):.3e}"
 
 
 def twice_equal(fn):
@@ -284,9 +285,9 @@ def test_embedding_backward(dtype, padding_idx):
     ids[0, :4] = 3  # repeated ids (and the padding row) accumulate
     dy = rnd(4, 16, 64, seed=72, dtype=dtype)
     with torch.enable_grad():
-        wd = w.to(DEV).requires_grad_(True)
+        wd = w.detach().to(DEV).clone().requires_grad_(True)
         K.embedding(ids.to(DEV), wd, padding_idx).backward(dy.to(DEV))
-        wr = w.float().requires_grad_(True)
+        wr = w.detach().float().clone().requires_grad_(True)
         F.embedding(ids, wr, padding_idx=padding_idx).backward(dy.float())
     if dtype == torch.float32:
         assert_close(wd.grad, wr.grad, atol=1e-5, what="embedding dw")
@@ -341,7 +342,7 @@ def test_ops_without_backward_still_refuse_grad():
 def _module_grads(layer, fwd, x, dy):
     layer.requires_grad_(True)
     with torch.enable_grad():
-        xd = x.to(DEV).requires_grad_(True)
+        xd = x.detach().to(DEV).clone().requires_grad_(True)
         y = fwd(layer, xd)
         y.backward(dy.to(DEV).to(y.dtype))
     grads = {n: p.grad.float().cpu() for n, p in layer.named_parameters()}
@@ -351,7 +352,7 @@ def _module_grads(layer, fwd, x, dy):
 def _oracle_grads(fn, p_dev, x, dy):
     p = {n: t.detach().float().cpu().requires_grad_(True) for n, t in p_dev.items()}
     with torch.enable_grad():
-        xc = x.float().cpu().requires_grad_(True)
+        xc = x.detach().float().cpu().clone().requires_grad_(True)
         y = fn(xc, p)
         y.backward(dy.float())
     return y.detach(), xc.grad, {n: t.grad for n, t in p.items()}
@@ -360,8 +361,10 @@ def _oracle_grads(fn, p_dev, x, dy):
 def _check_grads(got, ref, what, dtype):
     y, gx, gp = got
     ry, rgx, rgp = ref
+    # bf16: a layer's backward rounds each of its ~20 intermediates to bf16, so its gradients carry
+    # that accumulated rounding: max error within 5% of the largest |reference|, mean within 1.5%
     close = (lambda a, b, n: assert_close(a, b, atol=2e-3 * max(1.0, float(b.abs().max())), what=n)) \
-        if dtype == torch.float32 else (lambda a, b, n: assert_grad_close(a, b, n))
+        if dtype == torch.float32 else (lambda a, b, n: assert_grad_close(a, b, n, max_rel=5e-2, mean_rel=1.5e-2))
     close(y, ry, f"{what} output")
     close(gx, rgx, f"{what} d input")
     assert set(gp) == set(rgp)
