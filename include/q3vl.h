@@ -278,6 +278,20 @@ int q3_decode_attention_paged(const void* q, const void* k_pages, const void* v_
                               float scale, int dtype, void* workspace, int64_t workspace_bytes, int* status,
                               void* stream);
 
+/* q3_flash_attention_cache over a paged cache (no counterpart in the
+ * reference, whose cache grows by torch.cat, modules/attention.py:89-96): cache
+ * row r of sequence b is row r % page_rows of page block_table[b * max_pages +
+ * r / page_rows] of k_pages / v_pages (num_pages, Hkv, page_rows, D), read in
+ * place. strides = [qb, qh, qs, k page, kh, ks, v page, vh, vs, ob, oh, os].
+ * Same kernel and arithmetic as q3_flash_attention_cache (bit-identical
+ * output). bf16, D = 128, max_pages <= 512, fewer
+ * than 65535 pages, each pool under 2 GiB; else Q3_ERR_UNSUPPORTED. A page id
+ * outside [0, num_pages) reads as zero rows and sets bit 1 of *status. */
+int q3_flash_attention_cache_paged(const void* q, const void* k_pages, const void* v_pages, const int* block_table,
+                                   int64_t max_pages, int64_t page_rows, int64_t num_pages, int* kv_lens, void* o,
+                                   int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D, const int64_t* strides,
+                                   float scale, int advance, int dtype, int* status, void* stream);
+
 /* q3_decode_attention_step without a workspace argument, for callers that
  * cannot allocate (code under HIP-graph capture, tight serving loops). No
  * counterpart in the reference. The workspace lives in a static device array

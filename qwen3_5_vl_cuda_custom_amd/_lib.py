@@ -56,6 +56,8 @@ _SIGS: dict[str, tuple] = {
                                           c_int, _V]),
     "q3_flash_attention_cache": (c_int, [_V, _V, _V, _i32p, _V, _I, _I, _I, _I, _I, _I, _i64p, c_float, c_int,
                                          c_int, _V]),
+    "q3_flash_attention_cache_paged": (c_int, [_V, _V, _V, _i32p, _I, _I, _I, _i32p, _V, _I, _I, _I, _I, _I, _i64p,
+                                               c_float, c_int, c_int, _i32p, _V]),
     "q3_decode_attention_workspace_bytes": (c_int64, [_I, _I, _I, _I, _I]),
     "q3_decode_attention": (c_int, [_V, _V, _V, _i32p, _V, _I, _I, _I, _I, _I, _i64p, c_float, c_int, _V, _I, _V]),
     "q3_decode_attention_step": (c_int, [_V, _V, _V, _i32p, _V, _I, _I, _I, _I, _I, _i64p, c_float, c_int, _V, _I,

@@ -760,6 +760,7 @@ __global__ __launch_bounds__(256) void flash_decode_combine(const AttnParams p) 
 namespace fwdp {
 constexpr int kQ = 64;           // queries per block (32 per wave)
 constexpr int kKeys = 32;        // keys per tile
+constexpr int kPagedPrefillRegs = 8;  // paged prefill: page ids held per lane (64 * 8 = 512 pages a sequence)
 constexpr int kPipeStages = 8;   // K/V tile ring depth
 constexpr int kAhead = 6;        // step t issues tile t + kAhead (its slot held tile t - 2)
 constexpr int kTile = kKeys * kRowK;
@@ -826,7 +827,15 @@ __device__ __forceinline__ void q_norm_rope_frag(bf16x8 (&qf)[D / 16], const bf1
 }
 }  // namespace fwdp
 
-template <int D, bool MHA>
+// PAGED (GQA prefill over a paged KV cache, p.block_table set): cache row r of
+// sequence b is row r % page_rows of page block_table[b * max_pages + r /
+// page_rows], p.kb / p.vb are the page strides and Sk = max_pages * page_rows.
+// A 32-key tile lies inside one page (page_rows is a multiple of 32). Lane j
+// holds the id of the sequence's page j + 64 i in pg_ids[i] (loaded once, before
+// the first tile), so a tile's page base is a readlane away and the pipelined
+// loop never waits on memory for it. A page id outside [0, num_pages) reads as
+// zero rows and sets bit 1 of *status.
+template <int D, bool MHA, bool PAGED = false>
 __global__ __launch_bounds__(512) void flash_fwd_pipe_kernel(const AttnParams p) {
   using namespace fwdp;
   static_assert(D % 8 == 0 && D <= kRowK, "head_dim");
@@ -851,14 +860,18 @@ __global__ __launch_bounds__(512) void flash_fwd_pipe_kernel(const AttnParams p)
   const int n_qt = (Sq + QBLK - 1) / QBLK;
   const int qt = causal ? (n_qt - 1 - (int)blockIdx.y) : (int)blockIdx.y;  // heaviest first
   int yb = blockIdx.x;
-  int hg = 0;
-  if constexpr (!MHA) {
-    hg = yb % (p.groups / 4);
+  int kvh, b, hq;
+  if constexpr (MHA) {  // one query head per block (any groups; the vision tower's MHA is groups 1)
+    hq = yb % p.Hq;
+    b = yb / p.Hq;
+    kvh = hq / p.groups;
+  } else {
+    const int hg = yb % (p.groups / 4);
     yb /= p.groups / 4;
+    kvh = yb % p.Hkv;
+    b = yb / p.Hkv;
+    hq = kvh * p.groups + hg * 4 + hw;
   }
-  const int kvh = yb % p.Hkv;
-  const int b = yb / p.Hkv;
-  const int hq = MHA ? kvh : kvh * p.groups + hg * 4 + hw;
   // Packed sequences: this block's sequence starts at row `row0` of every
   // tensor and has Sq = Sk = its own length; tiles past it have nothing to do.
   int64_t qb_off = (int64_t)b * p.qb, kb_off = (int64_t)b * p.kb, vb_off = (int64_t)b * p.vb,
@@ -879,12 +892,41 @@ __global__ __launch_bounds__(512) void flash_fwd_pipe_kernel(const AttnParams p)
   const int klimit = causal ? min(Skb, q0 + QBLK + off) : Skb;
   const int nkt = (klimit + kKeys - 1) / kKeys;
 
-  const bf16* kbase = p.k + kb_off + (int64_t)kvh * p.kh;
-  const bf16* vbase = p.v + vb_off + (int64_t)kvh * p.vh;
   const int ks2 = (int)p.ks * 2, vs2 = (int)p.vs * 2;
-  const __amdgpu_buffer_rsrc_t krs = q3::make_rsrc(kbase, (int64_t)(Sk - 1) * ks2 + D * 2);
-  const __amdgpu_buffer_rsrc_t vrs = q3::make_rsrc(vbase, (int64_t)(Sk - 1) * vs2 + D * 2);
+  // Paged: the resources span the whole page pool from this KV head's rows.
+  const bf16* kbase = p.k + (PAGED ? 0 : kb_off) + (int64_t)kvh * p.kh;
+  const bf16* vbase = p.v + (PAGED ? 0 : vb_off) + (int64_t)kvh * p.vh;
+  const __amdgpu_buffer_rsrc_t krs =
+      q3::make_rsrc(kbase, PAGED ? (int64_t)p.num_pages * p.kb * 2 - (int64_t)kvh * p.kh * 2
+                                 : (int64_t)(Sk - 1) * ks2 + D * 2);
+  const __amdgpu_buffer_rsrc_t vrs =
+      q3::make_rsrc(vbase, PAGED ? (int64_t)p.num_pages * p.vb * 2 - (int64_t)kvh * p.vh * 2
+                                 : (int64_t)(Sk - 1) * vs2 + D * 2);
   const uint32_t lbase = q3::lds_addr(ring);
+  // Paged: register i of lane j holds the 16-bit ids of pages j + 128 i (low
+  // half) and j + 128 i + 64 (high half); 0xffff marks a page that reads as
+  // zeros. A vector type, so the ids stay in registers (a private array may be
+  // moved to LDS).
+  constexpr int kPgRegs = kPagedPrefillRegs / 2;
+  typedef uint32_t pg_vec_t __attribute__((ext_vector_type(kPagedPrefillRegs / 2)));
+  pg_vec_t pg_ids = {};
+  if constexpr (PAGED) {
+    const int npg = (klimit + p.page_rows - 1) / p.page_rows;  // pages this block reads
+#pragma unroll
+    for (int i = 0; i < 2 * kPgRegs; ++i) {
+      const int j = lane + 64 * i;
+      uint32_t id = 0xffffu;
+      if (j < npg) {
+        const int pg = p.block_table[(int64_t)b * p.max_pages + j];
+        if ((unsigned)pg < (unsigned)p.num_pages) {
+          id = (uint32_t)pg;
+        } else if (p.status && wave == 0) {
+          atomicOr(p.status, 2);
+        }
+      }
+      pg_ids[i >> 1] |= id << (16 * (i & 1));
+    }
+  }
 
   // Wave w loads rows 4w .. 4w + 3 of tile t's K and V (one instruction each);
   // chunks at or past D load as zeros (which pads D to the MFMA k-step).
@@ -896,10 +938,22 @@ __global__ __launch_bounds__(512) void flash_fwd_pipe_kernel(const AttnParams p)
   auto issue = [&](int t) {
     const uint32_t lk = lbase + (uint32_t)((t % kPipeStages) * 2 * kTile * 2) + (uint32_t)(4 * wave * kRowK * 2);
     const uint32_t lv = lk + kTile * 2;
-    const bool live = t < nkt;
+    bool live = t < nkt;
     const int row = t * kKeys;
-    q3::dma16(krs, live ? (uint32_t)((row + r0) * ks2) + kc0 : q3::kOOB, lk);
-    q3::dma16(vrs, live ? (uint32_t)((row + r0) * vs2) + vc0 : q3::kOOB, lv);
+    if constexpr (PAGED) {
+      const int pi = row / p.page_rows;  // the tile's page (uniform)
+      uint32_t sel = pg_ids[0];
+#pragma unroll
+      for (int i = 1; i < kPgRegs; ++i) sel = (pi >> 7) == i ? pg_ids[i] : sel;
+      const int pg = (int)((__builtin_amdgcn_readlane(sel, pi & 63) >> (16 * ((pi >> 6) & 1))) & 0xffffu);
+      live = live && pg != 0xffff;
+      const int prow = row - pi * p.page_rows + r0;  // row within the page
+      q3::dma16(krs, live ? (uint32_t)(pg * (int)p.kb * 2 + prow * ks2) + kc0 : q3::kOOB, lk);
+      q3::dma16(vrs, live ? (uint32_t)(pg * (int)p.vb * 2 + prow * vs2) + vc0 : q3::kOOB, lv);
+    } else {
+      q3::dma16(krs, live ? (uint32_t)((row + r0) * ks2) + kc0 : q3::kOOB, lk);
+      q3::dma16(vrs, live ? (uint32_t)((row + r0) * vs2) + vc0 : q3::kOOB, lv);
+    }
   };
 
   // Fused q prologue (GQA, D = 64 or 128): the first kAhead K/V tiles are
@@ -1203,23 +1257,24 @@ __global__ __launch_bounds__(128) void flash_generic_kernel(const AttnParams p, 
 
 bool mfma_head_dim(int64_t D) { return D == 64 || D == 72 || D == 80 || D == 96 || D == 128; }
 
-template <int D, bool MHA>
+template <int D, bool MHA, bool PAGED = false>
 int launch_fwd_pipe_t(const AttnParams& p, hipStream_t st) {
   const int n_qt = (int)q3_cdiv(p.Sq, MHA ? 4 * fwdp::kQ : fwdp::kQ);
   Q3_REQUIRE(n_qt <= 65535, Q3_ERR_UNSUPPORTED);
-  dim3 grid((unsigned)(p.B * p.Hkv * (MHA ? 1 : p.groups / 4)), (unsigned)n_qt);
-  hipLaunchKernelGGL((flash_fwd_pipe_kernel<D, MHA>), grid, dim3(512), 0, st, p);
+  dim3 grid((unsigned)(MHA ? p.B * p.Hq : p.B * p.Hkv * (p.groups / 4)), (unsigned)n_qt);
+  hipLaunchKernelGGL((flash_fwd_pipe_kernel<D, MHA, PAGED>), grid, dim3(512), 0, st, p);
   Q3_LAUNCH_CHECK();
   return Q3_OK;
 }
 
-// The pipelined kernel takes GQA groups that are a multiple of 4, and MHA
-// (groups 1) when the (longest) sequence fills most of its 256-query blocks.
+// The pipelined kernel takes GQA groups that are a multiple of 4 (a block per 4
+// query heads of a KV head), and a block per query head (MHA, groups 1) when the
+// (longest) sequence fills most of its 256-query blocks.
 bool pipe_eligible(const AttnParams& p) { return p.groups % 4 == 0 || (p.groups == 1 && p.Sq >= 192); }
 
 template <int D>
 int launch_fwd_pipe(const AttnParams& p, hipStream_t st) {
-  return p.groups == 1 ? launch_fwd_pipe_t<D, true>(p, st) : launch_fwd_pipe_t<D, false>(p, st);
+  return p.groups % 4 != 0 ? launch_fwd_pipe_t<D, true>(p, st) : launch_fwd_pipe_t<D, false>(p, st);
 }
 
 template <int D>
@@ -1268,7 +1323,9 @@ __global__ void lens_inc_kernel(int* lens, int B, int add) {
 int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t Hq, int64_t Hkv,
              int64_t Sq, int64_t Sk, int64_t D, const int64_t* strides, float scale, int is_causal, int dtype,
              const int* q_off, int* lens_add, void* stream, const int* cu_seqlens = nullptr,
-             const bf16* qn_w = nullptr, const float* rope_tab = nullptr, float qn_eps = 0.f) {
+             const bf16* qn_w = nullptr, const float* rope_tab = nullptr, float qn_eps = 0.f,
+             const int* block_table = nullptr, int64_t max_pages = 0, int64_t page_rows = 0, int64_t num_pages = 0,
+             int* status = nullptr) {
   Q3_REQUIRE(q && k && v && o && strides, Q3_ERR_NULL);
   Q3_REQUIRE(B >= 0 && Hq >= 1 && Hkv >= 1 && Sq >= 0 && Sk >= 0 && D >= 1, Q3_ERR_SHAPE);
   Q3_REQUIRE(Hq % Hkv == 0, Q3_ERR_SHAPE);
@@ -1309,6 +1366,28 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
   const bool aligned = q3_aligned(q, 16) && q3_aligned(k, 16) && q3_aligned(v, 16) && q3_aligned(o, 8) &&
                        strides_aligned8(strides, 12);
   int rc = Q3_OK;
+  if (block_table) {  // paged cache: the pipelined kernel at D = 128 only
+    Q3_REQUIRE(dtype == Q3_BF16, Q3_ERR_DTYPE);
+    Q3_REQUIRE(aligned, Q3_ERR_ALIGN);
+    Q3_REQUIRE(D == 128 && q_off != nullptr && rope_tab == nullptr && cu_seqlens == nullptr &&
+                   max_pages <= 64 * fwdp::kPagedPrefillRegs,
+               Q3_ERR_UNSUPPORTED);
+    p.block_table = block_table;
+    p.max_pages = (int)max_pages;
+    p.page_rows = (int)page_rows;
+    p.num_pages = (int)num_pages;
+    p.status = status;
+    // GQA groups of 4k: a block serves 4 query heads of a KV head; other groups:
+    // a block per query head (each reads its KV head's pages).
+    rc = p.groups % 4 == 0 ? launch_fwd_pipe_t<128, false, true>(p, st) : launch_fwd_pipe_t<128, true, true>(p, st);
+    if (rc != Q3_OK) return rc;
+    if (lens_add) {
+      hipLaunchKernelGGL(lens_inc_kernel, dim3((unsigned)q3_cdiv(B, 256)), dim3(256), 0, st, lens_add, (int)B,
+                         (int)Sq);
+      Q3_LAUNCH_CHECK();
+    }
+    return Q3_OK;
+  }
   if (rope_tab) {  // the fused q prologue exists in the pipelined GQA kernel only (D = 64 or 128)
     Q3_REQUIRE(dtype == Q3_BF16, Q3_ERR_DTYPE);
     Q3_REQUIRE(aligned && q3_aligned(qn_w, 16), Q3_ERR_ALIGN);
@@ -1318,7 +1397,10 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
   }
   // The MFMA path addresses K with 32-bit buffer offsets.
   if (dtype == Q3_BF16 && mfma_head_dim(D) && aligned && Sk > 0 && (Sk + 1) * strides[5] * 2 < 0x7fffffffLL) {
-    const bool pipe = pipe_eligible(p);
+    // A prefill over a KV cache always runs the pipelined kernel (a block per
+    // query head when the groups are not a multiple of 4), the kernel of its
+    // paged form, so paged and contiguous caches give the same output.
+    const bool pipe = pipe_eligible(p) || q_off != nullptr;
     switch (D) {
       case 64:
         rc = pipe ? launch_fwd_pipe<64>(p, st) : launch_fwd<64>(p, st);
@@ -1444,6 +1526,30 @@ int q3_flash_attention_cache(const void* q, const void* k_cache, const void* v_c
   Q3_REQUIRE(Sq <= cap, Q3_ERR_SHAPE);
   return fwd_impl(q, k_cache, v_cache, o, nullptr, B, Hq, Hkv, Sq, cap, D, strides, scale, 1, dtype, kv_lens,
                   advance ? kv_lens : nullptr, stream);
+}
+
+// The same over a paged cache: cache row r of sequence b is row r % page_rows
+// of page block_table[b * max_pages + r / page_rows] of k_pages / v_pages
+// (num_pages, Hkv, page_rows, D). strides = [qb, qh, qs, k page, kh, ks,
+// v page, vh, vs, ob, oh, os]. bf16, D = 128,
+// max_pages <= 512, fewer than 65535 pages, pools under 2 GiB (32-bit
+// offsets); else
+// Q3_ERR_UNSUPPORTED. A page id outside [0, num_pages) reads as zero rows and
+// sets bit 1 of *status (a device int32, or null).
+int q3_flash_attention_cache_paged(const void* q, const void* k_pages, const void* v_pages, const int* block_table,
+                                   int64_t max_pages, int64_t page_rows, int64_t num_pages, int* kv_lens, void* o,
+                                   int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D, const int64_t* strides,
+                                   float scale, int advance, int dtype, int* status, void* stream) {
+  Q3_REQUIRE(q && k_pages && v_pages && block_table && kv_lens && o && strides, Q3_ERR_NULL);
+  Q3_REQUIRE(max_pages >= 1 && num_pages >= 1 && page_rows >= 32 && page_rows % 32 == 0, Q3_ERR_SHAPE);
+  Q3_REQUIRE(max_pages * page_rows < (1ll << 31) && Sq <= max_pages * page_rows, Q3_ERR_SHAPE);
+  Q3_REQUIRE(num_pages < 0xffff && num_pages * strides[3] * 2 < 0x7fffffffLL &&
+                 num_pages * strides[6] * 2 < 0x7fffffffLL,
+             Q3_ERR_UNSUPPORTED);
+  Q3_REQUIRE(strides[3] >= Hkv * page_rows * D && strides[6] >= Hkv * page_rows * D, Q3_ERR_SHAPE);
+  return fwd_impl(q, k_pages, v_pages, o, nullptr, B, Hq, Hkv, Sq, max_pages * page_rows, D, strides, scale, 1, dtype,
+                  kv_lens, advance ? kv_lens : nullptr, stream, nullptr, nullptr, nullptr, 0.f, block_table, max_pages,
+                  page_rows, num_pages, status);
 }
 
 int64_t q3_decode_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t D) {

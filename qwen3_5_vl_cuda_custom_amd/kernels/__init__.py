@@ -7,6 +7,7 @@ from .cross_entropy import cross_entropy
 from .elementwise import gelu_tanh, residual_add, sigmoid_mul, swiglu
 from .embedding import embedding
 from .flash_attention import (decode_attention, decode_attention_paged, flash_attention, flash_attention_cache,
+                              flash_attention_cache_paged,
                               flash_attention_varlen, qk_norm_rope_attention, qk_norm_rope_attention_ok)
 from .matmul import (RMSNORM_MATMUL_MAX_ROWS, matmul, matmul_gelu, matmul_segments, matmul_swiglu,
                      rmsnorm_matmul_segments, rmsnorm_matmul_swiglu)
@@ -42,6 +43,7 @@ __all__ = [
     "decode_attention",
     "decode_attention_paged",
     "flash_attention_cache",
+    "flash_attention_cache_paged",
     "flash_attention_varlen",
     "matmul_gelu",
     "vision_rope_tables",

@@ -258,6 +258,51 @@ def flash_attention_cache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch
     return o
 
 
+
+def flash_attention_cache_paged(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor,
+                                block_table: torch.Tensor, kv_lens: torch.Tensor, scale: float,
+                                num_kv_groups: int = 1, *, out: torch.Tensor | None = None, advance: bool = False,
+                                status: torch.Tensor | None = None) -> torch.Tensor:
+    """flash_attention_cache over a paged cache, read in place through the block table (no copy).
+
+    q (B, Hq, Sq, D); k_pages/v_pages (num_pages, Hkv, page_rows, D) pools;
+    block_table (B, max_pages) int32 on the device (cache row r of sequence b is
+    row r % page_rows of page block_table[b, r // page_rows]); the chunk's rows
+    [kv_lens[b], kv_lens[b] + Sq) already hold its keys/values. Query i of
+    sequence b attends causally to cache rows [0, kv_lens[b] + i]; advance=True
+    adds Sq to kv_lens afterwards. Same kernel and arithmetic as
+    flash_attention_cache, so a paged call returns the contiguous call's output
+    bit for bit. bf16, D = 128, at most 512 pages a
+    sequence. A page id outside the pool reads as zero rows and sets bit 1 of
+    `status` (default: the device's status word).
+    """
+    check("flash_attention_cache_paged", q, k_pages, v_pages)
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    (q,) = _attn_operands("flash_attention_cache_paged", q.shape[-1], out, q)
+    B, Hq, Sq, D = q.shape
+    num_pages, Hkv, page_rows = k_pages.shape[0], k_pages.shape[1], k_pages.shape[2]
+    if k_pages.shape != v_pages.shape or k_pages.shape[3] != D or k_pages.stride(-1) != 1 or v_pages.stride(-1) != 1:
+        raise ValueError(f"flash_attention_cache_paged: q {tuple(q.shape)}, pages {tuple(k_pages.shape)}")
+    if Hkv * num_kv_groups != Hq:
+        raise ValueError(f"flash_attention_cache_paged: Hq={Hq} != Hkv={Hkv} * num_kv_groups={num_kv_groups}")
+    if (block_table.dtype != torch.int32 or not block_table.is_cuda or block_table.dim() != 2
+            or block_table.shape[0] != B or not block_table.is_contiguous()):
+        raise ValueError("flash_attention_cache_paged: block_table must be a contiguous int32 (B, max_pages) "
+                         "device tensor")
+    if kv_lens.dtype != torch.int32 or not kv_lens.is_cuda or kv_lens.shape != (B,) or kv_lens.stride(0) != 1:
+        raise ValueError("flash_attention_cache_paged: kv_lens must be a contiguous int32 (B,) device tensor")
+    o = out if out is not None else torch.empty((B, Hq, Sq, D), dtype=q.dtype, device=q.device)
+    if o.shape != (B, Hq, Sq, D) or o.stride(-1) != 1:
+        raise ValueError("flash_attention_cache_paged: out must be (B, Hq, Sq, D) with a contiguous head dim")
+    st = status if status is not None else _lib.status_word(q.device)
+    _lib.call("q3_flash_attention_cache_paged", q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(),
+              block_table.data_ptr(), block_table.shape[1], page_rows, num_pages, kv_lens.data_ptr(), o.data_ptr(),
+              B, Hq, Hkv, Sq, D,
+              _lib.i64s(*_s4(q), *_s4(k_pages), *_s4(v_pages), *_s4(o)), float(scale), int(bool(advance)),
+              _lib.dtype_code(q.dtype), st.data_ptr(), _lib.stream())
+    return o
+
 def flash_attention_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
                            max_seqlen: int, scale: float, is_causal: bool = False, num_kv_groups: int = 1, *,
                            out: torch.Tensor | None = None) -> torch.Tensor:

@@ -6,6 +6,7 @@ from torch import nn
 
 from ..kernels.backward import needs_grad
 from ..kernels import (apply_rope, decode_attention, decode_attention_paged, flash_attention, flash_attention_cache,
+                       flash_attention_cache_paged,
                        flash_attention_varlen, matmul_segments, qk_norm_rope, qk_norm_rope_attention,
                        qk_norm_rope_attention_ok, qk_norm_rope_paged, rmsnorm_matmul_segments)
 from .kv_cache import PagedKVCache, StaticKVCache
@@ -76,10 +77,9 @@ class CudaFullAttention(nn.Module):
                               ragged cache: decode when S == 1, else a
                               prefill chunk whose token i attends causally to
                               the cache rows up to its own (lens[b] + i)
-      kv_cache=PagedKVCache   the same over a paged cache: decode reads the
-                              pages through the block table; a prefill chunk
-                              attends over a contiguous copy of the pages its
-                              sequences hold; returns (k_pages, v_pages)
+      kv_cache=PagedKVCache   the same over a paged cache: decode and prefill
+                              chunks read the pages in place through the
+                              block table; returns (k_pages, v_pages)
       residual=tensor         added to o_proj's output in the GEMM epilogue
       input_norm=CudaRMSNorm  x is the layer input before this RMSNorm; for
                               decode shapes (at most 32 tokens, bf16) the norm
@@ -217,9 +217,7 @@ class CudaFullAttention(nn.Module):
             decode_attention_paged(q[:, 0], kv_cache.k_pages, kv_cache.v_pages, pt, kv_cache.lens, self.scale,
                                    out=o[:, 0], append=True)
         else:
-            # Prefill chunk: the pages the sequences hold, copied in row order, are
-            # a (B, Hkv, n * page_rows, D) cache for the ragged chunk kernel.
-            kc, vc = kv_cache.gather(kv_cache.max_len)
-            flash_attention_cache(q.transpose(1, 2), kc, vc, kv_cache.lens, self.scale, self.num_kv_groups,
-                                  out=o.transpose(1, 2), advance=True)
+            # Prefill chunk: the ragged chunk kernel reads the pages in place through the block table.
+            flash_attention_cache_paged(q.transpose(1, 2), kv_cache.k_pages, kv_cache.v_pages, pt, kv_cache.lens,
+                                        self.scale, self.num_kv_groups, out=o.transpose(1, 2), advance=True)
         return self.o_proj(o.view(B, S, Hq * D), residual=residual), (kv_cache.k_pages, kv_cache.v_pages)

@@ -730,11 +730,17 @@ def test_flash_attention_cache_ragged(Hq, Hkv, D, dtype, Sq, cap):
         assert_close(out, ref, atol=2e-5, what="chunk attention fp32")
     else:
         assert_bf16_close(out, ref, what=f"chunk attention D={D} groups={Hq // Hkv}")
-    # Empty cache: identical to plain causal attention over the chunk's own rows.
+    # Empty cache: plain causal attention over the chunk's own rows, bit for bit where both calls run
+    # the same kernel (GQA groups of 4k, fp32); for other groups the cache path runs the pipelined
+    # kernel per query head (the kernel of its paged form) and plain attention the four-wave one.
     z = torch.zeros(B, dtype=torch.int32, device=DEV)
     a = K.flash_attention_cache(gpu(q), gpu(kc), gpu(vc), z, D ** -0.5, Hq // Hkv)
     b = K.flash_attention(gpu(q), gpu(kc)[:, :, :Sq], gpu(vc)[:, :, :Sq], D ** -0.5, True, Hq // Hkv)
-    assert torch.equal(a, b), "an empty cache must give causal attention bit for bit"
+    if dtype == torch.float32 or (Hq // Hkv) % 4 == 0:
+        assert torch.equal(a, b), "an empty cache must give causal attention bit for bit"
+    else:
+        ref0 = O.flash_attention(f32(q), f32(kc)[:, :, :Sq], f32(vc)[:, :, :Sq], D ** -0.5, True, Hq // Hkv)
+        assert_bf16_close(a, ref0, what=f"empty cache, groups {Hq // Hkv}")
     assert torch.equal(z.cpu(), torch.zeros(B, dtype=torch.int32)), "advance=False leaves the lengths"
 
 

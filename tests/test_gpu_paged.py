@@ -250,3 +250,44 @@ def test_generate_paged_equals_static():
     b = m.generate(ids, max_new_tokens=40, prompt_lens=lens, page_rows=32)
     c = m.generate(ids, max_new_tokens=40, prompt_lens=lens, page_rows=64, use_graph=False)
     assert torch.equal(a, b) and torch.equal(a, c)
+
+
+@pytest.mark.parametrize("groups,P,Sq", [(4, 32, 77), (8, 64, 200), (4, 96, 33), (2, 32, 50), (1, 64, 90)])
+def test_paged_prefill_chunk_equals_contiguous(groups, P, Sq):
+    """A prefill chunk over a paged cache (read in place through the block table) returns the
+    contiguous cache's result bit for bit, and advances the lengths the same way."""
+    B, Hkv, cap = 5, 2, 1120
+    lens = torch.tensor([0, 5, 300, 640, cap - Sq], dtype=torch.int32)
+    kc, vc = rnd(B, Hkv, cap, D, seed=400), rnd(B, Hkv, cap, D, seed=401)
+    q = rnd(B, Hkv * groups, Sq, D, seed=402)
+    rows = (lens + Sq).tolist()
+    kp, vp, table = paginate(kc, vc, rows, P, math.ceil(cap / P), seed=403)
+    dl, pl = lens.to(DEV), lens.to(DEV)
+    ref = K.flash_attention_cache(q.to(DEV), kc.to(DEV), vc.to(DEV), dl, D ** -0.5, groups, advance=True)
+    st = torch.zeros(1, dtype=torch.int32, device=DEV)
+    got = K.flash_attention_cache_paged(q.to(DEV), kp.to(DEV), vp.to(DEV), table.to(DEV), pl, D ** -0.5, groups,
+                                        advance=True, status=st)
+    assert torch.equal(got, ref), "paged prefill must equal the contiguous kernel bit for bit"
+    assert torch.equal(pl.cpu(), lens + Sq) and torch.equal(dl.cpu(), lens + Sq)
+    assert int(st.item()) == 0
+    chk = O.chunk_attention(q.float(), kc.float(), vc.float(), lens.tolist(), D ** -0.5, groups)
+    assert_bf16_close(got, chk, what=f"paged chunk groups={groups} P={P}")
+
+
+def test_paged_prefill_bad_page_reads_zeros_and_sets_status():
+    B, Hkv, groups, P, Sq = 2, 2, 4, 32, 40
+    cap = 256
+    lens = torch.tensor([100, 60], dtype=torch.int32)
+    kc, vc = rnd(B, Hkv, cap, D, seed=410), rnd(B, Hkv, cap, D, seed=411)
+    q = rnd(B, Hkv * groups, Sq, D, seed=412)
+    kp, vp, table = paginate(kc, vc, (lens + Sq).tolist(), P, cap // P, seed=413)
+    table[0, 1] = 10_000  # past the pool: rows [32, 64) of sequence 0 read as zeros
+    kz, vz = kc.clone(), vc.clone()
+    kz[0, :, 32:64] = 0
+    vz[0, :, 32:64] = 0
+    st = torch.zeros(1, dtype=torch.int32, device=DEV)
+    got = K.flash_attention_cache_paged(q.to(DEV), kp.to(DEV), vp.to(DEV), table.to(DEV), lens.to(DEV), D ** -0.5,
+                                        groups, status=st)
+    ref = K.flash_attention_cache(q.to(DEV), kz.to(DEV), vz.to(DEV), lens.to(DEV), D ** -0.5, groups)
+    assert torch.equal(got, ref)
+    assert int(st.item()) & _lib.STATUS_BAD_PAGE
