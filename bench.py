@@ -146,11 +146,12 @@ def parity_leg(cases: dict) -> dict:
         w = float(ref.reshape(-1)[int((out.float() - ref).abs().argmax())])
         return 2.0 ** (math.frexp(abs(w))[1] - 8) if w else 0.0
 
-    res = {}
+    res, secs = {}, {}
     try:
         for name, (gpu_out, run) in cases.items():
             t0 = time.perf_counter()
             ref = run(L, O, ident)
+            secs[name] = time.perf_counter() - t0
             emu = run(L, O, O.round_bf16)
             ma, mr = metrics(gpu_out, ref)
             ema, emr = metrics(emu, ref)
@@ -164,7 +165,27 @@ def parity_leg(cases: dict) -> dict:
             log(f"parity {name}: {res[name]} ({time.perf_counter() - t0:.1f} s)")
     finally:
         torch.set_num_threads(prev)
-    return res
+    return res, secs
+
+
+# Work per run of each configuration's oracle (for the per-configuration CPU baseline).
+CPU_UNITS = {"c3_decode_b32": (32, "tokens/s", "one B=32 decode step of the 8B-shape layer (per-sequence "
+                                               "attention over each sequence's cache rows)"),
+             "c4_moe_layer_t4096": (4096, "tokens/s", "the 30B-A3B-shape MoE layer on 4096 tokens"),
+             "c5_vision_patch_embed_block": (3136, "patches/s", "C5 patch embed + vision block on 4 x 784 "
+                                                                "patches")}
+
+
+def cpu_baseline_other(secs: dict) -> dict:
+    """The oracle's own CPU run of each non-headline configuration (its fp32 pass of the parity leg:
+    torch CPU ops on the bf16-rounded inputs), as throughput: a reported baseline, not a target."""
+    out = {}
+    for name, (n, unit, what) in CPU_UNITS.items():
+        if name in secs:
+            out[name] = {"value": round(n / secs[name], 1), "unit": unit, "seconds": round(secs[name], 3),
+                         "cores": usable_cpus(), "kind": "port",
+                         "sample": f"oracle (torch CPU, fp32 math on bf16-rounded values): {what}, one run"}
+    return out
 
 
 def _params_cpu(module) -> dict:
@@ -501,12 +522,14 @@ def main() -> int:
         with torch.inference_mode():
             extra = other_configs(torch, W, dev, args.warmup, cases if not args.no_cpu_baseline else {})
 
-    cpu = parity = None
+    cpu = parity = cpu_other = None
     if not args.no_cpu_baseline:
         with torch.inference_mode():
             cpu = cpu_baseline(cfg, S, layer)
             log(f"cpu baseline: {cpu}")
-            parity = parity_leg(cases)
+            parity, secs = parity_leg(cases)
+            cpu_other = cpu_baseline_other(secs)
+            log(f"cpu baseline, other configurations: {cpu_other}")
 
     out = {
         "metric": "decoder-layer prefill tokens/s (8B, S=4096) + decode tok/s; % MFMA/HBM roofline",
@@ -534,6 +557,7 @@ def main() -> int:
         "decode": decode,
         "other_configs": extra,
         "cpu_baseline": cpu,
+        "cpu_baseline_other_configs": cpu_other,
         "parity": parity,
     }
     print(json.dumps(out), flush=True)
