@@ -648,20 +648,154 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
     __builtin_amdgcn_sched_group_barrier(0x008, NM - NR, 0);
   };
 
+  // Spread schedule (W ring one slot deeper than the X ring). A stage's DMA
+  // group is 64 KB at 256x256: issued within one K step it outruns the
+  // texture path, and a wave whose next instruction is a DMA that cannot
+  // issue stalls the MFMAs behind it. So stage j issues W(j + NST) during its
+  // first K steps, into the W slot stage j - 1 released (its barrier is
+  // behind us; the slot is next read in stage j + NST, so W keeps NST - 1
+  // stages and a half of lead), and only X(j + NST) in its last step. Issue
+  // order per wave: W(j + NST) then X(j + NST), stage by stage, so vmcnt
+  // bookkeeping is that of the burst schedule: at stage kt's barrier X(kt + 1)
+  // has landed once NST - 2 whole groups and W(kt + NST) remain, which is
+  // kWait. Same MFMA order, same results.
+  constexpr bool kSpreadW = NSTW == NST + 1;
+  constexpr int kWSteps = KS - 1 < 2 ? KS - 1 : 2;  // K steps that carry W DMAs
+  static_assert(!kSpreadW || kWSteps >= 1, "the spread schedule needs two K steps per stage");
+  auto dma_w = [&](int kw, int i) {
+    const int k = kw * BKT + dc * 8;
+    const uint32_t off = (k < K && woff[i] != kOOB) ? woff[i] + (uint32_t)k * 2u : kOOB;
+    dma16(make_rsrc(wsrc[i], (int64_t)wrows[i] * ldw * 2), off, wslot(kw) + (uint32_t)((wave + NW * i) * 1024));
+  };
+  auto read_one = [&](int buf, int kt, int ks, int f) {
+    const int c = ks * 2 + h;
+    if (f < TN) {
+      const bf16* sw = smem + NST * kStageX + (kt % NSTW) * kStageW;
+      const int r = rn + f * 32 + l32;
+      fa[buf][f] = *reinterpret_cast<const bf16x8*>(sw + r * BKT + ((c ^ dma_swz<BKT>(r)) << 3));
+    } else {
+      const bf16* sx = smem + (kt % NST) * kStageX;
+      const int r = rm + (f - TN) * 32 + l32;
+      fb[buf][f - TN] = *reinterpret_cast<const bf16x8*>(sx + r * BKT + ((c ^ dma_swz<BKT>(r)) << 3));
+    }
+  };
+  // K step ks of stage kt: its MFMAs, the fragment reads of step ks + 1
+  // (one after each of the first TN + TM MFMAs) and this step's share of
+  // W(kt + NST), evenly between the MFMAs; order pinned.
+  auto step_w = [&](auto active_c, int buf, int kt, int ks) {
+    constexpr bool kActive = decltype(active_c)::value;
+    constexpr int NR = TN + TM, NM = TN * TM;
+    const int d0 = ks * PW / kWSteps, d1 = (ks + 1) * PW / kWSteps;
+    const int nd = d1 - d0;
+    const int gap = nd > 0 ? (NM + nd - 1) / nd : NM + 1;
+    int d = d0;
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kActive) {
 #pragma unroll
-  for (int j = -NSTW; j <= -2; ++j) issue_group(j);
-  vm_wait<kWait>();  // stage 0 has landed
-  __syncthreads();
-  issue_group(-1);
+      for (int m = 0; m < NM; ++m) {
+        acc.c[m / TM][m % TM] = mfma32x32x16(fa[buf][m / TM], fb[buf][m % TM], acc.c[m / TM][m % TM]);
+        if (m < NR) read_one(buf ^ 1, kt, ks + 1, m);
+        if (d < d1 && m % gap == gap - 1) dma_w(kt + NST, d++);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+#pragma unroll
+    for (; d < d1; ++d) dma_w(kt + NST, d);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // The last K step of stage kt, which also crosses the stage's barrier. Its
+  // MFMAs run in diagonal order, so the first NQ = max(TN, TM) of them use
+  // every fragment of the step: once they have issued, this wave has no read
+  // of stage kt's slots in flight (their results are in registers). Then the
+  // wave waits for its own part of stage kt + 1 (vmcnt) and meets the other
+  // waves at a plain s_barrier; no lgkmcnt(0) drain is needed before it, and
+  // the MFMAs already issued keep the matrix core busy across the barrier.
+  // After it: the reads of stage kt + 1's first step and X(kt + NST) (into
+  // the X slot stage kt released) between the remaining MFMAs. Each
+  // accumulator still takes exactly one MFMA per step: same results.
+  auto last_step_x = [&](auto active_c, int buf, int kt) {
+    constexpr bool kActive = decltype(active_c)::value;
+    constexpr int NM = TN * TM, NR = TN + TM;
+    constexpr int NQ = TN > TM ? TN : TM;
+    const int kx = (kt + NST) * BKT + dc * 8;
+    const uint32_t sbx = xslot(kt + NST);
+    uint32_t doff[PX];
+#pragma unroll
+    for (int i = 0; i < PX; ++i) doff[i] = (kx < K && xoff[i] != kOOB) ? xoff[i] + (uint32_t)kx * 2u : kOOB;
+    // q-th MFMA of the step: diagonal q / NQ, position q % NQ along the longer side.
+    auto mfma_q = [&](int q) {
+      const int a = q % NQ, dg = q / NQ;
+      const int i = TN >= TM ? a : (a + dg) % TN;
+      const int j = TN >= TM ? (a + dg) % TM : a;
+      acc.c[i][j] = mfma32x32x16(fa[buf][i], fb[buf][j], acc.c[i][j]);
+    };
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kActive) {
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        mfma_q(q);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    vm_wait<kWait>();                         // this wave's part of stage kt + 1 has landed
+    asm volatile("s_barrier" ::: "memory");  // every wave's; no wave reads stage kt any more
+    __builtin_amdgcn_sched_barrier(0);
+    constexpr int NAFT = NM - NQ;
+    constexpr int gap = NAFT >= PX ? NAFT / PX : 1;
+    int d = 0;
+    if constexpr (kActive) {
+      // all of stage kt + 1's first-step reads at once, so the remaining
+      // MFMAs of this step cover their latency
+#pragma unroll
+      for (int r = 0; r < NR; ++r) read_one(buf ^ 1, kt + 1, 0, r);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int q = NQ; q < NM; ++q) {
+        mfma_q(q);
+        if (d < PX && (q - NQ) % gap == gap - 1) {
+          dma16(rx, doff[d], sbx + (uint32_t)((wave + NW * d) * 1024));
+          ++d;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+#pragma unroll
+    for (; d < PX; ++d) dma16(rx, doff[d], sbx + (uint32_t)((wave + NW * d) * 1024));
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  if constexpr (kSpreadW) {
+#pragma unroll
+    for (int j = 0; j < NST; ++j) {
+      issue_w(j);
+      issue_x(j);
+    }
+    vm_wait<(NST - 1) * (PX + PW)>();  // stage 0 has landed
+    __syncthreads();
+  } else {
+#pragma unroll
+    for (int j = -NSTW; j <= -2; ++j) issue_group(j);
+    vm_wait<kWait>();  // stage 0 has landed
+    __syncthreads();
+    issue_group(-1);
+  }
   auto main_loop = [&](auto active_c) {
     read(active_c, 0, 0, 0);
     for (int kt = 0; kt < nk; ++kt) {
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         if (ks + 1 < KS) {
+          if constexpr (kSpreadW) {
+            if (ks < kWSteps) {
+              step_w(active_c, ks & 1, kt, ks);
+              continue;
+            }
+          }
           read(active_c, (ks + 1) & 1, kt, ks + 1);
           mma(active_c, ks & 1);
           if constexpr (decltype(active_c)::value) interleave();
+        } else if constexpr (kSpreadW) {
+          last_step_x(active_c, ks & 1, kt);  // crosses the barrier; X(kt + NST) into the slot stage kt released
         } else {
           vm_wait<kWait>();                   // this wave's part of stage kt + 1 has landed
           __syncthreads();                    // every wave's; nobody reads stage kt any more
