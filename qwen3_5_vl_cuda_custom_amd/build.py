@@ -33,8 +33,10 @@ HIPFLAGS = [
 ]
 
 
-# Per-source extra flags (none at present).
-EXTRA_FLAGS: dict[str, list[str]] = {}
+# Per-source extra flags. attention.hip: MFMA results in arch VGPRs rather than
+# AGPRs (its kernels' whole state fits the 256 registers of 2 waves per SIMD;
+# with AGPRs the softmax copied every score tile out of them).
+EXTRA_FLAGS: dict[str, list[str]] = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _hipcc() -> str:

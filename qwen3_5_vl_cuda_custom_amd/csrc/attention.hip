@@ -755,8 +755,8 @@ __global__ __launch_bounds__(256) void flash_decode_combine(const AttnParams p) 
 //  * Software pipeline: step t runs O += V(t-1) P(t-1) and S(t+1) = K(t+1) Q^T
 //    (32 MFMAs, neither depends on step t's softmax) and the softmax of S(t),
 //    so the VALU work of the softmax runs under MFMAs already issued.
-//  * O lives in AGPRs (MFMA accumulators); the rare rescale reads, scales and
-//    writes them back in place, so the common path never copies them.
+//  * O and the S tiles live in arch VGPRs (see scale_acc), so the softmax reads
+//    S straight from the MFMA results and the rare rescale scales O in place.
 namespace fwdp {
 constexpr int kQ = 64;           // queries per block (32 per wave)
 constexpr int kKeys = 32;        // keys per tile
@@ -765,20 +765,14 @@ constexpr int kPipeStages = 8;   // K/V tile ring depth
 constexpr int kAhead = 6;        // step t issues tile t + kAhead (its slot held tile t - 2)
 constexpr int kTile = kKeys * kRowK;
 
-// acc *= alpha for an accumulator held in AGPRs. The leading s_nops give the
-// 18 wait states a 16-pass MFMA result needs before a VALU-side read; the
-// trailing ones cover the VALU write -> MFMA source-C read.
+// acc *= alpha (the rare rescale of O). This source is built with MFMA results
+// in arch VGPRs (build flag -amdgpu-mfma-vgpr-form): at 2 waves per SIMD a wave
+// has 256 registers, which the compiler otherwise splits 128 VGPRs + 128 AGPRs,
+// with the S tiles in AGPRs and 16 v_accvgpr_read copies per tile in the
+// softmax; in VGPRs the whole state fits (202 registers at D = 128).
 __device__ __forceinline__ void scale_acc(floatx16& acc, float alpha) {
-  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    float x = acc[r], tmp;
-    asm volatile("v_accvgpr_read_b32 %1, %0\n\tv_mul_f32 %1, %2, %1\n\tv_accvgpr_write_b32 %0, %1"
-                 : "+a"(x), "=&v"(tmp)
-                 : "v"(alpha));
-    acc[r] = x;
-  }
-  asm volatile("s_nop 4" ::: "memory");
+  for (int r = 0; r < 16; ++r) acc[r] *= alpha;
 }
 
 // The q prologue of the fused prefill on one query's fragments: the lane holds
@@ -806,7 +800,7 @@ __device__ __forceinline__ void q_norm_rope_frag(bf16x8 (&qf)[D / 16], const bf1
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float v = (float)qf[ks][e];
-      ss += v * v;
+      ss = fmaf(v, v, ss);
     }
   ss += __shfl_xor(ss, 32, 64);
   const float rstd = rsqrtf(ss / (float)D + eps);
@@ -820,8 +814,9 @@ __device__ __forceinline__ void q_norm_rope_frag(bf16x8 (&qf)[D / 16], const bf1
     for (int e = 0; e < 8; ++e) {
       const float lo = (float)qf[ks][e] * rstd * (float)wv[ks][e];
       const float hi = (float)qf[ks + HK][e] * rstd * (float)wv[ks + HK][e];
-      qf[ks][e] = (bf16)(lo * c[e] - hi * sn[e]);
-      qf[ks + HK][e] = (bf16)(hi * c[e] + lo * sn[e]);
+      // contraction spelled out, so the rounding does not depend on the compiler's choice
+      qf[ks][e] = (bf16)fmaf(lo, c[e], -(hi * sn[e]));
+      qf[ks + HK][e] = (bf16)fmaf(hi, c[e], lo * sn[e]);
     }
   }
 }
