@@ -97,12 +97,12 @@ int launch_generic(const void* x, const void* w, const void* w2, const void* bia
 // =====================================================================
 // Tiled MFMA path.
 // =====================================================================
-template <int BM, int BN, int WM, int WN, int EPI, int NST, int BKT, int NSTW = NST>
+template <int BM, int BN, int WM, int WN, int EPI, int NST, int BKT, int NSTW = NST, bool MF16 = false>
 int launch_tiled_cfg(GemmParams p, int64_t batch, hipStream_t st) {
   constexpr int BN_OUT = (EPI == kEpiSwiGLU) ? BN / 2 : BN;
   const int64_t tiles = q3_cdiv(p.M, BM) * q3_cdiv(p.N, BN_OUT);
   p.group_m = 8;
-  hipLaunchKernelGGL((gemm_bf16_dma_kernel<BM, BN, WM, WN, EPI, false, NST, BKT, NSTW>),
+  hipLaunchKernelGGL((gemm_bf16_dma_kernel<BM, BN, WM, WN, EPI, false, NST, BKT, NSTW, MF16>),
                      dim3((unsigned)tiles, 1, (unsigned)batch), dim3(WM * WN * 64), 0, st, p);
   Q3_LAUNCH_CHECK();
   return Q3_OK;
@@ -129,11 +129,16 @@ int launch_tiled_cfg(GemmParams p, int64_t batch, hipStream_t st) {
 // of the time of one wave of 256x256 tiles (estimate: 128 * 128 / 0.47).
 // Rings of 6 or 8 32-wide stages were no faster than 4.
 //
-// 256x192 tiles over K >= 2048 take a fourth W slot (W issued three stages
-// ahead; 2 X + 4 W slots fill the 160 KB). With the weights rotated over 384 MB
-// (past the MALL, as in a layer): M=4096 N=6144 K=4096 (q/k/v over three
-// segments) 186.1 -> 180.1 us, M=4096 N=5120 K=2048 98.4 -> 92.6 us; at
-// K=1152 10% slower.
+// The 256x256 tiles, and the 256x192 ones over K >= 2048, run the kernel's
+// 16x16x32 loop (MF16): these long K loops are power-limited, and for the same
+// work that instruction moves less data through the register file, so the
+// chip holds a higher clock. Same-box A/B, bit-identical outputs: the S=4096
+// decoder layer 1464.9 -> 1395.1 us (gate/up 633 -> 608, down 326 -> 307, o
+// 121 -> 116, q/k/v on 256x192); S=1024 475.7 -> 469.2 us. The 128x128 deep
+// ring (C5, S=1024) and the MoE expert tiles stay on 32x32x16: slower or no
+// faster with it. (The 256x192 tiles' former fourth W slot, worth 3% to q/k/v,
+// gives way: the 16x16x32 loop needs the W ring exactly one slot deeper than
+// the X ring.)
 template <int EPI>
 int launch_tiled(GemmParams p, int64_t batch, hipStream_t st) {
   constexpr int kCUs = 256;
@@ -154,16 +159,16 @@ int launch_tiled(GemmParams p, int64_t batch, hipStream_t st) {
   if constexpr (EPI == kEpiSwiGLU) {
     if (cost_c < cost_a && cost_c < cost_d) return launch_c();
     if (cost_d < cost_a) return launch_tiled_cfg<128, 256, 2, 4, EPI, 3, 64>(p, batch, st);
-    return launch_tiled_cfg<256, 256, 2, 4, EPI, 2, 64, 3>(p, batch, st);
+    return launch_tiled_cfg<256, 256, 2, 4, EPI, 2, 64, 3, true>(p, batch, st);
   } else {
     const double cost_b = waves(q3_cdiv(p.M, 256) * q3_cdiv(p.N, 192) * batch, kCUs) * 256.0 * 192.0 / 0.95;
     const double best = std::min(std::min(cost_a, cost_b), std::min(cost_c, cost_d));
     if (cost_c == best) return launch_c();
-    if (cost_b == best)  // a fourth W slot (the whole 160 KB) pays off over long K loops only
-      return p.K >= 2048 ? launch_tiled_cfg<256, 192, 4, 2, EPI, 2, 64, 4>(p, batch, st)
+    if (cost_b == best)  // long K loops: the 16x16x32 loop (power-limited); short ones the 32x32x16 loop
+      return p.K >= 2048 ? launch_tiled_cfg<256, 192, 4, 2, EPI, 2, 64, 3, true>(p, batch, st)
                          : launch_tiled_cfg<256, 192, 4, 2, EPI, 2, 64, 3>(p, batch, st);
     if (cost_d == best) return launch_tiled_cfg<128, 256, 2, 4, EPI, 3, 64>(p, batch, st);
-    return launch_tiled_cfg<256, 256, 2, 4, EPI, 2, 64, 3>(p, batch, st);
+    return launch_tiled_cfg<256, 256, 2, 4, EPI, 2, 64, 3, true>(p, batch, st);
   }
 }
 
@@ -270,7 +275,7 @@ int launch_split_k(const GemmParams& p0, int S, void* ws, hipStream_t st) {
   p.act = 0;
   p.seg.n = 1;
   p.seg.w[0] = p.W;
-  const int rc = launch_tiled_cfg<256, 256, 2, 4, kEpiStoreF32, 2, 64, 3>(p, S, st);
+  const int rc = launch_tiled_cfg<256, 256, 2, 4, kEpiStoreF32, 2, 64, 3, true>(p, S, st);
   if (rc != Q3_OK) return rc;
   const bool vec = p0.N % 8 == 0 && p0.ldc % 8 == 0 && q3_aligned(p0.C, 16) &&
                    (!p0.bias || q3_aligned(p0.bias, 16)) && (!p0.R || (q3_aligned(p0.R, 16) && p0.ldr % 8 == 0));

@@ -175,18 +175,73 @@ __device__ __forceinline__ const bf16* seg_bias(const WeightSegments& sg, int n)
 // stores 16 bytes per lane (kEpiStoreF32: 32 bytes of fp32, not rounded):
 // contiguous rows per instruction. LDS rows are BN_OUT fp32; 16-byte chunk c
 // of row r sits at chunk c ^ (r & 15).
-template <int BM, int BN_OUT, int WTM, int WTN, int TN, int TM, int EPI, int NW, int LDS_BYTES>
-__device__ __forceinline__ void store_tile_lds(const GemmParams& p, const TileCtx& t, const floatx16 (&c)[TN][TM],
-                                               int wm, int wn, int lane, float* lds) {
+// Accumulator visitors for the epilogues: f(mr, lrow, col, v) for every group
+// of 4 consecutive output columns a lane holds, where mr is the MFMA tile's
+// first row in the block tile (wave-uniform), lrow the lane's row in that
+// tile, col the group's first output column (block tile) and v its values
+// (SwiGLU applied). 32x32x16 tiles: lane l holds row l % 32 and columns 8 g +
+// 4 (l / 32) + q of register 4 g + q. SwiGLU pairs the gate / up 32-row W
+// tiles 2 i, 2 i + 1.
+template <int EPI, int WTM, int WTN, int TN, int TM, typename F>
+__device__ __forceinline__ void visit_acc32(const floatx16 (&c)[TN][TM], int wm, int wn, int lane, F&& f) {
+  constexpr int WTN_OUT = EPI == kEpiSwiGLU ? WTN / 2 : WTN;
+  constexpr int TN_OUT = EPI == kEpiSwiGLU ? TN / 2 : TN;
+  const int l32 = lane & 31, h = lane >> 5;
+#pragma unroll
+  for (int j = 0; j < TM; ++j) {
+#pragma unroll
+    for (int i = 0; i < TN_OUT; ++i) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        floatx4 v;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if constexpr (EPI == kEpiSwiGLU)
+            v[q] = silu_mul(c[2 * i][j][4 * g + q], c[2 * i + 1][j][4 * g + q]);
+          else
+            v[q] = c[i][j][4 * g + q];
+        }
+        f(wm * WTM + j * 32, l32, wn * WTN_OUT + i * 32 + 8 * g + 4 * h, v);
+      }
+    }
+  }
+}
+
+// 16x16x32 tiles: lane l holds row l % 16 and columns 4 (l / 16) + q (register
+// q). SwiGLU: the wave's W rows come in 64-row groups, 32 gate rows then the
+// 32 up rows of the same output columns, so output tile o pairs W tiles
+// 4 (o / 2) + o % 2 (gate) and that + 2 (up).
+template <int EPI, int WTM, int WTN, int TN, int TM, typename F>
+__device__ __forceinline__ void visit_acc16(const floatx4 (&c)[TN][TM], int wm, int wn, int lane, F&& f) {
+  constexpr int WTN_OUT = EPI == kEpiSwiGLU ? WTN / 2 : WTN;
+  constexpr int TN_OUT = EPI == kEpiSwiGLU ? TN / 2 : TN;
+  static_assert(EPI != kEpiSwiGLU || WTN % 64 == 0, "SwiGLU: whole 64-row gate/up groups per wave");
+  const int l16 = lane & 15, q4 = lane >> 4;
+#pragma unroll
+  for (int j = 0; j < TM; ++j) {
+#pragma unroll
+    for (int o = 0; o < TN_OUT; ++o) {
+      floatx4 v;
+      if constexpr (EPI == kEpiSwiGLU) {
+        const int gi = 4 * (o / 2) + o % 2;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = silu_mul(c[gi][j][q], c[gi + 2][j][q]);
+      } else {
+        v = c[o][j];
+      }
+      f(wm * WTM + j * 16, l16, wn * WTN_OUT + o * 16 + 4 * q4, v);
+    }
+  }
+}
+
+template <int BM, int BN_OUT, int EPI, int NW, int LDS_BYTES, typename VISIT>
+__device__ __forceinline__ void store_tile_lds(const GemmParams& p, const TileCtx& t, VISIT&& visit, float* lds) {
   constexpr int RP0 = LDS_BYTES / (BN_OUT * 4);
   constexpr int RP = RP0 >= 256 ? 256 : RP0 >= 128 ? 128 : RP0 >= 64 ? 64 : 32;  // rows per pass
   constexpr int NPASS = (BM + RP - 1) / RP;
   constexpr int C8 = BN_OUT / 8;                          // 8-column items per row
-  constexpr int WTN_OUT = EPI == kEpiSwiGLU ? WTN / 2 : WTN;
-  constexpr int TN_OUT = EPI == kEpiSwiGLU ? TN / 2 : TN;
   static_assert(BN_OUT % 64 == 0 && RP % 32 == 0, "epilogue tiling");
   const int m_begin = t.m_begin, rows_m = t.rows_m, n0_out = t.n0_out;
-  const int l32 = lane & 31, h = lane >> 5;
   const int N = p.N;
   const bool vec_ok = ((p.ldc & 7) == 0) && (reinterpret_cast<uintptr_t>(t.C) & 15) == 0 &&
                       (p.R == nullptr || ((p.ldr & 7) == 0 && (reinterpret_cast<uintptr_t>(p.R) & 15) == 0));
@@ -196,31 +251,10 @@ __device__ __forceinline__ void store_tile_lds(const GemmParams& p, const TileCt
   for (int pass = 0; pass < NPASS; ++pass) {
     const int r0 = pass * RP;
     // 1. this wave's accumulator rows of the pass -> LDS (fp32)
-#pragma unroll
-    for (int j = 0; j < TM; ++j) {
-      const int mr = wm * WTM + j * 32;  // tile row of this m-tile (wave-uniform)
-      if (mr < r0 || mr >= r0 + RP) continue;
-      const int lr = mr - r0 + l32;
-#pragma unroll
-      for (int i = 0; i < TN_OUT; ++i) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int col = wn * WTN_OUT + i * 32 + 8 * g + 4 * h;
-          floatx4 v;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            if constexpr (EPI == kEpiSwiGLU) {
-              const float gt = c[2 * i][j][4 * g + q];
-              const float up = c[2 * i + 1][j][4 * g + q];
-              v[q] = silu_mul(gt, up);
-            } else {
-              v[q] = c[i][j][4 * g + q];
-            }
-          }
-          *reinterpret_cast<floatx4*>(lds + slot(lr, col)) = v;
-        }
-      }
-    }
+    visit([&](int mr, int lrow, int col, floatx4 v) {
+      if (mr < r0 || mr >= r0 + RP) return;  // wave-uniform
+      *reinterpret_cast<floatx4*>(lds + slot(mr - r0 + lrow, col)) = v;
+    });
     __syncthreads();
     // 2. rows of the pass, 8 columns per lane, finished and stored
     const int nrows = min(RP, rows_m - r0);
@@ -317,10 +351,8 @@ __device__ __forceinline__ bool epi_rounds_first(const GemmParams& p, const Tile
 // flight before its stores. Values are those of store_tile_lds (one rounding,
 // same arithmetic). LDS rows are BN_OUT bf16; 16-byte chunk c of row r sits
 // at chunk c ^ (r & SWZ).
-template <int BM, int BN_OUT, int WTM, int WTN, int TN, int TM, int EPI, int NW, int LDS_BYTES>
-__device__ __forceinline__ void store_tile_lds_bf16(const GemmParams& p, const TileCtx& t,
-                                                    const floatx16 (&c)[TN][TM], int wm, int wn, int lane,
-                                                    bf16* lds) {
+template <int BM, int BN_OUT, int EPI, int NW, int LDS_BYTES, typename VISIT>
+__device__ __forceinline__ void store_tile_lds_bf16(const GemmParams& p, const TileCtx& t, VISIT&& visit, bf16* lds) {
   constexpr int RP0 = LDS_BYTES / (BN_OUT * 2);
   constexpr int RP1 = RP0 >= 256 ? 256 : RP0 >= 128 ? 128 : RP0 >= 64 ? 64 : 32;
   constexpr int RP = RP1 < BM ? RP1 : BM;  // rows per pass
@@ -330,14 +362,11 @@ __device__ __forceinline__ void store_tile_lds_bf16(const GemmParams& p, const T
   // blocks of 8), so a swizzled chunk stays in its row.
   constexpr int SWZ = C8 % 16 == 0 ? 15 : 7;
   static_assert(C8 % (SWZ + 1) == 0, "swizzle blocks must divide the row");
-  constexpr int WTN_OUT = EPI == kEpiSwiGLU ? WTN / 2 : WTN;
-  constexpr int TN_OUT = EPI == kEpiSwiGLU ? TN / 2 : TN;
   constexpr int NT = NW * 64;
   static_assert(BN_OUT % 64 == 0 && RP % 32 == 0, "epilogue tiling");
   constexpr int ITEMS = (RP * C8) / NT;  // chunks per thread in a full pass
   static_assert(ITEMS >= 1 && (RP * C8) % NT == 0, "whole chunks per thread");
   const int m_begin = t.m_begin, rows_m = t.rows_m, n0_out = t.n0_out;
-  const int l32 = lane & 31, h = lane >> 5;
   const int N = p.N;
   const bool vec_ok = ((p.ldc & 7) == 0) && (reinterpret_cast<uintptr_t>(t.C) & 15) == 0;
   const bool full_n = vec_ok && n0_out + BN_OUT <= N;
@@ -365,31 +394,13 @@ __device__ __forceinline__ void store_tile_lds_bf16(const GemmParams& p, const T
   for (int pass = 0; pass < NPASS; ++pass) {
     const int r0 = pass * RP;
     // 1. this wave's accumulator rows of the pass -> LDS, rounded once
+    visit([&](int mr, int lrow, int col, floatx4 v) {
+      if (mr < r0 || mr >= r0 + RP) return;  // wave-uniform
+      bf16x4 b;
 #pragma unroll
-    for (int j = 0; j < TM; ++j) {
-      const int mr = wm * WTM + j * 32;  // tile row of this m-tile (wave-uniform)
-      if (mr < r0 || mr >= r0 + RP) continue;
-      const int lr = mr - r0 + l32;
-#pragma unroll
-      for (int i = 0; i < TN_OUT; ++i) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int col = wn * WTN_OUT + i * 32 + 8 * g + 4 * h;
-          bf16x4 v;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            if constexpr (EPI == kEpiSwiGLU) {
-              const float gt = c[2 * i][j][4 * g + q];
-              const float up = c[2 * i + 1][j][4 * g + q];
-              v[q] = f2bf(silu_mul(gt, up));
-            } else {
-              v[q] = f2bf(c[i][j][4 * g + q]);
-            }
-          }
-          *reinterpret_cast<bf16x4*>(lds + slot(lr, col >> 3) + (col & 7)) = v;
-        }
-      }
-    }
+      for (int q = 0; q < 4; ++q) b[q] = f2bf(v[q]);
+      *reinterpret_cast<bf16x4*>(lds + slot(mr - r0 + lrow, col >> 3) + (col & 7)) = b;
+    });
     __syncthreads();
     // 2. rows of the pass -> memory, one 16-byte chunk per lane and item
     const int nrows = min(RP, rows_m - r0);
@@ -435,7 +446,13 @@ __device__ __forceinline__ int dma_swz(int r) {
 // q + 1 are read while the MFMAs of step q run, and each stage's barrier sits
 // before its last step's MFMAs (which overlap the first reads of the next
 // stage), so no wave starts a stage waiting on LDS.
-template <int BM, int BN, int WM, int WN, int EPI, bool GROUPED, int NST, int BKT, int NSTW = NST>
+//
+// MF16: the same ring with v_mfma_f32_16x16x32_bf16 instead of 32x32x16. For
+// the same work it moves less data through the register file (operands 4 KB
+// + accumulators 4 KB per 32K flops, against 2 KB + 8 KB): on random data
+// under the power cap a pure MFMA loop sustains ~2.03 PFLOP/s with it against
+// ~1.80 with 32x32x16 (MI355X), and these GEMMs run power-limited.
+template <int BM, int BN, int WM, int WN, int EPI, bool GROUPED, int NST, int BKT, int NSTW = NST, bool MF16 = false>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmParams p) {
   constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM;
@@ -567,6 +584,145 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
     issue_w(j + NSTW);
   };
 
+  if constexpr (MF16) {
+    // 16x16x32 loop. Per wave and 32-wide K step: T16N W fragments (A) and
+    // T16M X fragments (B), 16 rows x 32 k each (lane: row l % 16, 16-byte
+    // chunk 4 ks + l / 16 of the 64-wide stage row), T16N x T16M MFMAs in
+    // column order (X tile outer). W fragments are double-buffered; each X
+    // fragment is re-read for the next step right after its column's last
+    // MFMA (a single set: the accumulators take 128 registers at 128x64 per
+    // wave). Two K steps per stage: the first carries W(kt + NST), the last
+    // crosses the barrier as in the 32x32 loop (its first NQ MFMAs use every
+    // fragment of the step) and carries X(kt + NST).
+    static_assert(BKT == 64 && NSTW == NST + 1, "16x16x32 loop: 64-wide stages, W ring one slot deeper");
+    constexpr int T16N = WTN / 16, T16M = WTM / 16;
+    constexpr int NQ = T16N > T16M ? T16N : T16M;
+    constexpr int NM16 = T16N * T16M;
+    floatx4 a16[T16N][T16M];
+#pragma unroll
+    for (int i = 0; i < T16N; ++i)
+#pragma unroll
+      for (int j = 0; j < T16M; ++j) a16[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    bf16x8 fw[2][T16N], fx[T16M];
+    const int l16 = lane & 15, q4 = lane >> 4;
+    const int rn = wn * WTN, rm = wm * WTM;
+    auto rd_w = [&](int buf, int kt, int ks, int i) {
+      const bf16* sw = smem + NST * kStageX + (kt % NSTW) * kStageW;
+      const int r = rn + i * 16 + l16, c = ks * 4 + q4;
+      fw[buf][i] = *reinterpret_cast<const bf16x8*>(sw + r * BKT + ((c ^ dma_swz<BKT>(r)) << 3));
+    };
+    auto rd_x = [&](int kt, int ks, int j) {
+      const bf16* sx = smem + (kt % NST) * kStageX;
+      const int r = rm + j * 16 + l16, c = ks * 4 + q4;
+      fx[j] = *reinterpret_cast<const bf16x8*>(sx + r * BKT + ((c ^ dma_swz<BKT>(r)) << 3));
+    };
+    auto mf = [&](int buf, int i, int j) { a16[i][j] = mfma16x16x32(fw[buf][i], fx[j], a16[i][j]); };
+    // MFMA (i, j) is among the last step's first NQ (before the barrier)
+    auto pre = [](int i, int j) {
+      bool in = false;
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) in = in || (q % T16N == i && q % T16M == j);
+      return in;
+    };
+    auto dma_x = [&](int kx_stage, int d) {
+      const int k = kx_stage * BKT + dc * 8;
+      const uint32_t off = (k < K && xoff[d] != kOOB) ? xoff[d] + (uint32_t)k * 2u : kOOB;
+      dma16(rx, off, xslot(kx_stage) + (uint32_t)((wave + NW * d) * 1024));
+    };
+    auto dma_w16 = [&](int kw, int i) {
+      const int k = kw * BKT + dc * 8;
+      const uint32_t off = (k < K && woff[i] != kOOB) ? woff[i] + (uint32_t)k * 2u : kOOB;
+      dma16(make_rsrc(wsrc[i], (int64_t)wrows[i] * ldw * 2), off, wslot(kw) + (uint32_t)((wave + NW * i) * 1024));
+    };
+
+#pragma unroll
+    for (int j = 0; j < NST; ++j) {
+      issue_w(j);
+      issue_x(j);
+    }
+    vm_wait<(NST - 1) * (PX + PW)>();  // stage 0 has landed
+    __syncthreads();
+
+    auto main16 = [&](auto active_c) {
+      constexpr bool A = decltype(active_c)::value;
+      if constexpr (A) {
+#pragma unroll
+        for (int i = 0; i < T16N; ++i) rd_w(0, 0, 0, i);
+#pragma unroll
+        for (int j = 0; j < T16M; ++j) rd_x(0, 0, j);
+      }
+      for (int kt = 0; kt < nk; ++kt) {
+        // step 0: W(kt + NST) between the MFMAs, step 1's fragments read ahead
+        constexpr int gw = (NM16 + PW - 1) / PW;
+        int d = 0;
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (A) {
+#pragma unroll
+          for (int j = 0; j < T16M; ++j) {
+#pragma unroll
+            for (int i = 0; i < T16N; ++i) {
+              const int m = j * T16N + i;
+              mf(0, i, j);
+              if (m < T16N) rd_w(1, kt, 1, m);
+              if (i == T16N - 1) rd_x(kt, 1, j);
+              if (d < PW && m % gw == gw - 1) dma_w16(kt + NST, d++);
+              __builtin_amdgcn_sched_barrier(0);
+            }
+          }
+        }
+#pragma unroll
+        for (; d < PW; ++d) dma_w16(kt + NST, d);
+        __builtin_amdgcn_sched_barrier(0);
+        // step 1: the NQ MFMAs that use every fragment, the barrier, then the
+        // rest with stage kt + 1's first-step reads and X(kt + NST)
+        if constexpr (A) {
+#pragma unroll
+          for (int q = 0; q < NQ; ++q) {
+            mf(1, q % T16N, q % T16M);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+        vm_wait<kWait>();                         // this wave's part of stage kt + 1 has landed
+        asm volatile("s_barrier" ::: "memory");  // every wave's; no wave reads stage kt any more
+        __builtin_amdgcn_sched_barrier(0);
+        d = 0;
+        if constexpr (A) {
+#pragma unroll
+          for (int i = 0; i < T16N; ++i) rd_w(0, kt + 1, 0, i);
+          __builtin_amdgcn_sched_barrier(0);
+          constexpr int gx = (NM16 - NQ + PX - 1) / PX;
+          int m = 0;
+#pragma unroll
+          for (int j = 0; j < T16M; ++j) {
+#pragma unroll
+            for (int i = 0; i < T16N; ++i) {
+              if (!pre(i, j)) {
+                mf(1, i, j);
+                if (d < PX && m % gx == gx - 1) dma_x(kt + NST, d++);
+                ++m;
+              }
+              if (i == T16N - 1) rd_x(kt + 1, 0, j);
+              __builtin_amdgcn_sched_barrier(0);
+            }
+          }
+        }
+#pragma unroll
+        for (; d < PX; ++d) dma_x(kt + NST, d);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    if (rm < rows_m)
+      main16(std::true_type{});
+    else
+      main16(std::false_type{});
+    vm_wait<0>();  // the trailing zero-fill DMAs must land before the block's LDS is reused
+
+    auto visit = [&](auto&& f) { visit_acc16<EPI, WTM, WTN, T16N, T16M>(a16, wm, wn, lane, f); };
+    if (epi_rounds_first<EPI>(p, tc))
+      store_tile_lds_bf16<BM, BN_OUT, EPI, NW, kRing * 2>(p, tc, visit, smem);
+    else if constexpr (EPI == kEpiStore || EPI == kEpiStoreF32)
+      store_tile_lds<BM, BN_OUT, EPI, NW, kRing * 2>(p, tc, visit, reinterpret_cast<float*>(smem));
+  } else {
   WaveAcc<TN, TM> acc;
   acc.zero();
   const int l32 = lane & 31, h = lane >> 5;
@@ -811,11 +967,12 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
     main_loop(std::false_type{});
   vm_wait<0>();  // the trailing zero-fill DMAs must land before the block's LDS is reused
 
+  auto visit = [&](auto&& f) { visit_acc32<EPI, WTM, WTN, TN, TM>(acc.c, wm, wn, lane, f); };
   if (epi_rounds_first<EPI>(p, tc))
-    store_tile_lds_bf16<BM, BN_OUT, WTM, WTN, TN, TM, EPI, NW, kRing * 2>(p, tc, acc.c, wm, wn, lane, smem);
+    store_tile_lds_bf16<BM, BN_OUT, EPI, NW, kRing * 2>(p, tc, visit, smem);
   else if constexpr (EPI == kEpiStore || EPI == kEpiStoreF32)
-    store_tile_lds<BM, BN_OUT, WTM, WTN, TN, TM, EPI, NW, kRing * 2>(p, tc, acc.c, wm, wn, lane,
-                                                                    reinterpret_cast<float*>(smem));
+    store_tile_lds<BM, BN_OUT, EPI, NW, kRing * 2>(p, tc, visit, reinterpret_cast<float*>(smem));
+  }  // 32x32x16 loop
 }
 
 }  // namespace q3
