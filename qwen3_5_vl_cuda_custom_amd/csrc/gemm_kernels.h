@@ -474,7 +474,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
   constexpr int DX = BM / RPI, DW = BN / RPI;
   static_assert((DX + DW) % NW == 0 && DX % NW == 0, "DMA instructions must split evenly over the waves");
   constexpr int PX = DX / NW, PW = DW / NW;  // per wave and stage
-  static_assert(TN * TM >= TN + TM, "the interleave needs more MFMAs than fragment reads");
+  static_assert(MF16 || TN * TM >= TN + TM, "the interleave needs more MFMAs than fragment reads");
 
   __shared__ __attribute__((aligned(1024))) bf16 smem[kRing];
 
