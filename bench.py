@@ -57,6 +57,47 @@ def time_gpu(fn, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
+def time_launch_modes(step, first, steps: int, warmup: int):
+    """Time `step` with eager launches, then replayed from a HIP graph, each
+    as max(HIP events, host wall) per step. `first(out)` picks the tensor of a
+    step's output that every replay must reproduce bit for bit (checked before
+    and after the timed replays). Returns (ms, ms_eager, ms_graph, launch):
+    the faster mode's time, both times, and which mode that was.
+
+    On a box whose host is slow or contended, eager launches have left the GPU
+    idle between kernels (3.2 ms per S=4096 layer against 1.5 with every kernel
+    at its usual speed); with a fast host, eager launches run back to back and
+    the graph's node-to-node dispatch costs ~2-4 us per kernel more (1.382
+    against 1.435 ms in one run)."""
+    import torch
+    from qwen3_5_vl_cuda_custom_amd.modules import StepGraph
+
+    def timed(fn):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ms_events = time_gpu(fn, steps, 0)
+        torch.cuda.synchronize()
+        return max(ms_events, (time.perf_counter() - t0) * 1e3 / steps)
+
+    for _ in range(warmup):
+        step()
+    ms_eager = timed(step)
+    ref = first(step()).clone()
+    graph = StepGraph(step)
+    graph.replay()
+    torch.cuda.synchronize()
+    if not torch.equal(first(graph.out), ref):
+        raise RuntimeError("bench: the graph replay of the step differs from the eager step")
+    for _ in range(warmup):
+        graph.replay()
+    ms_graph = timed(graph.replay)
+    if not torch.equal(first(graph.out), ref):
+        raise RuntimeError("bench: a timed graph replay of the step differs from the eager step")
+    del graph
+    launch = "HIP graph replay" if ms_graph <= ms_eager else "eager launches"
+    return min(ms_graph, ms_eager), ms_eager, ms_graph, launch
+
+
 def usable_cpus() -> int:
     """CPUs this process may run on: its affinity set, capped by a cgroup CPU quota if one is set."""
     n = len(os.sched_getaffinity(0))
@@ -226,18 +267,21 @@ def decode_case(cfg, layer, x, pos, lens, k_cache, v_cache, y):
 
 def other_configs(torch, W, dev: str, warmup: int, cases: dict) -> dict:
     """The other BASELINE configurations, one GPU each: C2 at S=1024 and 16384,
-    the C4 MoE layer (4096 tokens) and the C5 patch embed + vision block."""
+    the C4 MoE layer (4096 tokens) and the C5 patch embed + vision block. Each
+    takes the faster of eager launches and a HIP graph replay (both reported,
+    the replay checked bit-identical to the eager step)."""
     out = {}
     for S in (1024, 16384):
         cfg = W.C2
         layer = W.make_text_layer(cfg, torch.bfloat16, dev, seed=0)
         x, pos = W.text_inputs(cfg, 1, S, torch.bfloat16, dev, seed=0)
         b = W.make_rope(cfg, dev).bind(pos)
-        ms = time_gpu(lambda: layer(x, b), 5, max(2, warmup // 2))
+        ms, me, mg, launch = time_launch_modes(lambda: layer(x, b), lambda o: o[0], 5, max(2, warmup // 2))
         fl = cfg.gemm_flops_per_token() * S + cfg.causal_attn_flops(S)
         out[f"c2_prefill_s{S}"] = {"ms": round(ms, 4), "tok_s": round(S / (ms / 1e3), 1),
                                    "tflops": round(fl / (ms / 1e3) / 1e12, 1),
-                                   "mfma_frac": round(fl / (ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+                                   "mfma_frac": round(fl / (ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                                   "launch": launch, "eager_ms": round(me, 4), "graph_ms": round(mg, 4)}
         log(f"C2 prefill S={S}: {out[f'c2_prefill_s{S}']}")
         del layer, x
     cfg = W.C4
@@ -246,7 +290,7 @@ def other_configs(torch, W, dev: str, warmup: int, cases: dict) -> dict:
     b = W.make_rope(cfg, dev).bind(pos)
     y, logits, _ = layer(x, b)
     cases["c4_moe_layer_t4096"] = text_layer_case(cfg, layer, x, pos, y, router_logits=logits)
-    ms = time_gpu(lambda: layer(x, b), 10, warmup)
+    ms, me, mg, launch = time_launch_modes(lambda: layer(x, b), lambda o: o[0], 10, warmup)
     fl = cfg.gemm_flops_per_token() * 4096 + cfg.causal_attn_flops(4096)
     # Both bounds: MFMA on the layer's FLOPs, HBM on the bytes it must move at
     # least once (every weight, the token activations in and out).
@@ -259,7 +303,8 @@ def other_configs(torch, W, dev: str, warmup: int, cases: dict) -> dict:
                                  "hbm_gbs": round((wbytes + abytes) / (ms / 1e3) / 1e9, 1),
                                  "hbm_frac": round((wbytes + abytes) / (ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
                                  "floor_ms": {"mfma": round(fl / PEAK_BF16_TFLOPS / 1e9, 4),
-                                              "hbm": round((wbytes + abytes) / PEAK_HBM_GBS / 1e6, 4)}}
+                                              "hbm": round((wbytes + abytes) / PEAK_HBM_GBS / 1e6, 4)},
+                                 "launch": launch, "eager_ms": round(me, 4), "graph_ms": round(mg, 4)}
     log(f"C4 MoE layer: {out['c4_moe_layer_t4096']}")
     del layer, x
     v = W.C5
@@ -282,12 +327,13 @@ def other_configs(torch, W, dev: str, warmup: int, cases: dict) -> dict:
                               sin=sc, eps=v.eps, rd=rd)
     cases["c5_vision_patch_embed_block"] = (yv.detach().float().cpu(), run_vis)
 
-    ms = time_gpu(vis, 10, warmup)
+    ms, me, mg, launch = time_launch_modes(vis, lambda o: o, 10, warmup)
     fl = v.flops()
     n = v.images * v.patches_per_image
     out["c5_vision_patch_embed_block"] = {"ms": round(ms, 4), "patches_s": round(n / (ms / 1e3), 1),
                                           "tflops": round(fl / (ms / 1e3) / 1e12, 1),
-                                          "mfma_frac": round(fl / (ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+                                          "mfma_frac": round(fl / (ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                                          "launch": launch, "eager_ms": round(me, 4), "graph_ms": round(mg, 4)}
     log(f"C5 vision: {out['c5_vision_patch_embed_block']}")
     return out
 
@@ -431,48 +477,15 @@ def main() -> int:
         log(f"per-kernel TFLOP/s: {detail}")
         del a, act, q, kk
 
-        for _ in range(args.warmup):
-            step()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        ms_events = time_gpu(step, args.steps, 0)
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        ms_eager = max(ms_events, wall * 1e3 / args.steps)
-        log(f"prefill S={S}, eager launches: {ms_eager:.3f} ms/layer (HIP events {ms_events:.3f} ms, host wall "
-            f"{wall * 1e3 / args.steps:.3f} ms per step)")
-        # The same step replayed from a HIP graph (one launch per step). The
-        # headline takes the faster of the two launch modes, both reported: on a
-        # box whose host is slow or contended, eager launches have left the GPU
-        # idle between kernels (3.2 ms per layer against 1.5 with every kernel
-        # at its usual speed); with a fast host, eager launches run back to back
-        # and the graph's node-to-node dispatch costs ~2-4 us per kernel more
-        # (1.382 against 1.435 ms in one run). The replay must equal the eager step.
-        ref = step()[0].clone()
-        graph = StepGraph(step)
-        graph.replay()
-        torch.cuda.synchronize()
-        if not torch.equal(graph.out[0], ref):
-            raise RuntimeError("bench: the graph replay of the layer step differs from the eager step")
-        for _ in range(args.warmup):
-            graph.replay()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        ms_events = time_gpu(graph.replay, args.steps, 0)
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        if not torch.equal(graph.out[0], ref):
-            raise RuntimeError("bench: a timed graph replay of the layer step differs from the eager step")
-        ms_graph = max(ms_events, wall * 1e3 / args.steps)
-        del graph
-        launch = "HIP graph replay" if ms_graph <= ms_eager else "eager launches"
-        ms = min(ms_graph, ms_eager)
+        # The headline takes the faster of eager launches and a HIP graph
+        # replay of the step, both reported; the replay must equal the eager step.
+        ms, ms_eager, ms_graph, launch = time_launch_modes(step, lambda o: o[0], args.steps, args.warmup)
         tok_s = S / (ms / 1e3)
         layer_flop = cfg.gemm_flops_per_token() * S + cfg.causal_attn_flops(S)
         layer_tflops = layer_flop / (ms / 1e3) / 1e12
         log(f"prefill S={S}: {ms:.3f} ms/layer, {tok_s:,.0f} tok/s, {layer_tflops:.1f} TFLOP/s "
-            f"({layer_tflops / PEAK_BF16_TFLOPS:.1%} of bf16 peak), {launch}; HIP graph replay {ms_graph:.3f} ms "
-            f"(HIP events {ms_events:.3f} ms, host wall {wall * 1e3 / args.steps:.3f} ms per step), eager {ms_eager:.3f} ms")
+            f"({layer_tflops / PEAK_BF16_TFLOPS:.1%} of bf16 peak), {launch}; HIP graph replay {ms_graph:.3f} ms, "
+            f"eager {ms_eager:.3f} ms")
 
         # Dominant kernel: the fused gate/up/SwiGLU GEMM on the post-attention activations.
         h = layer.post_attention_layernorm(x)
