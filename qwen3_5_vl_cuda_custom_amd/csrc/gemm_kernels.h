@@ -643,6 +643,18 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
     vm_wait<(NST - 1) * (PX + PW)>();  // stage 0 has landed
     __syncthreads();
 
+    // Wave priority (256-row tiles): a wave runs the second half of each stage
+    // (after the barrier: the next stage's first reads, the remaining MFMAs,
+    // X(kt + NST)) at priority 1 and the first half at 0. The two waves of a
+    // SIMD run the same schedule, so whichever has fallen behind, still in a
+    // second half while the other has started the next stage, issues first,
+    // and the pair meets the next barrier closer together. Same instructions,
+    // same results; same-box A/B at S=4096: gate/up 617 -> 604 and 620 -> 613
+    // us, down 311 -> 303 and 314 -> 307, the layer 1390.7 -> 1369.5 and
+    // 1404.2 -> 1387.7 us. The 128x128 ring (S=1024 o, C5) was no faster with
+    // it. Prioritising only the post-barrier reads, or the first half instead,
+    // gained nothing.
+    constexpr bool kPrio = BM == 256;
     auto main16 = [&](auto active_c) {
       constexpr bool A = decltype(active_c)::value;
       if constexpr (A) {
@@ -686,6 +698,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
         asm volatile("s_barrier" ::: "memory");  // every wave's; no wave reads stage kt any more
         __builtin_amdgcn_sched_barrier(0);
         d = 0;
+        if constexpr (kPrio) __builtin_amdgcn_s_setprio(1);
         if constexpr (A) {
 #pragma unroll
           for (int i = 0; i < T16N; ++i) rd_w(0, kt + 1, 0, i);
@@ -708,6 +721,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
         }
 #pragma unroll
         for (; d < PX; ++d) dma_x(kt + NST, d);
+        if constexpr (kPrio) __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_sched_barrier(0);
       }
     };
