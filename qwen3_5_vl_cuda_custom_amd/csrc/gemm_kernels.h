@@ -643,17 +643,19 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
     vm_wait<(NST - 1) * (PX + PW)>();  // stage 0 has landed
     __syncthreads();
 
-    // Wave priority (256-row tiles): a wave runs the second half of each stage
-    // (after the barrier: the next stage's first reads, the remaining MFMAs,
-    // X(kt + NST)) at priority 1 and the first half at 0. The two waves of a
-    // SIMD run the same schedule, so whichever has fallen behind, still in a
-    // second half while the other has started the next stage, issues first,
-    // and the pair meets the next barrier closer together. Same instructions,
-    // same results; same-box A/B at S=4096: gate/up 617 -> 604 and 620 -> 613
-    // us, down 311 -> 303 and 314 -> 307, the layer 1390.7 -> 1369.5 and
-    // 1404.2 -> 1387.7 us. The 128x128 ring (S=1024 o, C5) was no faster with
-    // it. Prioritising only the post-barrier reads, or the first half instead,
-    // gained nothing.
+    // Wave priority (256-row tiles), falling from one stage barrier to the
+    // next: 2 after the barrier (the next stage's first reads, the remaining
+    // MFMAs, X(kt + NST)), 1 for the first half of the next stage's first K
+    // step, 0 from there to the barrier. The two waves of a SIMD run the same
+    // schedule, so whichever has fallen behind issues first, and the pair
+    // meets the next barrier closer together. Same instructions, same
+    // results. Same-box A/Bs at S=4096, two levels (2 = 1 after the barrier,
+    // 0 elsewhere) against none: gate/up 617 -> 604 and 620 -> 613 us, down
+    // 311 -> 303 and 314 -> 307, the layer 1390.7 -> 1369.5 and 1404.2 ->
+    // 1387.7 us; three levels against two: the layer 1340.6 -> 1334.4 and
+    // 1421.4 -> 1409.8 us, C4 852 -> 846 us. The 128x128 ring (S=1024 o, C5)
+    // was no faster with it. Prioritising only the post-barrier reads, or the
+    // first half of the stage instead, gained nothing.
     constexpr bool kPrio = BM == 256;
     auto main16 = [&](auto active_c) {
       constexpr bool A = decltype(active_c)::value;
@@ -664,6 +666,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
         for (int j = 0; j < T16M; ++j) rd_x(0, 0, j);
       }
       for (int kt = 0; kt < nk; ++kt) {
+        if constexpr (kPrio) __builtin_amdgcn_s_setprio(1);
         // step 0: W(kt + NST) between the MFMAs, step 1's fragments read ahead
         constexpr int gw = (NM16 + PW - 1) / PW;
         int d = 0;
@@ -675,6 +678,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
             for (int i = 0; i < T16N; ++i) {
               const int m = j * T16N + i;
               mf(0, i, j);
+              if (kPrio && m == NM16 / 2) __builtin_amdgcn_s_setprio(0);
               if (m < T16N) rd_w(1, kt, 1, m);
               if (i == T16N - 1) rd_x(kt, 1, j);
               if (d < PW && m % gw == gw - 1) dma_w16(kt + NST, d++);
@@ -698,7 +702,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
         asm volatile("s_barrier" ::: "memory");  // every wave's; no wave reads stage kt any more
         __builtin_amdgcn_sched_barrier(0);
         d = 0;
-        if constexpr (kPrio) __builtin_amdgcn_s_setprio(1);
+        if constexpr (kPrio) __builtin_amdgcn_s_setprio(2);
         if constexpr (A) {
 #pragma unroll
           for (int i = 0; i < T16N; ++i) rd_w(0, kt + 1, 0, i);
@@ -721,9 +725,9 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
         }
 #pragma unroll
         for (; d < PX; ++d) dma_x(kt + NST, d);
-        if constexpr (kPrio) __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_sched_barrier(0);
       }
+      if constexpr (kPrio) __builtin_amdgcn_s_setprio(0);
     };
     if (rm < rows_m)
       main16(std::true_type{});
