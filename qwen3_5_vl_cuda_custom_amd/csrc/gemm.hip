@@ -112,10 +112,13 @@ int launch_tiled_cfg(GemmParams p, int64_t batch, hipStream_t st) {
 // times the block's work over its relative MFMA efficiency (measured on
 // MI355X): 256x256 (8 waves, 64-wide K stages: 2 X slots, 3 W slots, the
 // whole 160 KB of LDS; 1 block per CU) 1.0,
-// 128x256 (8 waves, 64-wide K stages x 3: the third stage, which only this
-// tile's 144 KB ring leaves room for, hides the HBM latency of weights read
-// once per layer: with weights rotated past the MALL, M=1024 gate/up 243 ->
-// 189 us, M=4096 o 165 -> 131 us) 0.9, 256x192 (8 waves, 64-wide K
+// 128x256 (8 waves, 64-wide K stages; over K >= 2048 the 16x16x32 loop with
+// 2 X and 3 W slots and the wave priority of the 256-row tiles, else the
+// 32x32x16 loop with 3 stages, 144 KB. The third stage hides the HBM latency
+// of weights read once per layer: with weights rotated past the MALL, M=1024
+// gate/up 243 -> 189 us, M=4096 o 165 -> 131 us. The 16x16x32 form with the
+// priority: M=1024 gate/up 184-185 -> 173-174 us, q/k/v 59-61 -> 58, the
+// S=1024 layer 464-466 -> 451-456 us, bit-identical) 0.9, 256x192 (8 waves, 64-wide K
 // stages, 2 X and 3 W slots; plain epilogue only) 0.95, 128x128 (4 waves; 2
 // blocks per CU) 0.75. The third W slot (weights are read from HBM once per
 // layer, activations from L2): M=4096 q/k/v 181 -> 170 us, gate/up 650 ->
@@ -134,9 +137,9 @@ int launch_tiled_cfg(GemmParams p, int64_t batch, hipStream_t st) {
 // work that instruction moves less data through the register file, so the
 // chip holds a higher clock. Same-box A/B, bit-identical outputs: the S=4096
 // decoder layer 1464.9 -> 1395.1 us (gate/up 633 -> 608, down 326 -> 307, o
-// 121 -> 116, q/k/v on 256x192); S=1024 475.7 -> 469.2 us. The 128x128 deep
-// ring (C5, S=1024) and the MoE expert tiles stay on 32x32x16: slower or no
-// faster with it. (The 256x192 tiles' former fourth W slot, worth 3% to q/k/v,
+// 121 -> 116, q/k/v on 256x192); S=1024 475.7 -> 469.2 us. The MoE expert
+// tiles stay on 32x32x16: no faster with it. (The 128x128 deep ring and the
+// 128x256 tiles take it in their own forms: launch_c, launch_d.) (The 256x192 tiles' former fourth W slot, worth 3% to q/k/v,
 // gives way: the 16x16x32 loop needs the W ring exactly one slot deeper than
 // the X ring.)
 template <int EPI>
@@ -163,9 +166,13 @@ int launch_tiled(GemmParams p, int64_t batch, hipStream_t st) {
     return c_deep ? launch_tiled_cfg<128, 128, 2, 2, EPI, 4, 64, 5>(p, batch, st)
                   : launch_tiled_cfg<128, 128, 2, 2, EPI, 4, 32>(p, batch, st);
   };
+  auto launch_d = [&]() {
+    return p.K >= 2048 ? launch_tiled_cfg<128, 256, 2, 4, EPI, 2, 64, 3, true>(p, batch, st)
+                       : launch_tiled_cfg<128, 256, 2, 4, EPI, 3, 64>(p, batch, st);
+  };
   if constexpr (EPI == kEpiSwiGLU) {
     if (cost_c < cost_a && cost_c < cost_d) return launch_c();
-    if (cost_d < cost_a) return launch_tiled_cfg<128, 256, 2, 4, EPI, 3, 64>(p, batch, st);
+    if (cost_d < cost_a) return launch_d();
     return launch_tiled_cfg<256, 256, 2, 4, EPI, 2, 64, 3, true>(p, batch, st);
   } else {
     const double cost_b = waves(q3_cdiv(p.M, 256) * q3_cdiv(p.N, 192) * batch, kCUs) * 256.0 * 192.0 / 0.95;
@@ -174,7 +181,7 @@ int launch_tiled(GemmParams p, int64_t batch, hipStream_t st) {
     if (cost_b == best)  // long K loops: the 16x16x32 loop (power-limited); short ones the 32x32x16 loop
       return p.K >= 2048 ? launch_tiled_cfg<256, 192, 4, 2, EPI, 2, 64, 3, true>(p, batch, st)
                          : launch_tiled_cfg<256, 192, 4, 2, EPI, 2, 64, 3>(p, batch, st);
-    if (cost_d == best) return launch_tiled_cfg<128, 256, 2, 4, EPI, 3, 64>(p, batch, st);
+    if (cost_d == best) return launch_d();
     return launch_tiled_cfg<256, 256, 2, 4, EPI, 2, 64, 3, true>(p, batch, st);
   }
 }

@@ -643,7 +643,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
     vm_wait<(NST - 1) * (PX + PW)>();  // stage 0 has landed
     __syncthreads();
 
-    // Wave priority (256-row tiles), falling from one stage barrier to the
+    // Wave priority (256-row and 128x256 tiles), falling from one stage barrier to the
     // next: 2 after the barrier (the next stage's first reads, the remaining
     // MFMAs, X(kt + NST)), 1 for the first half of the next stage's first K
     // step, 0 from there to the barrier. The two waves of a SIMD run the same
@@ -656,7 +656,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
     // 1421.4 -> 1409.8 us, C4 852 -> 846 us. The 128x128 ring (S=1024 o, C5)
     // was no faster with it. Prioritising only the post-barrier reads, or the
     // first half of the stage instead, gained nothing.
-    constexpr bool kPrio = BM == 256;
+    constexpr bool kPrio = BM == 256 || BN == 256;  // the 256-row and 128x256 tiles
     auto main16 = [&](auto active_c) {
       constexpr bool A = decltype(active_c)::value;
       if constexpr (A) {

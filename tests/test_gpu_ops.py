@@ -89,6 +89,25 @@ def test_matmul_split_k(M, N, Kd, bias, res):
     assert torch.equal(y, again), "the split-K path must be deterministic"
 
 
+@pytest.mark.parametrize("M,N,Kd,swiglu", [
+    (1024, 12288, 4096, True),   # the S=1024 gate/up: 768 tiles of 128x256 on the 16x16x32 loop
+    (1000, 6000, 4096, False),   # q/k/v-sized, ragged M and N: 128x256 tiles, 16x16x32 loop, bias
+    (1024, 6144, 1024, False),   # K < 2048: the same tiles on the 32x32x16 loop
+])
+def test_matmul_128x256_tiles(M, N, Kd, swiglu):
+    std = Kd ** -0.5
+    x = rnd(M, Kd, seed=90)
+    if swiglu:
+        wg, wu = rnd(N, Kd, seed=91, std=std / 2), rnd(N, Kd, seed=92, std=std / 2)
+        y = K.matmul_swiglu(gpu(x), gpu(wg), gpu(wu))
+        ref = O.swiglu(O.linear(f32(x), f32(wg)), O.linear(f32(x), f32(wu)))
+    else:
+        w, b = rnd(N, Kd, seed=91, std=std), rnd(N, seed=92, std=0.02)
+        y = K.matmul(gpu(x), gpu(w), gpu(b))
+        ref = O.linear(f32(x), f32(w), f32(b))
+    assert_bf16_close(y, ref, what=f"128x256 tiles {M}x{N}x{Kd} swiglu={swiglu}")
+
+
 @pytest.mark.parametrize("M", [7, 32, 300, 1024, 4100, 8192])
 def test_matmul_swiglu(M):
     x, wg, wu = rnd(M, 1024, seed=7), rnd(1536, 1024, seed=8, std=0.02), rnd(1536, 1024, seed=9, std=0.02)
