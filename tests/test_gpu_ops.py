@@ -178,6 +178,9 @@ def test_decode_gemv_shapes(M):
     (32, (128,), 2048, "plain"),           # router-sized: 8 rows per block, 16 blocks
     (17, (1024,), 16400, "residual"),      # M > 8, K > 16384: the stream-K kernel
     (17, (512,), 16384, "swiglu"),         # last K of the row-owned kernel
+    (20, (16000,), 2056, "residual"),      # 63 rows per block (4 row groups, 128-k stages), K tail
+    (13, (10000,), 1000, "bias"),          # 40 rows per block (3 row groups), one X tile
+    (30, (3000,), 1160, "swiglu"),         # 12 gate + 12 up rows per block, K tail inside a stage
 ])
 def test_gemv_edges(M, ns, Kd, kind):
     """Decode shapes (M <= 32) on the row-owned GEMV (M <= 8, or K <= 16384) and
@@ -218,6 +221,9 @@ def test_gemv_edges(M, ns, Kd, kind):
     (32, (12288,), 4096, "swiglu"),            # the decode gate/up shape (B=32)
     (5, (200,), 4104, "swiglu"),               # M <= 8 also stages X when fused
     (32, (512,), 20480, "plain"),              # K past the row-owned limit: still row-owned
+    (32, (6000,), 8192, "plain"),              # the norm weight's LDS copy at its largest K
+    (20, (3000,), 8200, "swiglu"),             # K past it: the norm staged through registers
+    (12, (16000,), 2056, "bias"),              # 63 rows per block, one X tile, K tail
 ])
 def test_rmsnorm_matmul_fused(M, ns, Kd, kind):
     """RMSNorm fused into the decode projection (q3_rmsnorm_matmul_segments /
