@@ -29,20 +29,20 @@
 //
 // The split-K reduction above costs a few microseconds of dependent memory
 // round trips at the end of every call (piece stores, counter atomics, the
-// last block's piece loads). Where that outweighs what split-K saves, the
-// row-owned kernel (gemv_rows_kernel) runs instead: each block owns r
-// consecutive weight rows of one segment over all of K, so nothing leaves the
-// block before the epilogue:
+// last block's piece loads). Where that outweighs what split-K saves, a
+// row-owned kernel runs instead: each block owns r consecutive weight rows of
+// one segment over all of K, so nothing leaves the block before the epilogue:
 //  * r is the smallest row count that gives every CU at most one block; the
 //    rows form 16-row groups of v_mfma_f32_16x16x32_bf16 (W as A, X as B),
 //    rows past r load as zeros (out-of-range offsets: no memory traffic).
-//  * W goes straight into VGPRs D k-steps (of 32) ahead of its MFMAs.
-//  * X, M <= 8: straight into VGPRs like W. Larger M: staged per 512-k chunk
-//    through LDS. Each wave loads whole 1 KB row pieces (contiguous reads,
-//    which the L2 serves ~3x faster per CU than 16-row fragment reads) and
-//    writes them to LDS; one barrier per chunk; the next chunk's loads are in
-//    flight while the current one is consumed.
-//  * The 4 waves take the k-steps round robin and sum their fp32 partials
+//  * gemv_rows_dma_kernel (every plain form, and the fused norm up to K =
+//    8192): weights and X rows go global -> LDS by direct-to-LDS loads in
+//    whole row pieces through a ring of k-stages, one barrier per stage.
+//  * gemv_rows_kernel (the fused norm beyond K = 8192): W straight into VGPRs
+//    D k-steps (of 32) ahead of its MFMAs; X staged per 512-k chunk through
+//    LDS in whole 1 KB row pieces (the L2 serves those ~3x faster per CU than
+//    16-row fragment reads).
+//  * The waves take the k-steps round robin and sum their fp32 partials
 //    through LDS in wave order (deterministic); the epilogue adds bias and
 //    residual or applies SwiGLU and rounds once.
 #include "gemv.h"
@@ -415,7 +415,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
 
 
 // ------------------------------------------------------------ row-owned GEMV
-constexpr int kRowsDirectMaxM = 8;   // X straight into VGPRs up to this many rows
+constexpr int kRowsDirectMaxM = 8;   // up to this many rows the row-owned kernels take any K
 constexpr int kRowsMaxK = 16384;     // staged-X kernel beats stream-K up to here (M > 8)
 constexpr int kRowsMaxRG = 4;        // at most 64 weight rows per block
 constexpr int kRowsKC = 512;         // staged X: k per LDS chunk (1 KB of each X row)
@@ -952,16 +952,15 @@ void rows_dma_launch(const RowsParams& p, int grid, hipStream_t st) {
   }
   rows_dma_launch_ks<RG, MT, SW, NORM, fits256 ? 256 : 128>(p, grid, st);
 }
+// Every plain form runs the DMA ring (at M <= 8 too: M = 1 / 8 down 20.9 ->
+// 18.1 / 23.4 -> 18.4 us, gate/up 43.3 -> 35.8 / 43.7 -> 34.9, o and q/k/v
+// 0.5-2 us faster than the register ring, outputs bit-identical); the
+// register ring stays for the fused norm past the LDS copy of its weight.
 template <int RG, int MT, bool SW>
 void rows_launch_x(const RowsParams& p, int grid, hipStream_t st) {
-  if (p.a.nw) {  // the fused norm: X through LDS
-    if (p.a.K <= kRowsDmaNormMaxK) rows_dma_launch<RG, MT, SW, true>(p, grid, st);
-    else rows_launch_d<RG, MT, SW, true, true>(p, grid, st);
-  } else if (p.a.M <= kRowsDirectMaxM) {
-    rows_launch_d<RG, 1, SW, false, false>(p, grid, st);
-  } else {
-    rows_dma_launch<RG, MT, SW, false>(p, grid, st);
-  }
+  if (p.a.nw && p.a.K > kRowsDmaNormMaxK) rows_launch_d<RG, MT, SW, true, true>(p, grid, st);
+  else if (p.a.nw) rows_dma_launch<RG, MT, SW, true>(p, grid, st);
+  else rows_dma_launch<RG, MT, SW, false>(p, grid, st);
 }
 template <bool SW>
 void rows_launch_rg(const RowsParams& p, int rg, int grid, hipStream_t st) {
