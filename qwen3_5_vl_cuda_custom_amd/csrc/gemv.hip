@@ -491,22 +491,23 @@ __device__ __forceinline__ void rows_epilogue(const RowsParams& p, const floatx4
   }
 }
 
-// NORM (staged X only): the X rows are RMS-normalised on their way in. The LDS
+// Row-owned GEMV with the RMSNorm fused (the form for K past the DMA ring's
+// LDS copy of the norm weight): W straight into a VGPR ring D k-steps ahead;
+// X staged per 512-k chunk through LDS, RMS-normalised on its way in. The LDS
 // copy holds bf16(x * w_norm); each staging lane keeps its rows' partial sums
 // of x^2 over the K it loads; the epilogue scales each row's dot products by
 // rsqrt(sum / K + eps), which equals projecting the normalised rows.
-template <int RG, int MT, bool SW, bool STAGED, int D, bool NORM>
+template <int RG, int MT, bool SW, int D>
 __global__ __launch_bounds__(256) void gemv_rows_kernel(const RowsParams p) {
-  static_assert(!NORM || STAGED, "the fused norm runs on the staged X path");
   constexpr int NW = 4;
   constexpr int RGT = SW ? 2 * RG : RG;
   constexpr int XR = 16 * MT;              // X rows of the MFMA B operand
   constexpr int XPW = XR / NW;             // staged X rows loaded per wave
   constexpr int SPC = kRowsKC / 32;        // k-steps per chunk
   constexpr int SPW = SPC / NW;            // k-steps per wave per chunk
-  __shared__ __attribute__((aligned(1024))) bf16 xs[STAGED ? 2 : 1][STAGED ? XR * kRowsKC : 8];
+  __shared__ __attribute__((aligned(1024))) bf16 xs[2][XR * kRowsKC];
   __shared__ floatx4 red[NW][RGT][MT][64];
-  __shared__ float rsum[NORM ? XR : 1];  // NORM: sum of x^2 of each X row
+  __shared__ float rsum[XR];  // sum of x^2 of each X row
   const GemvArgs& a = p.a;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -529,26 +530,21 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const RowsParams p) {
   uint32_t woff[RG];
 #pragma unroll
   for (int q = 0; q < RG; ++q) woff[q] = 16 * q + i < rows ? (uint32_t)((16 * q + i) * a.ldw * 2) : kOOB;
-  uint32_t xoff[MT];  // direct X: lane's row
-#pragma unroll
-  for (int t = 0; t < MT; ++t) xoff[t] = 16 * t + i < M ? (uint32_t)((16 * t + i) * a.ldx * 2) : kOOB;
 
-  const int S = (K + 31) / 32;              // k-steps of 32
   const int NC = (K + kRowsKC - 1) / kRowsKC;
-  // Wave step j -> k-step: staged, chunk j / SPW, in-chunk step wave + NW * (j % SPW)
-  // (every wave has NC * SPW steps; those past K load zeros); direct, wave + NW * j.
-  const int nsw = STAGED ? NC * SPW : (S - wave + NW - 1) / NW;
-  auto kstep = [&](int j) __attribute__((always_inline)) { return STAGED ? (j / SPW) * SPC + wave + NW * (j % SPW) : wave + NW * j; };
+  // Wave step j -> k-step: chunk j / SPW, in-chunk step wave + NW * (j % SPW)
+  // (every wave has NC * SPW steps; those past K load zeros).
+  const int nsw = NC * SPW;
+  auto kstep = [&](int j) __attribute__((always_inline)) { return (j / SPW) * SPC + wave + NW * (j % SPW); };
 
   bf16x8 wf[D][RGT];
-  bf16x8 xd[STAGED ? 1 : D][MT];
   floatx4 acc[RGT][MT];
 #pragma unroll
   for (int q = 0; q < RGT; ++q)
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[q][t] = floatx4{};
 
-  // Operands of wave step j into ring slot `slot`; k >= K loads zeros.
+  // W of wave step j into ring slot `slot`; k >= K loads zeros.
   auto load = [&](int j, int slot) __attribute__((always_inline)) {
     const int kk = 32 * kstep(j) + 8 * g;
     const uint32_t kmask = (uint32_t)((K - 1 - kk) >> 31) << 31;
@@ -559,72 +555,52 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const RowsParams p) {
       if constexpr (SW)
         wf[slot][RG + q] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(ru, o, 0, 0));
     }
-    if constexpr (!STAGED) {
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        const uint32_t o = (xoff[t] + (uint32_t)kk * 2u) | kmask;
-        xd[slot][t] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0));
-      }
-    }
   };
-  // Staged X, chunk c: wave loads rows wave * XPW .. + XPW, 16 B per lane of each
-  // row's 1 KB piece; lane l lands at slot l and fetches chunk l ^ (row & 15), so
-  // the fragment reads (16 rows, one chunk) hit 16 different bank groups.
-  // Two register buffers: chunk c's rows sit in xr[c & 1] from two chunks
-  // before their LDS store, so the W loads issued in between stay in flight.
-  // NORM: lane l loads chunk l of every row instead and stores it at slot
-  // l ^ (row & 15) (the same LDS layout), so one norm-weight piece per lane and
-  // chunk (wn) serves all of the lane's rows.
-  bf16x8 xr[2][STAGED ? XPW : 1];
-  bf16x8 wn[NORM ? 2 : 1];
-  float ss[NORM ? XPW : 1];
+  // X, chunk c: wave loads rows wave * XPW .. + XPW; lane l loads chunk l of
+  // every row and stores it at slot l ^ (row & 15), so the fragment reads (16
+  // rows, one chunk) hit 16 different bank groups and one norm-weight piece
+  // per lane and chunk (wn) serves all of the lane's rows. Two register
+  // buffers: chunk c's rows sit in xr[c & 1] from two chunks before their LDS
+  // store, so the W loads issued in between stay in flight.
+  bf16x8 xr[2][XPW];
+  bf16x8 wn[2];
+  float ss[XPW];
 #pragma unroll
-  for (int e = 0; e < (NORM ? XPW : 1); ++e) ss[e] = 0.f;
-  const __amdgpu_buffer_rsrc_t rn = make_rsrc(NORM ? a.nw : a.X, NORM ? (int64_t)K * 2 : 0);
+  for (int e = 0; e < XPW; ++e) ss[e] = 0.f;
+  const __amdgpu_buffer_rsrc_t rn = make_rsrc(a.nw, (int64_t)K * 2);
   auto xload = [&](int c, int rb) __attribute__((always_inline)) {
 #pragma unroll
     for (int e = 0; e < XPW; ++e) {
       const int m = wave * XPW + e;
-      const int kk = c * kRowsKC + 8 * (NORM ? lane : (lane ^ (m & 15)));
+      const int kk = c * kRowsKC + 8 * lane;
       const uint32_t o = (m < M && kk < K) ? (uint32_t)((m * a.ldx + kk) * 2) : kOOB;
       xr[rb][e] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0));
     }
-    if constexpr (NORM) {
-      const int kk = c * kRowsKC + 8 * lane;
-      wn[rb] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rn, kk < K ? (uint32_t)kk * 2u : kOOB, 0, 0));
-    }
+    const int kk = c * kRowsKC + 8 * lane;
+    wn[rb] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rn, kk < K ? (uint32_t)kk * 2u : kOOB, 0, 0));
   };
   auto xstore = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int e = 0; e < XPW; ++e) {
       const int m = wave * XPW + e;
-      if constexpr (NORM) {
-        bf16x8 y;
+      bf16x8 y;
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const float f = bf2f(xr[buf][e][q]);
-          ss[e] += f * f;
-          y[q] = f2bf(f * bf2f(wn[buf][q]));
-        }
-        *reinterpret_cast<bf16x8*>(&xs[buf][m * kRowsKC + 8 * (lane ^ (m & 15))]) = y;
-      } else {
-        *reinterpret_cast<bf16x8*>(&xs[buf][m * kRowsKC + 8 * lane]) = xr[buf][e];
+      for (int q = 0; q < 8; ++q) {
+        const float f = bf2f(xr[buf][e][q]);
+        ss[e] += f * f;
+        y[q] = f2bf(f * bf2f(wn[buf][q]));
       }
+      *reinterpret_cast<bf16x8*>(&xs[buf][m * kRowsKC + 8 * (lane ^ (m & 15))]) = y;
     }
   };
   auto comp = [&](int j, int slot) __attribute__((always_inline)) {
     bf16x8 xf[MT];
-    if constexpr (STAGED) {
-      const bf16* xb = xs[(j / SPW) & 1];
-      const int ch = 4 * (wave + NW * (j % SPW)) + g;  // 16-byte chunk of the row piece
+    const bf16* xb = xs[(j / SPW) & 1];
+    const int ch = 4 * (wave + NW * (j % SPW)) + g;  // 16-byte chunk of the row piece
 #pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        const int m = 16 * t + i;
-        xf[t] = *reinterpret_cast<const bf16x8*>(xb + m * kRowsKC + 8 * (ch ^ (m & 15)));
-      }
-    } else {
-#pragma unroll
-      for (int t = 0; t < MT; ++t) xf[t] = xd[slot][t];
+    for (int t = 0; t < MT; ++t) {
+      const int m = 16 * t + i;
+      xf[t] = *reinterpret_cast<const bf16x8*>(xb + m * kRowsKC + 8 * (ch ^ (m & 15)));
     }
 #pragma unroll
     for (int q = 0; q < RGT; ++q)
@@ -641,26 +617,24 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const RowsParams p) {
     xload(c + 2, cb);
     __syncthreads();
   };
-  if constexpr (STAGED) {
-    xload(0, 0);
-    xstore(0);
-    xload(1, 1);
-    xload(2, 0);
-  }
+  xload(0, 0);
+  xstore(0);
+  xload(1, 1);
+  xload(2, 0);
   // Loads sit outside any branch (only loop back-edges), so the compiler's
   // per-register waits keep D steps of loads in flight. The unrolled block is
-  // U steps (two chunks when staged, so chunk parities are static); the first
-  // and last blocks are peeled.
-  constexpr int U = STAGED ? 2 * SPW : D;
+  // U steps (two chunks, so chunk parities are static); the first and last
+  // blocks are peeled.
+  constexpr int U = 2 * SPW;
   static_assert(U % D == 0, "the unrolled block holds whole register rings");
   const int nfull = nsw / U;
   if (nfull >= 2) {
 #pragma unroll
     for (int jj = 0; jj < D; ++jj) load(jj, jj);
-    if constexpr (STAGED) __syncthreads();
+    __syncthreads();
 #pragma unroll
     for (int jj = 0; jj < U; ++jj) {
-      if (STAGED && jj % SPW == 0 && jj > 0) chunk(jj / SPW, (jj / SPW) & 1);
+      if (jj % SPW == 0 && jj > 0) chunk(jj / SPW, (jj / SPW) & 1);
       comp(jj, jj % D);
       load(D + jj, jj % D);
       __builtin_amdgcn_sched_barrier(0);  // keep each step's loads beside its MFMAs
@@ -668,7 +642,7 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const RowsParams p) {
     for (int j0 = U; j0 < (nfull - 1) * U; j0 += U) {
 #pragma unroll
       for (int jj = 0; jj < U; ++jj) {
-        if (STAGED && jj % SPW == 0) chunk((j0 + jj) / SPW, (jj / SPW) & 1);
+        if (jj % SPW == 0) chunk((j0 + jj) / SPW, (jj / SPW) & 1);
         comp(j0 + jj, jj % D);
         load(j0 + D + jj, jj % D);
         __builtin_amdgcn_sched_barrier(0);
@@ -677,17 +651,17 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const RowsParams p) {
     const int jl = (nfull - 1) * U;
 #pragma unroll
     for (int jj = 0; jj < U; ++jj) {
-      if (STAGED && jj % SPW == 0) chunk((jl + jj) / SPW, (jj / SPW) & 1);
+      if (jj % SPW == 0) chunk((jl + jj) / SPW, (jj / SPW) & 1);
       comp(jl + jj, jj % D);
       if (jj + D < U) load(jl + D + jj, (jj + D) % D);  // jj static: no runtime branch
       __builtin_amdgcn_sched_barrier(0);
     }
-  } else if constexpr (STAGED) {
+  } else {
     __syncthreads();
   }
   // Steps past the last full block (all of them for short K), unpipelined.
   for (int j = nfull >= 2 ? nfull * U : 0; j < nsw; ++j) {
-    if (STAGED && j % SPW == 0 && j > 0) {
+    if (j % SPW == 0 && j > 0) {
       const int c = j / SPW;
       if (c & 1) chunk(c, 1);
       else chunk(c, 0);
@@ -702,19 +676,17 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const RowsParams p) {
   for (int q = 0; q < RGT; ++q)
 #pragma unroll
     for (int t = 0; t < MT; ++t) red[wave][q][t][lane] = acc[q][t];
-  if constexpr (NORM) {
-    // The wave's rows: partial sums over its 64 lanes (each lane saw 8 of
-    // every 512 k of the row).
+  // The wave's rows: partial sums over its 64 lanes (each lane saw 8 of every
+  // 512 k of the row).
 #pragma unroll
-    for (int e = 0; e < XPW; ++e) {
-      float v = ss[e];
+  for (int e = 0; e < XPW; ++e) {
+    float v = ss[e];
 #pragma unroll
-      for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-      if (lane == 0) rsum[wave * XPW + e] = v;
-    }
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    if (lane == 0) rsum[wave * XPW + e] = v;
   }
   __syncthreads();
-  rows_epilogue<RG, MT, SW, NORM, NW, 64 * NW>(p, &red[0][0][0][0], rsum, s, n0, rows, seg_start + n0);
+  rows_epilogue<RG, MT, SW, true, NW, 64 * NW>(p, &red[0][0][0][0], rsum, s, n0, rows, seg_start + n0);
 }
 
 // ------------------------------------------------------------ row-owned GEMV, DMA ring
@@ -915,11 +887,11 @@ int device_cus() {
   return cached[dev];
 }
 
-template <int RG, int MT, bool SW, bool STAGED, bool NORM>
+template <int RG, int MT, bool SW>
 void rows_launch_d(const RowsParams& p, int grid, hipStream_t st) {
   constexpr int RGT = SW ? 2 * RG : RG;
   constexpr int D = RGT <= 4 ? 8 : 4;  // register ring: ~32-48 KB of W in flight per CU
-  hipLaunchKernelGGL((gemv_rows_kernel<RG, MT, SW, STAGED, D, NORM>), dim3(grid), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((gemv_rows_kernel<RG, MT, SW, D>), dim3(grid), dim3(256), 0, st, p);
 }
 // DMA-ring form. Longer row pieces stream faster from HBM (measured, M = 32:
 // gate/up with 512-byte pieces in 2 slots 38.2 us against 41.4 with 256-byte
@@ -958,7 +930,7 @@ void rows_dma_launch(const RowsParams& p, int grid, hipStream_t st) {
 // register ring stays for the fused norm past the LDS copy of its weight.
 template <int RG, int MT, bool SW>
 void rows_launch_x(const RowsParams& p, int grid, hipStream_t st) {
-  if (p.a.nw && p.a.K > kRowsDmaNormMaxK) rows_launch_d<RG, MT, SW, true, true>(p, grid, st);
+  if (p.a.nw && p.a.K > kRowsDmaNormMaxK) rows_launch_d<RG, MT, SW>(p, grid, st);
   else if (p.a.nw) rows_dma_launch<RG, MT, SW, true>(p, grid, st);
   else rows_dma_launch<RG, MT, SW, false>(p, grid, st);
 }

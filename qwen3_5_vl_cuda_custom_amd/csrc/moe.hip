@@ -92,43 +92,71 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const bf16* __restrict__
   const float inv = 1.0f / s;
 #pragma unroll
   for (int i = 0; i < MAXV; ++i) v[i] *= inv;
-  float sel_sum = 0.f;
-  float sel_v[32];
-  for (int r = 0; r < k; ++r) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
+  // Top-k by threshold (the same k entries in the same order as k rounds of a
+  // wave arg-max, without their shuffle chains). Probabilities are >= +0, so
+  // they order as their bit patterns: thr = the k-th largest key, found by a
+  // binary search over the bits with ballot counts. The entries above thr and
+  // the lowest-index entries equal to it make the k; each then takes its place
+  // (larger first, lower expert index among equals) by comparing itself with
+  // the selected entries one at a time.
+  uint32_t key[MAXV];
 #pragma unroll
-    for (int i = 0; i < MAXV; ++i) {
-      const int e = lane + 64 * i;
-      if (live[i] && (v[i] > bv || (v[i] == bv && e < bi))) {
-        bv = v[i];
-        bi = e;
-      }
+  for (int i = 0; i < MAXV; ++i) key[i] = __float_as_uint(v[i]);
+  uint32_t thr = 0;
+  for (int bit = 30; bit >= 0; --bit) {
+    const uint32_t cand = thr | (1u << bit);
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < MAXV; ++i) c += __builtin_popcountll(__ballot(live[i] && key[i] >= cand));
+    if (c >= k) thr = cand;
+  }
+  int need = k;  // entries equal to thr that are taken, lowest index first
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) need -= __builtin_popcountll(__ballot(live[i] && key[i] > thr));
+  bool sel[MAXV];
+  int eq_before = 0;
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) {
+    const uint64_t eq = __ballot(live[i] && key[i] == thr);
+    const int below = eq_before + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(eq >> 32),
+                                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)eq, 0u));
+    sel[i] = live[i] && (key[i] > thr || (key[i] == thr && below < need));
+    eq_before += __builtin_popcountll(eq);
+  }
+  int pos[MAXV];
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) pos[i] = 0;
+#pragma unroll
+  for (int j = 0; j < MAXV; ++j) {
+    uint64_t m = __ballot(sel[j]);
+    while (m) {
+      const int l = __builtin_ctzll(m);
+      m &= m - 1;
+      const uint32_t ky = (uint32_t)__builtin_amdgcn_readlane((int)key[j], l);
+      const int ey = l + 64 * j;
+#pragma unroll
+      for (int i = 0; i < MAXV; ++i) pos[i] += (ky > key[i] || (ky == key[i] && ey < lane + 64 * i)) ? 1 : 0;
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, 64);
-      const int oi = __shfl_xor(bi, o, 64);
-      if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < MAXV; ++i)
-      if (lane + 64 * i == bi) live[i] = false;
-    sel_v[r] = bv;
-    if (lane == 0) top_idx[(int64_t)t * k + r] = bi;
   }
   // Renormalise: the sum runs over the selected values in selection order.
-  for (int r = 0; r < k; ++r) sel_sum += sel_v[r];
-  if (lane == 0) {
-    for (int r = 0; r < k; ++r) {
-      const float w = norm ? sel_v[r] / sel_sum : sel_v[r];
-      top_w[(int64_t)t * k + r] = f2bf(w);
-      if (top_p) top_p[(int64_t)t * k + r] = sel_v[r];
+  float sel_sum = 0.f;
+  for (int r = 0; r < k; ++r) {
+    uint32_t vr = 0;
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+      const uint64_t m = __ballot(sel[j] && pos[j] == r);
+      if (m) vr = (uint32_t)__builtin_amdgcn_readlane((int)key[j], __builtin_ctzll(m));
     }
+    sel_sum += __uint_as_float(vr);
   }
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i)
+    if (sel[i]) {
+      const int64_t o = (int64_t)t * k + pos[i];
+      top_idx[o] = lane + 64 * i;
+      top_w[o] = f2bf(norm ? v[i] / sel_sum : v[i]);
+      if (top_p) top_p[o] = v[i];
+    }
 }
 
 // ------------------------------------------------------------------ permute
