@@ -198,38 +198,42 @@ __global__ __launch_bounds__(64) void moe_hist_kernel(const int* __restrict__ to
   for (int e = lane; e < E; e += 64) hist[(int64_t)c * E + e] = s_cnt[e];
 }
 
-// In-place exclusive scan of a[0, n) in LDS, n <= 2 * blockDim.x; tmp holds
-// blockDim.x ints. Returns the total. Every thread of the block calls it.
-__device__ int lds_excl_scan(int* a, int n, int* tmp) {
-  const int t = threadIdx.x, B = blockDim.x;
-  const int a0 = 2 * t < n ? a[2 * t] : 0, a1 = 2 * t + 1 < n ? a[2 * t + 1] : 0;
-  tmp[t] = a0 + a1;
-  __syncthreads();
-  for (int o = 1; o < B; o <<= 1) {
-    const int v = t >= o ? tmp[t - o] : 0;
-    __syncthreads();
-    tmp[t] += v;
-    __syncthreads();
+// Exclusive scan of a[0, n) in LDS by one wave (lane l takes a contiguous
+// run of ceil(n / 64) entries); returns the total to every lane.
+__device__ int wave_excl_scan(int* a, int n) {
+  const int lane = threadIdx.x & 63;
+  const int per = (n + 63) / 64, b0 = lane * per;
+  int loc = 0;
+  for (int i = 0; i < per; ++i)
+    if (b0 + i < n) loc += a[b0 + i];
+  int incl = loc;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int v = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += v;
   }
-  const int excl = tmp[t] - (a0 + a1);
-  const int total = tmp[B - 1];
-  __syncthreads();
-  if (2 * t < n) a[2 * t] = excl;
-  if (2 * t + 1 < n) a[2 * t + 1] = excl + a0;
-  __syncthreads();
-  return total;
+  int run = incl - loc;
+  for (int i = 0; i < per; ++i)
+    if (b0 + i < n) {
+      const int x = a[b0 + i];
+      a[b0 + i] = run;
+      run += x;
+    }
+  return __shfl(incl, 63, 64);
 }
 
 // One block of 1024 threads: per-expert counts and offsets (exclusive scan),
 // each chunk's first position per expert, and the m-tile table of the grouped
 // GEMMs (tiles of kMoeBM rows, expert-major). Thread (g, e) sums the chunk
 // range g of expert e (G = 1024 / E ranges; independent loads), so the chunk
-// prefix per expert is a short scan over the ranges.
+// prefix per expert is a short scan over the ranges; the two scans over the
+// experts run on one wave each (with a block-wide scan over 1024 threads,
+// ~40 barriers, the dispatch took 21.7 us at C4 against 18.7).
 __global__ __launch_bounds__(1024) void moe_plan_kernel(const int* __restrict__ hist, int NC, int E,
                                                         int* __restrict__ counts, int* __restrict__ offsets,
                                                         int* __restrict__ cstart, int* __restrict__ tile_table,
                                                         int* __restrict__ n_tiles) {
-  __shared__ int s_off[2048], s_til[2048], s_tmp[1024], s_part[1024];
+  __shared__ int s_off[2048], s_til[2048], s_part[1024], s_tot[2];
   const int tid = threadIdx.x;
   const int G = E <= 1024 ? 1024 / E : 1;  // chunk ranges per expert
   // Partial sums (for E > 1024 one range per expert, thread strides over experts).
@@ -266,8 +270,16 @@ __global__ __launch_bounds__(1024) void moe_plan_kernel(const int* __restrict__ 
     s_til[e] = (s_off[e] + kMoeBM - 1) / kMoeBM;
   }
   __syncthreads();
-  const int rows = lds_excl_scan(s_off, E, s_tmp);
-  const int tiles = lds_excl_scan(s_til, E, s_tmp);
+  // The two scans over the experts, one wave each.
+  if (tid < 64) {
+    const int tot = wave_excl_scan(s_off, E);
+    if (tid == 0) s_tot[0] = tot;
+  } else if (tid < 128) {
+    const int tot = wave_excl_scan(s_til, E);
+    if (tid == 64) s_tot[1] = tot;
+  }
+  __syncthreads();
+  const int rows = s_tot[0], tiles = s_tot[1];
   for (int e = tid; e < E; e += 1024) {
     const int off = s_off[e];
     offsets[e] = off;
