@@ -898,8 +898,9 @@ void rows_launch_d(const RowsParams& p, int grid, hipStream_t st) {
 // pieces in 5; down, K = 12288, with 1 KB pieces 25.0 against 26.1 with 512
 // bytes), so a stage takes the longest k that leaves at least two slots in
 // 144 KB: 512 for one plain row group over K >= 8192, else 256, else 128. As
-// many slots as fit (at most 6); 8 waves (two per SIMD) where the DMA count
-// splits evenly.
+// many slots as fit, at most 3 (deeper rings were no faster: the B=32 decode
+// step 209.3 us with at most 3, 209.7 with 4, 210.2 with 6); 8 waves (two per
+// SIMD) where the DMA count splits evenly.
 template <int RG, int MT, bool SW, bool NORM, int KS>
 void rows_dma_launch_ks(const RowsParams& p, int grid, hipStream_t st) {
   constexpr int RGT = SW ? 2 * RG : RG;
@@ -907,7 +908,7 @@ void rows_dma_launch_ks(const RowsParams& p, int grid, hipStream_t st) {
   constexpr int SLOT = (16 * RGT / RPI + 16 * MT / RPI) * 1024;
   constexpr int WNB = NORM ? kRowsDmaNormMaxK * 2 : 0;
   constexpr int NS0 = (144 * 1024 - WNB) / SLOT;
-  constexpr int NS = NS0 > 6 ? 6 : NS0;
+  constexpr int NS = NS0 > 3 ? 3 : NS0;
   constexpr int NW = MT == 2 && (16 * RGT / RPI + 16 * MT / RPI) % 8 == 0 ? 8 : 4;  // 8: 2 waves per SIMD
   hipLaunchKernelGGL((gemv_rows_dma_kernel<RG, MT, SW, NORM, KS, NS, NW>), dim3(grid), dim3(64 * NW), 0, st, p);
 }

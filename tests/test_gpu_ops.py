@@ -669,6 +669,23 @@ def test_moe_route_exact_indices():
     assert_bf16_close(w, rv / rv.sum(-1, keepdim=True), max_abs=4e-3, what="routing weights")
 
 
+@pytest.mark.parametrize("E,k,norm", [(8, 1, True), (8, 8, True), (64, 4, False), (100, 8, True), (256, 32, True),
+                                      (500, 16, False), (500, 32, True)])
+def test_moe_route_ties_and_widths(E, k, norm):
+    """Routing at expert counts of 1-8 registers per lane and k up to 32. The logits are
+    multiples of 1/4, so equal logits give exactly equal probabilities (ties, which the
+    lower expert index wins) and unequal ones differ by a factor >= e^0.25, which no
+    summation order can reorder: the indices are bit-exact against the oracle's top-k."""
+    g = torch.Generator().manual_seed(1000 + E + k)
+    logits = ((torch.randn(333, E, generator=g) * 2 * 4).round() / 4).to(torch.bfloat16)
+    idx, w = K.moe_route(gpu(logits), k, norm)
+    probs = O.softmax(logits.float())
+    rv, ri = O.topk(probs, k)
+    assert torch.equal(idx.cpu().long(), ri), f"top-k indices E={E} k={k}"
+    ref = rv / rv.sum(-1, keepdim=True) if norm else rv
+    assert_bf16_close(w, ref, max_abs=4e-3, what=f"routing weights E={E} k={k}")
+
+
 @pytest.mark.parametrize("T,H,E,k", [(4096, 2048, 128, 8), (1000, 2048, 128, 8), (333, 1024, 64, 4), (77, 520, 96, 2)])
 def test_moe_router_split_k(T, H, E, k):
     """The router with its logits GEMM split over K: logits against the fp32 oracle's linear,
