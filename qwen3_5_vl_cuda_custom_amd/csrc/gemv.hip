@@ -699,8 +699,9 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const RowsParams p) {
 // issues at about half the rate. NS stages in a ring keep NS - 1 of them in
 // flight; no VGPRs hold in-flight data. The lane that lands at 16-byte slot c
 // of row r fetches chunk c ^ (r & 15), so the 16 rows of a fragment read hit
-// 16 different bank groups. The 4 waves take the stage's k-steps round robin,
-// one barrier per stage, and sum their fp32 partials in wave order.
+// 16 different bank groups. The 4 waves of a group take the stage's k-steps
+// round robin (8 waves: two groups, one per X tile), one barrier per stage,
+// and sum their fp32 partials in wave order.
 // NORM: the RMSNorm weight sits in LDS for the whole call (K <= 8192); each
 // X fragment becomes bf16(x * w_norm) on its way into the MFMA, the lane keeps
 // the sum of x^2 over the k it sees, and the epilogue scales the row's dot
