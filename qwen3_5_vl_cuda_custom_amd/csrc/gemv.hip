@@ -804,14 +804,19 @@ __global__ __launch_bounds__(64 * NW) void gemv_rows_dma_kernel(const RowsParams
   for (int t = 0; t < TT; ++t) ss[t] = 0.f;
   const int t0 = NG == 1 ? 0 : h;  // first X tile of the wave
 
+  // Only stages below nst are issued, so at stage st at most one later stage
+  // (NS <= 3) is in flight, none at the last.
+  static_assert(NS <= 3, "the waits below count at most one stage in flight after st");
   const int nst = (K + KS - 1) / KS;
 #pragma unroll
-  for (int st = 0; st < NS - 1; ++st) issue(st, st);
+  for (int st = 0; st < NS - 1; ++st)
+    if (st < nst) issue(st, st);
   int cs = 0;  // ring slot of stage st
   for (int st = 0; st < nst; ++st) {
-    vm_wait<(NS - 2) * IPW>();  // this wave's pieces of stage st have landed
-    __syncthreads();            // everyone's have; everyone is done with stage st - 1
-    issue(st + NS - 1, cs == 0 ? NS - 1 : cs - 1);  // past the last stage: zeros, no traffic
+    if (st == nst - 1) vm_wait<0>();      // this wave's pieces of stage st have landed
+    else vm_wait<(NS - 2) * IPW>();
+    __syncthreads();  // everyone's have; everyone is done with stage st - 1
+    if (st + NS - 1 < nst) issue(st + NS - 1, cs == 0 ? NS - 1 : cs - 1);
     const char* sb = lds + cs * SLOT;
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
@@ -843,8 +848,8 @@ __global__ __launch_bounds__(64 * NW) void gemv_rows_dma_kernel(const RowsParams
     cs = cs + 1 == NS ? 0 : cs + 1;
   }
 
-  // The ring becomes the partials' buffer once the trailing (all-zero) stages
-  // have landed and every wave is past its last fragment read. Partials are
+  // The ring becomes the partials' buffer once every wave is past its last
+  // fragment read (no load is outstanding after the last stage's wait). Partials are
   // laid out [wave of the group][q][X tile][lane] and summed over the group's
   // 4 waves in order.
   vm_wait<0>();
