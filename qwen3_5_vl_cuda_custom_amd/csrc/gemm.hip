@@ -139,9 +139,12 @@ int launch_tiled_cfg(GemmParams p, int64_t batch, hipStream_t st) {
 // decoder layer 1464.9 -> 1395.1 us (gate/up 633 -> 608, down 326 -> 307, o
 // 121 -> 116, q/k/v on 256x192); S=1024 475.7 -> 469.2 us. The MoE expert
 // tiles stay on 32x32x16: no faster with it. (The 128x128 deep ring and the
-// 128x256 tiles take it in their own forms: launch_c, launch_d.) (The 256x192 tiles' former fourth W slot, worth 3% to q/k/v,
-// gives way: the 16x16x32 loop needs the W ring exactly one slot deeper than
-// the X ring.)
+// 128x256 tiles take it in their own forms: launch_c, launch_d.)
+//
+// The 128x256 tiles on that loop keep a fourth W slot (2 X + 4 W slots of 64-wide
+// stages, 160 KB): M=1024 gate/up 185.1 -> 181.5 us, q/k/v 56.6 -> 55.2 us, the
+// S=1024 layer 461 -> 450 us, bit-identical. A fourth W slot for the 256x192
+// tiles (also 160 KB) measured no faster: M=4096 q/k/v 166.0 -> 166.7 us.
 template <int EPI>
 int launch_tiled(GemmParams p, int64_t batch, hipStream_t st) {
   constexpr int kCUs = 256;
@@ -167,7 +170,7 @@ int launch_tiled(GemmParams p, int64_t batch, hipStream_t st) {
                   : launch_tiled_cfg<128, 128, 2, 2, EPI, 4, 32>(p, batch, st);
   };
   auto launch_d = [&]() {
-    return p.K >= 2048 ? launch_tiled_cfg<128, 256, 2, 4, EPI, 2, 64, 3, true>(p, batch, st)
+    return p.K >= 2048 ? launch_tiled_cfg<128, 256, 2, 4, EPI, 2, 64, 4, true>(p, batch, st)
                        : launch_tiled_cfg<128, 256, 2, 4, EPI, 3, 64>(p, batch, st);
   };
   if constexpr (EPI == kEpiSwiGLU) {

@@ -594,7 +594,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
     // wave). Two K steps per stage: the first carries W(kt + NST), the last
     // crosses the barrier as in the 32x32 loop (its first NQ MFMAs use every
     // fragment of the step) and carries X(kt + NST).
-    static_assert(BKT == 64 && NSTW == NST + 1, "16x16x32 loop: 64-wide stages, W ring one slot deeper");
+    static_assert(BKT == 64 && (NSTW == NST + 1 || (NSTW == NST + 2 && NST == 2)),
+                  "16x16x32 loop: 64-wide stages, W ring one slot deeper (two with two X slots)");
     constexpr int T16N = WTN / 16, T16M = WTM / 16;
     constexpr int NQ = T16N > T16M ? T16N : T16M;
     constexpr int NM16 = T16N * T16M;
@@ -640,7 +641,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
       issue_w(j);
       issue_x(j);
     }
-    vm_wait<(NST - 1) * (PX + PW)>();  // stage 0 has landed
+    if constexpr (NSTW == NST + 2) issue_w(NST);  // W one stage further ahead
+    vm_wait<(NST - 1) * (PX + PW) + (NSTW - NST - 1) * PW>();  // stage 0 has landed
     __syncthreads();
 
     // Wave priority (256-row and 128x256 tiles), falling from one stage barrier to the
@@ -667,7 +669,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
       }
       for (int kt = 0; kt < nk; ++kt) {
         if constexpr (kPrio) __builtin_amdgcn_s_setprio(1);
-        // step 0: W(kt + NST) between the MFMAs, step 1's fragments read ahead
+        // step 0: W(kt + NSTW - 1) between the MFMAs, step 1's fragments read ahead
         constexpr int gw = (NM16 + PW - 1) / PW;
         int d = 0;
         __builtin_amdgcn_sched_barrier(0);
@@ -681,13 +683,13 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
               if (kPrio && m == NM16 / 2) __builtin_amdgcn_s_setprio(0);
               if (m < T16N) rd_w(1, kt, 1, m);
               if (i == T16N - 1) rd_x(kt, 1, j);
-              if (d < PW && m % gw == gw - 1) dma_w16(kt + NST, d++);
+              if (d < PW && m % gw == gw - 1) dma_w16(kt + NSTW - 1, d++);
               __builtin_amdgcn_sched_barrier(0);
             }
           }
         }
 #pragma unroll
-        for (; d < PW; ++d) dma_w16(kt + NST, d);
+        for (; d < PW; ++d) dma_w16(kt + NSTW - 1, d);
         __builtin_amdgcn_sched_barrier(0);
         // step 1: the NQ MFMAs that use every fragment, the barrier, then the
         // rest with stage kt + 1's first-step reads and X(kt + NST)
