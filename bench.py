@@ -57,12 +57,18 @@ def time_gpu(fn, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
-def time_launch_modes(step, first, steps: int, warmup: int):
+def time_launch_modes(step, first, steps: int, warmup: int, warm_s: float = 0.0):
     """Time `step` with eager launches, then replayed from a HIP graph, each
     as max(HIP events, host wall) per step. `first(out)` picks the tensor of a
     step's output that every replay must reproduce bit for bit (checked before
     and after the timed replays). Returns (ms, ms_eager, ms_graph, launch):
     the faster mode's time, both times, and which mode that was.
+
+    `warm_s` > 0 keeps warming up past `warmup` steps until that much wall time
+    of back-to-back steps has passed (each mode): a GPU coming from idle runs
+    its first ~40 ms of load at a lower clock, which a short step's few
+    warm-up steps do not cover (the S=1024 layer measured ~0.51 ms after 2
+    warm-up steps against ~0.46 ms in steady rounds).
 
     On a box whose host is slow or contended, eager launches have left the GPU
     idle between kernels (3.2 ms per S=4096 layer against 1.5 with every kernel
@@ -79,8 +85,17 @@ def time_launch_modes(step, first, steps: int, warmup: int):
         torch.cuda.synchronize()
         return max(ms_events, (time.perf_counter() - t0) * 1e3 / steps)
 
-    for _ in range(warmup):
-        step()
+    def warm(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < warm_s:
+            for _ in range(4):
+                fn()
+            torch.cuda.synchronize()
+
+    warm(step)
     ms_eager = timed(step)
     ref = first(step()).clone()
     graph = StepGraph(step)
@@ -88,8 +103,7 @@ def time_launch_modes(step, first, steps: int, warmup: int):
     torch.cuda.synchronize()
     if not torch.equal(first(graph.out), ref):
         raise RuntimeError("bench: the graph replay of the step differs from the eager step")
-    for _ in range(warmup):
-        graph.replay()
+    warm(graph.replay)
     ms_graph = timed(graph.replay)
     if not torch.equal(first(graph.out), ref):
         raise RuntimeError("bench: a timed graph replay of the step differs from the eager step")
@@ -269,14 +283,16 @@ def other_configs(torch, W, dev: str, warmup: int, cases: dict) -> dict:
     """The other BASELINE configurations, one GPU each: C2 at S=1024 and 16384,
     the C4 MoE layer (4096 tokens) and the C5 patch embed + vision block. Each
     takes the faster of eager launches and a HIP graph replay (both reported,
-    the replay checked bit-identical to the eager step)."""
+    the replay checked bit-identical to the eager step), each mode after
+    0.25 s of back-to-back warm-up steps (steady clock)."""
     out = {}
     for S in (1024, 16384):
         cfg = W.C2
         layer = W.make_text_layer(cfg, torch.bfloat16, dev, seed=0)
         x, pos = W.text_inputs(cfg, 1, S, torch.bfloat16, dev, seed=0)
         b = W.make_rope(cfg, dev).bind(pos)
-        ms, me, mg, launch = time_launch_modes(lambda: layer(x, b), lambda o: o[0], 5, max(2, warmup // 2))
+        ms, me, mg, launch = time_launch_modes(lambda: layer(x, b), lambda o: o[0], 5 if S > 4096 else 20,
+                                                max(2, warmup // 2), warm_s=0.25)
         fl = cfg.gemm_flops_per_token() * S + cfg.causal_attn_flops(S)
         out[f"c2_prefill_s{S}"] = {"ms": round(ms, 4), "tok_s": round(S / (ms / 1e3), 1),
                                    "tflops": round(fl / (ms / 1e3) / 1e12, 1),
@@ -290,7 +306,7 @@ def other_configs(torch, W, dev: str, warmup: int, cases: dict) -> dict:
     b = W.make_rope(cfg, dev).bind(pos)
     y, logits, _ = layer(x, b)
     cases["c4_moe_layer_t4096"] = text_layer_case(cfg, layer, x, pos, y, router_logits=logits)
-    ms, me, mg, launch = time_launch_modes(lambda: layer(x, b), lambda o: o[0], 10, warmup)
+    ms, me, mg, launch = time_launch_modes(lambda: layer(x, b), lambda o: o[0], 20, warmup, warm_s=0.25)
     fl = cfg.gemm_flops_per_token() * 4096 + cfg.causal_attn_flops(4096)
     # Both bounds: MFMA on the layer's FLOPs, HBM on the bytes it must move at
     # least once (every weight, the token activations in and out).
@@ -327,7 +343,7 @@ def other_configs(torch, W, dev: str, warmup: int, cases: dict) -> dict:
                               sin=sc, eps=v.eps, rd=rd)
     cases["c5_vision_patch_embed_block"] = (yv.detach().float().cpu(), run_vis)
 
-    ms, me, mg, launch = time_launch_modes(vis, lambda o: o, 10, warmup)
+    ms, me, mg, launch = time_launch_modes(vis, lambda o: o, 40, warmup, warm_s=0.25)
     fl = v.flops()
     n = v.images * v.patches_per_image
     out["c5_vision_patch_embed_block"] = {"ms": round(ms, 4), "patches_s": round(n / (ms / 1e3), 1),
