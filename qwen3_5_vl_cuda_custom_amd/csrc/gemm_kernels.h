@@ -747,6 +747,10 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
   acc.zero();
   const int l32 = lane & 31, h = lane >> 5;
   const int rn = wn * WTN, rm = wm * WTM;
+  // A grouped tile's wave with fewer than WTM rows (an expert's last m-tile) runs the
+  // partial form (active_c == 2): the MFMAs of its 32-row blocks past the rows are
+  // skipped by uniform branches; the others run in the same order as in a full tile.
+  const int nact = __builtin_amdgcn_readfirstlane(min(TM, max(0, (rows_m - rm + 31) / 32)));
   bf16x8 fa[2][TN], fb[2][TM];
   // ACTIVE: the wave's m-range holds rows of the tile. A wave without rows still
   // issues its share of the DMAs and joins every barrier, but reads no fragments
@@ -769,16 +773,19 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
   };
   auto mma = [&](auto active_c, int buf) {
     if constexpr (!decltype(active_c)::value) return;
+    constexpr bool kPart = decltype(active_c)::value == 2;
 #pragma unroll
     for (int i = 0; i < TN; ++i)
 #pragma unroll
-      for (int j = 0; j < TM; ++j) acc.c[i][j] = mfma32x32x16(fa[buf][i], fb[buf][j], acc.c[i][j]);
+      for (int j = 0; j < TM; ++j)
+        if (!kPart || j < nact) acc.c[i][j] = mfma32x32x16(fa[buf][i], fb[buf][j], acc.c[i][j]);
   };
   // The stage's last k16 step with the next DMAs spread between its MFMAs
   // (one DMA after each MFMA, order pinned), so the matrix core is not idle
   // while a burst of DMA instructions issues after the barrier.
   auto last_step = [&](auto active_c, int buf, int kt) {  // issues the group of stage kt: X(kt + NST), W(kt + NSTW)
     constexpr bool kActive = decltype(active_c)::value;
+    constexpr bool kPart = decltype(active_c)::value == 2;
     constexpr int ND = PX + PW;
     const int kx = (kt + NST) * BKT + dc * 8, kw = (kt + NSTW) * BKT + dc * 8;
     const uint32_t sbx = xslot(kt + NST), sbw = wslot(kt + NSTW);
@@ -806,7 +813,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
       for (int i = 0; i < TN; ++i)
 #pragma unroll
         for (int j = 0; j < TM; ++j) {
-          acc.c[i][j] = mfma32x32x16(fa[buf][i], fb[buf][j], acc.c[i][j]);
+          if (!kPart || j < nact) acc.c[i][j] = mfma32x32x16(fa[buf][i], fb[buf][j], acc.c[i][j]);
           if (d < ND) dma(d++);
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -860,6 +867,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
   // W(kt + NST), evenly between the MFMAs; order pinned.
   auto step_w = [&](auto active_c, int buf, int kt, int ks) {
     constexpr bool kActive = decltype(active_c)::value;
+    constexpr bool kPart = decltype(active_c)::value == 2;
     constexpr int NR = TN + TM, NM = TN * TM;
     const int d0 = ks * PW / kWSteps, d1 = (ks + 1) * PW / kWSteps;
     const int nd = d1 - d0;
@@ -869,7 +877,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
     if constexpr (kActive) {
 #pragma unroll
       for (int m = 0; m < NM; ++m) {
-        acc.c[m / TM][m % TM] = mfma32x32x16(fa[buf][m / TM], fb[buf][m % TM], acc.c[m / TM][m % TM]);
+        if (!kPart || m % TM < nact)
+          acc.c[m / TM][m % TM] = mfma32x32x16(fa[buf][m / TM], fb[buf][m % TM], acc.c[m / TM][m % TM]);
         if (m < NR) read_one(buf ^ 1, kt, ks + 1, m);
         if (d < d1 && m % gap == gap - 1) dma_w(kt + NST, d++);
         __builtin_amdgcn_sched_barrier(0);
@@ -891,6 +900,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
   // accumulator still takes exactly one MFMA per step: same results.
   auto last_step_x = [&](auto active_c, int buf, int kt) {
     constexpr bool kActive = decltype(active_c)::value;
+    constexpr bool kPart = decltype(active_c)::value == 2;
     constexpr int NM = TN * TM, NR = TN + TM;
     constexpr int NQ = TN > TM ? TN : TM;
     const int kx = (kt + NST) * BKT + dc * 8;
@@ -903,7 +913,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
       const int a = q % NQ, dg = q / NQ;
       const int i = TN >= TM ? a : (a + dg) % TN;
       const int j = TN >= TM ? (a + dg) % TM : a;
-      acc.c[i][j] = mfma32x32x16(fa[buf][i], fb[buf][j], acc.c[i][j]);
+      if (!kPart || j < nact) acc.c[i][j] = mfma32x32x16(fa[buf][i], fb[buf][j], acc.c[i][j]);
     };
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (kActive) {
@@ -969,7 +979,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
           }
           read(active_c, (ks + 1) & 1, kt, ks + 1);
           mma(active_c, ks & 1);
-          if constexpr (decltype(active_c)::value) interleave();
+          if constexpr (decltype(active_c)::value == 1) interleave();
         } else if constexpr (kSpreadW) {
           last_step_x(active_c, ks & 1, kt);  // crosses the barrier; X(kt + NST) into the slot stage kt released
         } else {
@@ -981,10 +991,15 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmPa
       }
     }
   };
-  if (rm < rows_m)
-    main_loop(std::true_type{});
-  else
+  if (rm >= rows_m)
     main_loop(std::false_type{});
+  else if constexpr (GROUPED) {
+    if (nact < TM)
+      main_loop(std::integral_constant<int, 2>{});
+    else
+      main_loop(std::true_type{});
+  } else
+    main_loop(std::true_type{});
   vm_wait<0>();  // the trailing zero-fill DMAs must land before the block's LDS is reused
 
   auto visit = [&](auto&& f) { visit_acc32<EPI, WTM, WTN, TN, TM>(acc.c, wm, wn, lane, f); };
