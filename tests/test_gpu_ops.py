@@ -747,6 +747,33 @@ def test_moe_experts_skewed_routing():
     assert_bf16_close(out, ref[0], what="moe_experts skewed")
 
 
+
+def test_moe_experts_tile_row_counts():
+    """Expert row counts on both sides of every 32-row block and 128-row half of a 256-row
+    m-tile (a wave of the grouped tiles holds 128 rows as four 32-row blocks, and skips the
+    MFMAs of the blocks past its rows), plus one expert that takes every token's second
+    choice (2052 rows: eight full m-tiles and one of 4 rows)."""
+    from oracle.layers import sparse_moe
+    counts = [1, 31, 32, 33, 97, 128, 129, 161, 255, 256, 257, 289, 383]
+    E, T, H, I, k = len(counts) + 1, sum(counts), 256, 128, 2
+    g = torch.Generator().manual_seed(83)
+    x = torch.randn(1, T, H, generator=g).to(torch.bfloat16)
+    p = {"gate_weight": (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16),
+         "gate_up_proj": (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(torch.bfloat16),
+         "down_proj": (torch.randn(E, H, I, generator=g) * 0.02).to(torch.bfloat16)}
+    first = torch.repeat_interleave(torch.arange(len(counts)), torch.tensor(counts))
+    first = first[torch.randperm(T, generator=g)]
+    logits = torch.randn(T, E, generator=g)
+    logits[torch.arange(T), first] += 18.0
+    logits[:, E - 1] += 16.0  # every token's second choice (weights ~0.88 / ~0.12)
+    logits = logits.to(torch.bfloat16)
+    idx, w = K.moe_route(gpu(logits), k, True)
+    assert torch.bincount(idx.long().flatten().cpu(), minlength=E).tolist() == counts + [T]
+    out = K.moe_experts(gpu(x[0]), gpu(p["gate_up_proj"]), gpu(p["down_proj"]), idx, w)
+    pf = {n: f32(t) for n, t in p.items()}
+    ref, _ = sparse_moe(f32(x), pf, top_k=k, router_logits=logits.float())
+    assert_bf16_close(out, ref[0], what="moe_experts tile row counts")
+
 # ------------------------------------------------------------------ prefill chunk over a KV cache
 @pytest.mark.parametrize("Hq,Hkv,D,dtype,Sq,cap", [
     (8, 2, 128, torch.bfloat16, 77, 300),   # groups 4: the eight-wave pipelined kernel
