@@ -93,6 +93,8 @@ def test_matmul_split_k(M, N, Kd, bias, res):
     (1024, 12288, 4096, True),   # the S=1024 gate/up: 768 tiles of 128x256 on the 16x16x32 loop
     (1000, 6000, 4096, False),   # q/k/v-sized, ragged M and N: 128x256 tiles, 16x16x32 loop, bias
     (1024, 6144, 1024, False),   # K < 2048: the same tiles on the 32x32x16 loop
+    (1000, 6000, 2056, False),   # the 16x16x32 loop's shortest K loops, a 8-wide last stage
+    (1024, 12288, 2104, True),   # (its W ring runs two stages ahead of X: 2 X + 4 W slots)
 ])
 def test_matmul_128x256_tiles(M, N, Kd, swiglu):
     std = Kd ** -0.5
