@@ -113,7 +113,7 @@ int launch_tiled_cfg(GemmParams p, int64_t batch, hipStream_t st) {
 // MI355X): 256x256 (8 waves, 64-wide K stages: 2 X slots, 3 W slots, the
 // whole 160 KB of LDS; 1 block per CU) 1.0,
 // 128x256 (8 waves, 64-wide K stages; over K >= 2048 the 16x16x32 loop with
-// 2 X and 3 W slots and the wave priority of the 256-row tiles, else the
+// 2 X and 4 W slots and the wave priority of the 256-row tiles, else the
 // 32x32x16 loop with 3 stages, 144 KB. The third stage hides the HBM latency
 // of weights read once per layer: with weights rotated past the MALL, M=1024
 // gate/up 243 -> 189 us, M=4096 o 165 -> 131 us. The 16x16x32 form with the
