@@ -101,7 +101,7 @@ template <int BM, int BN, int WM, int WN, int EPI, int NST, int BKT, int NSTW = 
 int launch_tiled_cfg(GemmParams p, int64_t batch, hipStream_t st) {
   constexpr int BN_OUT = (EPI == kEpiSwiGLU) ? BN / 2 : BN;
   const int64_t tiles = q3_cdiv(p.M, BM) * q3_cdiv(p.N, BN_OUT);
-  p.group_m = 8;
+  p.group_m = 4;  // 4 along M: S=4096 gate/up 587 -> 582 us, o 112 -> 110, S=1024 layer 430.6 -> 425.4 (8 and 16: slower)
   hipLaunchKernelGGL((gemm_bf16_dma_kernel<BM, BN, WM, WN, EPI, false, NST, BKT, NSTW, MF16>),
                      dim3((unsigned)tiles, 1, (unsigned)batch), dim3(WM * WN * 64), 0, st, p);
   Q3_LAUNCH_CHECK();
